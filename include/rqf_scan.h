@@ -1,0 +1,189 @@
+/*
+ * rqf_scan.h -- C ABI of the MI355X (gfx950) complex linear-recurrence scan
+ * library (librqf_hip.so).
+ *
+ * Each entry point replaces one host->device launch of the reference's
+ * Triton kernels (Sequel-Institute/prospective-rqf, rqf_models/ops/).  The
+ * citations name the launch site being replaced.
+ *
+ * Conventions
+ *   - All pointers are device pointers into caller-owned memory.  The library
+ *     never allocates device memory.  Where scratch is needed, a *_workspace()
+ *     query returns its size and the caller passes the buffer in.
+ *   - Complex tensors are complex64 stored interleaved (re, im) as float
+ *     pairs.  Every tensor is dense and C-contiguous in the layout named.
+ *   - "FBT" layout: element (f, b, t) at (f*B + b)*T + t (channel-outermost).
+ *     "BTF" layout: element (b, t, f) at (b*T + t)*F + f.
+ *   - Launches are asynchronous on `stream` (a hipStream_t; NULL is the null
+ *     stream).  No function synchronises the host.
+ *   - Return value: RQF_OK (0) on success; a negative RQF_ERR_* for a bad
+ *     argument; a positive hipError_t when a launch fails.
+ *   - Results are deterministic: coefficient gradients are reduced from
+ *     per-row partial sums in a fixed order (no floating-point atomics).
+ *   - Calls are reentrant.  No mutable global state exists.
+ */
+#ifndef RQF_SCAN_H
+#define RQF_SCAN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *rqf_stream_t; /* hipStream_t */
+
+enum {
+  RQF_OK = 0,
+  RQF_ERR_ARG = -1,       /* null pointer, bad shape, or bad chunk */
+  RQF_ERR_WORKSPACE = -2, /* workspace missing or too small */
+  RQF_ERR_ALIGN = -3      /* a tensor is not 8-byte aligned */
+};
+
+/* Library version string and the offload target it was built for. */
+const char *rqf_version(void);
+/* Human-readable message for a return code of this library. */
+const char *rqf_error_string(int code);
+
+/* ------------------------------------------------------------------------ *
+ * Time-invariant scans in the reference's (batch, time, filters) API.       *
+ *   x[t] = C1*x[t-1] + C2*u[t]                           (plain)            *
+ *   x[t] = C1*x[t-1] + tap0*u[t] + tap1*u[t-1]           (prospective)      *
+ * c1, c2, tap0, tap1: (F,) complex.  u, out, states, grads: BTF complex.    *
+ * grad_c1 / grad_c2 / grad_tap0 / grad_tap1: (F,) complex, overwritten.     *
+ * ------------------------------------------------------------------------ */
+
+size_t rqf_btf_scan_workspace(int64_t B, int64_t T, int64_t F);
+
+/* Replaces `_chunked_scan_kernel[grid](...)`
+ * (rqf_models/ops/chunked_scan_kernel.py:238-247) including its two permute
+ * copies (:231, :249): works on (B,T,F) directly. */
+int rqf_chunked_scan_fwd(const float *c1, const float *c2, const float *u, float *out,
+                         int64_t B, int64_t T, int64_t F, void *workspace,
+                         size_t workspace_bytes, rqf_stream_t stream);
+
+/* Replaces `_chunked_scan_backward_kernel[grid](...)`
+ * (rqf_models/ops/chunked_scan_kernel.py:286-299): grad_u = conj(C2) g,
+ * grad_C1 = sum conj(x[t-1]) g, grad_C2 = sum conj(u) g. */
+int rqf_chunked_scan_bwd(const float *c1, const float *c2, const float *u,
+                         const float *states, const float *grad_out, float *grad_u,
+                         float *grad_c1, float *grad_c2, int64_t B, int64_t T, int64_t F,
+                         void *workspace, size_t workspace_bytes, rqf_stream_t stream);
+
+/* Replaces `_chunked_prospective_kernel[grid](...)`
+ * (rqf_models/ops/chunked_scan_kernel.py:459-469). */
+int rqf_chunked_prospective_fwd(const float *c1, const float *tap0, const float *tap1,
+                                const float *x, float *out, int64_t B, int64_t T, int64_t F,
+                                void *workspace, size_t workspace_bytes,
+                                rqf_stream_t stream);
+
+/* Replaces `_ChunkedProspectiveScanFunction.backward`
+ * (rqf_models/ops/chunked_scan_kernel.py:491-503): the chunked adjoint plus
+ * its PyTorch finisher, fused: grad_x = conj(tap0) g[t] + conj(tap1) g[t+1]. */
+int rqf_chunked_prospective_bwd(const float *c1, const float *tap0, const float *tap1,
+                                const float *x, const float *states, const float *grad_out,
+                                float *grad_x, float *grad_c1, float *grad_tap0,
+                                float *grad_tap1, int64_t B, int64_t T, int64_t F,
+                                void *workspace, size_t workspace_bytes,
+                                rqf_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
+ * Two-tap prospective scans in channel-outermost FBT layout.               *
+ *   raw[t] = C1*raw[t-1] + tap0*z[t] + tap1*z[t-1]                          *
+ *   act    = relu(Re raw) + i relu(Im raw)                                  *
+ * ------------------------------------------------------------------------ */
+
+/* Rows x NC entry states kept by the recompute variant (NC for a given T). */
+int64_t rqf_fbt_carry_chunks(int64_t T);
+size_t rqf_fbt_workspace(int64_t F, int64_t B, int64_t T);
+
+/* Replaces `_fbt_prospective_kernel[grid](...)`
+ * (rqf_models/ops/fbt_scan_kernel.py:269-282).  act may be NULL. */
+int rqf_fbt_prospective_fwd(const float *c1, const float *tap0, const float *tap1,
+                            const float *z, float *raw, float *act, int64_t F, int64_t B,
+                            int64_t T, rqf_stream_t stream);
+
+/* Replaces `_fbt_prospective_backward_kernel[grid](...)`
+ * (rqf_models/ops/fbt_scan_kernel.py:307-324).  With fuse_act the cotangent is
+ * on the split-ReLU output (mask from raw > 0). */
+int rqf_fbt_prospective_bwd(const float *c1, const float *tap0, const float *tap1,
+                            const float *z, const float *raw, const float *grad_out,
+                            int32_t fuse_act, float *grad_z, float *grad_c1,
+                            float *grad_tap0, float *grad_tap1, int64_t F, int64_t B,
+                            int64_t T, void *workspace, size_t workspace_bytes,
+                            rqf_stream_t stream);
+
+/* Replaces `_fbt_recompute_forward_kernel[grid](...)`
+ * (rqf_models/ops/fbt_scan_kernel.py:618-631).  Writes the split-ReLU output
+ * and carry: (F*B, rqf_fbt_carry_chunks(T)) complex entry states. */
+int rqf_fbt_recompute_fwd(const float *c1, const float *tap0, const float *tap1,
+                          const float *z, float *act, float *carry, int64_t F, int64_t B,
+                          int64_t T, rqf_stream_t stream);
+
+/* Replaces `_fbt_recompute_backward_kernel[grid](...)`
+ * (rqf_models/ops/fbt_scan_kernel.py:653-669). */
+int rqf_fbt_recompute_bwd(const float *c1, const float *tap0, const float *tap1,
+                          const float *z, const float *carry, const float *grad_out,
+                          float *grad_z, float *grad_c1, float *grad_tap0, float *grad_tap1,
+                          int64_t F, int64_t B, int64_t T, void *workspace,
+                          size_t workspace_bytes, rqf_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
+ * Selective fused scan (FBT layout).                                        *
+ * ------------------------------------------------------------------------ */
+
+/* Mirrors `SelectiveScanInputs` (rqf_models/ops/selective_scan.py:10-23)
+ * with its options tuple unpacked in the order of
+ * rqf_models/backbones/rqf/selective.py:249-262. */
+typedef struct rqf_selective_inputs {
+  int64_t F, B, T; /* channels, batch, time */
+  int64_t G;       /* rows of warp_logits (0 without a frequency warp) */
+  const float *gamma_logits; /* (F,B,T) f32, or NULL without gamma control */
+  const float *warp_logits;  /* (G,B,T) f32, or NULL */
+  const float *write_logits; /* (F,B,T) f32, or NULL */
+  const float *bias, *theta, *minimum, *span, *step, *horizon, *theta_minimum,
+      *theta_maximum;        /* (F,) f32 */
+  const int64_t *groups;     /* (F,) warp group of each channel, or NULL */
+  int32_t has_gamma, has_warp, has_write, log_shift;
+  float gamma_scale, warp_scale;
+  int32_t prospective, gamma_horizon, write_sigmoid;
+  float write_max, write_bias;
+  int32_t bound_warp;
+} rqf_selective_inputs;
+
+/* Replaces `_forward[(f*b,)](...)` in `selective_forward`
+ * (rqf_models/ops/selective_scan_kernel.py:497-513).
+ * z: (F,B,T) complex drive.  raw / act: (F,B,T) complex or NULL (not both).
+ * entries: (F*B, ceil(T/chunk)) complex, the state entering each chunk.
+ * chunk: positive power of two. */
+int rqf_selective_fwd(const rqf_selective_inputs *in, const float *z, int64_t chunk,
+                      float *raw, float *act, float *entries, rqf_stream_t stream);
+
+size_t rqf_selective_bwd_workspace(const rqf_selective_inputs *in, int64_t chunk);
+
+/* Replaces `_backward[(f*b,)](...)`, `_group_reduce[...]` and the fp64 partial
+ * sum of `selective_backward` (rqf_models/ops/selective_scan_kernel.py:530-560).
+ * gy (cotangent of raw) and gx (of act) are (F,B,T) complex or NULL.
+ * dz, dzw: (F,B,T) complex; pass dzw == dz unless truncated.
+ * dg, dw: (F,B,T) f32 (NULL when the head is absent); dd: (G,B,T) f32.
+ * dbias, dtheta: (F,) f32. */
+int rqf_selective_bwd(const rqf_selective_inputs *in, const float *z, const float *entries,
+                      int64_t chunk, const float *gy, const float *gx, int32_t activate,
+                      int32_t truncated, float *dz, float *dzw, float *dg, float *dd,
+                      float *dw, float *dbias, float *dtheta, void *workspace,
+                      size_t workspace_bytes, rqf_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
+ * Self-test of the wave-level scan primitives (no reference counterpart):   *
+ * in: 64 lanes x 4 complex (P, s) affine maps; out: inclusive prefix (fwd)  *
+ * and suffix (rev) compositions.                                            *
+ * ------------------------------------------------------------------------ */
+int rqf_selftest_wave_scan(const float *in, float *out_fwd, float *out_rev,
+                           rqf_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RQF_SCAN_H */

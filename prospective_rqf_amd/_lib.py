@@ -1,0 +1,139 @@
+"""ctypes binding of ``librqf_hip.so`` (declared in ``include/rqf_scan.h``).
+
+The library is loaded lazily on first use and fails loudly: there is no
+silent PyTorch substitute for any kernel in this package.  ``torch`` is
+imported first so that the process uses a single HIP runtime (torch's).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+from prospective_rqf_amd.build import LIB_PATH
+
+_lib = None
+
+# Every symbol the header declares, with (restype, argtypes).
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_SZ = ctypes.c_size_t
+
+
+class SelectiveInputsStruct(ctypes.Structure):
+    """ctypes image of ``rqf_selective_inputs``."""
+
+    _fields_ = [
+        ("F", _I64), ("B", _I64), ("T", _I64), ("G", _I64),
+        ("gamma_logits", _P), ("warp_logits", _P), ("write_logits", _P),
+        ("bias", _P), ("theta", _P), ("minimum", _P), ("span", _P), ("step", _P),
+        ("horizon", _P), ("theta_minimum", _P), ("theta_maximum", _P),
+        ("groups", _P),
+        ("has_gamma", _I32), ("has_warp", _I32), ("has_write", _I32), ("log_shift", _I32),
+        ("gamma_scale", ctypes.c_float), ("warp_scale", ctypes.c_float),
+        ("prospective", _I32), ("gamma_horizon", _I32), ("write_sigmoid", _I32),
+        ("write_max", ctypes.c_float), ("write_bias", ctypes.c_float),
+        ("bound_warp", _I32),
+    ]
+
+
+SIGNATURES = {
+    "rqf_version": (ctypes.c_char_p, []),
+    "rqf_error_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "rqf_btf_scan_workspace": (_SZ, [_I64, _I64, _I64]),
+    "rqf_chunked_scan_fwd": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
+    "rqf_chunked_scan_bwd": (
+        ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
+    "rqf_chunked_prospective_fwd": (
+        ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
+    "rqf_chunked_prospective_bwd": (
+        ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
+    "rqf_fbt_carry_chunks": (_I64, [_I64]),
+    "rqf_fbt_workspace": (_SZ, [_I64, _I64, _I64]),
+    "rqf_fbt_prospective_fwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
+    "rqf_fbt_prospective_bwd": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
+    "rqf_fbt_recompute_fwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
+    "rqf_fbt_recompute_bwd": (
+        ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
+    "rqf_selective_fwd": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P]),
+    "rqf_selective_bwd_workspace": (_SZ, [_P, _I64]),
+    "rqf_selective_bwd": (
+        ctypes.c_int,
+        [_P, _P, _P, _I64, _P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "rqf_selftest_wave_scan": (ctypes.c_int, [_P, _P, _P, _P]),
+}
+
+
+class RQFError(RuntimeError):
+    pass
+
+
+def lib_path() -> str:
+    return os.environ.get("RQF_HIP_LIB", LIB_PATH)
+
+
+def load():
+    """Load the library (idempotent).  Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = lib_path()
+    if not os.path.exists(path):
+        raise RQFError(
+            f"{path} is missing: build it with `python -m prospective_rqf_amd.build` "
+            "(the HIP kernels have no CPU fallback)"
+        )
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def available() -> bool:
+    """True when the library loads and a HIP device is visible."""
+    try:
+        load()
+    except (OSError, RQFError):
+        return False
+    return torch.cuda.is_available()
+
+
+def check(code: int, what: str) -> None:
+    if code != 0:
+        msg = load().rqf_error_string(code).decode()
+        raise RQFError(f"{what} failed: {msg} (code {code})")
+
+
+def ptr(t: torch.Tensor | None):
+    """Device pointer of a tensor (None -> NULL)."""
+    if t is None:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def require_device(*tensors: torch.Tensor | None) -> None:
+    """Every kernel input must live on a HIP device; raise otherwise."""
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RQFError(
+                "prospective_rqf_amd kernels run on HIP devices only; got a tensor on "
+                f"{t.device}"
+            )
+
+
+def workspace(nbytes: int, device) -> torch.Tensor | None:
+    if nbytes == 0:
+        return None
+    return torch.empty(int(nbytes), dtype=torch.uint8, device=device)

@@ -1,0 +1,239 @@
+// rqf_device.h -- device-side building blocks shared by the scan kernels.
+//
+// * c32: complex fp32 value held as two VGPRs (interleaved in memory).
+// * Wave-level inclusive scans of first-order affine maps over the 64 lanes of
+//   a CDNA wavefront.  Forward (prefix) scans use DPP row_shr + row_bcast;
+//   reverse (suffix) scans use DPP row_shl inside a 16-lane row and two
+//   ds_bpermute steps across rows.
+// * Elementwise math for the fused ZOH discretisation: exp via v_exp_f32,
+//   reciprocal via v_rcp_f32, and polynomial sin/cos/expm1 whose relative
+//   accuracy near zero is what the a -> 0 limits of the recurrence need.
+//
+// All wave-level helpers must be called with all 64 lanes active.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rqf {
+
+constexpr int kWave = 64;
+
+struct c32 {
+  float r, i;
+};
+
+__device__ __forceinline__ c32 mk(float r, float i) {
+  c32 v;
+  v.r = r;
+  v.i = i;
+  return v;
+}
+__device__ __forceinline__ c32 cadd(c32 a, c32 b) { return mk(a.r + b.r, a.i + b.i); }
+__device__ __forceinline__ c32 csub(c32 a, c32 b) { return mk(a.r - b.r, a.i - b.i); }
+__device__ __forceinline__ c32 cscale(float s, c32 a) { return mk(s * a.r, s * a.i); }
+// a*b
+__device__ __forceinline__ c32 cmul(c32 a, c32 b) {
+  return mk(fmaf(a.r, b.r, -a.i * b.i), fmaf(a.r, b.i, a.i * b.r));
+}
+// a*b + c
+__device__ __forceinline__ c32 cmad(c32 a, c32 b, c32 c) {
+  return mk(fmaf(a.r, b.r, fmaf(-a.i, b.i, c.r)), fmaf(a.r, b.i, fmaf(a.i, b.r, c.i)));
+}
+// conj(a)*b
+__device__ __forceinline__ c32 cjmul(c32 a, c32 b) {
+  return mk(fmaf(a.r, b.r, a.i * b.i), fmaf(a.r, b.i, -a.i * b.r));
+}
+// conj(a)*b + c
+__device__ __forceinline__ c32 cjmad(c32 a, c32 b, c32 c) {
+  return mk(fmaf(a.r, b.r, fmaf(a.i, b.i, c.r)), fmaf(a.r, b.i, fmaf(-a.i, b.r, c.i)));
+}
+__device__ __forceinline__ c32 conjg(c32 a) { return mk(a.r, -a.i); }
+
+// ---------------------------------------------------------------------------
+// Cross-lane primitives
+// ---------------------------------------------------------------------------
+
+// DPP move of `src` from the lane selected by CTRL; lanes whose source lane is
+// out of range (or whose row is masked off) receive `fill`.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp(float src, float fill) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(fill), __float_as_int(src),
+                                                    CTRL, ROW_MASK, 0xf, false));
+}
+
+// GFX9 DPP controls.
+constexpr int kRowShl1 = 0x101, kRowShl2 = 0x102, kRowShl4 = 0x104, kRowShl8 = 0x108;
+constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
+constexpr int kRowBcast15 = 0x142, kRowBcast31 = 0x143;
+
+__device__ __forceinline__ float bperm(float v, int src_lane) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(v)));
+}
+__device__ __forceinline__ float readlane(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+__device__ __forceinline__ c32 readlane(c32 v, int lane) {
+  return mk(readlane(v.r, lane), readlane(v.i, lane));
+}
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+// Value of `v` held by lane-1 (lane 0 receives `fill`).
+__device__ __forceinline__ c32 shift_up(c32 v, c32 fill, int lane) {
+  const int src = lane == 0 ? 0 : lane - 1;
+  c32 o = mk(bperm(v.r, src), bperm(v.i, src));
+  return lane == 0 ? fill : o;
+}
+// Value of `v` held by lane+1 (lane 63 receives `fill`).
+__device__ __forceinline__ c32 shift_down(c32 v, c32 fill, int lane) {
+  const int src = lane == kWave - 1 ? lane : lane + 1;
+  c32 o = mk(bperm(v.r, src), bperm(v.i, src));
+  return lane == kWave - 1 ? fill : o;
+}
+
+// One Hillis-Steele step of the prefix scan of affine maps x -> P x + s.
+// The map received from an earlier lane is applied first.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ void fwd_step(c32& P, c32& s) {
+  const c32 lp = mk(dpp<CTRL, ROW_MASK>(P.r, 1.0f), dpp<CTRL, ROW_MASK>(P.i, 0.0f));
+  const c32 ls = mk(dpp<CTRL, ROW_MASK>(s.r, 0.0f), dpp<CTRL, ROW_MASK>(s.i, 0.0f));
+  s = cmad(ls, P, s);
+  P = cmul(lp, P);
+}
+
+// Inclusive prefix scan over lanes: lane i ends with the composition of the
+// maps of lanes 0..i (lane 0's applied first).
+__device__ __forceinline__ void wave_scan_fwd(c32& P, c32& s) {
+  fwd_step<kRowShr1>(P, s);
+  fwd_step<kRowShr2>(P, s);
+  fwd_step<kRowShr4>(P, s);
+  fwd_step<kRowShr8>(P, s);
+  fwd_step<kRowBcast15, 0xa>(P, s);
+  fwd_step<kRowBcast31, 0xc>(P, s);
+}
+
+// One step of the suffix scan of maps d -> Q d + r, where the map received
+// from a later lane is applied first (it is closer to the end of time).
+template <int CTRL>
+__device__ __forceinline__ void rev_step(c32& Q, c32& r) {
+  const c32 lq = mk(dpp<CTRL>(Q.r, 1.0f), dpp<CTRL>(Q.i, 0.0f));
+  const c32 lr = mk(dpp<CTRL>(r.r, 0.0f), dpp<CTRL>(r.i, 0.0f));
+  r = cmad(Q, lr, r);
+  Q = cmul(Q, lq);
+}
+__device__ __forceinline__ void rev_cross(c32& Q, c32& r, int src, bool valid) {
+  c32 lq = mk(bperm(Q.r, src), bperm(Q.i, src));
+  c32 lr = mk(bperm(r.r, src), bperm(r.i, src));
+  if (!valid) {
+    lq = mk(1.0f, 0.0f);
+    lr = mk(0.0f, 0.0f);
+  }
+  r = cmad(Q, lr, r);
+  Q = cmul(Q, lq);
+}
+
+// Inclusive suffix scan over lanes: lane i ends with the composition of the
+// maps of lanes i..63 (lane 63's applied first).
+__device__ __forceinline__ void wave_scan_rev(c32& Q, c32& r, int lane) {
+  rev_step<kRowShl1>(Q, r);
+  rev_step<kRowShl2>(Q, r);
+  rev_step<kRowShl4>(Q, r);
+  rev_step<kRowShl8>(Q, r);
+  // Each lane now covers the rest of its 16-lane row; add whole rows after it.
+  const int row = lane >> 4;
+  rev_cross(Q, r, ((row + 1) & 3) << 4, row < 3);
+  rev_cross(Q, r, ((row + 2) & 3) << 4, row < 2);
+}
+
+// Sum of a double over the wave (result valid in every lane).
+__device__ __forceinline__ double wave_sum(double v) {
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Elementwise math
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float fexp(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+__device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float fsigmoid(float x) { return frcp(1.0f + fexp(-x)); }
+// tanh(x) = 1 - 2/(e^{2x} + 1); saturates to +-1 without overflow trouble.
+__device__ __forceinline__ float ftanh(float x) {
+  return fmaf(-2.0f, frcp(fexp(2.0f * x) + 1.0f), 1.0f);
+}
+
+// expm1(x) given e = exp(x): Taylor series for |x| < 0.5, else e - 1.
+__device__ __forceinline__ float fexpm1(float x, float e) {
+  if (fabsf(x) < 0.5f) {
+    float p = fmaf(x, 1.0f / 362880.0f, 1.0f / 40320.0f);
+    p = fmaf(x, p, 1.0f / 5040.0f);
+    p = fmaf(x, p, 1.0f / 720.0f);
+    p = fmaf(x, p, 1.0f / 120.0f);
+    p = fmaf(x, p, 1.0f / 24.0f);
+    p = fmaf(x, p, 1.0f / 6.0f);
+    p = fmaf(x, p, 0.5f);
+    return fmaf(x * x, p, x);
+  }
+  return e - 1.0f;
+}
+
+// For an angle x: sin(x), and 2 sin^2(x/2) = 1 - cos(x).  The argument is
+// reduced to r = x - 2*pi*q with |r| <= pi (Cody-Waite, two-part 2*pi), then
+// h = r/2 in [-pi/2, pi/2] goes through Taylor polynomials:
+//   sin x = 2 sin(h) cos(h),  1 - cos x = 2 sin^2(h).
+__device__ __forceinline__ void fsin_vers(float x, float& s, float& vers) {
+  const float q = rintf(x * 0.15915494309189535f);
+  float r = fmaf(-q, 6.28318548202514648f, x);   // 2*pi rounded to fp32
+  r = fmaf(-q, -1.7484556000744487e-07f, r);     // 2*pi - fp32(2*pi)
+  const float h = 0.5f * r;
+  const float h2 = h * h;
+  float sp = fmaf(h2, 1.6059043836821613e-10f, -2.5052108385441720e-08f);
+  sp = fmaf(h2, sp, 2.7557319223985888e-06f);
+  sp = fmaf(h2, sp, -1.9841269841269841e-04f);
+  sp = fmaf(h2, sp, 8.3333333333333333e-03f);
+  sp = fmaf(h2, sp, -1.6666666666666667e-01f);
+  const float sh = fmaf(h * h2, sp, h);
+  float cp = fmaf(h2, -1.1470745597729725e-11f, 2.0876756987868099e-09f);
+  cp = fmaf(h2, cp, -2.7557319223985890e-07f);
+  cp = fmaf(h2, cp, 2.4801587301587302e-05f);
+  cp = fmaf(h2, cp, -1.3888888888888889e-03f);
+  cp = fmaf(h2, cp, 4.1666666666666667e-02f);
+  cp = fmaf(h2, cp, -0.5f);
+  const float ch = fmaf(h2, cp, 1.0f);
+  s = 2.0f * sh * ch;
+  vers = 2.0f * sh * sh;
+}
+
+// Zero-order-hold pieces for a = ar + i ai:
+//   A   = exp(a)
+//   phi = (exp(a) - 1)/a, with the cubic series 1 + a/2 + a^2/6 + a^3/24 when
+//         |a|^2 < 1e-8 (the reference's threshold, selective_scan.py:49-54)
+// inv_den returns 1/|a|^2 (0 on the series branch) for reuse by the VJP.
+__device__ __forceinline__ void zoh(float ar, float ai, c32& A, c32& phi, float& inv_den) {
+  const float e = fexp(ar);
+  float sn, vers;
+  fsin_vers(ai, sn, vers);
+  A = mk(e * (1.0f - vers), e * sn);
+  const float den = fmaf(ar, ar, ai * ai);
+  if (den < 1.0e-8f) {
+    // 1 + a*(1/2 + a*(1/6 + a/24))
+    c32 a = mk(ar, ai);
+    c32 t = cmad(a, mk(1.0f / 24.0f, 0.0f), mk(1.0f / 6.0f, 0.0f));
+    t = cmad(a, t, mk(0.5f, 0.0f));
+    phi = cmad(a, t, mk(1.0f, 0.0f));
+    inv_den = 0.0f;
+  } else {
+    // Re(e^a - 1) = expm1(ar) cos(ai) - (1 - cos ai) = expm1(ar)*(1 - vers) - vers:
+    // both terms stay small near a = 0, so there is no cancellation.
+    const float em1 = fexpm1(ar, e);
+    const float er = fmaf(em1, 1.0f - vers, -vers);
+    const float ei = e * sn;
+    inv_den = frcp(den);
+    phi = mk(fmaf(er, ar, ei * ai) * inv_den, fmaf(ei, ar, -er * ai) * inv_den);
+  }
+}
+
+}  // namespace rqf

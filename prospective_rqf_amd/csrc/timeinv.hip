@@ -1,0 +1,650 @@
+// timeinv.hip -- time-invariant two-tap scans for gfx950.
+//
+//   y[t] = c1*y[t-1] + k0*x[t] + k1*x[t-1]      (k1 = 0: plain C2 scan)
+//
+// Two families:
+//
+// FBT (channel-outermost, rows contiguous in time): one wavefront per
+// (channel, batch) row, tiles of 64*8 steps, lane l holding 8 consecutive
+// steps (four float4 loads).  Tile = lane-serial composition -> DPP wave scan
+// -> lane-serial replay, as in the selective kernels.  The backward runs the
+// adjoint g[t] = e[t] + conj(c1) g[t+1] the same way in suffix order and
+// keeps raw[t-1] and g[t+1] in registers, so it needs none of the
+// reference's divisions by c1 (fbt_scan_kernel.py:157-160, 518-521).
+//
+// BTF (the reference's (batch, time, filters) API): lanes map to
+// (batch, time segment, channel) tasks with the channel fastest, so a
+// wavefront reads 64 consecutive complex values per step.  Each task scans
+// its segment serially; segments are stitched by a second pass that folds the
+// end states of the earlier segments with c1^L (three-phase scan; no permute
+// copies, unlike chunked_scan_kernel.py:212-249).
+//
+// Coefficient gradients are reduced deterministically: per-task partial sums
+// in fp64, then an ordered reduction per channel.
+#include "rqf_device.h"
+#include "rqf_scan.h"
+
+using namespace rqf;
+
+namespace {
+
+constexpr int kTiK = 8;
+constexpr int kTiTile = kWave * kTiK;
+constexpr int kTiWaves = 4;
+
+__device__ __forceinline__ c32 ldc(const float* p, int64_t i) { return mk(p[2 * i], p[2 * i + 1]); }
+__device__ __forceinline__ void stc(float* p, int64_t i, c32 v) {
+  p[2 * i] = v.r;
+  p[2 * i + 1] = v.i;
+}
+__device__ __forceinline__ c32 relu2(c32 v) { return mk(fmaxf(v.r, 0.0f), fmaxf(v.i, 0.0f)); }
+__device__ __forceinline__ c32 mask_by(c32 g, c32 raw) {
+  return mk(raw.r > 0.0f ? g.r : 0.0f, raw.i > 0.0f ? g.i : 0.0f);
+}
+
+// VEC: T even and 16-byte aligned rows: a lane's 8 steps are all in or all out
+// of range when T % 8 == 0; otherwise the tail uses guarded scalar access.
+template <bool VEC>
+__device__ __forceinline__ void load8(const float* __restrict__ row, int64_t tb, int64_t T,
+                                      c32 (&v)[kTiK]) {
+  if (VEC && tb + kTiK <= T) {
+#pragma unroll
+    for (int j = 0; j < kTiK / 2; ++j) {
+      const float4 a = *reinterpret_cast<const float4*>(row + 2 * tb + 4 * j);
+      v[2 * j] = mk(a.x, a.y);
+      v[2 * j + 1] = mk(a.z, a.w);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < kTiK; ++k) v[k] = (tb + k < T) ? ldc(row, tb + k) : mk(0.0f, 0.0f);
+  }
+}
+template <bool VEC>
+__device__ __forceinline__ void store8(float* __restrict__ row, int64_t tb, int64_t T,
+                                       const c32 (&v)[kTiK]) {
+  if (VEC && tb + kTiK <= T) {
+#pragma unroll
+    for (int j = 0; j < kTiK / 2; ++j)
+      *reinterpret_cast<float4*>(row + 2 * tb + 4 * j) =
+          make_float4(v[2 * j].r, v[2 * j].i, v[2 * j + 1].r, v[2 * j + 1].i);
+  } else {
+#pragma unroll
+    for (int k = 0; k < kTiK; ++k)
+      if (tb + k < T) stc(row, tb + k, v[k]);
+  }
+}
+
+// a^n for small n >= 0 (uniform or per lane).
+__device__ __forceinline__ c32 cpow_small(c32 a, int n) {
+  c32 r = mk(1.0f, 0.0f);
+  for (int k = 0; k < n; ++k) r = cmul(r, a);
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// FBT forward: raw (optional), split-ReLU act (optional), entry carry per tile
+// (optional).
+// ---------------------------------------------------------------------------
+template <bool VEC>
+__global__ __launch_bounds__(kTiWaves* kWave) void fbt_fwd_kernel(
+    const float* __restrict__ c1, const float* __restrict__ tap0, const float* __restrict__ tap1,
+    const float* __restrict__ z, float* __restrict__ raw, float* __restrict__ act,
+    float* __restrict__ carry, int64_t F, int64_t B, int64_t T, int64_t nc) {
+  const int lane = lane_id();
+  const int64_t row = (int64_t)blockIdx.x * kTiWaves + (threadIdx.x >> 6);
+  if (row >= F * B) return;
+  const int64_t f = row / B;
+  const c32 a = ldc(c1, f), k0 = ldc(tap0, f), k1 = ldc(tap1, f);
+  c32 apow = cpow_small(a, kTiK);  // composition of a full lane
+  const float* zr = z + 2 * row * T;
+  float* rawr = raw ? raw + 2 * row * T : nullptr;
+  float* actr = act ? act + 2 * row * T : nullptr;
+  c32 y = mk(0.0f, 0.0f), zlast = mk(0.0f, 0.0f);
+  for (int64_t t0 = 0, tile = 0; t0 < T; t0 += kTiTile, ++tile) {
+    if (carry && lane == 0) stc(carry, row * nc + tile, y);
+    const int64_t tb = t0 + lane * kTiK;
+    c32 zv[kTiK];
+    load8<VEC>(zr, tb, T, zv);
+    const c32 zp0 = shift_up(zv[kTiK - 1], zlast, lane);
+    c32 u[kTiK];
+#pragma unroll
+    for (int k = 0; k < kTiK; ++k) u[k] = cmad(k1, k ? zv[k - 1] : zp0, cmul(k0, zv[k]));
+    const int cnt = (int)min<int64_t>(max<int64_t>(T - tb, 0), kTiK);
+    c32 s = mk(0.0f, 0.0f);
+#pragma unroll
+    for (int k = 0; k < kTiK; ++k)
+      if (k < cnt) s = cmad(a, s, u[k]);
+    c32 P = cnt == kTiK ? apow : cpow_small(a, cnt);
+    if (lane == 0) s = cmad(P, y, s);
+    wave_scan_fwd(P, s);
+    c32 yk = shift_up(s, y, lane);
+    c32 out[kTiK];
+#pragma unroll
+    for (int k = 0; k < kTiK; ++k) {
+      yk = cmad(a, yk, u[k]);
+      out[k] = yk;
+    }
+    if (rawr) store8<VEC>(rawr, tb, T, out);
+    if (actr) {
+#pragma unroll
+      for (int k = 0; k < kTiK; ++k) out[k] = relu2(out[k]);
+      store8<VEC>(actr, tb, T, out);
+    }
+    y = readlane(s, kWave - 1);
+    zlast = readlane(zv[kTiK - 1], kWave - 1);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// FBT backward.  REPLAY: raw recomputed from the per-tile carry; otherwise raw
+// is read.  MASK: cotangent is on the split-ReLU output.
+// partial: per row, 6 doubles (gc1.re, gc1.im, gk0.re, gk0.im, gk1.re, gk1.im).
+// ---------------------------------------------------------------------------
+template <bool VEC, bool REPLAY>
+__global__ __launch_bounds__(kTiWaves* kWave) void fbt_bwd_kernel(
+    const float* __restrict__ c1, const float* __restrict__ tap0, const float* __restrict__ tap1,
+    const float* __restrict__ z, const float* __restrict__ raw, const float* __restrict__ carry,
+    const float* __restrict__ gout, int mask, float* __restrict__ gz,
+    double* __restrict__ partial, int64_t F, int64_t B, int64_t T, int64_t nc) {
+  const int lane = lane_id();
+  const int64_t row = (int64_t)blockIdx.x * kTiWaves + (threadIdx.x >> 6);
+  if (row >= F * B) return;
+  const int64_t f = row / B;
+  const c32 a = ldc(c1, f), k0 = ldc(tap0, f), k1 = ldc(tap1, f);
+  const c32 ac = conjg(a);
+  const c32 apow = cpow_small(a, kTiK), acpow = conjg(apow);
+  const float* zr = z + 2 * row * T;
+  const float* rr = REPLAY ? nullptr : raw + 2 * row * T;
+  const float* gr = gout + 2 * row * T;
+  float* gzr = gz + 2 * row * T;
+  c32 gcarry = mk(0.0f, 0.0f);
+  double s1r = 0, s1i = 0, s0r = 0, s0i = 0, s2r = 0, s2i = 0;
+  const int64_t ntiles = (T + kTiTile - 1) / kTiTile;
+  for (int64_t tile = ntiles - 1; tile >= 0; --tile) {
+    const int64_t t0 = tile * kTiTile;
+    const int64_t tb = t0 + lane * kTiK;
+    const int cnt = (int)min<int64_t>(max<int64_t>(T - tb, 0), kTiK);
+    c32 zv[kTiK], yv[kTiK], ev[kTiK];
+    load8<VEC>(zr, tb, T, zv);
+    load8<VEC>(gr, tb, T, ev);
+    const c32 zprev_tile = t0 > 0 ? ldc(zr, t0 - 1) : mk(0.0f, 0.0f);
+    const c32 zp0 = shift_up(zv[kTiK - 1], zprev_tile, lane);
+    c32 yp0;
+    if (REPLAY) {
+      c32 u[kTiK];
+#pragma unroll
+      for (int k = 0; k < kTiK; ++k) u[k] = cmad(k1, k ? zv[k - 1] : zp0, cmul(k0, zv[k]));
+      const c32 y0 = ldc(carry, row * nc + tile);
+      c32 s = mk(0.0f, 0.0f);
+#pragma unroll
+      for (int k = 0; k < kTiK; ++k)
+        if (k < cnt) s = cmad(a, s, u[k]);
+      c32 P = cnt == kTiK ? apow : cpow_small(a, cnt);
+      if (lane == 0) s = cmad(P, y0, s);
+      wave_scan_fwd(P, s);
+      c32 yk = shift_up(s, y0, lane);
+      yp0 = yk;
+#pragma unroll
+      for (int k = 0; k < kTiK; ++k) {
+        yk = cmad(a, yk, u[k]);
+        yv[k] = yk;
+      }
+    } else {
+      load8<VEC>(rr, tb, T, yv);
+      const c32 rprev_tile = t0 > 0 ? ldc(rr, t0 - 1) : mk(0.0f, 0.0f);
+      yp0 = shift_up(yv[kTiK - 1], rprev_tile, lane);
+    }
+    if (mask) {
+#pragma unroll
+      for (int k = 0; k < kTiK; ++k) ev[k] = mask_by(ev[k], yv[k]);
+    }
+    // Suffix composition of g -> e + conj(a) g over the lane's valid steps.
+    c32 r = mk(0.0f, 0.0f);
+#pragma unroll
+    for (int k = kTiK - 1; k >= 0; --k)
+      if (k < cnt) r = cmad(ac, r, ev[k]);
+    c32 Q = cnt == kTiK ? acpow : conjg(cpow_small(a, cnt));
+    if (lane == kWave - 1) r = cmad(Q, gcarry, r);
+    wave_scan_rev(Q, r, lane);
+    c32 gnext = shift_down(r, gcarry, lane);
+    gcarry = readlane(r, 0);
+    c32 go[kTiK];
+    float a1r = 0, a1i = 0, a0r = 0, a0i = 0, a2r = 0, a2i = 0;
+#pragma unroll
+    for (int k = kTiK - 1; k >= 0; --k) {
+      const c32 g = cmad(ac, gnext, ev[k]);
+      go[k] = cjmad(k1, gnext, cjmul(k0, g));
+      const c32 yp = k ? yv[k - 1] : yp0;
+      const c32 zp = k ? zv[k - 1] : zp0;
+      const c32 t1 = cjmul(yp, g), t0c = cjmul(zv[k], g), t2 = cjmul(zp, g);
+      const bool in = k < cnt;
+      a1r += in ? t1.r : 0.0f;
+      a1i += in ? t1.i : 0.0f;
+      a0r += in ? t0c.r : 0.0f;
+      a0i += in ? t0c.i : 0.0f;
+      a2r += in ? t2.r : 0.0f;
+      a2i += in ? t2.i : 0.0f;
+      gnext = g;
+    }
+    store8<VEC>(gzr, tb, T, go);
+    s1r += a1r;
+    s1i += a1i;
+    s0r += a0r;
+    s0i += a0i;
+    s2r += a2r;
+    s2i += a2i;
+  }
+  s1r = wave_sum(s1r);
+  s1i = wave_sum(s1i);
+  s0r = wave_sum(s0r);
+  s0i = wave_sum(s0i);
+  s2r = wave_sum(s2r);
+  s2i = wave_sum(s2i);
+  if (lane == 0) {
+    double* o = partial + 6 * row;
+    o[0] = s1r;
+    o[1] = s1i;
+    o[2] = s0r;
+    o[3] = s0i;
+    o[4] = s2r;
+    o[5] = s2i;
+  }
+}
+
+// grad[f] = sum over m of partial[(f*M + m)*6 + j] (fp64, ascending m) for the
+// FBT layout; for BTF tasks ((b*S + s)*F + f) pass stride_f = 1, stride_m = F.
+__global__ __launch_bounds__(256) void coef_reduce_kernel(const double* __restrict__ partial,
+                                                          int64_t F, int64_t M, int64_t stride_f,
+                                                          int64_t stride_m, float* __restrict__ gc1,
+                                                          float* __restrict__ gk0,
+                                                          float* __restrict__ gk1) {
+  const int64_t f = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (f >= F) return;
+  double s[6] = {0, 0, 0, 0, 0, 0};
+  for (int64_t m = 0; m < M; ++m) {
+    const double* p = partial + 6 * (f * stride_f + m * stride_m);
+#pragma unroll
+    for (int j = 0; j < 6; ++j) s[j] += p[j];
+  }
+  gc1[2 * f] = (float)s[0];
+  gc1[2 * f + 1] = (float)s[1];
+  gk0[2 * f] = (float)s[2];
+  gk0[2 * f + 1] = (float)s[3];
+  if (gk1) {
+    gk1[2 * f] = (float)s[4];
+    gk1[2 * f + 1] = (float)s[5];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// BTF three-phase scans.  task = (b*S + seg)*F + f; segment seg covers
+// [seg*L, min(T, seg*L + L)).
+// ---------------------------------------------------------------------------
+struct BtfShape {
+  int64_t B, T, F, S, L;
+};
+
+__device__ __forceinline__ c32 cpow_int(c32 a, int64_t n) {
+  c32 r = mk(1.0f, 0.0f);
+  while (n > 0) {
+    if (n & 1) r = cmul(r, a);
+    a = cmul(a, a);
+    n >>= 1;
+  }
+  return r;
+}
+
+// Phase 1 of the forward: segment end states from a zero entry.
+__global__ __launch_bounds__(256) void btf_fwd_local_kernel(
+    const float* __restrict__ c1, const float* __restrict__ k0p, const float* __restrict__ k1p,
+    const float* __restrict__ x, float* __restrict__ seg_end, BtfShape sh) {
+  const int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (task >= sh.B * sh.S * sh.F) return;
+  const int64_t f = task % sh.F, bs = task / sh.F, seg = bs % sh.S, b = bs / sh.S;
+  const c32 a = ldc(c1, f), k0 = ldc(k0p, f), k1 = k1p ? ldc(k1p, f) : mk(0.0f, 0.0f);
+  const int64_t t_beg = seg * sh.L, t_end = min(sh.T, t_beg + sh.L);
+  const float* xb = x + 2 * (b * sh.T * sh.F + f);
+  c32 xprev = (k1p && t_beg > 0) ? ldc(xb, (t_beg - 1) * sh.F) : mk(0.0f, 0.0f);
+  c32 y = mk(0.0f, 0.0f);
+#pragma unroll 8
+  for (int64_t t = t_beg; t < t_end; ++t) {
+    const c32 xt = ldc(xb, t * sh.F);
+    y = cmad(a, y, cmad(k1, xprev, cmul(k0, xt)));
+    xprev = xt;
+  }
+  stc(seg_end, task, y);
+}
+
+// Phase 2 of the forward: fold earlier segments' end states into the entry
+// state, then rescan the segment writing the output.
+__global__ __launch_bounds__(256) void btf_fwd_final_kernel(
+    const float* __restrict__ c1, const float* __restrict__ k0p, const float* __restrict__ k1p,
+    const float* __restrict__ x, const float* __restrict__ seg_end, float* __restrict__ out,
+    BtfShape sh) {
+  const int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (task >= sh.B * sh.S * sh.F) return;
+  const int64_t f = task % sh.F, bs = task / sh.F, seg = bs % sh.S, b = bs / sh.S;
+  const c32 a = ldc(c1, f), k0 = ldc(k0p, f), k1 = k1p ? ldc(k1p, f) : mk(0.0f, 0.0f);
+  c32 y = mk(0.0f, 0.0f);
+  if (seg > 0) {
+    const c32 aL = cpow_int(a, sh.L);
+    for (int64_t s = 0; s < seg; ++s) y = cmad(aL, y, ldc(seg_end, (b * sh.S + s) * sh.F + f));
+  }
+  const int64_t t_beg = seg * sh.L, t_end = min(sh.T, t_beg + sh.L);
+  const float* xb = x + 2 * (b * sh.T * sh.F + f);
+  float* ob = out + 2 * (b * sh.T * sh.F + f);
+  c32 xprev = (k1p && t_beg > 0) ? ldc(xb, (t_beg - 1) * sh.F) : mk(0.0f, 0.0f);
+#pragma unroll 8
+  for (int64_t t = t_beg; t < t_end; ++t) {
+    const c32 xt = ldc(xb, t * sh.F);
+    y = cmad(a, y, cmad(k1, xprev, cmul(k0, xt)));
+    xprev = xt;
+    stc(ob, t * sh.F, y);
+  }
+}
+
+// Phase 1 of the backward: adjoint at each segment's first step from a zero
+// carry after the segment.
+__global__ __launch_bounds__(256) void btf_bwd_local_kernel(const float* __restrict__ c1,
+                                                            const float* __restrict__ gout,
+                                                            float* __restrict__ seg_beg,
+                                                            BtfShape sh) {
+  const int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (task >= sh.B * sh.S * sh.F) return;
+  const int64_t f = task % sh.F, bs = task / sh.F, seg = bs % sh.S, b = bs / sh.S;
+  const c32 ac = conjg(ldc(c1, f));
+  const int64_t t_beg = seg * sh.L, t_end = min(sh.T, t_beg + sh.L);
+  const float* gb = gout + 2 * (b * sh.T * sh.F + f);
+  c32 g = mk(0.0f, 0.0f);
+#pragma unroll 8
+  for (int64_t t = t_end - 1; t >= t_beg; --t) g = cmad(ac, g, ldc(gb, t * sh.F));
+  stc(seg_beg, task, g);
+}
+
+// Phase 2 of the backward: carry from the later segments, reverse serial
+// pass, grad_x and per-task coefficient partial sums.
+__global__ __launch_bounds__(256) void btf_bwd_final_kernel(
+    const float* __restrict__ c1, const float* __restrict__ k0p, const float* __restrict__ k1p,
+    const float* __restrict__ x, const float* __restrict__ states, const float* __restrict__ gout,
+    const float* __restrict__ seg_beg, float* __restrict__ gx, double* __restrict__ partial,
+    BtfShape sh) {
+  const int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (task >= sh.B * sh.S * sh.F) return;
+  const int64_t f = task % sh.F, bs = task / sh.F, seg = bs % sh.S, b = bs / sh.S;
+  const c32 a = ldc(c1, f), k0 = ldc(k0p, f), k1 = k1p ? ldc(k1p, f) : mk(0.0f, 0.0f);
+  const c32 ac = conjg(a);
+  c32 gnext = mk(0.0f, 0.0f);
+  if (seg + 1 < sh.S) {
+    const c32 acL = conjg(cpow_int(a, sh.L));
+    for (int64_t s = sh.S - 1; s > seg; --s) gnext = cmad(acL, gnext, ldc(seg_beg, (b * sh.S + s) * sh.F + f));
+  }
+  const int64_t t_beg = seg * sh.L, t_end = min(sh.T, t_beg + sh.L);
+  const int64_t base = b * sh.T * sh.F + f;
+  const float* xb = x + 2 * base;
+  const float* yb = states + 2 * base;
+  const float* gb = gout + 2 * base;
+  float* gxb = gx + 2 * base;
+  double s1r = 0, s1i = 0, s0r = 0, s0i = 0, s2r = 0, s2i = 0;
+#pragma unroll 4
+  for (int64_t t = t_end - 1; t >= t_beg; --t) {
+    const c32 g = cmad(ac, gnext, ldc(gb, t * sh.F));
+    const c32 xt = ldc(xb, t * sh.F);
+    const c32 xp = t > 0 ? ldc(xb, (t - 1) * sh.F) : mk(0.0f, 0.0f);
+    const c32 yp = t > 0 ? ldc(yb, (t - 1) * sh.F) : mk(0.0f, 0.0f);
+    stc(gxb, t * sh.F, cjmad(k1, gnext, cjmul(k0, g)));
+    const c32 t1 = cjmul(yp, g), t0c = cjmul(xt, g), t2 = cjmul(xp, g);
+    s1r += t1.r;
+    s1i += t1.i;
+    s0r += t0c.r;
+    s0i += t0c.i;
+    s2r += t2.r;
+    s2i += t2.i;
+    gnext = g;
+  }
+  double* o = partial + 6 * task;
+  o[0] = s1r;
+  o[1] = s1i;
+  o[2] = s0r;
+  o[3] = s0i;
+  o[4] = s2r;
+  o[5] = s2i;
+}
+
+inline bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15) == 0; }
+inline bool aligned8(const void* p) { return p == nullptr || ((uintptr_t)p & 7) == 0; }
+inline size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+int launch_status() {
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? RQF_OK : (int)err;
+}
+
+BtfShape btf_shape(int64_t B, int64_t T, int64_t F) {
+  BtfShape sh;
+  sh.B = B;
+  sh.T = T;
+  sh.F = F;
+  // Enough segments for ~64K lanes, but at least 16 steps per segment.
+  const int64_t lanes = B * F > 0 ? B * F : 1;
+  int64_t S = (65536 + lanes - 1) / lanes;
+  const int64_t smax = T / 16 > 1 ? T / 16 : 1;
+  if (S > smax) S = smax;
+  if (S < 1) S = 1;
+  sh.L = T > 0 ? (T + S - 1) / S : 1;
+  sh.S = T > 0 ? (T + sh.L - 1) / sh.L : 1;
+  return sh;
+}
+
+size_t btf_ws(int64_t B, int64_t T, int64_t F) {
+  const BtfShape sh = btf_shape(B, T, F);
+  const size_t tasks = (size_t)(B * sh.S * F);
+  return round256(sizeof(float) * 2 * tasks) + round256(sizeof(double) * 6 * tasks);
+}
+
+int btf_fwd(const float* c1, const float* k0, const float* k1, const float* x, float* out,
+            int64_t B, int64_t T, int64_t F, void* ws, size_t ws_bytes, hipStream_t s) {
+  if (B < 0 || T < 0 || F < 0) return RQF_ERR_ARG;
+  if (B * T * F == 0) return RQF_OK;
+  if (!c1 || !k0 || !x || !out) return RQF_ERR_ARG;
+  if (!aligned8(x) || !aligned8(out)) return RQF_ERR_ALIGN;
+  const size_t need = btf_ws(B, T, F);
+  if (!ws || ws_bytes < need) return RQF_ERR_WORKSPACE;
+  const BtfShape sh = btf_shape(B, T, F);
+  const int64_t tasks = B * sh.S * F;
+  const dim3 grid((unsigned)((tasks + 255) / 256)), block(256);
+  float* seg = (float*)ws;
+  if (sh.S > 1) hipLaunchKernelGGL(btf_fwd_local_kernel, grid, block, 0, s, c1, k0, k1, x, seg, sh);
+  hipLaunchKernelGGL(btf_fwd_final_kernel, grid, block, 0, s, c1, k0, k1, x, seg, out, sh);
+  return launch_status();
+}
+
+int btf_bwd(const float* c1, const float* k0, const float* k1, const float* x,
+            const float* states, const float* gout, float* gx, float* gc1, float* gk0,
+            float* gk1, int64_t B, int64_t T, int64_t F, void* ws, size_t ws_bytes,
+            hipStream_t s) {
+  if (B < 0 || T < 0 || F < 0) return RQF_ERR_ARG;
+  if (F == 0) return RQF_OK;
+  if (!c1 || !k0 || !gc1 || !gk0 || (k1 && !gk1)) return RQF_ERR_ARG;
+  if (B * T > 0 && (!x || !states || !gout || !gx)) return RQF_ERR_ARG;
+  if (!aligned8(x) || !aligned8(states) || !aligned8(gout) || !aligned8(gx)) return RQF_ERR_ALIGN;
+  const size_t need = btf_ws(B, T, F);
+  if (need && (!ws || ws_bytes < need)) return RQF_ERR_WORKSPACE;
+  const BtfShape sh = btf_shape(B, T, F);
+  const int64_t tasks = B * sh.S * F;
+  float* seg = (float*)ws;
+  double* partial = (double*)((char*)ws + round256(sizeof(float) * 2 * (size_t)tasks));
+  if (tasks > 0 && T > 0) {
+    const dim3 grid((unsigned)((tasks + 255) / 256)), block(256);
+    if (sh.S > 1) hipLaunchKernelGGL(btf_bwd_local_kernel, grid, block, 0, s, c1, gout, seg, sh);
+    hipLaunchKernelGGL(btf_bwd_final_kernel, grid, block, 0, s, c1, k0, k1, x, states, gout, seg,
+                       gx, partial, sh);
+    hipLaunchKernelGGL(coef_reduce_kernel, dim3((unsigned)((F + 255) / 256)), dim3(256), 0, s,
+                       partial, F, B * sh.S, (int64_t)1, F, gc1, gk0, gk1);
+  } else {
+    hipLaunchKernelGGL(coef_reduce_kernel, dim3((unsigned)((F + 255) / 256)), dim3(256), 0, s,
+                       partial, F, (int64_t)0, (int64_t)1, F, gc1, gk0, gk1);
+  }
+  return launch_status();
+}
+
+int fbt_fwd(const float* c1, const float* t0, const float* t1, const float* z, float* raw,
+            float* act, float* carry, int64_t F, int64_t B, int64_t T, hipStream_t s) {
+  if (F < 0 || B < 0 || T < 0) return RQF_ERR_ARG;
+  const int64_t R = F * B;
+  if (R == 0 || T == 0) return RQF_OK;
+  if (!c1 || !t0 || !t1 || !z || (!raw && !act)) return RQF_ERR_ARG;
+  if (!aligned8(z) || !aligned8(raw) || !aligned8(act) || !aligned8(carry)) return RQF_ERR_ALIGN;
+  const int64_t nc = (T + kTiTile - 1) / kTiTile;
+  const dim3 grid((unsigned)((R + kTiWaves - 1) / kTiWaves)), block(kTiWaves * kWave);
+  const bool vec = T % 2 == 0 && aligned16(z) && aligned16(raw) && aligned16(act);
+  if (vec)
+    hipLaunchKernelGGL(fbt_fwd_kernel<true>, grid, block, 0, s, c1, t0, t1, z, raw, act, carry, F,
+                       B, T, nc);
+  else
+    hipLaunchKernelGGL(fbt_fwd_kernel<false>, grid, block, 0, s, c1, t0, t1, z, raw, act, carry,
+                       F, B, T, nc);
+  return launch_status();
+}
+
+size_t fbt_ws(int64_t F, int64_t B) { return round256(sizeof(double) * 6 * (size_t)(F * B)); }
+
+int fbt_bwd(const float* c1, const float* t0, const float* t1, const float* z, const float* raw,
+            const float* carry, const float* gout, int mask, float* gz, float* gc1, float* gt0,
+            float* gt1, int64_t F, int64_t B, int64_t T, void* ws, size_t ws_bytes,
+            hipStream_t s) {
+  if (F < 0 || B < 0 || T < 0) return RQF_ERR_ARG;
+  if (F == 0) return RQF_OK;
+  if (!gc1 || !gt0 || !gt1) return RQF_ERR_ARG;
+  if (B * T > 0 && (!c1 || !t0 || !t1 || !z || !gout || !gz || (!raw && !carry)))
+    return RQF_ERR_ARG;
+  if (!aligned8(z) || !aligned8(raw) || !aligned8(gout) || !aligned8(gz)) return RQF_ERR_ALIGN;
+  const size_t need = fbt_ws(F, B);
+  if (need && (!ws || ws_bytes < need)) return RQF_ERR_WORKSPACE;
+  double* partial = (double*)ws;
+  const int64_t R = F * B;
+  if (R > 0 && T > 0) {
+    const int64_t nc = (T + kTiTile - 1) / kTiTile;
+    const dim3 grid((unsigned)((R + kTiWaves - 1) / kTiWaves)), block(kTiWaves * kWave);
+    const bool vec = T % 2 == 0 && aligned16(z) && aligned16(raw) && aligned16(gout) && aligned16(gz);
+    if (carry) {
+      if (vec)
+        hipLaunchKernelGGL((fbt_bwd_kernel<true, true>), grid, block, 0, s, c1, t0, t1, z, raw,
+                           carry, gout, mask, gz, partial, F, B, T, nc);
+      else
+        hipLaunchKernelGGL((fbt_bwd_kernel<false, true>), grid, block, 0, s, c1, t0, t1, z, raw,
+                           carry, gout, mask, gz, partial, F, B, T, nc);
+    } else {
+      if (vec)
+        hipLaunchKernelGGL((fbt_bwd_kernel<true, false>), grid, block, 0, s, c1, t0, t1, z, raw,
+                           carry, gout, mask, gz, partial, F, B, T, nc);
+      else
+        hipLaunchKernelGGL((fbt_bwd_kernel<false, false>), grid, block, 0, s, c1, t0, t1, z, raw,
+                           carry, gout, mask, gz, partial, F, B, T, nc);
+    }
+    hipLaunchKernelGGL(coef_reduce_kernel, dim3((unsigned)((F + 255) / 256)), dim3(256), 0, s,
+                       partial, F, B, B, (int64_t)1, gc1, gt0, gt1);
+  } else {
+    hipLaunchKernelGGL(coef_reduce_kernel, dim3((unsigned)((F + 255) / 256)), dim3(256), 0, s,
+                       partial, F, (int64_t)0, B, (int64_t)1, gc1, gt0, gt1);
+  }
+  return launch_status();
+}
+
+}  // namespace
+
+// ------------------------------- C ABI ------------------------------------
+
+extern "C" size_t rqf_btf_scan_workspace(int64_t B, int64_t T, int64_t F) {
+  return btf_ws(B, T, F);
+}
+
+extern "C" int rqf_chunked_scan_fwd(const float* c1, const float* c2, const float* u, float* out,
+                                    int64_t B, int64_t T, int64_t F, void* ws, size_t ws_bytes,
+                                    rqf_stream_t stream) {
+  return btf_fwd(c1, c2, nullptr, u, out, B, T, F, ws, ws_bytes, (hipStream_t)stream);
+}
+
+extern "C" int rqf_chunked_scan_bwd(const float* c1, const float* c2, const float* u,
+                                    const float* states, const float* grad_out, float* grad_u,
+                                    float* grad_c1, float* grad_c2, int64_t B, int64_t T,
+                                    int64_t F, void* ws, size_t ws_bytes, rqf_stream_t stream) {
+  return btf_bwd(c1, c2, nullptr, u, states, grad_out, grad_u, grad_c1, grad_c2, nullptr, B, T, F,
+                 ws, ws_bytes, (hipStream_t)stream);
+}
+
+extern "C" int rqf_chunked_prospective_fwd(const float* c1, const float* tap0, const float* tap1,
+                                           const float* x, float* out, int64_t B, int64_t T,
+                                           int64_t F, void* ws, size_t ws_bytes,
+                                           rqf_stream_t stream) {
+  if (!tap1) return RQF_ERR_ARG;
+  return btf_fwd(c1, tap0, tap1, x, out, B, T, F, ws, ws_bytes, (hipStream_t)stream);
+}
+
+extern "C" int rqf_chunked_prospective_bwd(const float* c1, const float* tap0, const float* tap1,
+                                           const float* x, const float* states,
+                                           const float* grad_out, float* grad_x, float* grad_c1,
+                                           float* grad_tap0, float* grad_tap1, int64_t B,
+                                           int64_t T, int64_t F, void* ws, size_t ws_bytes,
+                                           rqf_stream_t stream) {
+  if (!tap1 || !grad_tap1) return RQF_ERR_ARG;
+  return btf_bwd(c1, tap0, tap1, x, states, grad_out, grad_x, grad_c1, grad_tap0, grad_tap1, B, T,
+                 F, ws, ws_bytes, (hipStream_t)stream);
+}
+
+extern "C" int64_t rqf_fbt_carry_chunks(int64_t T) { return T > 0 ? (T + kTiTile - 1) / kTiTile : 0; }
+
+extern "C" size_t rqf_fbt_workspace(int64_t F, int64_t B, int64_t T) {
+  (void)T;
+  return fbt_ws(F, B);
+}
+
+extern "C" int rqf_fbt_prospective_fwd(const float* c1, const float* tap0, const float* tap1,
+                                       const float* z, float* raw, float* act, int64_t F,
+                                       int64_t B, int64_t T, rqf_stream_t stream) {
+  if (!raw && F * B * T > 0) return RQF_ERR_ARG;
+  return fbt_fwd(c1, tap0, tap1, z, raw, act, nullptr, F, B, T, (hipStream_t)stream);
+}
+
+extern "C" int rqf_fbt_prospective_bwd(const float* c1, const float* tap0, const float* tap1,
+                                       const float* z, const float* raw, const float* grad_out,
+                                       int32_t fuse_act, float* grad_z, float* grad_c1,
+                                       float* grad_tap0, float* grad_tap1, int64_t F, int64_t B,
+                                       int64_t T, void* ws, size_t ws_bytes, rqf_stream_t stream) {
+  if (!raw && F * B * T > 0) return RQF_ERR_ARG;
+  return fbt_bwd(c1, tap0, tap1, z, raw, nullptr, grad_out, fuse_act, grad_z, grad_c1, grad_tap0,
+                 grad_tap1, F, B, T, ws, ws_bytes, (hipStream_t)stream);
+}
+
+extern "C" int rqf_fbt_recompute_fwd(const float* c1, const float* tap0, const float* tap1,
+                                     const float* z, float* act, float* carry, int64_t F,
+                                     int64_t B, int64_t T, rqf_stream_t stream) {
+  if ((!act || !carry) && F * B * T > 0) return RQF_ERR_ARG;
+  return fbt_fwd(c1, tap0, tap1, z, nullptr, act, carry, F, B, T, (hipStream_t)stream);
+}
+
+extern "C" int rqf_fbt_recompute_bwd(const float* c1, const float* tap0, const float* tap1,
+                                     const float* z, const float* carry, const float* grad_out,
+                                     float* grad_z, float* grad_c1, float* grad_tap0,
+                                     float* grad_tap1, int64_t F, int64_t B, int64_t T, void* ws,
+                                     size_t ws_bytes, rqf_stream_t stream) {
+  if (!carry && F * B * T > 0) return RQF_ERR_ARG;
+  return fbt_bwd(c1, tap0, tap1, z, nullptr, carry, grad_out, 1, grad_z, grad_c1, grad_tap0,
+                 grad_tap1, F, B, T, ws, ws_bytes, (hipStream_t)stream);
+}
+
+extern "C" const char* rqf_version(void) { return "rqf_hip 0.1.0 (gfx950)"; }
+
+extern "C" const char* rqf_error_string(int code) {
+  switch (code) {
+    case RQF_OK:
+      return "ok";
+    case RQF_ERR_ARG:
+      return "invalid argument (null pointer, shape or chunk)";
+    case RQF_ERR_WORKSPACE:
+      return "workspace missing or too small";
+    case RQF_ERR_ALIGN:
+      return "tensor not 8-byte aligned";
+    default:
+      return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
+  }
+}

@@ -1,0 +1,135 @@
+"""Channel-outermost ``(filters, batch, time)`` two-tap prospective scans.
+
+Mirrors rqf_models/ops/fbt_scan_kernel.py: ``_FBTProspectiveScan`` /
+``fbt_prospective_scan`` (:245-357) and ``_FBTRecompute`` /
+``fbt_recompute_scan`` (:575-689), same signatures and return values, on the
+HIP kernels ``rqf_fbt_*``.
+
+The recompute variant stores only the split-ReLU output plus the state that
+enters every tile of 512 steps, and replays the tile in the backward; its
+carry granularity is internal to the autograd context.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch.autograd.function import once_differentiable
+
+from prospective_rqf_amd import _lib
+
+
+def _c64(t):
+    if not t.is_complex():
+        t = t.to(torch.cfloat)
+    return t.to(torch.complex64).resolve_conj().contiguous()
+
+
+def _coefs(C1, tap0, tap1, filters):
+    out = [_c64(c) for c in (C1, tap0, tap1)]
+    for c in out:
+        if c.shape != (filters,):
+            raise ValueError(f"coefficients must have shape ({filters},), got {tuple(c.shape)}")
+    return out
+
+
+def _bwd_grads(F, device):
+    return [torch.empty(F, dtype=torch.complex64, device=device) for _ in range(3)]
+
+
+class _FBTProspectiveScan(torch.autograd.Function):
+    """Two-tap prospective scan on (F,B,T); optional fused split-ReLU output."""
+
+    @staticmethod
+    def forward(ctx, C1, tap0, tap1, x_fbt, fuse_act):
+        x = _c64(x_fbt)
+        _lib.require_device(x)
+        filters, batch, time = x.shape
+        C1, tap0, tap1 = _coefs(C1, tap0, tap1, filters)
+        raw = torch.empty_like(x)
+        act = torch.empty_like(x) if fuse_act else None
+        _lib.check(
+            _lib.load().rqf_fbt_prospective_fwd(
+                _lib.ptr(C1), _lib.ptr(tap0), _lib.ptr(tap1), _lib.ptr(x), _lib.ptr(raw),
+                _lib.ptr(act), filters, batch, time, _lib.stream_of(x)),
+            "rqf_fbt_prospective_fwd",
+        )
+        ctx.save_for_backward(C1, tap0, tap1, x, raw)
+        ctx.fuse_act = fuse_act
+        return act if fuse_act else raw
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad_output):
+        C1, tap0, tap1, x, raw = ctx.saved_tensors
+        filters, batch, time = x.shape
+        g = _c64(grad_output)
+        grad_z = torch.empty_like(x)
+        gc1, gt0, gt1 = _bwd_grads(filters, x.device)
+        lib = _lib.load()
+        n = lib.rqf_fbt_workspace(filters, batch, time)
+        ws = _lib.workspace(n, x.device)
+        _lib.check(
+            lib.rqf_fbt_prospective_bwd(
+                _lib.ptr(C1), _lib.ptr(tap0), _lib.ptr(tap1), _lib.ptr(x), _lib.ptr(raw),
+                _lib.ptr(g), int(bool(ctx.fuse_act)), _lib.ptr(grad_z), _lib.ptr(gc1),
+                _lib.ptr(gt0), _lib.ptr(gt1), filters, batch, time, _lib.ptr(ws), n,
+                _lib.stream_of(x)),
+            "rqf_fbt_prospective_bwd",
+        )
+        return gc1, gt0, gt1, grad_z, None
+
+
+def fbt_prospective_scan(C1, tap0, tap1, x_fbt, fuse_act=False):
+    """x_out[n] = C1 x_out[n-1] + tap0 x[n] + tap1 x[n-1] on (F,B,T).
+
+    Returns the split-ReLU output when ``fuse_act``, else the raw state."""
+    return _FBTProspectiveScan.apply(C1, tap0, tap1, x_fbt, fuse_act)
+
+
+class _FBTRecompute(torch.autograd.Function):
+    """Split-ReLU prospective scan that replays the raw state in the backward."""
+
+    @staticmethod
+    def forward(ctx, C1, tap0, tap1, x_fbt):
+        x = _c64(x_fbt)
+        _lib.require_device(x)
+        filters, batch, time = x.shape
+        C1, tap0, tap1 = _coefs(C1, tap0, tap1, filters)
+        lib = _lib.load()
+        nchunks = lib.rqf_fbt_carry_chunks(time)
+        act = torch.empty_like(x)
+        carry = torch.empty((filters * batch, max(nchunks, 1)), dtype=torch.complex64,
+                            device=x.device)
+        _lib.check(
+            lib.rqf_fbt_recompute_fwd(
+                _lib.ptr(C1), _lib.ptr(tap0), _lib.ptr(tap1), _lib.ptr(x), _lib.ptr(act),
+                _lib.ptr(carry), filters, batch, time, _lib.stream_of(x)),
+            "rqf_fbt_recompute_fwd",
+        )
+        ctx.save_for_backward(C1, tap0, tap1, x, carry)
+        return act
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad_output):
+        C1, tap0, tap1, x, carry = ctx.saved_tensors
+        filters, batch, time = x.shape
+        g = _c64(grad_output)
+        grad_z = torch.empty_like(x)
+        gc1, gt0, gt1 = _bwd_grads(filters, x.device)
+        lib = _lib.load()
+        n = lib.rqf_fbt_workspace(filters, batch, time)
+        ws = _lib.workspace(n, x.device)
+        _lib.check(
+            lib.rqf_fbt_recompute_bwd(
+                _lib.ptr(C1), _lib.ptr(tap0), _lib.ptr(tap1), _lib.ptr(x), _lib.ptr(carry),
+                _lib.ptr(g), _lib.ptr(grad_z), _lib.ptr(gc1), _lib.ptr(gt0), _lib.ptr(gt1),
+                filters, batch, time, _lib.ptr(ws), n, _lib.stream_of(x)),
+            "rqf_fbt_recompute_bwd",
+        )
+        return gc1, gt0, gt1, grad_z
+
+
+def fbt_recompute_scan(C1, tap0, tap1, x_fbt):
+    """Split-ReLU prospective scan; stores the output plus per-tile entry states."""
+    return _FBTRecompute.apply(C1, tap0, tap1, x_fbt)

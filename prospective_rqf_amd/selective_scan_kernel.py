@@ -1,0 +1,129 @@
+"""Host side of the fused selective scan: allocation and launch.
+
+Mirrors ``selective_forward`` / ``selective_backward`` of the reference
+(rqf_models/ops/selective_scan_kernel.py:491-561): same arguments, same
+returned tensors and shapes.  The compute runs in ``librqf_hip.so``
+(``rqf_selective_fwd`` / ``rqf_selective_bwd``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from prospective_rqf_amd import _lib
+
+
+def _real_ptr(t: torch.Tensor | None):
+    """Pointer to the interleaved (re, im) storage of a complex tensor."""
+    if t is None:
+        return None
+    if t.is_conj():
+        t = t.resolve_conj()
+    return _lib.ptr(t)
+
+
+def inputs_struct(z: torch.Tensor, inputs) -> tuple[_lib.SelectiveInputsStruct, list]:
+    """Pack ``SelectiveScanInputs`` into the C struct; returns (struct, keep-alive list)."""
+    f, b, t = z.shape
+    o = inputs.options
+    has_gamma, has_warp, has_write = bool(o[0]), bool(o[1]), bool(o[2])
+
+    def vec(v):
+        return v.to(device=z.device, dtype=torch.float32).contiguous()
+
+    gl = vec(inputs.gamma_logits) if has_gamma else None
+    dl = vec(inputs.warp_logits) if has_warp else None
+    wl = vec(inputs.write_logits) if has_write else None
+    params = [vec(getattr(inputs, n)) for n in (
+        "bias", "theta", "minimum", "span", "step", "horizon", "theta_minimum", "theta_maximum")]
+    groups = inputs.groups.to(device=z.device, dtype=torch.int64).contiguous() if has_warp else None
+    for name, v, rows in (("gamma_logits", gl, f), ("write_logits", wl, f)):
+        if v is not None and tuple(v.shape) != (rows, b, t):
+            raise ValueError(f"{name} must have shape {(rows, b, t)}, got {tuple(v.shape)}")
+    g = 0
+    if dl is not None:
+        if dl.dim() != 3 or tuple(dl.shape[1:]) != (b, t):
+            raise ValueError(f"warp_logits must have shape (G, {b}, {t}), got {tuple(dl.shape)}")
+        g = dl.shape[0]
+        if groups is None or groups.shape != (f,):
+            raise ValueError("groups must be a (F,) index tensor when the warp head is on")
+    for name, v in zip(("bias", "theta", "minimum", "span", "step", "horizon",
+                        "theta_minimum", "theta_maximum"), params):
+        if v.shape != (f,):
+            raise ValueError(f"{name} must have shape ({f},), got {tuple(v.shape)}")
+    s = _lib.SelectiveInputsStruct(
+        f, b, t, g,
+        *(None if v is None else v.data_ptr() for v in (gl, dl, wl)),
+        *(v.data_ptr() for v in params),
+        None if groups is None else groups.data_ptr(),
+        int(has_gamma), int(has_warp), int(has_write), int(bool(o[3])),
+        float(o[4]), float(o[5]),
+        int(bool(o[6])), int(bool(o[7])), int(bool(o[8])),
+        float(o[9]), float(o[10]),
+        int(bool(o[11])),
+    )
+    return s, [gl, dl, wl, groups, *params]
+
+
+def selective_forward(z, inputs, activate, write_raw, chunk):
+    """Fused forward: returns ``(raw|None, act|None, entries)``.
+
+    z: (F,B,T) complex64 drive.  entries: (F*B, ceil(T/chunk)) complex64 state
+    entering each chunk (consumed by :func:`selective_backward`).
+    """
+    _lib.require_device(z)
+    if z.dtype != torch.complex64:
+        raise TypeError("selective_forward expects a complex64 drive")
+    z = z.resolve_conj().contiguous()
+    f, b, t = z.shape
+    nc = -(-t // chunk)
+    raw = torch.empty_like(z) if write_raw else None
+    act = torch.empty_like(z) if activate else None
+    entries = torch.empty((f * b, nc), dtype=z.dtype, device=z.device)
+    s, keep = inputs_struct(z, inputs)
+    lib = _lib.load()
+    _lib.check(
+        lib.rqf_selective_fwd(ctypes.byref(s), _real_ptr(z), chunk, _real_ptr(raw),
+                              _real_ptr(act), _real_ptr(entries), _lib.stream_of(z)),
+        "rqf_selective_fwd",
+    )
+    del keep
+    return raw, act, entries
+
+
+def selective_backward(z, inputs, entries, gy, gx, activate, truncated, chunk):
+    """Fused backward: ``(dz, dzw, dg|None, dd_group|None, dw|None, dbias, dtheta)``.
+
+    ``dzw`` is the same tensor as ``dz`` unless ``truncated``.
+    """
+    _lib.require_device(z, entries, gy, gx)
+    z = z.resolve_conj().contiguous()
+    f, b, t = z.shape
+    o = inputs.options
+    dz = torch.empty_like(z)
+    dzw = torch.empty_like(z) if truncated else dz
+    dg = torch.empty((f, b, t), dtype=torch.float32, device=z.device) if o[0] else None
+    dw = torch.empty((f, b, t), dtype=torch.float32, device=z.device) if o[2] else None
+    s, keep = inputs_struct(z, inputs)
+    dd = torch.empty((s.G, b, t), dtype=torch.float32, device=z.device) if o[1] else None
+    dbias = torch.empty(f, dtype=torch.float32, device=z.device)
+    dtheta = torch.empty(f, dtype=torch.float32, device=z.device)
+    gy = None if gy is None else gy.resolve_conj().to(torch.complex64).contiguous()
+    gx = None if gx is None else gx.resolve_conj().to(torch.complex64).contiguous()
+    entries = entries.contiguous()
+    lib = _lib.load()
+    nbytes = lib.rqf_selective_bwd_workspace(ctypes.byref(s), chunk)
+    ws = _lib.workspace(nbytes, z.device)
+    _lib.check(
+        lib.rqf_selective_bwd(
+            ctypes.byref(s), _real_ptr(z), _real_ptr(entries), chunk, _real_ptr(gy),
+            _real_ptr(gx), int(bool(activate)), int(bool(truncated)), _real_ptr(dz),
+            _real_ptr(dzw), _lib.ptr(dg), _lib.ptr(dd), _lib.ptr(dw), _lib.ptr(dbias),
+            _lib.ptr(dtheta), _lib.ptr(ws), nbytes, _lib.stream_of(z),
+        ),
+        "rqf_selective_bwd",
+    )
+    del keep
+    return dz, dzw, dg, dd, dw, dbias, dtheta

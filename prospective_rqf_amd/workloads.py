@@ -1,0 +1,117 @@
+"""Synthetic workloads of the benchmark configurations (seeded, no datasets).
+
+Per-channel parameters follow the reference's resonant "paper recipe"
+(rqf_models/backbones/rqf/filter.py:250-262, 330-358, 371-377):
+
+* theta = 2*pi*f*tau log-uniform in [log(2*pi*tau/seq_duration), log(2*pi)]
+* gamma = theta/(1+theta) (critical damping), gamma bounds [1e-6, 1-1e-6],
+  projected to the interior margin (selective.py:126-136, filter.py:398-400)
+* eta = dt/tau, horizon = 1 (prospective_tau None)
+* theta band [2*pi*f_min*tau, min(2*pi*f_max*tau, pi*tau/dt)] with
+  f_min = 1/seq_duration, f_max = 1/tau
+* warp groups = rank(theta) * G // F (selective.py:164-165)
+* sigmoid gamma link: bias = logit((gamma - lo)/span) (selective.py:227-236)
+
+ZOH two-tap coefficients for the static (non-selective) scans follow
+``RQF.compute_two_tap_coefficients`` (filter.py:630-646).
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from prospective_rqf_amd.selective_scan import SelectiveScanInputs
+
+LN_1_25 = math.log(1.25)
+
+
+def recipe_params(F: int, *, samp: float, tau: float, seq_duration: float, margin: float = 1e-3,
+                  generator: torch.Generator | None = None, dtype=torch.float64):
+    """Per-channel (theta, gamma, eta, lo, span, theta_lo, theta_hi) in fp64."""
+    dt = 1.0 / samp
+    lo_t = math.log(2 * math.pi * tau / seq_duration)
+    hi_t = math.log(2 * math.pi)
+    theta = torch.exp(lo_t + torch.rand(F, generator=generator, dtype=dtype) * (hi_t - lo_t))
+    lo, hi = 1e-6, 1.0 - 1e-6
+    span = hi - lo
+    gamma = (theta / (1 + theta)).clamp(lo + margin * span, hi - margin * span)
+    theta_lo = torch.full((F,), 2 * math.pi * (1.0 / seq_duration) * tau, dtype=dtype)
+    theta_hi = torch.full((F,), min(2 * math.pi * (1.0 / tau) * tau, math.pi * tau / dt),
+                          dtype=dtype)
+    eta = torch.full((F,), dt / tau, dtype=dtype)
+    return dict(theta=theta, gamma=gamma, eta=eta, lo=torch.full((F,), lo, dtype=dtype),
+                span=torch.full((F,), span, dtype=dtype), theta_lo=theta_lo, theta_hi=theta_hi)
+
+
+def zoh_two_tap(gamma, theta, eta, ratio):
+    """(C1, tap0, tap1) of the impulse-ZOH prospective recurrence (filter.py:630-646)."""
+    a = torch.complex(-gamma * eta, (1 - gamma) * theta * eta)
+    C1 = torch.exp(a)
+    small = a.abs() < 1e-4
+    safe = torch.where(small, torch.ones_like(a), a)
+    phi = torch.where(small, 1 + a * (0.5 + a * (1 / 6 + a / 24)), torch.expm1(a) / safe)
+    extra = gamma * ratio * C1
+    return C1, gamma * eta * phi + extra, -extra
+
+
+def selective_inputs(F, B, T, *, G=8, gamma=True, write=True, warp="grouped", log_shift=False,
+                     prospective=True, gamma_horizon=False, write_sigmoid=True, write_max=2.0,
+                     gamma_scale=LN_1_25, warp_scale=LN_1_25, bound_warp=True, samp=16000.0,
+                     tau=5.0 / 16000.0, seq_duration=1.0, logit_std=1.0, device="cpu", seed=0):
+    """SelectiveScanInputs with N(0, logit_std^2) logits and recipe parameters."""
+    g = torch.Generator().manual_seed(seed)
+    p = recipe_params(F, samp=samp, tau=tau, seq_duration=seq_duration, generator=g)
+    n_warp = 0 if warp == "none" else (1 if warp == "global" else G)
+    if log_shift:
+        bias = torch.log(p["gamma"]) - gamma_scale  # resting log gamma below the ceiling
+    elif gamma:
+        bias = torch.logit((p["gamma"] - p["lo"]) / p["span"])
+    else:
+        bias = p["gamma"]
+    ranks = p["theta"].argsort(stable=True).argsort()
+    groups = ranks * n_warp // F if n_warp else None
+
+    def logits(rows):
+        return (logit_std * torch.randn(rows, B, T, generator=g)).float()
+
+    options = (
+        bool(gamma), n_warp > 0, bool(write), bool(log_shift), float(gamma_scale),
+        float(warp_scale), bool(prospective), bool(gamma_horizon), bool(write and write_sigmoid),
+        float(write_max), -math.log(write_max - 1), bool(n_warp > 0 and bound_warp),
+    )
+    f32 = lambda v: v.float().to(device)  # noqa: E731
+    return SelectiveScanInputs(
+        logits(F).to(device) if gamma else torch.empty(0, B, T, device=device),
+        logits(n_warp).to(device) if n_warp else torch.empty(0, B, T, device=device),
+        logits(F).to(device) if write else torch.empty(0, B, T, device=device),
+        f32(bias), f32(p["theta"]), None if groups is None else groups.to(device),
+        f32(p["lo"]), f32(p["span"]), f32(p["eta"]), f32(torch.ones(F, dtype=torch.float64)),
+        f32(p["theta_lo"]), f32(p["theta_hi"]), options,
+    )
+
+
+def randn_c64(*shape, generator=None, device="cpu"):
+    re = torch.randn(*shape, generator=generator)
+    im = torch.randn(*shape, generator=generator)
+    return torch.complex(re, im).to(device)
+
+
+def raw_waveform(B, T, *, samp=16000.0, generator=None):
+    """Sum of 3 random sinusoids in [50, 4000] Hz plus N(0, 0.05^2), clipped to [-1, 1]."""
+    t = torch.arange(T, dtype=torch.float64) / samp
+    f = 50 + (4000 - 50) * torch.rand(B, 3, 1, generator=generator, dtype=torch.float64)
+    ph = 2 * math.pi * torch.rand(B, 3, 1, generator=generator, dtype=torch.float64)
+    x = torch.sin(2 * math.pi * f * t + ph).sum(1) / 3
+    x = x + 0.05 * torch.randn(B, T, generator=generator, dtype=torch.float64)
+    return x.clamp(-1, 1).float()
+
+
+def static_two_tap(F, *, samp=16000.0, tau=5.0 / 16000.0, seq_duration=1.0, seed=0,
+                   device="cpu"):
+    """(C1, tap0, tap1) complex64 per channel for the static prospective RQF."""
+    g = torch.Generator().manual_seed(seed)
+    p = recipe_params(F, samp=samp, tau=tau, seq_duration=seq_duration, margin=0.0, generator=g)
+    c1, t0, t1 = zoh_two_tap(p["gamma"], p["theta"], p["eta"], torch.ones_like(p["gamma"]))
+    return tuple(v.to(torch.complex64).to(device) for v in (c1, t0, t1))

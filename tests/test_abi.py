@@ -1,0 +1,80 @@
+"""The C-ABI library loads and exports every entry point the header declares
+(CPU only: no compute call is made)."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from prospective_rqf_amd import _lib
+from prospective_rqf_amd.build import LIB_PATH
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "rqf_scan.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rqf_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def built_lib():
+    if not os.path.exists(LIB_PATH):
+        from prospective_rqf_amd.build import build
+
+        build()
+    return LIB_PATH
+
+
+def test_header_declares_the_expected_entry_points():
+    names = header_functions()
+    assert "rqf_selective_fwd" in names and "rqf_selective_bwd" in names
+    assert "rqf_fbt_recompute_fwd" in names and "rqf_chunked_scan_bwd" in names
+
+
+def test_library_exports_every_declared_symbol(built_lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", built_lib], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\b(rqf_[a-z0-9_]+)\b", out))
+    missing = [n for n in header_functions() if n not in exported]
+    assert not missing, missing
+
+
+def test_binding_covers_the_header_exactly():
+    assert sorted(_lib.SIGNATURES) == header_functions()
+
+
+def test_library_loads_and_reports_version(built_lib):
+    lib = _lib.load()
+    assert b"gfx950" in lib.rqf_version()
+    assert lib.rqf_error_string(-2) == b"workspace missing or too small"
+    # Pure host-side queries (no device access).
+    assert lib.rqf_fbt_carry_chunks(16000) == 32
+    assert lib.rqf_fbt_workspace(128, 32, 16000) >= 6 * 8 * 128 * 32
+    assert lib.rqf_btf_scan_workspace(4, 161, 64) > 0
+    s = _lib.SelectiveInputsStruct(F=256, B=64, T=16000, G=8, has_warp=1)
+    assert lib.rqf_selective_bwd_workspace(ctypes.byref(s), 256) >= 2 * 8 * 256 * 64
+
+
+def test_struct_layout_matches_header():
+    # Offsets of the C struct: 4 int64, 12 pointers, then 4+2+3+2+1 scalars.
+    s = _lib.SelectiveInputsStruct
+    assert s.gamma_logits.offset == 32
+    assert s.groups.offset == 32 + 11 * 8
+    assert s.has_gamma.offset == 32 + 12 * 8
+    assert ctypes.sizeof(s) == 32 + 12 * 8 + 12 * 4
+
+
+def test_product_refuses_cpu_tensors():
+    import torch
+
+    from prospective_rqf_amd.fbt_scan_kernel import fbt_prospective_scan
+
+    z = torch.zeros(2, 1, 4, dtype=torch.complex64)
+    c = torch.zeros(2, dtype=torch.complex64)
+    with pytest.raises(_lib.RQFError):
+        fbt_prospective_scan(c, c, c, z)

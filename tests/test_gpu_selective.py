@@ -1,0 +1,226 @@
+"""GPU parity of the fused selective scan against the fp64 oracle.
+
+Mirrors the reference's kernel suite (tests/test_selective_cuda.py:193-261):
+every controller case x prospective x truncated, chunk/tile edges, output
+consumers, saturated writes, clipped warps, interior-gamma edges, horizons,
+tiny and collapsed poles, conjugate cotangents, long sequences.  The bar is
+tighter than the reference's 4e-4 / 4e-3: normwise max relative error
+<= 1e-4 for every output and gradient tensor.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle, torch_ref
+from prospective_rqf_amd.selective_scan import selective_layer_scan
+from prospective_rqf_amd.selective_scan_kernel import selective_backward, selective_forward
+from tests.helpers import PARITY_RTOL, crandn, relerr
+from tests.selective_cases import CASES, case_id, make_inputs, rounded_to_f32, to_torch
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+
+
+def _c64(a):
+    return np.asarray(a, dtype=np.complex64).astype(np.complex128)
+
+
+def run_case(F, B, T, case, *, prospective=True, truncated=False, activate=True, write_raw=True,
+             chunk=32, seed=0, conj_cot=False, edit=None, **kw):
+    rng = np.random.default_rng(seed)
+    inp = make_inputs(F, B, T, case, rng, prospective=prospective, **kw)
+    z = crandn(rng, F, B, T)
+    if edit is not None:
+        edit(inp, z)
+    inp = rounded_to_f32(inp)
+    z = _c64(z)
+    gy = _c64(crandn(rng, F, B, T)) if write_raw else None
+    gx = _c64(crandn(rng, F, B, T)) if activate else None
+    if conj_cot:
+        gy = None if gy is None else np.conj(gy)
+        gx = None if gx is None else np.conj(gx)
+    ti = to_torch(inp, device="cuda")
+    zt = torch.as_tensor(z.astype(np.complex64), device="cuda")
+    dev = lambda a: None if a is None else torch.as_tensor(a.astype(np.complex64), device="cuda")  # noqa: E731
+    raw, act, entries = selective_forward(zt, ti, activate, write_raw, chunk)
+    out = selective_backward(zt, ti, entries, dev(gy), dev(gx), activate, truncated, chunk)
+    raw_o, act_o = oracle.selective_fwd(z, inp)
+    ref = oracle.selective_bwd(z, inp, gy, gx, truncated=truncated)
+    errs = {}
+    if write_raw:
+        errs["raw"] = relerr(raw, raw_o)
+    else:
+        assert raw is None
+    if activate:
+        errs["act"] = relerr(act, act_o)
+    else:
+        assert act is None
+    nc = -(-T // chunk)
+    ent_ref = np.zeros((F * B, nc), complex)
+    rr = raw_o.reshape(F * B, T)
+    for j in range(1, nc):
+        ent_ref[:, j] = rr[:, j * chunk - 1]
+    errs["entries"] = relerr(entries, ent_ref)
+    for name, got, want in zip(("dz", "dzw", "dg", "dd", "dw", "dbias", "dtheta"), out, ref):
+        if want is None:
+            assert got is None, name
+        else:
+            errs[name] = relerr(got, want)
+    bad = {k: v for k, v in errs.items() if not v <= PARITY_RTOL}
+    assert not bad, bad
+    return errs
+
+
+@pytest.mark.parametrize("truncated", [False, True])
+@pytest.mark.parametrize("prospective", [False, True])
+@pytest.mark.parametrize("case", CASES, ids=case_id)
+def test_controller_cases(case, prospective, truncated):
+    print(f"case: {case_id(case)} prospective={prospective} truncated={truncated}", flush=True)
+    run_case(5, 2, 33, case, prospective=prospective, truncated=truncated,
+             gamma_horizon=prospective and case["gamma"] and not case["log_shift"],
+             seed=len(case_id(case)))
+
+
+CASE_ALL = dict(gamma=True, write=True, warp="grouped", log_shift=False, write_sigmoid=True)
+CASE_LOG = dict(gamma=True, write=True, warp="global", log_shift=True, write_sigmoid=True)
+
+
+@pytest.mark.parametrize("outputs", [(True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("truncated", [False, True])
+@pytest.mark.parametrize("T", [1, 7, 31, 32, 33, 63, 65, 129, 256, 257, 300])
+def test_chunk_edges_and_output_consumers(T, truncated, outputs):
+    print(f"case: T={T} truncated={truncated} outputs={outputs}", flush=True)
+    run_case(5, 2, T, CASE_ALL, truncated=truncated, activate=outputs[0], write_raw=outputs[1],
+             seed=T)
+
+
+@pytest.mark.parametrize("truncated", [False, True])
+@pytest.mark.parametrize("T,chunk", [(1, 1), (255, 256), (256, 256), (257, 256), (4097, 256),
+                                     (1000, 4), (1000, 512), (3000, 1024), (700, 2048)])
+def test_automatic_and_large_chunks(T, chunk, truncated):
+    print(f"case: T={T} chunk={chunk} truncated={truncated}", flush=True)
+    run_case(4, 3, T, CASE_LOG, truncated=truncated, chunk=chunk, seed=T + chunk)
+
+
+@pytest.mark.parametrize("prospective,truncated", [(False, False), (True, True), (True, False)])
+@pytest.mark.parametrize("maximum,saturated", [(1.25, False), (3.0, True)])
+def test_sigmoid_write_bound_and_saturation(prospective, truncated, maximum, saturated):
+    def edit(inp, z):
+        if saturated:
+            inp.write_logits[0, 0, :3] = [-1000.0, 0.0, 1000.0]
+
+    print(f"case: write max={maximum} saturated={saturated}", flush=True)
+    run_case(5, 2, 33, CASE_ALL, prospective=prospective, truncated=truncated,
+             write_max=maximum, edit=edit, seed=3)
+
+
+@pytest.mark.parametrize("truncated", [False, True])
+def test_clipped_frequency_warp(truncated):
+    """Interior and clipped samples (reference test_selective_cuda.py:234-238)."""
+    case = dict(gamma=False, write=True, warp="global", log_shift=False, write_sigmoid=True)
+
+    def edit(inp, z):
+        lo, hi = inp.theta_minimum, inp.theta_maximum
+        inp.theta[:] = np.sqrt(lo * hi)
+        pattern = np.array([-2.0, 0.1, 2.0])
+        inp.warp_logits[0] = np.resize(pattern, inp.warp_logits.shape[1:])
+
+    print(f"case: clipped warp truncated={truncated}", flush=True)
+    run_case(5, 2, 33, case, truncated=truncated, warp_scale=math.log(40.0), edit=edit, seed=9)
+
+
+@pytest.mark.parametrize("truncated", [False, True])
+def test_interior_gamma_edges(truncated):
+    case = dict(gamma=True, write=True, warp="none", log_shift=False, write_sigmoid=True)
+
+    def edit(inp, z):
+        margin = 1e-3
+        inp.bias[:2] = math.log(margin / (1 - margin))
+        inp.bias[2:] = -math.log(margin / (1 - margin))
+        inp.gamma_logits[:] = np.linspace(-0.5, 0.5, inp.gamma_logits.shape[-1])
+
+    print(f"case: gamma edges truncated={truncated}", flush=True)
+    run_case(5, 2, 33, case, truncated=truncated, edit=edit, seed=10)
+
+
+@pytest.mark.parametrize("truncated", [False, True])
+@pytest.mark.parametrize("mode,horizon", [("tau", None), ("tau", 0.0), ("tau", 1.6),
+                                          ("gamma", None)])
+def test_horizons(mode, horizon, truncated):
+    print(f"case: horizon mode={mode} horizon={horizon}", flush=True)
+    run_case(5, 2, 40, CASE_LOG if mode == "tau" else CASE_ALL, truncated=truncated,
+             gamma_horizon=mode == "gamma", horizon=horizon, seed=11)
+
+
+@pytest.mark.parametrize("truncated", [False, True])
+@pytest.mark.parametrize("kind", ["tiny", "collapse", "conj"])
+def test_numerical_edges(kind, truncated):
+    case = dict(gamma=False, write=True, warp="none", log_shift=False, write_sigmoid=True)
+
+    def edit(inp, z):
+        if kind == "tiny":
+            inp.bias[:] = math.exp(-70.0)
+            inp.theta[:] = math.exp(-50.0)
+
+    print(f"case: {kind} truncated={truncated}", flush=True)
+    run_case(5, 2, 33, case if kind != "conj" else CASE_LOG, truncated=truncated,
+             eta=1000.0 / 0.05 if kind == "collapse" else 0.2, edit=edit,
+             conj_cot=kind == "conj", seed=12)
+
+
+def test_long_rows_subset_of_north_star_shape():
+    """T = 16000 rows with the config-3 option set (grouped warp, sigmoid write)."""
+    print("case: long rows T=16000", flush=True)
+    run_case(6, 3, 16000, CASE_ALL, chunk=256, G=2, seed=13)
+
+
+@pytest.mark.parametrize("truncated", [False, True])
+def test_layer_scan_autograd_with_drive_gemm(truncated):
+    """selective_layer_scan (GEMM + kernels) vs float64 autograd of the restatement."""
+    print(f"case: layer scan truncated={truncated}", flush=True)
+    rng = np.random.default_rng(21)
+    I, F, B, T = 3, 5, 2, 65
+    inp = rounded_to_f32(make_inputs(F, B, T, CASE_ALL, rng, prospective=True, G=2))
+    x = _c64(crandn(rng, I, B, T))
+    W = _c64(0.5 * crandn(rng, F, I))
+    cot_raw, cot_act = crandn(rng, F, B, T), crandn(rng, F, B, T)
+
+    # GPU
+    ti = to_torch(inp, device="cuda")
+    leaves = [ti.gamma_logits, ti.warp_logits, ti.write_logits, ti.bias, ti.theta]
+    for v in leaves:
+        v.requires_grad_(True)
+    xg = torch.as_tensor(x.astype(np.complex64), device="cuda").requires_grad_(True)
+    Wg = torch.as_tensor(W.astype(np.complex64), device="cuda").requires_grad_(True)
+    raw, act = selective_layer_scan(xg, Wg, ti, truncated=truncated)
+    loss = ((torch.as_tensor(cot_raw, dtype=torch.complex64, device="cuda").conj() * raw).real.sum()
+            + (torch.as_tensor(cot_act, dtype=torch.complex64, device="cuda").conj() * act).real.sum())
+    grads = torch.autograd.grad(loss, [xg, Wg, *leaves])
+
+    # float64 CPU reference of reference_layer_scan semantics
+    tr = to_torch(inp, dtype=torch.float64)
+    rl = [tr.gamma_logits, tr.warp_logits, tr.write_logits, tr.bias, tr.theta]
+    for v in rl:
+        v.requires_grad_(True)
+    xr = torch.as_tensor(x).requires_grad_(True)
+    Wr = torch.as_tensor(W).requires_grad_(True)
+    z = (Wr @ xr.reshape(I, B * T)).reshape(F, B, T)
+    z_lag = (Wr @ xr.detach().reshape(I, B * T)).reshape(F, B, T) if truncated else z
+    raw_r = torch_ref.selective_scan(z, tr, truncated=truncated, z_lag=z_lag)
+    act_r = torch_ref.split_relu(raw_r)
+    loss_r = ((torch.as_tensor(cot_raw).conj() * raw_r).real.sum()
+              + (torch.as_tensor(cot_act).conj() * act_r).real.sum())
+    grads_r = torch.autograd.grad(loss_r, [xr, Wr, *rl])
+    assert relerr(raw, raw_r) <= PARITY_RTOL
+    assert relerr(act, act_r) <= PARITY_RTOL
+    for name, g, gr in zip(("x", "W", "g", "d", "w", "bias", "theta"), grads, grads_r):
+        err = relerr(g, gr)
+        assert err <= PARITY_RTOL, (name, err)

@@ -24,6 +24,22 @@ def _real_ptr(t: torch.Tensor | None):
     return _lib.ptr(t)
 
 
+_VALID_GROUPS: dict = {}
+
+
+def _check_groups(groups: torch.Tensor, n_groups: int) -> None:
+    """Warp-group indices must address rows of warp_logits (the kernel reads
+    warp_logits[groups[f]]).  Checked once per tensor version."""
+    key = (groups.data_ptr(), groups._version, groups.numel(), n_groups)
+    if _VALID_GROUPS.get(key):
+        return
+    if groups.numel() and (int(groups.min()) < 0 or int(groups.max()) >= n_groups):
+        raise ValueError(f"groups must index the {n_groups} warp-logit rows")
+    if len(_VALID_GROUPS) > 64:
+        _VALID_GROUPS.clear()
+    _VALID_GROUPS[key] = True
+
+
 def inputs_struct(z: torch.Tensor, inputs) -> tuple[_lib.SelectiveInputsStruct, list]:
     """Pack ``SelectiveScanInputs`` into the C struct; returns (struct, keep-alive list)."""
     f, b, t = z.shape
@@ -49,6 +65,7 @@ def inputs_struct(z: torch.Tensor, inputs) -> tuple[_lib.SelectiveInputsStruct, 
         g = dl.shape[0]
         if groups is None or groups.shape != (f,):
             raise ValueError("groups must be a (F,) index tensor when the warp head is on")
+        _check_groups(groups, g)
     for name, v in zip(("bias", "theta", "minimum", "span", "step", "horizon",
                         "theta_minimum", "theta_maximum"), params):
         if v.shape != (f,):

@@ -39,7 +39,21 @@ def _args():
     ap.add_argument("--no-cpu-baseline", dest="cpu", action="store_false")
     ap.add_argument("--cpu-steps", type=int, default=0,
                     help="time steps of the CPU baseline sample (0: auto, ~10-30 s)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 5 plain 1 GiB device copies (scale for FETCH/WRITE_SIZE)")
     return ap.parse_args()
+
+
+def copy_calibration():
+    """Five device-to-device copies of exactly 1 GiB each (read 1 GiB, write 1 GiB)."""
+    import torch
+
+    src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": src.numel() * 4, "copies": 5}), flush=True)
 
 
 # ---------------------------------------------------------------------------
@@ -141,6 +155,9 @@ def main():
         print("bench.py: this build measures one GPU only (single-GPU scan kernels; "
               "no collectives). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
     import torch
 
     from prospective_rqf_amd import _lib

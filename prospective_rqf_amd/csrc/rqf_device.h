@@ -165,44 +165,45 @@ __device__ __forceinline__ float ftanh(float x) {
   return fmaf(-2.0f, frcp(fexp(2.0f * x) + 1.0f), 1.0f);
 }
 
-// expm1(x) given e = exp(x): Taylor series for |x| < 0.5, else e - 1.
+// expm1(x) given e = exp(x): for |x| < 0.5 the degree-7 polynomial
+// x + x^2 * r(x), r fitted (weighted least squares, Lawson iteration) to
+// (expm1(x) - x)/x^2 on [-0.5, 0.5]: max relative error 3.1e-9 in fp64;
+// otherwise e - 1 (no cancellation for |x| >= 0.5).
 __device__ __forceinline__ float fexpm1(float x, float e) {
   if (fabsf(x) < 0.5f) {
-    float p = fmaf(x, 1.0f / 362880.0f, 1.0f / 40320.0f);
-    p = fmaf(x, p, 1.0f / 5040.0f);
-    p = fmaf(x, p, 1.0f / 720.0f);
-    p = fmaf(x, p, 1.0f / 120.0f);
-    p = fmaf(x, p, 1.0f / 24.0f);
-    p = fmaf(x, p, 1.0f / 6.0f);
-    p = fmaf(x, p, 0.5f);
-    return fmaf(x * x, p, x);
+    float r = fmaf(x, 1.9990473167705037e-04f, 1.3997542041360440e-03f);
+    r = fmaf(x, r, 8.3330821525987070e-03f);
+    r = fmaf(x, r, 4.1665312400424060e-02f);
+    r = fmaf(x, r, 1.6666667932516960e-01f);
+    r = fmaf(x, r, 5.0000004193574390e-01f);
+    return fmaf(x * x, r, x);
   }
   return e - 1.0f;
 }
 
-// For an angle x: sin(x), and 2 sin^2(x/2) = 1 - cos(x).  The argument is
-// reduced to r = x - 2*pi*q with |r| <= pi (Cody-Waite, two-part 2*pi), then
-// h = r/2 in [-pi/2, pi/2] goes through Taylor polynomials:
+// For an angle x: sin(x), and vers(x) = 1 - cos(x) = 2 sin^2(x/2).  The
+// argument is reduced to r = x - 2*pi*q, |r| <= pi (Cody-Waite, two-part
+// 2*pi); h = r/2 in [-pi/2, pi/2] goes through fitted polynomials
+//   sin(h) = h * P(h^2)       degree 9, max relative error 4.3e-9
+//   cos(h) = 1 + h^2 Q(h^2)   degree 10, max absolute error 2.4e-10
+// (weighted least squares, Lawson iteration, on [0, (pi/2)^2]); then
 //   sin x = 2 sin(h) cos(h),  1 - cos x = 2 sin^2(h).
 __device__ __forceinline__ void fsin_vers(float x, float& s, float& vers) {
   const float q = rintf(x * 0.15915494309189535f);
-  float r = fmaf(-q, 6.28318548202514648f, x);   // 2*pi rounded to fp32
-  r = fmaf(-q, -1.7484556000744487e-07f, r);     // 2*pi - fp32(2*pi)
+  float r = fmaf(-q, 6.28318548202514648f, x);  // 2*pi rounded to fp32
+  r = fmaf(-q, -1.7484556000744487e-07f, r);    // 2*pi - fp32(2*pi)
   const float h = 0.5f * r;
-  const float h2 = h * h;
-  float sp = fmaf(h2, 1.6059043836821613e-10f, -2.5052108385441720e-08f);
-  sp = fmaf(h2, sp, 2.7557319223985888e-06f);
-  sp = fmaf(h2, sp, -1.9841269841269841e-04f);
-  sp = fmaf(h2, sp, 8.3333333333333333e-03f);
-  sp = fmaf(h2, sp, -1.6666666666666667e-01f);
-  const float sh = fmaf(h * h2, sp, h);
-  float cp = fmaf(h2, -1.1470745597729725e-11f, 2.0876756987868099e-09f);
-  cp = fmaf(h2, cp, -2.7557319223985890e-07f);
-  cp = fmaf(h2, cp, 2.4801587301587302e-05f);
-  cp = fmaf(h2, cp, -1.3888888888888889e-03f);
-  cp = fmaf(h2, cp, 4.1666666666666667e-02f);
-  cp = fmaf(h2, cp, -0.5f);
-  const float ch = fmaf(h2, cp, 1.0f);
+  const float u = h * h;
+  float sp = fmaf(u, 2.6052247914144940e-06f, -1.9809075229821477e-04f);
+  sp = fmaf(u, sp, 8.3330510624972130e-03f);
+  sp = fmaf(u, sp, -1.6666657991867140e-01f);
+  sp = fmaf(u, sp, 9.9999999573276810e-01f);
+  const float sh = h * sp;
+  float cp = fmaf(u, -2.6077094002825570e-07f, 2.4761885527010584e-05f);
+  cp = fmaf(u, cp, -1.3888403492119570e-03f);
+  cp = fmaf(u, cp, 4.1666640726599230e-02f);
+  cp = fmaf(u, cp, -4.9999999549513570e-01f);
+  const float ch = fmaf(u, cp, 1.0f);
   s = 2.0f * sh * ch;
   vers = 2.0f * sh * sh;
 }

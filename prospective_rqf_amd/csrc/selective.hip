@@ -8,152 +8,210 @@
 // The coefficients never touch HBM: only z, the logits, the outputs and the
 // per-chunk entry states cross the kernel boundary.
 //
-// Work decomposition: one wavefront owns one (channel, batch) row and walks
-// it in tiles of 64*K consecutive steps.  Lane l holds steps [l*K, l*K+K) of
-// the tile, so every global access is a contiguous 64*K*elem-byte stretch
-// (float4 loads when T % 4 == 0).  A tile is scanned as
+// Tiles: a wavefront walks one (channel, batch) row in tiles of 64*K steps.
+// Lane l holds steps [l*K, l*K+K) of a tile, so each global access is one
+// contiguous stretch (float4 when T % 4 == 0).  A tile is scanned as
 //   1. per-lane serial composition of its K affine maps,
 //   2. DPP wave scan of the 64 lane maps (tile entry state folded into lane 0),
 //   3. per-lane serial replay from the lane's entry state,
-// and the tile's exit state is carried to the next tile in a register.
+// and the tile's exit state is carried to the next tile in a register.  Full
+// tiles run without per-step range masks; only the last (partial) tile has them.
 //
-// The backward walks the tiles in reverse: it replays the forward from the
-// stored entry state (for the ReLU mask and y[t-1]), runs the adjoint
+// Scheduling: rows are processed batch-major and blocks are dealt to the 8
+// XCDs in contiguous ranges, so all channels of a batch element run on one
+// XCD and share its L2 for the group-wise warp logits.
+//
+// Backward: the tiles are walked in reverse.  Each tile replays its forward
+// from the stored entry state (ReLU mask and y[t-1]), runs the adjoint
 //   d[t] = e[t] + conj(A[t+1]) d[t+1]
 // with the same three-step structure in suffix order, and forms every
-// gradient in registers (the reference's _backward, selective_scan_kernel.py:250-462).
+// gradient in registers (the reference's _backward,
+// selective_scan_kernel.py:250-462).  The warp-logit gradient is written per
+// channel and summed over each group's channels by a separate pass in a fixed
+// order; per-channel parameter gradients are per-row fp64 partial sums reduced
+// in a fixed order.  No floating-point atomics: results are deterministic.
 #include "rqf_device.h"
 #include "rqf_scan.h"
 
+#include <initializer_list>
+
 using namespace rqf;
+
+#ifndef RQF_SEL_FWD_K
+#define RQF_SEL_FWD_K 4
+#endif
+#ifndef RQF_SEL_BWD_K
+#define RQF_SEL_BWD_K 4
+#endif
+#ifndef RQF_BWD_WAVES_PER_EU
+#define RQF_BWD_WAVES_PER_EU 1
+#endif
+// Optional scheduling fence between the per-step bodies of the backward
+// (keeps the scheduler from interleaving steps, which bounds register pressure).
+#ifdef RQF_BWD_STEP_FENCE
+#define RQF_STEP_FENCE() __builtin_amdgcn_sched_barrier(0)
+#else
+#define RQF_STEP_FENCE() ((void)0)
+#endif
 
 namespace {
 
-constexpr int kSelK = 4;                     // steps per lane per tile
-constexpr int kSelTile = kWave * kSelK;      // steps per tile
-constexpr int kSelWaves = 4;                 // wavefronts per block
+constexpr int kFwdK = RQF_SEL_FWD_K;  // steps per lane per tile, forward
+constexpr int kBwdK = RQF_SEL_BWD_K;  // steps per lane per tile, backward
+constexpr int kRowsPerBlock = 4;      // wavefronts (rows) per block
+constexpr int kXcds = 8;              // MI355X: 8 XCDs, blocks dealt round-robin
 
-// Wave-uniform per-channel parameters.
+// Blocks are dispatched round-robin over the XCDs; remap so that XCD x runs a
+// contiguous range of logical blocks.
+__device__ __forceinline__ int64_t xcd_remap(int64_t P, int64_t n) {
+  const int64_t x = P % kXcds, j = P / kXcds, q = n / kXcds, r = n % kXcds;
+  return x * q + (x < r ? x : r) + j;
+}
+
+// Wave-uniform per-channel parameters and option reciprocals.
 struct Chan {
-  float bias, theta, lo, span, eta, horizon, thlo, thhi;
-  int64_t warp_base;  // element offset of this row's warp logits
+  float bias, theta, lo, span, inv_span, eta, horizon, thlo, thhi, inv_theta;
+  float inv_write_max, inv_gamma_scale;
 };
 
-__device__ __forceinline__ Chan load_chan(const rqf_selective_inputs& p, int64_t f, int64_t b) {
+__device__ __forceinline__ Chan load_chan(const rqf_selective_inputs& p, int64_t f) {
   Chan c;
   c.bias = p.bias[f];
   c.theta = p.theta[f];
   c.lo = p.minimum[f];
   c.span = p.span[f];
+  c.inv_span = 1.0f / c.span;
   c.eta = p.step[f];
   c.horizon = p.horizon[f];
   c.thlo = p.theta_minimum[f];
   c.thhi = p.theta_maximum[f];
-  c.warp_base = p.has_warp ? (p.groups[f] * p.B + b) * p.T : 0;
+  c.inv_theta = 1.0f / c.theta;
+  c.inv_write_max = 1.0f / p.write_max;
+  c.inv_gamma_scale = 1.0f / p.gamma_scale;
   return c;
 }
 
-// Controller + ZOH + prospective taps for one element
-// (rqf_models/ops/selective_scan_kernel.py:16-101).
-struct Coef {
-  c32 A, phi, bp, bn;  // bp, bn: taps before the write gate
-  float gamma, theta, gate, sig, warp, inv_den, ratio;
+// Controller links (rqf_models/ops/selective_scan_kernel.py:16-72).
+struct Ctl {
+  float gamma, theta_u, gate;  // theta_u: warped theta before the band clamp
+  float wt;                    // tanh(warp logit), 0 without a warp head
 };
 
-__device__ __forceinline__ void coef(const rqf_selective_inputs& p, const Chan& c, float gv,
-                                     float dv, float wv, Coef& e) {
-  float gamma = c.bias, sig = 0.0f;
+__device__ __forceinline__ Ctl controller(const rqf_selective_inputs& p, const Chan& c, float gv,
+                                          float dv, float wv) {
+  Ctl o;
+  o.gamma = c.bias;
   if (p.has_gamma) {
-    if (p.log_shift) {
-      sig = ftanh(gv);
-      gamma = fexp(fmaf(p.gamma_scale, sig, c.bias));
-    } else {
-      sig = fsigmoid(c.bias + gv);
-      gamma = fmaf(c.span, sig, c.lo);
-    }
+    if (p.log_shift)
+      o.gamma = fexp(fmaf(p.gamma_scale, ftanh(gv), c.bias));
+    else
+      o.gamma = fmaf(c.span, fsigmoid(c.bias + gv), c.lo);
   }
-  float theta = c.theta, warp = 0.0f;
-  if (p.has_warp) {
-    warp = ftanh(dv);
-    theta *= fexp(p.warp_scale * warp);
-    if (p.bound_warp) theta = fminf(fmaxf(theta, c.thlo), c.thhi);
-  }
-  float gate = 1.0f;
-  if (p.has_write) gate = p.write_sigmoid ? p.write_max * fsigmoid(wv + p.write_bias) : 1.0f + wv;
-  zoh(-gamma * c.eta, (1.0f - gamma) * theta * c.eta, e.A, e.phi, e.inv_den);
-  e.bp = cscale(gamma * c.eta, e.phi);
-  e.bn = mk(0.0f, 0.0f);
-  e.ratio = 0.0f;
-  if (p.prospective) {
-    e.ratio = p.gamma_horizon ? frcp(gamma) : c.horizon;
-    const c32 ex = cscale(e.ratio * gamma, e.A);
-    e.bp = cadd(e.bp, ex);
-    e.bn = mk(-ex.r, -ex.i);
-  }
-  e.gamma = gamma;
-  e.theta = theta;
-  e.gate = gate;
-  e.sig = sig;
-  e.warp = warp;
+  o.wt = p.has_warp ? ftanh(dv) : 0.0f;
+  o.theta_u = p.has_warp ? c.theta * fexp(p.warp_scale * o.wt) : c.theta;
+  o.gate = 1.0f;
+  if (p.has_write) o.gate = p.write_sigmoid ? p.write_max * fsigmoid(wv + p.write_bias) : 1.0f + wv;
+  return o;
 }
 
+__device__ __forceinline__ float clamp_theta(const rqf_selective_inputs& p, const Chan& c, float th) {
+  return p.bound_warp ? fminf(fmaxf(th, c.thlo), c.thhi) : th;
+}
+
+// ratio * gamma of the prospective tap: 1 in gamma-horizon mode (ratio = 1/gamma).
+__device__ __forceinline__ float ratio_gamma(const rqf_selective_inputs& p, const Chan& c,
+                                             float gamma) {
+  return p.gamma_horizon ? 1.0f : c.horizon * gamma;
+}
+
+// A and the gated drive u = gate*(bp z + bn zp) of one step, with
+// bp z + bn zp = gamma*eta*phi*z + ratio*gamma*A*(z - zp).
+__device__ __forceinline__ void step_coef(const rqf_selective_inputs& p, const Chan& c,
+                                          const Ctl& q, c32 zk, c32 zp, c32& A, c32& phi,
+                                          c32& u) {
+  float inv_den;
+  zoh(-q.gamma * c.eta, (1.0f - q.gamma) * clamp_theta(p, c, q.theta_u) * c.eta, A, phi,
+      inv_den);
+  c32 drive = cscale(q.gamma * c.eta, cmul(phi, zk));
+  if (p.prospective) drive = cmad(cscale(ratio_gamma(p, c, q.gamma), A), csub(zk, zp), drive);
+  u = cscale(q.gate, drive);
+}
+
+// Streamed tensors are read and written once: optionally mark the accesses
+// non-temporal so they do not displace the L2-resident warp logits.
+#ifdef RQF_NT_STREAM
+typedef float v4f __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld4(const float* p) {
+  const v4f v = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st4(float* p, float4 v) {
+  const v4f w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<v4f*>(p));
+}
+#else
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+#endif
+
 // ---------------------------------------------------------------------------
-// Tile loads / stores.  VEC: T % 4 == 0 and 16-byte aligned bases, so each
-// lane's K = 4 steps are either all inside [0, T) or all outside.
+// Tile loads / stores with 32-bit in-row offsets.  VEC: T % 4 == 0 and
+// 16-byte aligned rows; then a float4 group is entirely inside or outside
+// [0, T).  TAIL: the tile may extend past T (range checks on).
 // ---------------------------------------------------------------------------
-template <bool VEC>
-__device__ __forceinline__ void load_c4(const float* __restrict__ row, int64_t tb, int64_t T,
-                                        c32 (&v)[kSelK]) {
+template <int K, bool VEC, bool TAIL>
+__device__ __forceinline__ void load_c(const float* __restrict__ row, int tb, int T, c32 (&v)[K]) {
   if (VEC) {
-    if (tb < T) {
-      const float4 a = *reinterpret_cast<const float4*>(row + 2 * tb);
-      const float4 b = *reinterpret_cast<const float4*>(row + 2 * tb + 4);
-      v[0] = mk(a.x, a.y);
-      v[1] = mk(a.z, a.w);
-      v[2] = mk(b.x, b.y);
-      v[3] = mk(b.z, b.w);
-    } else {
 #pragma unroll
-      for (int k = 0; k < kSelK; ++k) v[k] = mk(0.0f, 0.0f);
+    for (int j = 0; j < K / 2; ++j) {
+      if (!TAIL || tb + 2 * j < T) {
+        const float4 a = ld4(row + 2 * tb + 4 * j);
+        v[2 * j] = mk(a.x, a.y);
+        v[2 * j + 1] = mk(a.z, a.w);
+      } else {
+        v[2 * j] = mk(0.0f, 0.0f);
+        v[2 * j + 1] = mk(0.0f, 0.0f);
+      }
     }
   } else {
 #pragma unroll
-    for (int k = 0; k < kSelK; ++k)
+    for (int k = 0; k < K; ++k)
       v[k] = (tb + k < T) ? mk(row[2 * (tb + k)], row[2 * (tb + k) + 1]) : mk(0.0f, 0.0f);
   }
 }
 
-template <bool VEC>
-__device__ __forceinline__ void load_f4(const float* __restrict__ row, int64_t tb, int64_t T,
-                                        float (&v)[kSelK]) {
+template <int K, bool VEC, bool TAIL>
+__device__ __forceinline__ void load_f(const float* __restrict__ row, int tb, int T, float (&v)[K]) {
   if (VEC) {
-    if (tb < T) {
-      const float4 a = *reinterpret_cast<const float4*>(row + tb);
-      v[0] = a.x;
-      v[1] = a.y;
-      v[2] = a.z;
-      v[3] = a.w;
-    } else {
 #pragma unroll
-      for (int k = 0; k < kSelK; ++k) v[k] = 0.0f;
+    for (int j = 0; j < K / 4; ++j) {
+      if (!TAIL || tb + 4 * j < T) {
+        const float4 a = ld4(row + tb + 4 * j);
+        v[4 * j] = a.x;
+        v[4 * j + 1] = a.y;
+        v[4 * j + 2] = a.z;
+        v[4 * j + 3] = a.w;
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[4 * j + q] = 0.0f;
+      }
     }
   } else {
 #pragma unroll
-    for (int k = 0; k < kSelK; ++k) v[k] = (tb + k < T) ? row[tb + k] : 0.0f;
+    for (int k = 0; k < K; ++k) v[k] = (tb + k < T) ? row[tb + k] : 0.0f;
   }
 }
 
-template <bool VEC>
-__device__ __forceinline__ void store_c4(float* __restrict__ row, int64_t tb, int64_t T,
-                                         const c32 (&v)[kSelK]) {
+template <int K, bool VEC, bool TAIL>
+__device__ __forceinline__ void store_c(float* __restrict__ row, int tb, int T, const c32 (&v)[K]) {
   if (VEC) {
-    if (tb < T) {
-      *reinterpret_cast<float4*>(row + 2 * tb) = make_float4(v[0].r, v[0].i, v[1].r, v[1].i);
-      *reinterpret_cast<float4*>(row + 2 * tb + 4) = make_float4(v[2].r, v[2].i, v[3].r, v[3].i);
-    }
+#pragma unroll
+    for (int j = 0; j < K / 2; ++j)
+      if (!TAIL || tb + 2 * j < T)
+        st4(row + 2 * tb + 4 * j, make_float4(v[2 * j].r, v[2 * j].i, v[2 * j + 1].r, v[2 * j + 1].i));
   } else {
 #pragma unroll
-    for (int k = 0; k < kSelK; ++k)
+    for (int k = 0; k < K; ++k)
       if (tb + k < T) {
         row[2 * (tb + k)] = v[k].r;
         row[2 * (tb + k) + 1] = v[k].i;
@@ -161,359 +219,510 @@ __device__ __forceinline__ void store_c4(float* __restrict__ row, int64_t tb, in
   }
 }
 
-template <bool VEC>
-__device__ __forceinline__ void store_f4(float* __restrict__ row, int64_t tb, int64_t T,
-                                         const float (&v)[kSelK]) {
+template <int K, bool VEC, bool TAIL>
+__device__ __forceinline__ void store_f(float* __restrict__ row, int tb, int T, const float (&v)[K]) {
   if (VEC) {
-    if (tb < T) *reinterpret_cast<float4*>(row + tb) = make_float4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+    for (int j = 0; j < K / 4; ++j)
+      if (!TAIL || tb + 4 * j < T)
+        st4(row + tb + 4 * j, make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]));
   } else {
 #pragma unroll
-    for (int k = 0; k < kSelK; ++k)
+    for (int k = 0; k < K; ++k)
       if (tb + k < T) row[tb + k] = v[k];
   }
 }
 
+
+template <int K>
+__device__ __forceinline__ void zero(float (&v)[K]) {
+#pragma unroll
+  for (int k = 0; k < K; ++k) v[k] = 0.0f;
+}
 __device__ __forceinline__ c32 relu2(c32 v) { return mk(fmaxf(v.r, 0.0f), fmaxf(v.i, 0.0f)); }
+
+// Row coordinates of logical row L (batch-major order).
+struct RowId {
+  int64_t f, b, row;
+};
+__device__ __forceinline__ RowId row_id(const rqf_selective_inputs& p, int64_t L) {
+  RowId r;
+  r.b = L / p.F;
+  r.f = L - r.b * p.F;
+  r.row = r.f * p.B + r.b;
+  return r;
+}
 
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
-template <bool VEC>
-__global__ __launch_bounds__(kSelWaves* kWave) void selective_fwd_kernel(
-    const rqf_selective_inputs p, const float* __restrict__ z, float* __restrict__ raw,
-    float* __restrict__ act, float* __restrict__ entries, int64_t chunk, int64_t nc) {
-  const int lane = lane_id();
-  const int64_t row = (int64_t)blockIdx.x * kSelWaves + (threadIdx.x >> 6);
-  const int64_t T = p.T;
-  if (row >= p.F * p.B) return;  // whole wavefronts exit together
-  const int64_t f = row / p.B, b = row - f * p.B;
-  const Chan c = load_chan(p, f, b);
-  const float* zr = z + 2 * row * T;
-  const float* gr = p.has_gamma ? p.gamma_logits + row * T : nullptr;
-  const float* wr = p.has_write ? p.write_logits + row * T : nullptr;
-  const float* dr = p.has_warp ? p.warp_logits + c.warp_base : nullptr;
-  float* rawr = raw ? raw + 2 * row * T : nullptr;
-  float* actr = act ? act + 2 * row * T : nullptr;
-  float* ent = entries + 2 * row * nc;
-  if (lane == 0) {
-    ent[0] = 0.0f;
-    ent[1] = 0.0f;
-  }
-  c32 y = mk(0.0f, 0.0f), zlast = mk(0.0f, 0.0f);
-  for (int64_t t0 = 0; t0 < T; t0 += kSelTile) {
-    const int64_t tb = t0 + lane * kSelK;
-    c32 zv[kSelK];
-    float gv[kSelK], wv[kSelK], dv[kSelK];
-    load_c4<VEC>(zr, tb, T, zv);
-    if (gr) load_f4<VEC>(gr, tb, T, gv);
-    else
-#pragma unroll
-      for (int k = 0; k < kSelK; ++k) gv[k] = 0.0f;
-    if (wr) load_f4<VEC>(wr, tb, T, wv);
-    else
-#pragma unroll
-      for (int k = 0; k < kSelK; ++k) wv[k] = 0.0f;
-    if (dr) load_f4<VEC>(dr, tb, T, dv);
-    else
-#pragma unroll
-      for (int k = 0; k < kSelK; ++k) dv[k] = 0.0f;
-    const c32 zp0 = shift_up(zv[kSelK - 1], zlast, lane);
+struct FwdRow {
+  const float* zr;
+  const float* gr;
+  const float* wr;
+  const float* dr;
+  float* rawr;
+  float* actr;
+  float* ent;
+  int T, chunk;
+  c32 y, zlast;
+};
 
-    c32 A[kSelK], u[kSelK];
+// Inputs of one forward tile (per lane).
+template <int K>
+struct FwdIn {
+  c32 zv[K];
+  float gv[K], wv[K], dv[K];
+};
+
+template <int K, bool VEC, bool TAIL>
+__device__ __forceinline__ void fwd_load(const FwdRow& r, int t0, int lane, FwdIn<K>& in) {
+  const int T = r.T;
+  const int tb = t0 + lane * K;
+  load_c<K, VEC, TAIL>(r.zr, tb, T, in.zv);
+  if (r.gr) load_f<K, VEC, TAIL>(r.gr, tb, T, in.gv); else zero(in.gv);
+  if (r.wr) load_f<K, VEC, TAIL>(r.wr, tb, T, in.wv); else zero(in.wv);
+  if (r.dr) load_f<K, VEC, TAIL>(r.dr, tb, T, in.dv); else zero(in.dv);
+}
+
+template <int K, bool VEC, bool TAIL>
+__device__ __forceinline__ void fwd_compute(const rqf_selective_inputs& p, const Chan& c, FwdRow& r,
+                                            int t0, int lane, const FwdIn<K>& in) {
+  const int T = r.T;
+  const int tb = t0 + lane * K;
+  const c32 (&zv)[K] = in.zv;
+  const float (&gv)[K] = in.gv;
+  const float (&wv)[K] = in.wv;
+  const float (&dv)[K] = in.dv;
+  const c32 zp0 = shift_up(zv[K - 1], r.zlast, lane);
+  c32 A[K], u[K];
 #pragma unroll
-    for (int k = 0; k < kSelK; ++k) {
-      Coef e;
-      coef(p, c, gv[k], dv[k], wv[k], e);
-      c32 drive = cmul(e.bp, zv[k]);
-      if (p.prospective) drive = cmad(e.bn, k ? zv[k - 1] : zp0, drive);
-      const bool in = tb + k < T;
-      A[k] = in ? e.A : mk(1.0f, 0.0f);
-      u[k] = in ? cscale(e.gate, drive) : mk(0.0f, 0.0f);
+  for (int k = 0; k < K; ++k) {
+    const Ctl q = controller(p, c, gv[k], dv[k], wv[k]);
+    c32 phi;
+    step_coef(p, c, q, zv[k], k ? zv[k - 1] : zp0, A[k], phi, u[k]);
+    if (TAIL && tb + k >= T) {
+      A[k] = mk(1.0f, 0.0f);
+      u[k] = mk(0.0f, 0.0f);
     }
-    // 1. lane-local composition
-    c32 P = A[0], s = u[0];
+  }
+  // 1. lane-local composition
+  c32 P = A[0], s = u[0];
 #pragma unroll
-    for (int k = 1; k < kSelK; ++k) {
-      s = cmad(A[k], s, u[k]);
-      P = cmul(A[k], P);
+  for (int k = 1; k < K; ++k) {
+    s = cmad(A[k], s, u[k]);
+    P = cmul(A[k], P);
+  }
+  if (lane == 0) s = cmad(P, r.y, s);
+  // 2. wave scan: s becomes the state after the lane's last step
+  wave_scan_fwd(P, s);
+  // 3. replay from the lane's entry state
+  c32 yk = shift_up(s, r.y, lane);
+  c32 out[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    yk = cmad(A[k], yk, u[k]);
+    out[k] = yk;
+  }
+  // Entry states: the state after step t with (t+1) % chunk == 0 enters chunk (t+1)/chunk.
+  if (r.chunk >= K) {
+    const int t1 = tb + K;
+    if (t1 < T && (t1 & (r.chunk - 1)) == 0) {
+      r.ent[2 * (t1 / r.chunk)] = out[K - 1].r;
+      r.ent[2 * (t1 / r.chunk) + 1] = out[K - 1].i;
     }
-    if (lane == 0) s = cmad(P, y, s);
-    // 2. wave scan: s becomes the state after the lane's last step
-    wave_scan_fwd(P, s);
-    // 3. replay from the lane's entry state
-    c32 yk = shift_up(s, y, lane);
-    c32 out[kSelK];
+  } else {
 #pragma unroll
-    for (int k = 0; k < kSelK; ++k) {
-      yk = cmad(A[k], yk, u[k]);
-      out[k] = yk;
-      const int64_t t = tb + k;
-      if (t + 1 < T && ((t + 1) & (chunk - 1)) == 0) {
-        const int64_t j = (t + 1) / chunk;
-        ent[2 * j] = yk.r;
-        ent[2 * j + 1] = yk.i;
+    for (int k = 0; k < K; ++k) {
+      const int t1 = tb + k + 1;
+      if (t1 < T && (t1 & (r.chunk - 1)) == 0) {
+        r.ent[2 * (t1 / r.chunk)] = out[k].r;
+        r.ent[2 * (t1 / r.chunk) + 1] = out[k].i;
       }
     }
-    if (rawr) store_c4<VEC>(rawr, tb, T, out);
-    if (actr) {
-#pragma unroll
-      for (int k = 0; k < kSelK; ++k) out[k] = relu2(out[k]);
-      store_c4<VEC>(actr, tb, T, out);
-    }
-    y = readlane(s, kWave - 1);
-    zlast = readlane(zv[kSelK - 1], kWave - 1);
   }
+  if (r.rawr) store_c<K, VEC, TAIL>(r.rawr, tb, T, out);
+  if (r.actr) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) out[k] = relu2(out[k]);
+    store_c<K, VEC, TAIL>(r.actr, tb, T, out);
+  }
+  r.y = readlane(s, kWave - 1);
+  r.zlast = readlane(zv[K - 1], kWave - 1);
+}
+
+template <int K, bool VEC, bool TAIL>
+__device__ __forceinline__ void fwd_tile(const rqf_selective_inputs& p, const Chan& c, FwdRow& r,
+                                         int t0, int lane) {
+  FwdIn<K> in;
+  fwd_load<K, VEC, TAIL>(r, t0, lane, in);
+  fwd_compute<K, VEC, TAIL>(p, c, r, t0, lane, in);
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kRowsPerBlock* kWave) void selective_fwd_kernel(
+    const rqf_selective_inputs p, const float* __restrict__ z, float* __restrict__ raw,
+    float* __restrict__ act, float* __restrict__ entries, int chunk, int nc) {
+  constexpr int K = kFwdK, TILE = kWave * K;
+  const int lane = lane_id();
+  const int64_t L = xcd_remap(blockIdx.x, gridDim.x) * kRowsPerBlock + (threadIdx.x >> 6);
+  if (L >= p.F * p.B) return;  // whole wavefronts exit together
+  const RowId id = row_id(p, L);
+  const Chan c = load_chan(p, id.f);
+  FwdRow r;
+  r.T = (int)p.T;
+  r.chunk = chunk;
+  const int64_t base = id.row * r.T;
+  r.zr = z + 2 * base;
+  r.gr = p.has_gamma ? p.gamma_logits + base : nullptr;
+  r.wr = p.has_write ? p.write_logits + base : nullptr;
+  r.dr = p.has_warp ? p.warp_logits + (p.groups[id.f] * p.B + id.b) * r.T : nullptr;
+  r.rawr = raw ? raw + 2 * base : nullptr;
+  r.actr = act ? act + 2 * base : nullptr;
+  r.ent = entries + 2 * id.row * nc;
+  if (lane == 0) {
+    r.ent[0] = 0.0f;
+    r.ent[1] = 0.0f;
+  }
+  r.y = mk(0.0f, 0.0f);
+  r.zlast = mk(0.0f, 0.0f);
+  const int full = VEC ? r.T / TILE : 0;
+  int t0 = 0;
+#ifdef RQF_FWD_PREFETCH
+  if (full > 0) {
+    // The next tile's loads are issued before the current tile's math.
+    FwdIn<K> cur;
+    fwd_load<K, VEC, false>(r, 0, lane, cur);
+    for (int i = 0; i < full; ++i, t0 += TILE) {
+      FwdIn<K> nxt;
+      if (i + 1 < full) fwd_load<K, VEC, false>(r, t0 + TILE, lane, nxt);
+      fwd_compute<K, VEC, false>(p, c, r, t0, lane, cur);
+      cur = nxt;
+    }
+  }
+#else
+  for (int i = 0; i < full; ++i, t0 += TILE) fwd_tile<K, VEC, false>(p, c, r, t0, lane);
+#endif
+  for (; t0 < r.T; t0 += TILE) fwd_tile<K, VEC, true>(p, c, r, t0, lane);
 }
 
 // ---------------------------------------------------------------------------
 // Backward
 // ---------------------------------------------------------------------------
 struct BwdOut {
-  float* dz;   // x-path drive gradient (only written when truncated)
-  float* dzw;  // W-path drive gradient (== dz when not truncated)
+  float* dz;        // x-path drive gradient (only written when truncated)
+  float* dzw;       // W-path drive gradient (== dz when not truncated)
   float* dg;
-  float* ddc;  // per-channel warp gradient (F,B,T) scratch
   float* dw;
-  double* partial;  // (2, F*B): sum over t of d/dbias and d/dtheta per row
+  float* ddc;       // (F, B, T) per-channel warp-logit gradient
+  double* partial;  // (2, F*B): per row sums of d/dbias and d/dtheta
 };
 
-template <bool VEC>
-__global__ __launch_bounds__(kSelWaves* kWave) void selective_bwd_kernel(
-    const rqf_selective_inputs p, const float* __restrict__ z,
-    const float* __restrict__ entries, int64_t chunk, int64_t nc,
-    const float* __restrict__ gy, const float* __restrict__ gx, int truncated, BwdOut o) {
-  const int lane = lane_id();
-  const int64_t row = (int64_t)blockIdx.x * kSelWaves + (threadIdx.x >> 6);
-  const int64_t T = p.T, R = p.F * p.B;
-  if (row >= R) return;
-  const int64_t f = row / p.B, b = row - f * p.B;
-  const Chan c = load_chan(p, f, b);
-  const float* zr = z + 2 * row * T;
-  const float* gr = p.has_gamma ? p.gamma_logits + row * T : nullptr;
-  const float* wr = p.has_write ? p.write_logits + row * T : nullptr;
-  const float* dr = p.has_warp ? p.warp_logits + c.warp_base : nullptr;
-  const float* gyr = gy ? gy + 2 * row * T : nullptr;
-  const float* gxr = gx ? gx + 2 * row * T : nullptr;
-  const float* ent = entries + 2 * row * nc;
-  float* dzr = o.dz + 2 * row * T;
-  float* dzwr = o.dzw + 2 * row * T;
-  float* dgr = o.dg ? o.dg + row * T : nullptr;
-  float* dwr = o.dw ? o.dw + row * T : nullptr;
-  float* ddr = o.ddc ? o.ddc + row * T : nullptr;
+struct BwdRow {
+  const float* zr;
+  const float* gr;
+  const float* wr;
+  const float* dr;
+  const float* gyr;
+  const float* gxr;
+  const float* ent;
+  float* dzr;
+  float* dzwr;
+  float* dgr;
+  float* dwr;
+  float* ddr;
+  int T, chunk, truncated;
+  c32 dcarry;  // adjoint (truncated: cotangent) at the next tile's first step
+  c32 Afirst;  // A at the next tile's first step (0 past the end)
+  float cfirst;  // gate*ratio*gamma at the next tile's first step
+  double sum_bias, sum_theta;
+};
 
-  c32 dcarry = mk(0.0f, 0.0f);   // adjoint (or, truncated, cotangent) at the next tile's first step
-  c32 Afirst = mk(0.0f, 0.0f);   // A at the next tile's first step (0 past the end)
-  c32 nfirst = mk(0.0f, 0.0f);   // gated lag tap at the next tile's first step
-  double sum_bias = 0.0, sum_theta = 0.0;
-  const int64_t ntiles = (T + kSelTile - 1) / kSelTile;
+template <int K, bool VEC, bool TAIL>
+__device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Chan& c, BwdRow& r,
+                                         int t0, int lane) {
+  const int T = r.T;
+  const int tb = t0 + lane * K;
+  c32 zv[K];
+  float gv[K], wv[K], dv[K];
+  load_c<K, VEC, TAIL>(r.zr, tb, T, zv);
+  if (r.gr) load_f<K, VEC, TAIL>(r.gr, tb, T, gv); else zero(gv);
+  if (r.wr) load_f<K, VEC, TAIL>(r.wr, tb, T, wv); else zero(wv);
+  if (r.dr) load_f<K, VEC, TAIL>(r.dr, tb, T, dv); else zero(dv);
+  const c32 zprev_tile = t0 > 0 ? mk(r.zr[2 * (t0 - 1)], r.zr[2 * (t0 - 1) + 1]) : mk(0.0f, 0.0f);
+  const c32 zp0 = shift_up(zv[K - 1], zprev_tile, lane);
 
-  for (int64_t tile = ntiles - 1; tile >= 0; --tile) {
-    const int64_t t0 = tile * kSelTile;
-    const int64_t tb = t0 + lane * kSelK;
-    c32 zv[kSelK], ey[kSelK], ex[kSelK];
-    float gv[kSelK], wv[kSelK], dv[kSelK];
-    load_c4<VEC>(zr, tb, T, zv);
-    if (gr) load_f4<VEC>(gr, tb, T, gv);
-    else
+  // Coefficients; kept per step: A, phi, gamma, theta_u, gate, tanh(warp logit).
+  c32 A[K], phi[K], u[K];
+  float gam[K], thu[K], gate[K], wtk[K];
 #pragma unroll
-      for (int k = 0; k < kSelK; ++k) gv[k] = 0.0f;
-    if (wr) load_f4<VEC>(wr, tb, T, wv);
-    else
+  for (int k = 0; k < K; ++k) {
+    const Ctl q = controller(p, c, gv[k], dv[k], wv[k]);
+    step_coef(p, c, q, zv[k], k ? zv[k - 1] : zp0, A[k], phi[k], u[k]);
+    gam[k] = q.gamma;
+    thu[k] = q.theta_u;
+    gate[k] = q.gate;
+    wtk[k] = q.wt;
+    if (TAIL && tb + k >= T) u[k] = mk(0.0f, 0.0f);
+    RQF_STEP_FENCE();
+  }
+  // Forward replay from the tile's entry state.
+  const c32 y0 = mk(r.ent[2 * (t0 / r.chunk)], r.ent[2 * (t0 / r.chunk) + 1]);
+  c32 yprev[K], ecot[K];
+  {
+    c32 Am[K];
 #pragma unroll
-      for (int k = 0; k < kSelK; ++k) wv[k] = 0.0f;
-    if (dr) load_f4<VEC>(dr, tb, T, dv);
-    else
+    for (int k = 0; k < K; ++k) Am[k] = (TAIL && tb + k >= T) ? mk(1.0f, 0.0f) : A[k];
+    c32 P = Am[0], s = u[0];
 #pragma unroll
-      for (int k = 0; k < kSelK; ++k) dv[k] = 0.0f;
-    if (gyr) load_c4<VEC>(gyr, tb, T, ey);
-    else
-#pragma unroll
-      for (int k = 0; k < kSelK; ++k) ey[k] = mk(0.0f, 0.0f);
-    if (gxr) load_c4<VEC>(gxr, tb, T, ex);
-    else
-#pragma unroll
-      for (int k = 0; k < kSelK; ++k) ex[k] = mk(0.0f, 0.0f);
-    // z[t0-1] (uniform address) feeds lane 0's lag tap.
-    const c32 zprev_tile = t0 > 0 ? mk(zr[2 * (t0 - 1)], zr[2 * (t0 - 1) + 1]) : mk(0.0f, 0.0f);
-    const c32 zp0 = shift_up(zv[kSelK - 1], zprev_tile, lane);
-
-    Coef e[kSelK];
-    c32 A[kSelK], u[kSelK];
-#pragma unroll
-    for (int k = 0; k < kSelK; ++k) {
-      coef(p, c, gv[k], dv[k], wv[k], e[k]);
-      c32 drive = cmul(e[k].bp, zv[k]);
-      if (p.prospective) drive = cmad(e[k].bn, k ? zv[k - 1] : zp0, drive);
-      const bool in = tb + k < T;
-      A[k] = in ? e[k].A : mk(1.0f, 0.0f);
-      u[k] = in ? cscale(e[k].gate, drive) : mk(0.0f, 0.0f);
-    }
-    // Forward replay from the tile's entry state.
-    const c32 y0 = mk(ent[2 * (t0 / chunk)], ent[2 * (t0 / chunk) + 1]);
-    c32 P = A[0], s = u[0];
-#pragma unroll
-    for (int k = 1; k < kSelK; ++k) {
-      s = cmad(A[k], s, u[k]);
-      P = cmul(A[k], P);
+    for (int k = 1; k < K; ++k) {
+      s = cmad(Am[k], s, u[k]);
+      P = cmul(Am[k], P);
     }
     if (lane == 0) s = cmad(P, y0, s);
     wave_scan_fwd(P, s);
     c32 yk = shift_up(s, y0, lane);
-    c32 yprev[kSelK], ecot[kSelK];
+    c32 ey[K], ex[K];
+    if (r.gyr) {
+      load_c<K, VEC, TAIL>(r.gyr, tb, T, ey);
+    } else {
 #pragma unroll
-    for (int k = 0; k < kSelK; ++k) {
+      for (int k = 0; k < K; ++k) ey[k] = mk(0.0f, 0.0f);
+    }
+    if (r.gxr) {
+      load_c<K, VEC, TAIL>(r.gxr, tb, T, ex);
+    } else {
+#pragma unroll
+      for (int k = 0; k < K; ++k) ex[k] = mk(0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
       yprev[k] = yk;
-      yk = cmad(A[k], yk, u[k]);
-      // raw-output cotangent, plus the split-ReLU cotangent where raw > 0
+      yk = cmad(Am[k], yk, u[k]);
+      // raw-output cotangent plus the split-ReLU cotangent where raw > 0
       ecot[k] = mk(ey[k].r + (yk.r > 0.0f ? ex[k].r : 0.0f), ey[k].i + (yk.i > 0.0f ? ex[k].i : 0.0f));
     }
-    // Neighbour coefficients A[t+1], gated n[t+1] (0 past the end).
-    c32 An[kSelK], nn[kSelK];
-#pragma unroll
-    for (int k = 0; k < kSelK; ++k) {
-      const bool in = tb + k < T;
-      A[k] = in ? A[k] : mk(0.0f, 0.0f);
-      u[k] = in ? cscale(e[k].gate, e[k].bn) : mk(0.0f, 0.0f);  // reuse: gated lag tap
-    }
-#pragma unroll
-    for (int k = 0; k < kSelK - 1; ++k) {
-      An[k] = A[k + 1];
-      nn[k] = u[k + 1];
-    }
-    An[kSelK - 1] = shift_down(A[0], Afirst, lane);
-    nn[kSelK - 1] = shift_down(u[0], nfirst, lane);
-    Afirst = readlane(A[0], 0);
-    nfirst = readlane(u[0], 0);
-
-    // Adjoint d[t] = e[t] + conj(A[t+1]) d[t+1]  (truncated: d = e).
-    c32 dnext;
-    if (truncated) {
-      dnext = shift_down(ecot[0], dcarry, lane);
-      dcarry = readlane(ecot[0], 0);
-    } else {
-      c32 Q = mk(1.0f, 0.0f), r = mk(0.0f, 0.0f);
-#pragma unroll
-      for (int k = kSelK - 1; k >= 0; --k) {
-        r = cjmad(An[k], r, ecot[k]);
-        Q = cjmul(An[k], Q);
-      }
-      if (lane == kWave - 1) r = cmad(Q, dcarry, r);
-      wave_scan_rev(Q, r, lane);
-      dnext = shift_down(r, dcarry, lane);
-      dcarry = readlane(r, 0);
-    }
-
-    c32 gz[kSelK], gzw[kSelK];
-    float gg[kSelK], gw[kSelK], gd[kSelK];
-    float tile_bias = 0.0f, tile_theta = 0.0f;
-#pragma unroll
-    for (int k = kSelK - 1; k >= 0; --k) {
-      const Coef& q = e[k];
-      const c32 d = truncated ? ecot[k] : cjmad(An[k], dnext, ecot[k]);
-      const c32 cur = cjmul(cscale(q.gate, q.bp), d);
-      gz[k] = cur;
-      gzw[k] = cjmad(nn[k], dnext, cur);
-      dnext = d;
-      // Gradients of the gated taps and of A.
-      const c32 zp = k ? zv[k - 1] : zp0;
-      const c32 dp = cjmul(zv[k], d);
-      const c32 dn = cjmul(zp, d);
-      c32 dA = cjmul(yprev[k], d);
-      const float dgate = q.bp.r * dp.r + q.bp.i * dp.i + q.bn.r * dn.r + q.bn.i * dn.i;
-      const c32 dbp = cscale(q.gate, dp), dbn = cscale(q.gate, dn);
-      float dgamma = 0.0f;
-      if (p.prospective) {
-        const c32 qd = csub(dbp, dbn);
-        if (!p.gamma_horizon) dgamma = q.ratio * (qd.r * q.A.r + qd.i * q.A.i);
-        dA = cadd(dA, cscale(q.ratio * q.gamma, qd));
-      }
-      // phi'(a) = (A - phi)/a, or its series for |a|^2 < 1/64 (cubic below 1e-8);
-      // selective_scan_kernel.py:119-148.
-      const float ar = -q.gamma * c.eta, ai = (1.0f - q.gamma) * q.theta * c.eta;
-      const float den = fmaf(ar, ar, ai * ai);
-      c32 fp;
-      const c32 a = mk(ar, ai);
-      if (den < 0.015625f) {
-        if (den < 1.0e-8f) {
-          fp = cmad(a, cmad(a, mk(1.0f / 8.0f, 0.0f), mk(1.0f / 3.0f, 0.0f)), mk(0.5f, 0.0f));
-        } else {
-          c32 sr = mk(1.0f / 45360.0f, 0.0f);
-          sr = cmad(a, sr, mk(1.0f / 5760.0f, 0.0f));
-          sr = cmad(a, sr, mk(1.0f / 840.0f, 0.0f));
-          sr = cmad(a, sr, mk(1.0f / 144.0f, 0.0f));
-          sr = cmad(a, sr, mk(1.0f / 30.0f, 0.0f));
-          sr = cmad(a, sr, mk(1.0f / 8.0f, 0.0f));
-          sr = cmad(a, sr, mk(1.0f / 3.0f, 0.0f));
-          fp = cmad(a, sr, mk(0.5f, 0.0f));
-        }
-      } else {
-        const c32 x = csub(q.A, q.phi);
-        fp = cscale(q.inv_den, cmul(x, conjg(a)));
-      }
-      const float gh = q.gamma * c.eta;
-      // da = conj(A) dA + gamma*eta*conj(phi') dbp
-      const c32 da = cadd(cjmul(q.A, dA), cscale(gh, cjmul(fp, dbp)));
-      dgamma += c.eta * (q.phi.r * dbp.r + q.phi.i * dbp.i - da.r - q.theta * da.i);
-      float dth = c.eta * (1.0f - q.gamma) * da.i;
-      const bool in = tb + k < T;
-      // controller chain rules (selective_scan_kernel.py:441-460)
-      float dbias;
-      if (p.has_gamma) {
-        if (p.log_shift) {
-          dbias = dgamma * q.gamma;
-          gg[k] = dbias * p.gamma_scale * (1.0f - q.sig * q.sig);
-        } else {
-          dbias = dgamma * c.span * q.sig * (1.0f - q.sig);
-          gg[k] = dbias;
-        }
-      } else {
-        dbias = dgamma;
-        gg[k] = 0.0f;
-      }
-      if (p.has_warp) {
-        const float scale = fexp(p.warp_scale * q.warp);
-        if (p.bound_warp) {
-          const float unclamped = c.theta * scale;
-          // torch.clamp passes the gradient at both exact edges
-          if (!(unclamped >= c.thlo && unclamped <= c.thhi)) dth = 0.0f;
-        }
-        gd[k] = dth * q.theta * p.warp_scale * (1.0f - q.warp * q.warp);
-        dth *= scale;
-      } else {
-        gd[k] = 0.0f;
-      }
-      gw[k] = p.write_sigmoid ? dgate * q.gate * (1.0f - q.gate / p.write_max) : dgate;
-      tile_bias += in ? dbias : 0.0f;
-      tile_theta += in ? dth : 0.0f;
-    }
-    sum_bias += (double)tile_bias;
-    sum_theta += (double)tile_theta;
-    store_c4<VEC>(dzwr, tb, T, gzw);
-    if (truncated) store_c4<VEC>(dzr, tb, T, gz);
-    if (dgr) store_f4<VEC>(dgr, tb, T, gg);
-    if (dwr) store_f4<VEC>(dwr, tb, T, gw);
-    if (ddr) store_f4<VEC>(ddr, tb, T, gd);
   }
-  sum_bias = wave_sum(sum_bias);
-  sum_theta = wave_sum(sum_theta);
+  if (TAIL) {
+    // Past-the-end steps have A = 0 and no lag tap for the adjoint.
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (tb + k >= T) {
+        A[k] = mk(0.0f, 0.0f);
+        gate[k] = 0.0f;
+      }
+  }
+  // Lag-tap weight cn = gate*ratio*gamma (gated n = -cn*A) of the lane's first step.
+  const float c0 = p.prospective ? gate[0] * ratio_gamma(p, c, gam[0]) : 0.0f;
+  const c32 A_lane_next = shift_down(A[0], r.Afirst, lane);
+  const c32 cn_lane_next = shift_down(mk(c0, 0.0f), mk(r.cfirst, 0.0f), lane);
+  r.Afirst = readlane(A[0], 0);
+  r.cfirst = readlane(c0, 0);
+
+  // Adjoint d[t] = e[t] + conj(A[t+1]) d[t+1]  (truncated: d = e).
+  c32 dnext;
+  if (r.truncated) {
+    dnext = shift_down(ecot[0], r.dcarry, lane);
+    r.dcarry = readlane(ecot[0], 0);
+  } else {
+    c32 Q = mk(1.0f, 0.0f), rr = mk(0.0f, 0.0f);
+#pragma unroll
+    for (int k = K - 1; k >= 0; --k) {
+      const c32 An = k + 1 < K ? A[k + 1] : A_lane_next;
+      rr = cjmad(An, rr, ecot[k]);
+      Q = cjmul(An, Q);
+    }
+    if (lane == kWave - 1) rr = cmad(Q, r.dcarry, rr);
+    wave_scan_rev(Q, rr, lane);
+    dnext = shift_down(rr, r.dcarry, lane);
+    r.dcarry = readlane(rr, 0);
+  }
+
+  c32 gz[K], gzw[K];
+  float gg[K], gw[K], gd[K];
+  float tile_bias = 0.0f, tile_theta = 0.0f;
+#pragma unroll
+  for (int k = K - 1; k >= 0; --k) {
+    const c32 An = k + 1 < K ? A[k + 1] : A_lane_next;
+    float cn;
+    if (k + 1 < K)
+      cn = p.prospective ? gate[k + 1] * ratio_gamma(p, c, gam[k + 1]) : 0.0f;
+    else
+      cn = cn_lane_next.r;
+    const c32 d = r.truncated ? ecot[k] : cjmad(An, dnext, ecot[k]);
+    const float gamma = gam[k], gt = gate[k];
+    const float rg = p.prospective ? ratio_gamma(p, c, gamma) : 0.0f;
+    const float gh = gamma * c.eta;
+    // un-gated taps: bp = gamma*eta*phi + rg*A, bn = -rg*A
+    const c32 bp = cmad(mk(rg, 0.0f), A[k], cscale(gh, phi[k]));
+    const c32 bn = cscale(-rg, A[k]);
+    const c32 cur = cscale(gt, cjmul(bp, d));
+    gz[k] = cur;
+    // lag tap of step t+1: conj(n[t+1]) d[t+1] with n[t+1] = -cn*A[t+1]
+    gzw[k] = cjmad(cscale(-cn, An), dnext, cur);
+    dnext = d;
+    const c32 zp = k ? zv[k - 1] : zp0;
+    const c32 dp = cjmul(zv[k], d);
+    const c32 dn = cjmul(zp, d);
+    c32 dA = cjmul(yprev[k], d);
+    const float dgate = bp.r * dp.r + bp.i * dp.i + bn.r * dn.r + bn.i * dn.i;
+    const c32 dbp = cscale(gt, dp);
+    float dgamma = 0.0f;
+    if (p.prospective) {
+      const c32 qd = csub(dbp, cscale(gt, dn));
+      if (!p.gamma_horizon) dgamma = c.horizon * (qd.r * A[k].r + qd.i * A[k].i);
+      dA = cmad(mk(rg, 0.0f), qd, dA);
+    }
+    // phi'(a) = (A - phi)/a, or its series for |a|^2 < 1/64 (cubic below 1e-8);
+    // selective_scan_kernel.py:119-148.
+    const float theta = clamp_theta(p, c, thu[k]);
+    const float ar = -gh, ai = (1.0f - gamma) * theta * c.eta;
+    const float den = fmaf(ar, ar, ai * ai);
+    const c32 a = mk(ar, ai);
+    c32 fp;
+    if (den < 0.015625f) {
+      if (den < 1.0e-8f) {
+        fp = cmad(a, cmad(a, mk(1.0f / 8.0f, 0.0f), mk(1.0f / 3.0f, 0.0f)), mk(0.5f, 0.0f));
+      } else {
+        c32 sr = mk(1.0f / 45360.0f, 0.0f);
+        sr = cmad(a, sr, mk(1.0f / 5760.0f, 0.0f));
+        sr = cmad(a, sr, mk(1.0f / 840.0f, 0.0f));
+        sr = cmad(a, sr, mk(1.0f / 144.0f, 0.0f));
+        sr = cmad(a, sr, mk(1.0f / 30.0f, 0.0f));
+        sr = cmad(a, sr, mk(1.0f / 8.0f, 0.0f));
+        sr = cmad(a, sr, mk(1.0f / 3.0f, 0.0f));
+        fp = cmad(a, sr, mk(0.5f, 0.0f));
+      }
+    } else {
+      fp = cscale(frcp(den), cmul(csub(A[k], phi[k]), conjg(a)));
+    }
+    // da = conj(A) dA + gamma*eta*conj(phi') dbp
+    const c32 da = cmad(mk(gh, 0.0f), cjmul(fp, dbp), cjmul(A[k], dA));
+    dgamma += c.eta * (phi[k].r * dbp.r + phi[k].i * dbp.i - da.r - theta * da.i);
+    float dth = c.eta * (1.0f - gamma) * da.i;
+    // controller chain rules (selective_scan_kernel.py:441-460)
+    float dbias;
+    if (p.has_gamma) {
+      if (p.log_shift) {
+        dbias = dgamma * gamma;
+        // tanh of the gamma logit, from gamma = exp(bias + scale*tanh)
+        const float sg =
+            (__builtin_amdgcn_logf(gamma) * 0.6931471805599453f - c.bias) * c.inv_gamma_scale;
+        gg[k] = dbias * p.gamma_scale * (1.0f - sg * sg);
+      } else {
+        const float sg = (gamma - c.lo) * c.inv_span;
+        dbias = dgamma * c.span * sg * (1.0f - sg);
+        gg[k] = dbias;
+      }
+    } else {
+      dbias = dgamma;
+      gg[k] = 0.0f;
+    }
+    if (p.has_warp) {
+      const float ws = thu[k] * c.inv_theta;  // exp(scale*w) = d theta_u / d theta
+      const float wt = wtk[k];
+      // torch.clamp passes the gradient at both exact edges
+      if (p.bound_warp && !(thu[k] >= c.thlo && thu[k] <= c.thhi)) dth = 0.0f;
+      gd[k] = dth * theta * p.warp_scale * (1.0f - wt * wt);
+      dth *= ws;
+    } else {
+      gd[k] = 0.0f;
+    }
+    gw[k] = p.write_sigmoid ? dgate * gt * (1.0f - gt * c.inv_write_max) : dgate;
+    if (TAIL && tb + k >= T) {
+      dbias = 0.0f;
+      dth = 0.0f;
+    }
+    tile_bias += dbias;
+    tile_theta += dth;
+  }
+  r.sum_bias += (double)tile_bias;
+  r.sum_theta += (double)tile_theta;
+  store_c<K, VEC, TAIL>(r.dzwr, tb, T, gzw);
+  if (r.truncated) store_c<K, VEC, TAIL>(r.dzr, tb, T, gz);
+  if (r.dgr) store_f<K, VEC, TAIL>(r.dgr, tb, T, gg);
+  if (r.dwr) store_f<K, VEC, TAIL>(r.dwr, tb, T, gw);
+  if (r.ddr) store_f<K, VEC, TAIL>(r.ddr, tb, T, gd);
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kRowsPerBlock* kWave)
+    __attribute__((amdgpu_waves_per_eu(RQF_BWD_WAVES_PER_EU))) void selective_bwd_kernel(
+        const rqf_selective_inputs p, const float* __restrict__ z,
+        const float* __restrict__ entries, int chunk, int nc, const float* __restrict__ gy,
+        const float* __restrict__ gx, int truncated, BwdOut o) {
+  constexpr int K = kBwdK, TILE = kWave * K;
+  const int lane = lane_id();
+  const int64_t L = xcd_remap(blockIdx.x, gridDim.x) * kRowsPerBlock + (threadIdx.x >> 6);
+  if (L >= p.F * p.B) return;
+  const RowId id = row_id(p, L);
+  const Chan c = load_chan(p, id.f);
+  BwdRow r;
+  r.T = (int)p.T;
+  r.chunk = chunk;
+  r.truncated = truncated;
+  const int64_t base = id.row * r.T;
+  r.zr = z + 2 * base;
+  r.gr = p.has_gamma ? p.gamma_logits + base : nullptr;
+  r.wr = p.has_write ? p.write_logits + base : nullptr;
+  r.dr = p.has_warp ? p.warp_logits + (p.groups[id.f] * p.B + id.b) * r.T : nullptr;
+  r.gyr = gy ? gy + 2 * base : nullptr;
+  r.gxr = gx ? gx + 2 * base : nullptr;
+  r.ent = entries + 2 * id.row * nc;
+  r.dzr = o.dz + 2 * base;
+  r.dzwr = o.dzw + 2 * base;
+  r.dgr = o.dg ? o.dg + base : nullptr;
+  r.dwr = o.dw ? o.dw + base : nullptr;
+  r.ddr = o.ddc ? o.ddc + base : nullptr;
+  r.dcarry = mk(0.0f, 0.0f);
+  r.Afirst = mk(0.0f, 0.0f);
+  r.cfirst = 0.0f;
+  r.sum_bias = 0.0;
+  r.sum_theta = 0.0;
+  const int ntiles = (r.T + TILE - 1) / TILE;
+  const int full = VEC ? r.T / TILE : 0;
+  int tile = ntiles - 1;
+  for (; tile >= full; --tile) bwd_tile<K, VEC, true>(p, c, r, tile * TILE, lane);
+  for (; tile >= 0; --tile) bwd_tile<K, VEC, false>(p, c, r, tile * TILE, lane);
+  const double sb = wave_sum(r.sum_bias);
+  const double st = wave_sum(r.sum_theta);
   if (lane == 0) {
-    o.partial[row] = sum_bias;
-    o.partial[R + row] = sum_theta;
+    o.partial[id.row] = sb;
+    o.partial[p.F * p.B + id.row] = st;
   }
 }
 
-// dd[g, i] = sum over channels f of group g (ascending f) of ddc[f, i], i over B*T.
+// dd[g, i] = sum over the channels f of group g (ascending f) of ddc[f, i];
+// i runs over B*T.  Each thread keeps its G accumulators in LDS.
+constexpr int kReduceGroupsLds = 32;
 __global__ __launch_bounds__(256) void group_reduce_kernel(const float* __restrict__ ddc,
                                                            const int64_t* __restrict__ groups,
-                                                           float* __restrict__ dd, int64_t F,
-                                                           int64_t G, int64_t N) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= N) return;
-  for (int64_t g = 0; g < G; ++g) {
-    float acc = 0.0f;
-    for (int64_t f = 0; f < F; ++f)
-      if (groups[f] == g) acc += ddc[f * N + i];
-    dd[g * N + i] = acc;
+                                                           float* __restrict__ dd, int F, int G,
+                                                           int64_t N) {
+  __shared__ float acc[kReduceGroupsLds][256];
+  const int tid = threadIdx.x;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + tid;
+  const bool in = i < N;
+  if (G <= kReduceGroupsLds) {
+    for (int g = 0; g < G; ++g) acc[g][tid] = 0.0f;
+    int f = 0;
+    for (; f + 4 <= F; f += 4) {
+      float v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = in ? ddc[(int64_t)(f + q) * N + i] : 0.0f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[groups[f + q]][tid] += v[q];
+    }
+    for (; f < F; ++f) acc[groups[f]][tid] += in ? ddc[(int64_t)f * N + i] : 0.0f;
+    if (in)
+      for (int g = 0; g < G; ++g) dd[(int64_t)g * N + i] = acc[g][tid];
+  } else if (in) {
+    for (int g = 0; g < G; ++g) {
+      float s = 0.0f;
+      for (int f = 0; f < F; ++f)
+        if (groups[f] == g) s += ddc[(int64_t)f * N + i];
+      dd[(int64_t)g * N + i] = s;
+    }
   }
 }
 
@@ -565,6 +774,8 @@ inline bool aligned16(const void* ptr) { return ptr == nullptr || ((uintptr_t)pt
 inline bool aligned8(const void* ptr) { return ptr == nullptr || ((uintptr_t)ptr & 7) == 0; }
 inline size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
 inline bool pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+// Chunk as a kernel int: anything >= 2^30 behaves like 2^30 since T < 2^30.
+inline int chunk_int(int64_t chunk) { return (int)(chunk > (1 << 30) ? (1 << 30) : chunk); }
 
 int launch_status() {
   const hipError_t err = hipGetLastError();
@@ -573,6 +784,7 @@ int launch_status() {
 
 int check_inputs(const rqf_selective_inputs* in) {
   if (!in || in->F < 0 || in->B < 0 || in->T < 0) return RQF_ERR_ARG;
+  if (in->T >= ((int64_t)1 << 30)) return RQF_ERR_ARG;  // in-row offsets are 32-bit
   if (!in->bias || !in->theta || !in->minimum || !in->span || !in->step || !in->horizon ||
       !in->theta_minimum || !in->theta_maximum)
     return RQF_ERR_ARG;
@@ -591,6 +803,23 @@ bool vec_ok(const rqf_selective_inputs* in, std::initializer_list<const void*> p
   return true;
 }
 
+dim3 row_grid(const rqf_selective_inputs* in) {
+  return dim3((unsigned)((in->F * in->B + kRowsPerBlock - 1) / kRowsPerBlock));
+}
+
+void launch_fwd(const rqf_selective_inputs* in, const float* z, float* raw, float* act,
+                float* entries, int chunk, int nc, bool vec, hipStream_t s) {
+  const dim3 grid = row_grid(in), block(kRowsPerBlock * kWave);
+  if (vec)
+    hipLaunchKernelGGL(selective_fwd_kernel<true>, grid, block, 0, s, *in, z, raw, act, entries,
+                       chunk, nc);
+  else
+    hipLaunchKernelGGL(selective_fwd_kernel<false>, grid, block, 0, s, *in, z, raw, act, entries,
+                       chunk, nc);
+}
+
+constexpr int kBwdTile = kWave * kBwdK;
+
 }  // namespace
 
 extern "C" int rqf_selective_fwd(const rqf_selective_inputs* in, const float* z, int64_t chunk,
@@ -602,15 +831,9 @@ extern "C" int rqf_selective_fwd(const rqf_selective_inputs* in, const float* z,
   if (st) return st;
   if (!z || !entries || (!raw && !act)) return RQF_ERR_ARG;
   if (!aligned8(z) || !aligned8(raw) || !aligned8(act) || !aligned8(entries)) return RQF_ERR_ALIGN;
-  const int64_t nc = (in->T + chunk - 1) / chunk;
-  const dim3 grid((unsigned)((R + kSelWaves - 1) / kSelWaves)), block(kSelWaves * kWave);
-  hipStream_t s = (hipStream_t)stream;
-  if (vec_ok(in, {z, raw, act}))
-    hipLaunchKernelGGL(selective_fwd_kernel<true>, grid, block, 0, s, *in, z, raw, act, entries,
-                       chunk, nc);
-  else
-    hipLaunchKernelGGL(selective_fwd_kernel<false>, grid, block, 0, s, *in, z, raw, act, entries,
-                       chunk, nc);
+  const int nc = (int)((in->T + chunk - 1) / chunk);
+  launch_fwd(in, z, raw, act, entries, chunk_int(chunk), nc, vec_ok(in, {z, raw, act}),
+             (hipStream_t)stream);
   return launch_status();
 }
 
@@ -624,7 +847,8 @@ SelWs sel_ws_layout(const rqf_selective_inputs* in, int64_t chunk) {
   w.partial = 0;
   size_t off = round256(sizeof(double) * 2 * (size_t)R);
   w.tile_entries = off;
-  if (chunk > kSelTile) off += round256(sizeof(float) * 2 * (size_t)R * ((in->T + kSelTile - 1) / kSelTile + 1));
+  if (chunk > kBwdTile)
+    off += round256(sizeof(float) * 2 * (size_t)R * ((in->T + kBwdTile - 1) / kBwdTile + 1));
   w.ddc = off;
   if (in->has_warp) off += round256(sizeof(float) * (size_t)R * (size_t)in->T);
   w.total = off;
@@ -633,7 +857,7 @@ SelWs sel_ws_layout(const rqf_selective_inputs* in, int64_t chunk) {
 }  // namespace
 
 extern "C" size_t rqf_selective_bwd_workspace(const rqf_selective_inputs* in, int64_t chunk) {
-  if (!in) return 0;
+  if (!in || in->F < 0 || in->B < 0 || in->T < 0) return 0;
   return sel_ws_layout(in, chunk).total;
 }
 
@@ -663,22 +887,16 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
   hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)workspace;
   double* partial = (double*)(ws + w.partial);
-  if (R > 0 && T > 0) {
-    const dim3 grid((unsigned)((R + kSelWaves - 1) / kSelWaves)), block(kSelWaves * kWave);
-    const float* ent = entries;
-    int64_t ent_chunk = chunk, nc = (T + chunk - 1) / chunk;
+  if (nonempty) {
     const bool vec = vec_ok(in, {z, gy, gx, dz, dzw, dg, dw});
-    if (chunk > kSelTile) {
-      // Entry states every tile: replay the forward once with chunk = tile.
+    const float* ent = entries;
+    int ent_chunk = chunk_int(chunk), nc = (int)((T + chunk - 1) / chunk);
+    if (chunk > kBwdTile) {
+      // Entry states at every backward tile: replay the forward once.
       float* te = (float*)(ws + w.tile_entries);
-      ent_chunk = kSelTile;
-      nc = (T + kSelTile - 1) / kSelTile;
-      if (vec)
-        hipLaunchKernelGGL(selective_fwd_kernel<true>, grid, block, 0, s, *in, z, nullptr,
-                           nullptr, te, ent_chunk, nc);
-      else
-        hipLaunchKernelGGL(selective_fwd_kernel<false>, grid, block, 0, s, *in, z, nullptr,
-                           nullptr, te, ent_chunk, nc);
+      ent_chunk = kBwdTile;
+      nc = (int)((T + kBwdTile - 1) / kBwdTile);
+      launch_fwd(in, z, nullptr, nullptr, te, ent_chunk, nc, vec, s);
       ent = te;
     }
     BwdOut o;
@@ -688,16 +906,17 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
     o.dw = in->has_write ? dw : nullptr;
     o.ddc = in->has_warp ? (float*)(ws + w.ddc) : nullptr;
     o.partial = partial;
+    const dim3 grid = row_grid(in), block(kRowsPerBlock * kWave);
     if (vec)
-      hipLaunchKernelGGL(selective_bwd_kernel<true>, grid, block, 0, s, *in, z, ent, ent_chunk,
-                         nc, gy, gx, (int)truncated, o);
+      hipLaunchKernelGGL(selective_bwd_kernel<true>, grid, block, 0, s, *in, z, ent, ent_chunk, nc,
+                         gy, gx, (int)truncated, o);
     else
       hipLaunchKernelGGL(selective_bwd_kernel<false>, grid, block, 0, s, *in, z, ent, ent_chunk,
                          nc, gy, gx, (int)truncated, o);
     if (in->has_warp) {
       const int64_t N = in->B * T;
       hipLaunchKernelGGL(group_reduce_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, s,
-                         o.ddc, in->groups, dd, in->F, in->G, N);
+                         o.ddc, in->groups, dd, (int)in->F, (int)in->G, N);
     }
   } else {
     zero_words(partial, 4 * R, s);

@@ -39,6 +39,8 @@ def _args():
     ap.add_argument("--no-cpu-baseline", dest="cpu", action="store_false")
     ap.add_argument("--cpu-steps", type=int, default=0,
                     help="time steps of the CPU baseline sample (0: auto, ~10-30 s)")
+    ap.add_argument("--batch", type=int, default=0,
+                    help="override the config's batch size (experiments only)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 plain 1 GiB device copies (scale for FETCH/WRITE_SIZE)")
     return ap.parse_args()
@@ -178,6 +180,9 @@ def main():
         seq_duration, samp, tau = 4096.0, 1.0, 5.0
     else:
         raise SystemExit("configs 2 and 5 are measured by bench_fbt (not yet wired)")
+    if args.batch:
+        B = args.batch
+        workload += f" [batch overridden to {B}]"
     chunk = 256
     inputs, z, gy, gx = selective_workload(F, B, T, G, dev, log_scale=log_scale,
                                            seq_duration=seq_duration, samp=samp, tau=tau)

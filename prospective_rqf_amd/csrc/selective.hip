@@ -17,9 +17,10 @@
 // and the tile's exit state is carried to the next tile in a register.  Full
 // tiles run without per-step range masks; only the last (partial) tile has them.
 //
-// Scheduling: rows are processed batch-major and blocks are dealt to the 8
-// XCDs in contiguous ranges, so all channels of a batch element run on one
-// XCD and share its L2 for the group-wise warp logits.
+// Scheduling: each XCD takes one contiguous chunk of the batch (blocks are
+// dealt to the 8 XCDs in contiguous ranges) and walks it channel-major, so all
+// channels of a batch element run on one XCD and share its L2 for the
+// group-wise warp logits, while concurrently streamed rows stay adjacent.
 //
 // Backward: the tiles are walked in reverse.  Each tile replays its forward
 // from the stored entry state (ReLU mask and y[t-1]), runs the adjoint
@@ -45,6 +46,14 @@ using namespace rqf;
 #endif
 #ifndef RQF_BWD_WAVES_PER_EU
 #define RQF_BWD_WAVES_PER_EU 1
+#endif
+#ifndef RQF_FWD_WAVES_PER_EU
+#define RQF_FWD_WAVES_PER_EU 1
+#endif
+// Backward form: 1 = teams of channels reduce the warp gradient in LDS;
+// 0 = one wavefront per row, per-channel warp gradient + group pass.
+#ifndef RQF_BWD_TEAMS
+#define RQF_BWD_TEAMS 1
 #endif
 // Optional scheduling fence between the per-step bodies of the backward
 // (keeps the scheduler from interleaving steps, which bounds register pressure).
@@ -242,13 +251,26 @@ __device__ __forceinline__ void zero(float (&v)[K]) {
 __device__ __forceinline__ c32 relu2(c32 v) { return mk(fmaxf(v.r, 0.0f), fmaxf(v.i, 0.0f)); }
 
 // Row coordinates of logical row L (batch-major order).
+// Logical row order: the batch is cut into kXcds chunks of bc = ceil(B/8)
+// elements, chunk c = XCD c's share (with the XCD-contiguous block remap).
+// Inside a chunk rows go channel-major, batch-minor: the bc rows of one
+// channel are adjacent in memory, so the rows a chunk streams concurrently
+// cover few address ranges, and all channels of a batch element stay on one
+// XCD (its L2 keeps the chunk's warp logits).  Logical rows past B are idle.
 struct RowId {
   int64_t f, b, row;
+  bool valid;
 };
+__device__ __forceinline__ int64_t batch_chunk(const rqf_selective_inputs& p) {
+  return (p.B + kXcds - 1) / kXcds;
+}
 __device__ __forceinline__ RowId row_id(const rqf_selective_inputs& p, int64_t L) {
   RowId r;
-  r.b = L / p.F;
-  r.f = L - r.b * p.F;
+  const int64_t bc = batch_chunk(p), per = p.F * bc;
+  const int64_t c = L / per, rem = L - c * per;
+  r.f = rem / bc;
+  r.b = c * bc + (rem - r.f * bc);
+  r.valid = c < kXcds && r.b < p.B;
   r.row = r.f * p.B + r.b;
   return r;
 }
@@ -360,14 +382,15 @@ __device__ __forceinline__ void fwd_tile(const rqf_selective_inputs& p, const Ch
 }
 
 template <bool VEC>
-__global__ __launch_bounds__(kRowsPerBlock* kWave) void selective_fwd_kernel(
+__global__ __launch_bounds__(kRowsPerBlock* kWave)
+    __attribute__((amdgpu_waves_per_eu(RQF_FWD_WAVES_PER_EU))) void selective_fwd_kernel(
     const rqf_selective_inputs p, const float* __restrict__ z, float* __restrict__ raw,
     float* __restrict__ act, float* __restrict__ entries, int chunk, int nc) {
   constexpr int K = kFwdK, TILE = kWave * K;
   const int lane = lane_id();
   const int64_t L = xcd_remap(blockIdx.x, gridDim.x) * kRowsPerBlock + (threadIdx.x >> 6);
-  if (L >= p.F * p.B) return;  // whole wavefronts exit together
   const RowId id = row_id(p, L);
+  if (!id.valid) return;  // whole wavefronts exit together
   const Chan c = load_chan(p, id.f);
   FwdRow r;
   r.T = (int)p.T;
@@ -414,7 +437,8 @@ struct BwdOut {
   float* dzw;       // W-path drive gradient (== dz when not truncated)
   float* dg;
   float* dw;
-  float* ddc;       // (F, B, T) per-channel warp-logit gradient
+  float* ddc;       // (F, B, T) per-channel warp-logit gradient (per-row kernel)
+  float* dd_part;   // (S, B, T) warp-logit gradient summed over each team (team kernel)
   double* partial;  // (2, F*B): per row sums of d/dbias and d/dtheta
 };
 
@@ -430,7 +454,8 @@ struct BwdRow {
   float* dzwr;
   float* dgr;
   float* dwr;
-  float* ddr;
+  float* ddr;     // per-channel warp-logit gradient (global), or
+  float4* sdd;    // this wavefront's slot of the team's LDS warp-gradient tile
   int T, chunk, truncated;
   c32 dcarry;  // adjoint (truncated: cotangent) at the next tile's first step
   c32 Afirst;  // A at the next tile's first step (0 past the end)
@@ -643,6 +668,10 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
   if (r.dgr) store_f<K, VEC, TAIL>(r.dgr, tb, T, gg);
   if (r.dwr) store_f<K, VEC, TAIL>(r.dwr, tb, T, gw);
   if (r.ddr) store_f<K, VEC, TAIL>(r.ddr, tb, T, gd);
+  if (r.sdd) {
+    static_assert(K == 4, "one float4 of warp gradient per lane");
+    r.sdd[lane] = make_float4(gd[0], gd[1], gd[2], gd[3]);
+  }
 }
 
 template <bool VEC>
@@ -654,8 +683,8 @@ __global__ __launch_bounds__(kRowsPerBlock* kWave)
   constexpr int K = kBwdK, TILE = kWave * K;
   const int lane = lane_id();
   const int64_t L = xcd_remap(blockIdx.x, gridDim.x) * kRowsPerBlock + (threadIdx.x >> 6);
-  if (L >= p.F * p.B) return;
   const RowId id = row_id(p, L);
+  if (!id.valid) return;
   const Chan c = load_chan(p, id.f);
   BwdRow r;
   r.T = (int)p.T;
@@ -674,6 +703,7 @@ __global__ __launch_bounds__(kRowsPerBlock* kWave)
   r.dgr = o.dg ? o.dg + base : nullptr;
   r.dwr = o.dw ? o.dw + base : nullptr;
   r.ddr = o.ddc ? o.ddc + base : nullptr;
+  r.sdd = nullptr;
   r.dcarry = mk(0.0f, 0.0f);
   r.Afirst = mk(0.0f, 0.0f);
   r.cfirst = 0.0f;
@@ -690,6 +720,160 @@ __global__ __launch_bounds__(kRowsPerBlock* kWave)
     o.partial[id.row] = sb;
     o.partial[p.F * p.B + id.row] = st;
   }
+}
+
+// ---------------------------------------------------------------------------
+// Backward, team form: a block is a team of up to kTeam wavefronts, one
+// channel each, all of one warp group and one batch element.  Per tile the
+// team sums its warp-logit gradient in LDS (fixed order over channels, one
+// barrier per tile with double-buffered LDS), so only one partial per team
+// reaches HBM; a small pass then sums the teams of each group in order.
+// ---------------------------------------------------------------------------
+constexpr int kTeam = kRowsPerBlock;
+
+// Team table built on the device (no host round trip).  Channels are ordered
+// by (warp group, channel index); a team is up to kTeam consecutive channels
+// of one group.  Without a warp head all channels form one group.
+struct Teams {
+  const int* order;   // (F,) channels sorted by group
+  const int* first;   // (S,) index into order of the team's first channel
+  const int* count;   // (S,) channels in the team
+  const int* group;   // (S,) warp group of the team
+  const int* nteams;  // (1,) number of teams in use
+  int slots;          // S: upper bound on the number of teams
+};
+
+__global__ __launch_bounds__(256) void team_build_kernel(const int64_t* __restrict__ groups,
+                                                         int F, int G, int* order, int* first,
+                                                         int* count, int* group, int* gteam,
+                                                         int* nteams, int* gcount, int* moff) {
+  const int tid = threadIdx.x;
+  for (int g = tid; g < G; g += blockDim.x) {
+    int n = 0;
+    for (int f = 0; f < F; ++f) n += groups ? (groups[f] == g) : 1;
+    gcount[g] = n;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int off = 0, toff = 0;
+    for (int g = 0; g < G; ++g) {
+      moff[g] = off;
+      gteam[g] = toff;
+      off += gcount[g];
+      toff += (gcount[g] + kTeam - 1) / kTeam;
+    }
+    gteam[G] = toff;
+    *nteams = toff;
+  }
+  __syncthreads();
+  for (int f = tid; f < F; f += blockDim.x) {
+    const int g = groups ? (int)groups[f] : 0;
+    int rank = 0;
+    for (int q = 0; q < f; ++q) rank += groups ? (groups[q] == g) : 1;
+    order[moff[g] + rank] = f;
+  }
+  for (int g = tid; g < G; g += blockDim.x) {
+    const int n = gcount[g], nt = (n + kTeam - 1) / kTeam;
+    for (int t = 0; t < nt; ++t) {
+      const int id = gteam[g] + t;
+      first[id] = moff[g] + t * kTeam;
+      count[id] = min(kTeam, n - t * kTeam);
+      group[id] = g;
+    }
+  }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kTeam* kWave)
+    __attribute__((amdgpu_waves_per_eu(RQF_BWD_WAVES_PER_EU))) void selective_bwd_team_kernel(
+        const rqf_selective_inputs p, const float* __restrict__ z,
+        const float* __restrict__ entries, int chunk, int nc, const float* __restrict__ gy,
+        const float* __restrict__ gx, int truncated, Teams tm, BwdOut o) {
+  constexpr int K = kBwdK, TILE = kWave * K;
+  static_assert(TILE == kTeam * kWave, "team reduction: one tile element per thread");
+  __shared__ float4 s_dd[2][kTeam][kWave];
+  const int lane = lane_id();
+  const int w = threadIdx.x >> 6;
+  // Logical block -> (batch chunk, team slot, batch element), XCD-contiguous chunks.
+  const int64_t bc = batch_chunk(p);
+  const int64_t L = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t per = (int64_t)tm.slots * bc;
+  const int64_t ci = L / per, rem = L - ci * per;
+  const int slot = (int)(rem / bc);
+  const int64_t b = ci * bc + (rem - (int64_t)slot * bc);
+  if (ci >= kXcds || b >= p.B || slot >= *tm.nteams) return;  // block-uniform
+  const int members = tm.count[slot];
+  const bool active = w < members;
+  const int64_t f = tm.order[tm.first[slot] + (active ? w : 0)];
+  const int64_t row = f * p.B + b;
+  const Chan c = load_chan(p, f);
+  BwdRow r;
+  r.T = (int)p.T;
+  r.chunk = chunk;
+  r.truncated = truncated;
+  const int64_t base = row * r.T;
+  r.zr = z + 2 * base;
+  r.gr = p.has_gamma ? p.gamma_logits + base : nullptr;
+  r.wr = p.has_write ? p.write_logits + base : nullptr;
+  r.dr = p.has_warp ? p.warp_logits + ((int64_t)tm.group[slot] * p.B + b) * r.T : nullptr;
+  r.gyr = gy ? gy + 2 * base : nullptr;
+  r.gxr = gx ? gx + 2 * base : nullptr;
+  r.ent = entries + 2 * row * nc;
+  r.dzr = o.dz + 2 * base;
+  r.dzwr = o.dzw + 2 * base;
+  r.dgr = o.dg ? o.dg + base : nullptr;
+  r.dwr = o.dw ? o.dw + base : nullptr;
+  r.ddr = nullptr;
+  r.sdd = nullptr;
+  r.dcarry = mk(0.0f, 0.0f);
+  r.Afirst = mk(0.0f, 0.0f);
+  r.cfirst = 0.0f;
+  r.sum_bias = 0.0;
+  r.sum_theta = 0.0;
+  float* ddp = p.has_warp ? o.dd_part + ((int64_t)slot * p.B + b) * r.T : nullptr;
+  const int ntiles = (r.T + TILE - 1) / TILE;
+  const int full = VEC ? r.T / TILE : 0;
+  int parity = 0;
+  for (int tile = ntiles - 1; tile >= 0; --tile) {
+    const int t0 = tile * TILE;
+    if (ddp) r.sdd = &s_dd[parity][w][0];
+    if (active) {
+      if (tile >= full)
+        bwd_tile<K, VEC, true>(p, c, r, t0, lane);
+      else
+        bwd_tile<K, VEC, false>(p, c, r, t0, lane);
+    }
+    if (ddp) {
+      __syncthreads();
+      const float* sd = reinterpret_cast<const float*>(&s_dd[parity][0][0]);
+      float acc = 0.0f;
+      for (int m = 0; m < members; ++m) acc += sd[m * TILE + threadIdx.x];
+      const int t = t0 + threadIdx.x;
+      if (t < r.T) ddp[t] = acc;
+      parity ^= 1;
+    }
+  }
+  if (active) {
+    const double sb = wave_sum(r.sum_bias);
+    const double st = wave_sum(r.sum_theta);
+    if (lane == 0) {
+      o.partial[row] = sb;
+      o.partial[p.F * p.B + row] = st;
+    }
+  }
+}
+
+// dd[g, b, t] = sum over the teams of group g (fixed order) of dd_part[team, b, t].
+__global__ __launch_bounds__(256) void team_reduce_kernel(const float* __restrict__ dd_part,
+                                                          const int* __restrict__ gteam,
+                                                          float* __restrict__ dd, int64_t G,
+                                                          int64_t N) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= G * N) return;
+  const int64_t g = i / N, n = i - g * N;
+  float acc = 0.0f;
+  for (int s = gteam[g]; s < gteam[g + 1]; ++s) acc += dd_part[(int64_t)s * N + n];
+  dd[i] = acc;
 }
 
 // dd[g, i] = sum over the channels f of group g (ascending f) of ddc[f, i];
@@ -804,7 +988,8 @@ bool vec_ok(const rqf_selective_inputs* in, std::initializer_list<const void*> p
 }
 
 dim3 row_grid(const rqf_selective_inputs* in) {
-  return dim3((unsigned)((in->F * in->B + kRowsPerBlock - 1) / kRowsPerBlock));
+  const int64_t rows = kXcds * in->F * ((in->B + kXcds - 1) / kXcds);  // logical rows
+  return dim3((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
 }
 
 void launch_fwd(const rqf_selective_inputs* in, const float* z, float* raw, float* act,
@@ -839,18 +1024,27 @@ extern "C" int rqf_selective_fwd(const rqf_selective_inputs* in, const float* z,
 
 namespace {
 struct SelWs {
-  size_t partial, tile_entries, ddc, total;
+  size_t partial, tile_entries, teams, dd, total;
+  int slots, G;
 };
 SelWs sel_ws_layout(const rqf_selective_inputs* in, int64_t chunk) {
   SelWs w;
   const int64_t R = in->F * in->B;
+  w.G = in->has_warp ? (int)in->G : 1;
+  w.slots = (int)(w.G + (in->F + kTeam - 1) / kTeam);
   w.partial = 0;
   size_t off = round256(sizeof(double) * 2 * (size_t)R);
   w.tile_entries = off;
   if (chunk > kBwdTile)
     off += round256(sizeof(float) * 2 * (size_t)R * ((in->T + kBwdTile - 1) / kBwdTile + 1));
-  w.ddc = off;
+  w.teams = off;
+  off += round256(sizeof(int) * (size_t)(in->F + 3 * w.slots + 3 * w.G + 2));
+  w.dd = off;
+#if RQF_BWD_TEAMS
+  if (in->has_warp) off += round256(sizeof(float) * (size_t)w.slots * in->B * in->T);
+#else
   if (in->has_warp) off += round256(sizeof(float) * (size_t)R * (size_t)in->T);
+#endif
   w.total = off;
   return w;
 }
@@ -904,8 +1098,44 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
     o.dzw = dzw;
     o.dg = in->has_gamma ? dg : nullptr;
     o.dw = in->has_write ? dw : nullptr;
-    o.ddc = in->has_warp ? (float*)(ws + w.ddc) : nullptr;
+    o.ddc = nullptr;
+    o.dd_part = nullptr;
     o.partial = partial;
+#if RQF_BWD_TEAMS
+    int* order = (int*)(ws + w.teams);
+    int* first = order + in->F;
+    int* count = first + w.slots;
+    int* group = count + w.slots;
+    int* gteam = group + w.slots;
+    int* nteams = gteam + (w.G + 1);
+    int* gcount = nteams + 1;
+    int* moff = gcount + w.G;
+    hipLaunchKernelGGL(team_build_kernel, dim3(1), dim3(256), 0, s,
+                       in->has_warp ? in->groups : (const int64_t*)nullptr, (int)in->F, w.G,
+                       order, first, count, group, gteam, nteams, gcount, moff);
+    Teams tm;
+    tm.order = order;
+    tm.first = first;
+    tm.count = count;
+    tm.group = group;
+    tm.nteams = nteams;
+    tm.slots = w.slots;
+    o.dd_part = in->has_warp ? (float*)(ws + w.dd) : nullptr;
+    const int64_t bc = (in->B + kXcds - 1) / kXcds;
+    const dim3 grid((unsigned)(kXcds * w.slots * bc)), block(kTeam * kWave);
+    if (vec)
+      hipLaunchKernelGGL(selective_bwd_team_kernel<true>, grid, block, 0, s, *in, z, ent,
+                         ent_chunk, nc, gy, gx, (int)truncated, tm, o);
+    else
+      hipLaunchKernelGGL(selective_bwd_team_kernel<false>, grid, block, 0, s, *in, z, ent,
+                         ent_chunk, nc, gy, gx, (int)truncated, tm, o);
+    if (in->has_warp) {
+      const int64_t N = in->B * T;
+      hipLaunchKernelGGL(team_reduce_kernel, dim3((unsigned)((in->G * N + 255) / 256)), dim3(256),
+                         0, s, o.dd_part, gteam, dd, in->G, N);
+    }
+#else
+    o.ddc = in->has_warp ? (float*)(ws + w.dd) : nullptr;
     const dim3 grid = row_grid(in), block(kRowsPerBlock * kWave);
     if (vec)
       hipLaunchKernelGGL(selective_bwd_kernel<true>, grid, block, 0, s, *in, z, ent, ent_chunk, nc,
@@ -918,6 +1148,7 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
       hipLaunchKernelGGL(group_reduce_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, s,
                          o.ddc, in->groups, dd, (int)in->F, (int)in->G, N);
     }
+#endif
   } else {
     zero_words(partial, 4 * R, s);
     if (in->has_warp && dd) zero_words(dd, in->G * in->B * T, s);

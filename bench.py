@@ -6,10 +6,22 @@ and write heads, prospective tau-mode input, intermediate-layer contract
 (raw + split-ReLU outputs, cotangents on both, full BPTT).  One step = one
 forward + one backward of the scan kernels over the whole batch; inputs are
 resident in HBM before timing starts.  The drive and logit GEMMs are outside
-the metric (BASELINE.md section 2).
+the metric.
 
-Prints ONE JSON line (rank 0).  ``--config`` 2/4/5 select the other configs
-for manual runs.
+``--config`` selects the other BASELINE.json configs (1-based) for manual runs:
+  1  Pure RQF depth 2, (B,T,F) chunked scan, B=4 T=161 F=64 (latency-bound)
+  2  non-selective two-tap FBT recompute scan, B=32 T=16000 F=128
+  3  selective fused scan, B=64 T=16000 F=256 G=8 (default)
+  4  selective token-copy shape, two layers, B=64 T=4096 F=256 G=4
+  5  long-sequence Pure RQF, 4 FBT recompute layers, B=16 T=16384 F=256
+
+Every entry point is bracketed by HIP events on the stream the kernels run on
+(torch's current stream, which the C ABI receives).  ``roofline`` describes
+the entry point with the largest share of the step; ``traffic`` is read from
+the committed rocprofv3 FETCH_SIZE/WRITE_SIZE table (profiles/traffic.md)
+when it has a row for the workload, else null.
+
+Prints ONE JSON line.
 """
 
 from __future__ import annotations
@@ -27,6 +39,8 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+METRIC = "scan Gelem/s (B·T·H complex) fwd+bwd at T=16000; % of HBM roofline"
+TRAFFIC_TABLE = os.path.join(ROOT, "profiles", "traffic.md")
 
 
 def _args():
@@ -34,13 +48,15 @@ def _args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=3, choices=[2, 3, 4, 5])
+    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--cpu-baseline", dest="cpu", action="store_true", default=True)
     ap.add_argument("--no-cpu-baseline", dest="cpu", action="store_false")
     ap.add_argument("--cpu-steps", type=int, default=0,
-                    help="time steps of the CPU baseline sample (0: auto, ~10-30 s)")
+                    help="time steps of the CPU baseline sample (0: the config's default)")
     ap.add_argument("--batch", type=int, default=0,
                     help="override the config's batch size (experiments only)")
+    ap.add_argument("--act-only", action="store_true",
+                    help="config 3 with the act-only contract (no raw output, no gy)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 plain 1 GiB device copies (scale for FETCH/WRITE_SIZE)")
     return ap.parse_args()
@@ -59,91 +75,416 @@ def copy_calibration():
 
 
 # ---------------------------------------------------------------------------
-# Workloads
+# Plans: a step is a list of named entry-point calls
 # ---------------------------------------------------------------------------
 
 
-def selective_workload(F, B, T, G, device, *, log_scale, seq_duration=1.0, samp=16000.0,
-                       tau=5.0 / 16000.0, write_raw=True, activate=True, seed=0):
+class Plan:
+    """One benchmark step as a sequence of named entry-point calls.
+
+    ``ops`` is a list of ``(name, fn)``; each fn takes the step's state dict.
+    ``bytes`` maps an op name to its algorithmic HBM bytes per call."""
+
+    def __init__(self, workload, config, elems, ops, nbytes, kernels, cpu=None, contract=""):
+        self.workload = workload
+        self.config = config
+        self.elems = elems
+        self.ops = ops
+        self.bytes = nbytes
+        self.kernels = kernels
+        self.cpu = cpu
+        self.contract = contract
+
+
+def _cn(g, device, *shape):
     import torch
 
-    from prospective_rqf_amd import workloads
-
-    inputs = workloads.selective_inputs(
-        F, B, T, G=G, gamma=True, write=True, warp="grouped", write_sigmoid=True, write_max=2.0,
-        gamma_scale=math.log(1.25), warp_scale=log_scale, prospective=True, samp=samp, tau=tau,
-        seq_duration=seq_duration, device=device, seed=seed)
-    g = torch.Generator(device=device).manual_seed(seed + 1)
-
-    def cn(*shape):
-        return torch.complex(torch.randn(*shape, generator=g, device=device),
-                             torch.randn(*shape, generator=g, device=device))
-
-    z = cn(F, B, T)
-    gy = cn(F, B, T) if write_raw else None
-    gx = cn(F, B, T) if activate else None
-    return inputs, z, gy, gx
+    return torch.complex(torch.randn(*shape, generator=g, device=device),
+                         torch.randn(*shape, generator=g, device=device))
 
 
-def selective_bytes(F, B, T, G, chunk, *, write_raw=True, activate=True):
-    """Algorithmic HBM bytes (each boundary tensor once) for fwd and bwd."""
+def selective_bytes(F, B, T, G, chunk, *, write_raw=True, activate=True, truncated=False):
+    """Algorithmic HBM bytes (each boundary tensor once) of one selective fwd and bwd call.
+
+    fwd: z, gamma/write logits, warp logits, raw and/or act, entries.
+    bwd: z, logits, entries, gy/gx, dz (+dzw when truncated), logit gradients."""
     N = F * B * T
     nc = -(-T // chunk)
     ent = 8 * F * B * nc
     warp = 4 * G * B * T
     fwd = N * (8 + 4 + 4 + 8 * write_raw + 8 * activate) + warp + ent
-    bwd = N * (8 + 4 + 4 + 8 * write_raw + 8 * activate + 8 + 4 + 4) + 2 * warp + ent
+    bwd = (N * (8 + 4 + 4 + 8 * write_raw + 8 * activate + 8 + 8 * truncated + 4 + 4)
+           + 2 * warp + ent)
     return fwd, bwd
 
 
+def fbt_recompute_bytes(F, B, T):
+    """Algorithmic bytes of one FBT recompute fwd and bwd call (x, act, carries; x, gy, gx)."""
+    from prospective_rqf_amd import _lib
+
+    N = F * B * T
+    carry = 8 * F * B * max(_lib.load().rqf_fbt_carry_chunks(T), 1)
+    return N * 16 + carry, N * 24 + carry
+
+
+def plan_selective(cfg, args, dev):
+    import torch
+
+    from prospective_rqf_amd import workloads
+    from prospective_rqf_amd.selective_scan_kernel import selective_backward, selective_forward
+
+    if cfg == 3:
+        F, B, T, G, log_scale = 256, 64, 16000, 8, math.log(1.25)
+        samp, tau, seq = 16000.0, 5.0 / 16000.0, 1.0
+        layers = [(not args.act_only, True)]
+        name = "selective fused scan B=64 T=16000 H=256 G=8 (config 3)"
+        contract = ("act only, gx cotangent, full BPTT" if args.act_only
+                    else "raw+act outputs, gy+gx cotangents, full BPTT")
+    else:
+        F, B, T, G, log_scale = 256, 64, 4096, 4, math.log(4.0)
+        samp, tau, seq = 1.0, 5.0, 4096.0
+        layers = [(True, True), (True, False)]
+        name = "selective token-copy shape B=64 T=4096 H=256 G=4, depth 2 (config 4)"
+        contract = "layer 0: raw+act, gy+gx; layer 1: raw only, gy; full BPTT"
+    if args.batch:
+        B = args.batch
+        name += f" [batch overridden to {B}]"
+    chunk = 256
+    g = torch.Generator(device=dev).manual_seed(1)
+    state = {}
+    layer_inputs = []
+    for li, (write_raw, activate) in enumerate(layers):
+        inputs = workloads.selective_inputs(
+            F, B, T, G=G, gamma=True, write=True, warp="grouped", write_sigmoid=True,
+            write_max=2.0, gamma_scale=math.log(1.25), warp_scale=log_scale, prospective=True,
+            samp=samp, tau=tau, seq_duration=seq, device=dev, seed=li)
+        layer_inputs.append((inputs, write_raw, activate))
+    if cfg == 3:
+        state["z0"] = _cn(g, dev, F, B, T)
+    else:
+        # Token-copy drive: one-hot tokens (16 markers in the first T-16 steps,
+        # noise tokens elsewhere), a fixed random 16->64 embedding and a complex
+        # 64->H input map.  Layer 1's drive maps [Re; Im] of layer 0's act.
+        gc = torch.Generator().manual_seed(2)
+        tok = torch.randint(1, 15, (B, T), generator=gc)
+        for b in range(B):
+            pos = torch.randperm(T - 16, generator=gc)[:16]
+            tok[b, pos] = 15
+        emb = torch.randn(16, 64, generator=gc)
+        x = emb[tok].to(dev)  # (B, T, 64)
+        w0 = _cn(g, dev, F, 64) / 8.0
+        xt = x.reshape(B * T, 64).t().contiguous().to(w0.dtype)
+        state["z0"] = (w0 @ xt).reshape(F, B, T).contiguous()
+        raw0, act0, _ = selective_forward(state["z0"], layer_inputs[0][0], True, True, chunk)
+        feat = torch.cat([act0.real, act0.imag], dim=0).reshape(2 * F, B * T)
+        w1 = _cn(g, dev, F, 2 * F) / math.sqrt(2 * F)
+        state["z1"] = (w1 @ feat.to(w1.dtype)).reshape(F, B, T).contiguous()
+        del raw0, act0, feat
+    for li, (_, write_raw, activate) in enumerate(layer_inputs):
+        state[f"gy{li}"] = _cn(g, dev, F, B, T) if write_raw else None
+        state[f"gx{li}"] = _cn(g, dev, F, B, T) if activate else None
+
+    ops, nbytes = [], {}
+    for li, (inputs, write_raw, activate) in enumerate(layer_inputs):
+        def fwd(st, li=li, inputs=inputs, write_raw=write_raw, activate=activate):
+            st[f"out{li}"] = selective_forward(st[f"z{li}"], inputs, activate, write_raw, chunk)
+
+        ops.append((f"rqf_selective_fwd[L{li}]", fwd))
+    for li in reversed(range(len(layer_inputs))):
+        inputs, write_raw, activate = layer_inputs[li]
+
+        def bwd(st, li=li, inputs=inputs, activate=activate):
+            entries = st.pop(f"out{li}")[2]
+            st[f"grads{li}"] = selective_backward(st[f"z{li}"], inputs, entries, st[f"gy{li}"],
+                                                  st[f"gx{li}"], activate, False, chunk)
+
+        ops.append((f"rqf_selective_bwd[L{li}]", bwd))
+    for li, (_, write_raw, activate) in enumerate(layer_inputs):
+        fb, bb = selective_bytes(F, B, T, G, chunk, write_raw=write_raw, activate=activate)
+        nbytes[f"rqf_selective_fwd[L{li}]"] = fb
+        nbytes[f"rqf_selective_bwd[L{li}]"] = bb
+    kernels = {
+        "rqf_selective_fwd": "selective_fwd_kernel",
+        "rqf_selective_bwd": ("team_build_kernel + selective_bwd_team_kernel + "
+                              "team_reduce_kernel + partial_reduce_kernel"),
+    }
+    config = {"workload": name, "F": F, "B": B, "T": T, "G": G, "layers": len(layers),
+              "chunk": chunk, "contract": contract}
+    cpu_steps = args.cpu_steps or (200 if cfg == 3 else 100)
+
+    def cpu():
+        return cpu_baseline_selective(F, min(B, 64), G, cpu_steps, log_scale, samp, tau, seq,
+                                      layers)
+
+    return Plan(name, config, F * B * T * len(layers), (state, ops), nbytes, kernels, cpu,
+                contract)
+
+
+def plan_fbt(cfg, args, dev):
+    import torch
+
+    from prospective_rqf_amd import workloads
+    from prospective_rqf_amd.fbt_scan_kernel import (
+        fbt_recompute_backward_raw,
+        fbt_recompute_forward_raw,
+    )
+
+    if cfg == 2:
+        F, B, T, L = 128, 32, 16000, 1
+        coef = dict(samp=16000.0, tau=5.0 / 16000.0, seq_duration=1.0)
+        name = "non-selective two-tap FBT recompute scan B=32 T=16000 H=128 (config 2)"
+    else:
+        F, B, T, L = 256, 16, 16384, 4
+        coef = dict(samp=16384.0, tau=5.0 / 16384.0, seq_duration=2 * math.pi,
+                    max_freq_factor=0.25)
+        name = "long-sequence Pure RQF B=16 T=16384 H=256, 4 FBT recompute layers (config 5)"
+    if args.batch:
+        B = args.batch
+        name += f" [batch overridden to {B}]"
+    g = torch.Generator(device=dev).manual_seed(1)
+    gcpu = torch.Generator().manual_seed(3)
+    state = {}
+    coefs = [workloads.static_two_tap(F, seed=li, device=dev, **coef) for li in range(L)]
+    if cfg == 2:
+        u = workloads.raw_waveform(B, T, samp=16000.0, generator=gcpu).to(dev)  # (B, T)
+        w = _cn(g, dev, F)
+        state["x0"] = (w[:, None, None] * u[None].to(w.dtype)).contiguous()
+    else:
+        # Flattened 128x128 images of uniform 8-bit pixels; layer l > 0 is driven
+        # by a residual-stream stand-in of the same shape.
+        img = torch.randint(0, 256, (B, T), generator=gcpu).float().div_(255.0).to(dev)
+        state["x0"] = (img[None].expand(F, B, T).to(torch.complex64) * _cn(g, dev, F)[:, None, None]
+                       ).contiguous()
+        for li in range(1, L):
+            state[f"x{li}"] = _cn(g, dev, F, B, T)
+    for li in range(L):
+        state[f"gy{li}"] = _cn(g, dev, F, B, T)
+
+    ops = []
+    for li in range(L):
+        def fwd(st, li=li):
+            st[f"out{li}"] = fbt_recompute_forward_raw(*coefs[li], st[f"x{li}"])
+
+        ops.append((f"rqf_fbt_recompute_fwd[L{li}]", fwd))
+    for li in reversed(range(L)):
+        def bwd(st, li=li):
+            act, carry, (c1, t0, t1, x) = st.pop(f"out{li}")
+            st[f"grads{li}"] = fbt_recompute_backward_raw(c1, t0, t1, x, carry, st[f"gy{li}"])
+
+        ops.append((f"rqf_fbt_recompute_bwd[L{li}]", bwd))
+    fb, bb = fbt_recompute_bytes(F, B, T)
+    nbytes = {}
+    for li in range(L):
+        nbytes[f"rqf_fbt_recompute_fwd[L{li}]"] = fb
+        nbytes[f"rqf_fbt_recompute_bwd[L{li}]"] = bb
+    kernels = {"rqf_fbt_recompute_fwd": "fbt_fwd_kernel",
+               "rqf_fbt_recompute_bwd": "fbt_bwd_kernel<replay> + coef_reduce_kernel"}
+    config = {"workload": name, "F": F, "B": B, "T": T, "layers": L,
+              "contract": "split-ReLU output, per-tile carries; gy cotangent, full BPTT"}
+    cpu_steps = args.cpu_steps or (1000 if cfg == 2 else 500)
+
+    def cpu():
+        return cpu_baseline_timeinv(F, B, cpu_steps, L, prospective=True, coef=coef)
+
+    return Plan(name, config, F * B * T * L, (state, ops), nbytes, kernels, cpu, config["contract"])
+
+
+def plan_chunked(cfg, args, dev):
+    import torch
+
+    from prospective_rqf_amd.chunked_scan_kernel import (
+        _chunked_scan_backward_raw,
+        _chunked_scan_forward_raw,
+    )
+
+    B, T, F, L = 4, 161, 64, 2
+    if args.batch:
+        B = args.batch
+    name = "Pure RQF encoder depth 2, (B,T,F) chunked scan B=4 T=161 F=64 (config 1)"
+    gcpu = torch.Generator().manual_seed(0)
+    state, coefs = {}, []
+    for li in range(L):
+        r = 0.9 + 0.099 * torch.rand(F, generator=gcpu, dtype=torch.float64)
+        ph = math.pi * torch.rand(F, generator=gcpu, dtype=torch.float64)
+        c1 = torch.polar(r, ph)
+        a = torch.log(c1)
+        c2 = -a.real * (c1 - 1) / a  # ZOH gain with a = log C1
+        coefs.append((c1.to(torch.complex64).to(dev), c2.to(torch.complex64).to(dev)))
+        state[f"u{li}"] = torch.complex(torch.randn(B, T, F, generator=gcpu),
+                                        torch.randn(B, T, F, generator=gcpu)).to(dev)
+        state[f"gy{li}"] = torch.complex(torch.randn(B, T, F, generator=gcpu),
+                                         torch.randn(B, T, F, generator=gcpu)).to(dev)
+    ops = []
+    for li in range(L):
+        def fwd(st, li=li):
+            st[f"out{li}"] = _chunked_scan_forward_raw(*coefs[li], st[f"u{li}"])
+
+        ops.append((f"rqf_chunked_scan_fwd[L{li}]", fwd))
+    for li in reversed(range(L)):
+        def bwd(st, li=li):
+            states = st.pop(f"out{li}")
+            st[f"grads{li}"] = _chunked_scan_backward_raw(*coefs[li], st[f"u{li}"], states,
+                                                          st[f"gy{li}"])
+
+        ops.append((f"rqf_chunked_scan_bwd[L{li}]", bwd))
+    N = B * T * F
+    nbytes = {}
+    for li in range(L):
+        nbytes[f"rqf_chunked_scan_fwd[L{li}]"] = 16 * N
+        nbytes[f"rqf_chunked_scan_bwd[L{li}]"] = 24 * N
+    kernels = {"rqf_chunked_scan_fwd": "btf_fwd_local + btf_fwd_final",
+               "rqf_chunked_scan_bwd": "btf_bwd_local + btf_bwd_final + coef_reduce_kernel"}
+    config = {"workload": name, "F": F, "B": B, "T": T, "layers": L,
+              "contract": "(B,T,F) scan, full BPTT; latency-bound, cache-resident"}
+
+    def cpu():
+        return cpu_baseline_timeinv(F, B, T, L, prospective=False, coef=None, btf=(coefs, T))
+
+    return Plan(name, config, N * L, (state, ops), nbytes, kernels, cpu, config["contract"])
+
+
 # ---------------------------------------------------------------------------
-# CPU baseline: fp32 PyTorch restatement of the reference CPU path
+# CPU baselines: fp32 PyTorch restatement of the reference CPU path
 # ---------------------------------------------------------------------------
 
 
-def cpu_baseline_selective(F, B, G, steps, log_scale):
+def _cpu_threads():
+    import torch
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    return threads
+
+
+def _median_time(run, reps=3):
+    run()  # warm-up
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2]
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline_selective(F, B, G, steps, log_scale, samp, tau, seq, layers):
     import torch
 
     from oracle import torch_ref
     from prospective_rqf_amd import workloads
 
-    threads = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
-    inp = workloads.selective_inputs(F, B, steps, G=G, warp_scale=log_scale, device="cpu",
-                                     seed=0)
-    leaves = [inp.gamma_logits, inp.warp_logits, inp.write_logits, inp.bias, inp.theta]
+    threads = _cpu_threads()
     g = torch.Generator().manual_seed(1)
-    z = workloads.randn_c64(F, B, steps, generator=g)
-    cot = workloads.randn_c64(F, B, steps, generator=g)
+    per_layer = []
+    for li, (write_raw, activate) in enumerate(layers):
+        inp = workloads.selective_inputs(F, B, steps, G=G, warp_scale=log_scale, samp=samp,
+                                         tau=tau, seq_duration=seq, device="cpu", seed=li)
+        z = workloads.randn_c64(F, B, steps, generator=g)
+        cot = workloads.randn_c64(F, B, steps, generator=g)
+        per_layer.append((inp, z, cot, write_raw, activate))
 
     def run():
-        for v in leaves:
-            v.requires_grad_(True)
-            v.grad = None
-        zz = z.clone().requires_grad_(True)
-        raw = torch_ref.selective_scan(zz, inp)
-        act = torch_ref.split_relu(raw)
-        loss = (cot.conj() * raw).real.sum() + (cot.conj() * act).real.sum()
-        loss.backward()
+        for inp, z, cot, write_raw, activate in per_layer:
+            leaves = [inp.gamma_logits, inp.warp_logits, inp.write_logits, inp.bias, inp.theta]
+            for v in leaves:
+                v.requires_grad_(True)
+                v.grad = None
+            zz = z.clone().requires_grad_(True)
+            raw = torch_ref.selective_scan(zz, inp)
+            loss = (cot.conj() * raw).real.sum() if write_raw else 0.0
+            if activate:
+                loss = loss + (cot.conj() * torch_ref.split_relu(raw)).real.sum()
+            loss.backward()
 
-    run()  # warm-up
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    t = times[1]
+    t = _median_time(run)
     return {
-        "value": F * B * steps / t / 1e9,
+        "value": F * B * steps * len(layers) / t / 1e9,
         "unit": "Gelem/s",
         "cores": threads,
         "kind": "port",
         "sample": (f"fp32 PyTorch restatement of reference_layer_scan after the drive GEMM "
-                   f"(oracle/torch_ref.py), fwd + autograd bwd, F={F} B={B} T={steps} "
-                   f"(T reduced from 16000), median of 3 after 1 warm-up; "
-                   f"torch threads={threads}, cpu={platform.processor() or platform.machine()}"),
+                   f"(oracle/torch_ref.py), fwd + autograd bwd, {len(layers)} layer(s), F={F} "
+                   f"B={B} T={steps} (T reduced from the GPU shape), median of 3 after 1 "
+                   f"warm-up; torch threads={threads}, os.cpu_count()={os.cpu_count()}, "
+                   f"cpu={_cpu_model()}"),
     }
+
+
+def cpu_baseline_timeinv(F, B, steps, L, *, prospective, coef, btf=None):
+    """_sequential_scan_cpu (+ _apply_prospective_taps) in (B,T,F), fwd + autograd bwd."""
+    import torch
+
+    from oracle import torch_ref
+    from prospective_rqf_amd import workloads
+
+    threads = _cpu_threads()
+    g = torch.Generator().manual_seed(1)
+    layers = []
+    for li in range(L):
+        if btf is not None:
+            c1, c2 = (c.cpu() for c in btf[0][li])
+            t0 = t1 = None
+        else:
+            c1, t0, t1 = workloads.static_two_tap(F, seed=li, **coef)
+            c2 = torch.ones_like(c1)
+        u = workloads.randn_c64(B, steps, F, generator=g)
+        cot = workloads.randn_c64(B, steps, F, generator=g)
+        layers.append((c1, c2, t0, t1, u, cot))
+
+    def run():
+        for c1, c2, t0, t1, u, cot in layers:
+            uu = u.clone().requires_grad_(True)
+            cc = c1.clone().requires_grad_(True)
+            drive = torch_ref.prospective_drive(uu, t0, t1) if prospective else uu
+            y = torch_ref.sequential_scan(cc, c2, drive)
+            out = torch_ref.split_relu(y) if prospective else y
+            (cot.conj() * out).real.sum().backward()
+
+    t = _median_time(run)
+    what = ("_sequential_scan_cpu + _apply_prospective_taps + split-ReLU" if prospective
+            else "_sequential_scan_cpu")
+    return {
+        "value": F * B * steps * L / t / 1e9,
+        "unit": "Gelem/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"fp32 PyTorch restatement of {what} (oracle/torch_ref.py), (B,T,F) layout, "
+                   f"fwd + autograd bwd, {L} layer(s), F={F} B={B} T={steps}, median of 3 after "
+                   f"1 warm-up; torch threads={threads}, os.cpu_count()={os.cpu_count()}, "
+                   f"cpu={_cpu_model()}"),
+    }
+
+
+# ---------------------------------------------------------------------------
+# Traffic table (rocprofv3 FETCH_SIZE / WRITE_SIZE, committed under profiles/)
+# ---------------------------------------------------------------------------
+
+
+def traffic_from_table(workload_key, entry):
+    """HBM bytes per call of ``entry`` for ``workload_key`` from profiles/traffic.md, or None.
+
+    Rows look like ``| config3 | rqf_selective_bwd | <fetch bytes> | <write bytes> | ... |``
+    with bytes already scaled by the copy-kernel calibration."""
+    try:
+        with open(TRAFFIC_TABLE) as fh:
+            for line in fh:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) >= 4 and cells[0] == workload_key and cells[1] == entry:
+                    return int(float(cells[2]) + float(cells[3]))
+    except (OSError, ValueError):
+        return None
+    return None
 
 
 # ---------------------------------------------------------------------------
@@ -163,101 +504,91 @@ def main():
     import torch
 
     from prospective_rqf_amd import _lib
-    from prospective_rqf_amd.selective_scan_kernel import selective_backward, selective_forward
 
     _lib.load()
     dev = torch.device("cuda:0")
     cfg = args.config
-    if cfg == 3:
-        F, B, T, G, layers = 256, 64, 16000, 8, 1
-        log_scale = math.log(1.25)
-        workload = "selective fused scan B=64 T=16000 H=256 G=8 (config 3)"
-        seq_duration, samp, tau = 1.0, 16000.0, 5.0 / 16000.0
-    elif cfg == 4:
-        F, B, T, G, layers = 256, 64, 4096, 4, 1
-        log_scale = math.log(4.0)
-        workload = "selective fused scan B=64 T=4096 H=256 G=4 (config 4, one layer)"
-        seq_duration, samp, tau = 4096.0, 1.0, 5.0
+    if cfg in (3, 4):
+        plan = plan_selective(cfg, args, dev)
+    elif cfg in (2, 5):
+        plan = plan_fbt(cfg, args, dev)
     else:
-        raise SystemExit("configs 2 and 5 are measured by bench_fbt (not yet wired)")
-    if args.batch:
-        B = args.batch
-        workload += f" [batch overridden to {B}]"
-    chunk = 256
-    inputs, z, gy, gx = selective_workload(F, B, T, G, dev, log_scale=log_scale,
-                                           seq_duration=seq_duration, samp=samp, tau=tau)
+        plan = plan_chunked(cfg, args, dev)
+    state, ops = plan.ops
     torch.cuda.synchronize()
 
-    def step(ev=None):
-        if ev:
-            ev[0].record()
-        raw, act, entries = selective_forward(z, inputs, True, True, chunk)
-        if ev:
-            ev[1].record()
-        outs = selective_backward(z, inputs, entries, gy, gx, True, False, chunk)
-        if ev:
-            ev[2].record()
-        return raw, act, outs
+    def step(events=None):
+        for i, (_, fn) in enumerate(ops):
+            if events is not None:
+                events[i].record()
+            fn(state)
+        if events is not None:
+            events[len(ops)].record()
+        for k in [k for k in state if k.startswith("grads")]:
+            del state[k]
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(ops) + 1)]
+              for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        out = step(events[i])
-        del out
+        step(events[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    fwd_ms = [e[0].elapsed_time(e[1]) for e in events]
-    bwd_ms = [e[1].elapsed_time(e[2]) for e in events]
-    fwd = sum(fwd_ms) / len(fwd_ms)
-    bwd = sum(bwd_ms) / len(bwd_ms)
-    ms_per_step = wall * 1e3 / args.steps
-    elems = F * B * T * layers
-    fwd_bytes, bwd_bytes = selective_bytes(F, B, T, G, chunk)
-    value = elems / ((fwd + bwd) * 1e-3) / 1e9
-    achieved_bwd = bwd_bytes / (bwd * 1e-3) / 1e9
-    achieved_fwd = fwd_bytes / (fwd * 1e-3) / 1e9
+
+    per_op = {name: sum(ev[i].elapsed_time(ev[i + 1]) for ev in events) / args.steps
+              for i, (name, _) in enumerate(ops)}
+    scan_ms = sum(per_op.values())
+    fwd_ms = sum(v for k, v in per_op.items() if "_fwd" in k)
+    bwd_ms = scan_ms - fwd_ms
+    value = plan.elems / (scan_ms * 1e-3) / 1e9
+    dom = max(per_op, key=per_op.get)
+    entry = dom.split("[")[0]
+    dom_bytes = plan.bytes[dom]
+    achieved = dom_bytes / (per_op[dom] * 1e-3) / 1e9
+    all_bytes = sum(plan.bytes.values())
+    traffic = traffic_from_table(f"config{cfg}", entry) if not args.batch else None
     result = {
-        "metric": "scan Gelem/s (B·T·H complex) fwd+bwd at T=16000; % of HBM roofline",
+        "metric": METRIC,
         "value": round(value, 3),
         "unit": "Gelem/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32 (complex64 state)",
         "data": "synthetic (seeded N(0,1) drive, logits and cotangents; recipe parameters)",
-        "config": {"workload": workload, "F": F, "B": B, "T": T, "G": G, "chunk": chunk,
-                   "contract": "raw+act outputs, gy+gx cotangents, full BPTT"},
+        "config": plan.config,
         "roofline": {
             "bound": "hbm",
-            "kernel": "rqf_selective_bwd (selective_bwd_kernel + group/partial reductions)",
-            "achieved": round(achieved_bwd, 1),
+            "kernel": f"{entry}: {plan.kernels[entry]}",
+            "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(achieved_bwd / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "alg_bytes": dom_bytes,
+            "avg_ms": round(per_op[dom], 4),
         },
         "detail": {
-            "fwd_ms": round(fwd, 4),
-            "bwd_ms": round(bwd, 4),
-            "fwd_GBs": round(achieved_fwd, 1),
-            "fwd_frac": round(achieved_fwd / HBM_PEAK_GBS, 4),
-            "fwd_bwd_frac": round((fwd_bytes + bwd_bytes) / ((fwd + bwd) * 1e-3) / 1e9
-                                  / HBM_PEAK_GBS, 4),
-            "alg_bytes_fwd": fwd_bytes,
-            "alg_bytes_bwd": bwd_bytes,
+            "scan_ms": round(scan_ms, 4),
+            "fwd_ms": round(fwd_ms, 4),
+            "bwd_ms": round(bwd_ms, 4),
+            "per_entry_ms": {k: round(v, 4) for k, v in per_op.items()},
+            "per_entry_GBs": {k: round(plan.bytes[k] / (v * 1e-3) / 1e9, 1)
+                              for k, v in per_op.items()},
+            "step_frac_of_hbm": round(all_bytes / (scan_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "alg_bytes_step": all_bytes,
         },
     }
     if args.cpu:
-        steps = args.cpu_steps or 200
-        result["cpu_baseline"] = cpu_baseline_selective(F, B, G, steps, log_scale)
+        result["cpu_baseline"] = plan.cpu()
     print(json.dumps(result), flush=True)
 
 

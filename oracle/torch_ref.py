@@ -81,14 +81,17 @@ def split_relu(y):
 
 
 def sequential_scan(C1, C2, u):
-    """x[t] = C1 x[t-1] + C2 u[t] on (B,T,F), serial over t."""
+    """x[t] = C1 x[t-1] + C2 u[t] on (B,T,F), serial over t.
+
+    Like the reference, each step's state is written into a preallocated
+    output by slice assignment (so autograd cost matches the reference's)."""
     B, T, F = u.shape
     prev = torch.zeros(B, F, dtype=u.dtype, device=u.device)
-    outs = []
+    out = torch.empty(B, T, F, dtype=u.dtype, device=u.device)
     for t in range(T):
         prev = C1 * prev + C2 * u[:, t, :]
-        outs.append(prev)
-    return torch.stack(outs, dim=1) if outs else u.new_zeros((B, 0, F))
+        out[:, t, :] = prev
+    return out
 
 
 def prospective_drive(u, tap0, tap1, time_dim=1):

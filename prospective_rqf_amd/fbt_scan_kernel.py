@@ -86,26 +86,50 @@ def fbt_prospective_scan(C1, tap0, tap1, x_fbt, fuse_act=False):
     return _FBTProspectiveScan.apply(C1, tap0, tap1, x_fbt, fuse_act)
 
 
+def fbt_recompute_forward_raw(C1, tap0, tap1, x):
+    """Kernel-only forward of :func:`fbt_recompute_scan`: ``(act, carry, coefs)``."""
+    x = _c64(x)
+    _lib.require_device(x)
+    filters, batch, time = x.shape
+    C1, tap0, tap1 = _coefs(C1, tap0, tap1, filters)
+    lib = _lib.load()
+    nchunks = lib.rqf_fbt_carry_chunks(time)
+    act = torch.empty_like(x)
+    carry = torch.empty((filters * batch, max(nchunks, 1)), dtype=torch.complex64, device=x.device)
+    _lib.check(
+        lib.rqf_fbt_recompute_fwd(
+            _lib.ptr(C1), _lib.ptr(tap0), _lib.ptr(tap1), _lib.ptr(x), _lib.ptr(act),
+            _lib.ptr(carry), filters, batch, time, _lib.stream_of(x)),
+        "rqf_fbt_recompute_fwd",
+    )
+    return act, carry, (C1, tap0, tap1, x)
+
+
+def fbt_recompute_backward_raw(C1, tap0, tap1, x, carry, grad_output):
+    """Kernel-only backward of :func:`fbt_recompute_scan`: ``(gC1, gtap0, gtap1, gx)``."""
+    filters, batch, time = x.shape
+    g = _c64(grad_output)
+    grad_z = torch.empty_like(x)
+    gc1, gt0, gt1 = _bwd_grads(filters, x.device)
+    lib = _lib.load()
+    n = lib.rqf_fbt_workspace(filters, batch, time)
+    ws = _lib.workspace(n, x.device)
+    _lib.check(
+        lib.rqf_fbt_recompute_bwd(
+            _lib.ptr(C1), _lib.ptr(tap0), _lib.ptr(tap1), _lib.ptr(x), _lib.ptr(carry),
+            _lib.ptr(g), _lib.ptr(grad_z), _lib.ptr(gc1), _lib.ptr(gt0), _lib.ptr(gt1),
+            filters, batch, time, _lib.ptr(ws), n, _lib.stream_of(x)),
+        "rqf_fbt_recompute_bwd",
+    )
+    return gc1, gt0, gt1, grad_z
+
+
 class _FBTRecompute(torch.autograd.Function):
     """Split-ReLU prospective scan that replays the raw state in the backward."""
 
     @staticmethod
     def forward(ctx, C1, tap0, tap1, x_fbt):
-        x = _c64(x_fbt)
-        _lib.require_device(x)
-        filters, batch, time = x.shape
-        C1, tap0, tap1 = _coefs(C1, tap0, tap1, filters)
-        lib = _lib.load()
-        nchunks = lib.rqf_fbt_carry_chunks(time)
-        act = torch.empty_like(x)
-        carry = torch.empty((filters * batch, max(nchunks, 1)), dtype=torch.complex64,
-                            device=x.device)
-        _lib.check(
-            lib.rqf_fbt_recompute_fwd(
-                _lib.ptr(C1), _lib.ptr(tap0), _lib.ptr(tap1), _lib.ptr(x), _lib.ptr(act),
-                _lib.ptr(carry), filters, batch, time, _lib.stream_of(x)),
-            "rqf_fbt_recompute_fwd",
-        )
+        act, carry, (C1, tap0, tap1, x) = fbt_recompute_forward_raw(C1, tap0, tap1, x_fbt)
         ctx.save_for_backward(C1, tap0, tap1, x, carry)
         return act
 
@@ -113,21 +137,7 @@ class _FBTRecompute(torch.autograd.Function):
     @once_differentiable
     def backward(ctx, grad_output):
         C1, tap0, tap1, x, carry = ctx.saved_tensors
-        filters, batch, time = x.shape
-        g = _c64(grad_output)
-        grad_z = torch.empty_like(x)
-        gc1, gt0, gt1 = _bwd_grads(filters, x.device)
-        lib = _lib.load()
-        n = lib.rqf_fbt_workspace(filters, batch, time)
-        ws = _lib.workspace(n, x.device)
-        _lib.check(
-            lib.rqf_fbt_recompute_bwd(
-                _lib.ptr(C1), _lib.ptr(tap0), _lib.ptr(tap1), _lib.ptr(x), _lib.ptr(carry),
-                _lib.ptr(g), _lib.ptr(grad_z), _lib.ptr(gc1), _lib.ptr(gt0), _lib.ptr(gt1),
-                filters, batch, time, _lib.ptr(ws), n, _lib.stream_of(x)),
-            "rqf_fbt_recompute_bwd",
-        )
-        return gc1, gt0, gt1, grad_z
+        return fbt_recompute_backward_raw(C1, tap0, tap1, x, carry, grad_output)
 
 
 def fbt_recompute_scan(C1, tap0, tap1, x_fbt):

@@ -28,11 +28,15 @@ LN_1_25 = math.log(1.25)
 
 
 def recipe_params(F: int, *, samp: float, tau: float, seq_duration: float, margin: float = 1e-3,
-                  generator: torch.Generator | None = None, dtype=torch.float64):
-    """Per-channel (theta, gamma, eta, lo, span, theta_lo, theta_hi) in fp64."""
+                  max_freq_factor: float = 1.0, generator: torch.Generator | None = None,
+                  dtype=torch.float64):
+    """Per-channel (theta, gamma, eta, lo, span, theta_lo, theta_hi) in fp64.
+
+    theta is log-uniform in [2*pi*tau/seq_duration, 2*pi*max_freq_factor]
+    (filter_max_freq_factor of filter.py:330-345)."""
     dt = 1.0 / samp
     lo_t = math.log(2 * math.pi * tau / seq_duration)
-    hi_t = math.log(2 * math.pi)
+    hi_t = math.log(2 * math.pi * max_freq_factor)
     theta = torch.exp(lo_t + torch.rand(F, generator=generator, dtype=dtype) * (hi_t - lo_t))
     lo, hi = 1e-6, 1.0 - 1e-6
     span = hi - lo
@@ -108,10 +112,11 @@ def raw_waveform(B, T, *, samp=16000.0, generator=None):
     return x.clamp(-1, 1).float()
 
 
-def static_two_tap(F, *, samp=16000.0, tau=5.0 / 16000.0, seq_duration=1.0, seed=0,
-                   device="cpu"):
+def static_two_tap(F, *, samp=16000.0, tau=5.0 / 16000.0, seq_duration=1.0, max_freq_factor=1.0,
+                   seed=0, device="cpu"):
     """(C1, tap0, tap1) complex64 per channel for the static prospective RQF."""
     g = torch.Generator().manual_seed(seed)
-    p = recipe_params(F, samp=samp, tau=tau, seq_duration=seq_duration, margin=0.0, generator=g)
+    p = recipe_params(F, samp=samp, tau=tau, seq_duration=seq_duration, margin=0.0,
+                      max_freq_factor=max_freq_factor, generator=g)
     c1, t0, t1 = zoh_two_tap(p["gamma"], p["theta"], p["eta"], torch.ones_like(p["gamma"]))
     return tuple(v.to(torch.complex64).to(device) for v in (c1, t0, t1))

@@ -49,6 +49,27 @@ __device__ __forceinline__ c32 cjmad(c32 a, c32 b, c32 c) {
   return mk(fmaf(a.r, b.r, fmaf(a.i, b.i, c.r)), fmaf(a.r, b.i, fmaf(-a.i, b.r, c.i)));
 }
 __device__ __forceinline__ c32 conjg(c32 a) { return mk(a.r, -a.i); }
+// s*a + c for real s (two FMAs; a complex product with a zero imaginary part
+// would keep its multiplications by zero under IEEE rules)
+__device__ __forceinline__ c32 csmad(float s, c32 a, c32 c) {
+  return mk(fmaf(s, a.r, c.r), fmaf(s, a.i, c.i));
+}
+// a*b + c for real c
+__device__ __forceinline__ c32 cmadr(c32 a, c32 b, float c) {
+  return mk(fmaf(a.r, b.r, fmaf(-a.i, b.i, c)), fmaf(a.r, b.i, a.i * b.r));
+}
+// a*s + c for real s and c (first step of a Horner scheme with real coefficients)
+__device__ __forceinline__ c32 cmadrr(c32 a, float s, float c) { return mk(fmaf(a.r, s, c), a.i * s); }
+// Re(conj(a) b)
+__device__ __forceinline__ float cdot(c32 a, c32 b) { return fmaf(a.r, b.r, a.i * b.i); }
+
+// Index of this wavefront within its block, as a wave-uniform (scalar) value:
+// the compiler cannot prove threadIdx.x >> 6 uniform, and everything derived
+// from a divergent value (row pointers, per-channel parameters) would occupy
+// vector registers.
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
 
 // ---------------------------------------------------------------------------
 // Cross-lane primitives
@@ -222,9 +243,9 @@ __device__ __forceinline__ void zoh(float ar, float ai, c32& A, c32& phi, float&
   if (den < 1.0e-8f) {
     // 1 + a*(1/2 + a*(1/6 + a/24))
     c32 a = mk(ar, ai);
-    c32 t = cmad(a, mk(1.0f / 24.0f, 0.0f), mk(1.0f / 6.0f, 0.0f));
-    t = cmad(a, t, mk(0.5f, 0.0f));
-    phi = cmad(a, t, mk(1.0f, 0.0f));
+    c32 t = cmadrr(a, 1.0f / 24.0f, 1.0f / 6.0f);
+    t = cmadr(a, t, 0.5f);
+    phi = cmadr(a, t, 1.0f);
     inv_den = 0.0f;
   } else {
     // Re(e^a - 1) = expm1(ar) cos(ai) - (1 - cos ai) = expm1(ar)*(1 - vers) - vers:

@@ -35,6 +35,7 @@
 #include "rqf_scan.h"
 
 #include <initializer_list>
+#include <type_traits>
 
 using namespace rqf;
 
@@ -62,6 +63,11 @@ using namespace rqf;
 #else
 #define RQF_STEP_FENCE() ((void)0)
 #endif
+#ifdef RQF_BWD_PHASE_FENCE
+#define RQF_PHASE_FENCE() __builtin_amdgcn_sched_barrier(0)
+#else
+#define RQF_PHASE_FENCE() ((void)0)
+#endif
 
 namespace {
 
@@ -76,6 +82,57 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t P, int64_t n) {
   const int64_t x = P % kXcds, j = P / kXcds, q = n / kXcds, r = n % kXcds;
   return x * q + (x < r ? x : r) + j;
 }
+
+// Option specialisation.  Like the reference's constexpr kernel flags
+// (selective_scan_kernel.py:35-46), the structural options can be compile-time
+// constants: a kernel instantiated with O >= 0 takes its switches from the
+// bits of O and every option branch folds away, so one tile is one basic
+// block the scheduler can interleave.  O = kOptRuntime reads them from the
+// inputs.  Bits that cannot matter are cleared (normalise_options) so that
+// equivalent option sets share one instantiation.
+enum : int {
+  kOptGamma = 1,
+  kOptLogShift = 2,
+  kOptWarp = 4,
+  kOptBound = 8,
+  kOptWrite = 16,
+  kOptWriteSigmoid = 32,
+  kOptProspective = 64,
+  kOptGammaHorizon = 128,
+  kOptRuntime = -1,
+};
+
+__host__ __device__ constexpr int normalise_options(int o) {
+  return (o & kOptGamma ? o : o & ~kOptLogShift) & (o & kOptWarp ? ~0 : ~kOptBound) &
+         (o & kOptWrite ? ~0 : ~kOptWriteSigmoid) & (o & kOptProspective ? ~0 : ~kOptGammaHorizon);
+}
+
+template <int O>
+__device__ __forceinline__ rqf_selective_inputs with_options(rqf_selective_inputs p) {
+  if constexpr (O >= 0) {
+    p.has_gamma = (O & kOptGamma) != 0;
+    p.log_shift = (O & kOptLogShift) != 0;
+    p.has_warp = (O & kOptWarp) != 0;
+    p.bound_warp = (O & kOptBound) != 0;
+    p.has_write = (O & kOptWrite) != 0;
+    p.write_sigmoid = (O & kOptWriteSigmoid) != 0;
+    p.prospective = (O & kOptProspective) != 0;
+    p.gamma_horizon = (O & kOptGammaHorizon) != 0;
+  }
+  return p;
+}
+
+// Compiled option sets (normalised).  Anything else runs the kOptRuntime kernels.
+//  - sigmoid gamma + grouped/global warp with band bound + sigmoid write + prospective
+//    (the selective-copying cell, experiment/selective_copying.yaml)
+//  - sigmoid gamma + prospective; sigmoid gamma alone (pure_rqf_selective.yaml)
+//  - the same three without the band bound / with a gamma-mode horizon are left
+//    to the run-time kernels.
+constexpr int kOptSets[] = {
+    kOptGamma | kOptWarp | kOptBound | kOptWrite | kOptWriteSigmoid | kOptProspective,
+    kOptGamma | kOptProspective,
+    kOptGamma,
+};
 
 // Wave-uniform per-channel parameters and option reciprocals.
 struct Chan {
@@ -106,8 +163,9 @@ struct Ctl {
   float wt;                    // tanh(warp logit), 0 without a warp head
 };
 
-__device__ __forceinline__ Ctl controller(const rqf_selective_inputs& p, const Chan& c, float gv,
-                                          float dv, float wv) {
+// With the warp head's wt = tanh(warp logit) and ws = exp(warp_scale * wt) given.
+__device__ __forceinline__ Ctl controller_w(const rqf_selective_inputs& p, const Chan& c, float gv,
+                                            float wt, float ws, float wv) {
   Ctl o;
   o.gamma = c.bias;
   if (p.has_gamma) {
@@ -116,15 +174,29 @@ __device__ __forceinline__ Ctl controller(const rqf_selective_inputs& p, const C
     else
       o.gamma = fmaf(c.span, fsigmoid(c.bias + gv), c.lo);
   }
-  o.wt = p.has_warp ? ftanh(dv) : 0.0f;
-  o.theta_u = p.has_warp ? c.theta * fexp(p.warp_scale * o.wt) : c.theta;
+  o.wt = p.has_warp ? wt : 0.0f;
+  o.theta_u = p.has_warp ? c.theta * ws : c.theta;
   o.gate = 1.0f;
   if (p.has_write) o.gate = p.write_sigmoid ? p.write_max * fsigmoid(wv + p.write_bias) : 1.0f + wv;
   return o;
 }
 
+__device__ __forceinline__ float warp_tanh(const rqf_selective_inputs& p, float dv) {
+  return p.has_warp ? ftanh(dv) : 0.0f;
+}
+__device__ __forceinline__ float warp_factor(const rqf_selective_inputs& p, float wt) {
+  return p.has_warp ? fexp(p.warp_scale * wt) : 1.0f;
+}
+
+__device__ __forceinline__ Ctl controller(const rqf_selective_inputs& p, const Chan& c, float gv,
+                                          float dv, float wv) {
+  const float wt = warp_tanh(p, dv);
+  return controller_w(p, c, gv, wt, warp_factor(p, wt), wv);
+}
+
+// The band clamp applies to the warped frequency only (selective_scan_kernel.py:59-64).
 __device__ __forceinline__ float clamp_theta(const rqf_selective_inputs& p, const Chan& c, float th) {
-  return p.bound_warp ? fminf(fmaxf(th, c.thlo), c.thhi) : th;
+  return p.has_warp && p.bound_warp ? fminf(fmaxf(th, c.thlo), c.thhi) : th;
 }
 
 // ratio * gamma of the prospective tap: 1 in gamma-horizon mode (ratio = 1/gamma).
@@ -381,14 +453,15 @@ __device__ __forceinline__ void fwd_tile(const rqf_selective_inputs& p, const Ch
   fwd_compute<K, VEC, TAIL>(p, c, r, t0, lane, in);
 }
 
-template <bool VEC>
+template <int O, bool VEC>
 __global__ __launch_bounds__(kRowsPerBlock* kWave)
     __attribute__((amdgpu_waves_per_eu(RQF_FWD_WAVES_PER_EU))) void selective_fwd_kernel(
-    const rqf_selective_inputs p, const float* __restrict__ z, float* __restrict__ raw,
+    const rqf_selective_inputs pin, const float* __restrict__ z, float* __restrict__ raw,
     float* __restrict__ act, float* __restrict__ entries, int chunk, int nc) {
   constexpr int K = kFwdK, TILE = kWave * K;
+  const rqf_selective_inputs p = with_options<O>(pin);
   const int lane = lane_id();
-  const int64_t L = xcd_remap(blockIdx.x, gridDim.x) * kRowsPerBlock + (threadIdx.x >> 6);
+  const int64_t L = xcd_remap(blockIdx.x, gridDim.x) * kRowsPerBlock + wave_id();
   const RowId id = row_id(p, L);
   if (!id.valid) return;  // whole wavefronts exit together
   const Chan c = load_chan(p, id.f);
@@ -456,6 +529,8 @@ struct BwdRow {
   float* dwr;
   float* ddr;     // per-channel warp-logit gradient (global), or
   float4* sdd;    // this wavefront's slot of the team's LDS warp-gradient tile
+  const float* swt;  // team LDS stage of the tile: tanh(warp logit) per step
+  const float* sws;  // and exp(warp_scale * tanh)
   int T, chunk, truncated;
   c32 dcarry;  // adjoint (truncated: cotangent) at the next tile's first step
   c32 Afirst;  // A at the next tile's first step (0 past the end)
@@ -463,7 +538,19 @@ struct BwdRow {
   double sum_bias, sum_theta;
 };
 
-template <int K, bool VEC, bool TAIL>
+// Warp values of the lane's K steps from the team's LDS stage (SHARED).
+template <int K>
+__device__ __forceinline__ void lds_warp(const BwdRow& r, int lane, float (&wt)[K], float (&ws)[K]) {
+  static_assert(K == 4, "one float4 of staged warp values per lane");
+  const float4 a = reinterpret_cast<const float4*>(r.swt)[lane];
+  const float4 b = reinterpret_cast<const float4*>(r.sws)[lane];
+  wt[0] = a.x, wt[1] = a.y, wt[2] = a.z, wt[3] = a.w;
+  ws[0] = b.x, ws[1] = b.y, ws[2] = b.z, ws[3] = b.w;
+}
+
+// SHARED: tanh(warp logit) and exp(warp_scale * tanh) of the tile come from
+// the team's LDS stage (r.swt, r.sws) instead of per-lane loads and math.
+template <int K, bool VEC, bool TAIL, bool SHARED>
 __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Chan& c, BwdRow& r,
                                          int t0, int lane) {
   const int T = r.T;
@@ -473,28 +560,53 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
   load_c<K, VEC, TAIL>(r.zr, tb, T, zv);
   if (r.gr) load_f<K, VEC, TAIL>(r.gr, tb, T, gv); else zero(gv);
   if (r.wr) load_f<K, VEC, TAIL>(r.wr, tb, T, wv); else zero(wv);
-  if (r.dr) load_f<K, VEC, TAIL>(r.dr, tb, T, dv); else zero(dv);
+  if (!SHARED && r.dr) load_f<K, VEC, TAIL>(r.dr, tb, T, dv); else zero(dv);
   const c32 zprev_tile = t0 > 0 ? mk(r.zr[2 * (t0 - 1)], r.zr[2 * (t0 - 1) + 1]) : mk(0.0f, 0.0f);
   const c32 zp0 = shift_up(zv[K - 1], zprev_tile, lane);
 
-  // Coefficients; kept per step: A, phi, gamma, theta_u, gate, tanh(warp logit).
+  // Coefficients; kept per step: A, phi, gamma, gate and (unless SHARED)
+  // theta_u and tanh(warp logit).
   c32 A[K], phi[K], u[K];
   float gam[K], thu[K], gate[K], wtk[K];
+  float swt[K], sws[K];
+  if (SHARED) lds_warp<K>(r, lane, swt, sws);
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    const Ctl q = controller(p, c, gv[k], dv[k], wv[k]);
+    const Ctl q = SHARED ? controller_w(p, c, gv[k], swt[k], sws[k], wv[k])
+                         : controller(p, c, gv[k], dv[k], wv[k]);
     step_coef(p, c, q, zv[k], k ? zv[k - 1] : zp0, A[k], phi[k], u[k]);
     gam[k] = q.gamma;
-    thu[k] = q.theta_u;
     gate[k] = q.gate;
-    wtk[k] = q.wt;
+    if (!SHARED) {
+      thu[k] = q.theta_u;
+      wtk[k] = q.wt;
+    }
     if (TAIL && tb + k >= T) u[k] = mk(0.0f, 0.0f);
     RQF_STEP_FENCE();
   }
-  // Forward replay from the tile's entry state.
-  const c32 y0 = mk(r.ent[2 * (t0 / r.chunk)], r.ent[2 * (t0 / r.chunk) + 1]);
+  RQF_PHASE_FENCE();
+#ifdef RQF_LOAD_FENCE
+  __asm__ volatile("" ::: "memory");
+#endif
+  // Forward states y[t-1] of every step, and the cotangent e[t] on raw: the
+  // raw output plus the split-ReLU cotangent where raw > 0.
   c32 yprev[K], ecot[K];
+  c32 ey[K], ex[K];
+  if (r.gyr) {
+    load_c<K, VEC, TAIL>(r.gyr, tb, T, ey);
+  } else {
+#pragma unroll
+    for (int k = 0; k < K; ++k) ey[k] = mk(0.0f, 0.0f);
+  }
+  if (r.gxr) {
+    load_c<K, VEC, TAIL>(r.gxr, tb, T, ex);
+  } else {
+#pragma unroll
+    for (int k = 0; k < K; ++k) ex[k] = mk(0.0f, 0.0f);
+  }
   {
+    // Replay the forward from the tile's entry state.
+    const c32 y0 = mk(r.ent[2 * (t0 / r.chunk)], r.ent[2 * (t0 / r.chunk) + 1]);
     c32 Am[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) Am[k] = (TAIL && tb + k >= T) ? mk(1.0f, 0.0f) : A[k];
@@ -507,24 +619,10 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
     if (lane == 0) s = cmad(P, y0, s);
     wave_scan_fwd(P, s);
     c32 yk = shift_up(s, y0, lane);
-    c32 ey[K], ex[K];
-    if (r.gyr) {
-      load_c<K, VEC, TAIL>(r.gyr, tb, T, ey);
-    } else {
-#pragma unroll
-      for (int k = 0; k < K; ++k) ey[k] = mk(0.0f, 0.0f);
-    }
-    if (r.gxr) {
-      load_c<K, VEC, TAIL>(r.gxr, tb, T, ex);
-    } else {
-#pragma unroll
-      for (int k = 0; k < K; ++k) ex[k] = mk(0.0f, 0.0f);
-    }
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       yprev[k] = yk;
       yk = cmad(Am[k], yk, u[k]);
-      // raw-output cotangent plus the split-ReLU cotangent where raw > 0
       ecot[k] = mk(ey[k].r + (yk.r > 0.0f ? ex[k].r : 0.0f), ey[k].i + (yk.i > 0.0f ? ex[k].i : 0.0f));
     }
   }
@@ -544,6 +642,7 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
   r.Afirst = readlane(A[0], 0);
   r.cfirst = readlane(c0, 0);
 
+  RQF_PHASE_FENCE();
   // Adjoint d[t] = e[t] + conj(A[t+1]) d[t+1]  (truncated: d = e).
   c32 dnext;
   if (r.truncated) {
@@ -563,6 +662,13 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
     r.dcarry = readlane(rr, 0);
   }
 
+  RQF_PHASE_FENCE();
+  if (SHARED) {
+    // Re-read the staged warp values here rather than keep them live across
+    // the scans (the compiler barrier stops it from reusing the first read).
+    __asm__ volatile("" ::: "memory");
+    lds_warp<K>(r, lane, swt, sws);
+  }
   c32 gz[K], gzw[K];
   float gg[K], gw[K], gd[K];
   float tile_bias = 0.0f, tile_theta = 0.0f;
@@ -578,52 +684,57 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
     const float gamma = gam[k], gt = gate[k];
     const float rg = p.prospective ? ratio_gamma(p, c, gamma) : 0.0f;
     const float gh = gamma * c.eta;
-    // un-gated taps: bp = gamma*eta*phi + rg*A, bn = -rg*A
-    const c32 bp = cmad(mk(rg, 0.0f), A[k], cscale(gh, phi[k]));
-    const c32 bn = cscale(-rg, A[k]);
-    const c32 cur = cscale(gt, cjmul(bp, d));
+    // Step map: y = A y_prev + gt*(gh*phi*z + rg*A*(z - zp)); the un-gated taps
+    // are bp = gh*phi + rg*A on z and bn = -rg*A on zp.
+    // x-path input gradient conj(gt*bp) d, and the W-path one adds the next
+    // step's lag tap conj(n[t+1]) d[t+1] with n[t+1] = -cn*A[t+1].
+    const c32 gphi = cscale(gt * gh, phi[k]);
+    const c32 gbp = p.prospective ? csmad(gt * rg, A[k], gphi) : gphi;
+    const c32 cur = cjmul(gbp, d);
     gz[k] = cur;
-    // lag tap of step t+1: conj(n[t+1]) d[t+1] with n[t+1] = -cn*A[t+1]
-    gzw[k] = cjmad(cscale(-cn, An), dnext, cur);
+    gzw[k] = p.prospective ? cjmad(cscale(-cn, An), dnext, cur) : cur;
     dnext = d;
-    const c32 zp = k ? zv[k - 1] : zp0;
-    const c32 dp = cjmul(zv[k], d);
-    const c32 dn = cjmul(zp, d);
-    c32 dA = cjmul(yprev[k], d);
-    const float dgate = bp.r * dp.r + bp.i * dp.i + bn.r * dn.r + bn.i * dn.i;
-    const c32 dbp = cscale(gt, dp);
-    float dgamma = 0.0f;
+    // cz = conj(z) d; for the prospective tap cw = conj(z - zp) d.
+    const c32 cz = cjmul(zv[k], d);
+    const float pz = cdot(phi[k], cz);  // Re(conj(phi z) d)
+    float dgate = gh * pz;              // dL/dgate = Re(conj(drive) d)
+    float dgamma = gt * c.eta * pz;     // through gh = gamma*eta
+    c32 dA = cjmul(yprev[k], d);        // dL/dA = conj(y_prev + gt*rg*(z - zp)) d
     if (p.prospective) {
-      const c32 qd = csub(dbp, cscale(gt, dn));
-      if (!p.gamma_horizon) dgamma = c.horizon * (qd.r * A[k].r + qd.i * A[k].i);
-      dA = cmad(mk(rg, 0.0f), qd, dA);
+      const c32 zp = k ? zv[k - 1] : zp0;
+      const c32 cw = cjmul(csub(zv[k], zp), d);
+      const float aw = cdot(A[k], cw);  // Re(conj(A (z - zp)) d)
+      dgate = fmaf(rg, aw, dgate);
+      if (!p.gamma_horizon) dgamma = fmaf(gt * c.horizon, aw, dgamma);  // through rg
+      dA = csmad(gt * rg, cw, dA);
     }
     // phi'(a) = (A - phi)/a, or its series for |a|^2 < 1/64 (cubic below 1e-8);
     // selective_scan_kernel.py:119-148.
-    const float theta = clamp_theta(p, c, thu[k]);
+    const float th_u = SHARED ? (p.has_warp ? c.theta * sws[k] : c.theta) : thu[k];
+    const float theta = clamp_theta(p, c, th_u);
     const float ar = -gh, ai = (1.0f - gamma) * theta * c.eta;
     const float den = fmaf(ar, ar, ai * ai);
     const c32 a = mk(ar, ai);
     c32 fp;
     if (den < 0.015625f) {
       if (den < 1.0e-8f) {
-        fp = cmad(a, cmad(a, mk(1.0f / 8.0f, 0.0f), mk(1.0f / 3.0f, 0.0f)), mk(0.5f, 0.0f));
+        fp = cmadr(a, cmadrr(a, 1.0f / 8.0f, 1.0f / 3.0f), 0.5f);
       } else {
-        c32 sr = mk(1.0f / 45360.0f, 0.0f);
-        sr = cmad(a, sr, mk(1.0f / 5760.0f, 0.0f));
-        sr = cmad(a, sr, mk(1.0f / 840.0f, 0.0f));
-        sr = cmad(a, sr, mk(1.0f / 144.0f, 0.0f));
-        sr = cmad(a, sr, mk(1.0f / 30.0f, 0.0f));
-        sr = cmad(a, sr, mk(1.0f / 8.0f, 0.0f));
-        sr = cmad(a, sr, mk(1.0f / 3.0f, 0.0f));
-        fp = cmad(a, sr, mk(0.5f, 0.0f));
+        c32 sr = cmadrr(a, 1.0f / 45360.0f, 1.0f / 5760.0f);
+        sr = cmadr(a, sr, 1.0f / 840.0f);
+        sr = cmadr(a, sr, 1.0f / 144.0f);
+        sr = cmadr(a, sr, 1.0f / 30.0f);
+        sr = cmadr(a, sr, 1.0f / 8.0f);
+        sr = cmadr(a, sr, 1.0f / 3.0f);
+        fp = cmadr(a, sr, 0.5f);
       }
     } else {
       fp = cscale(frcp(den), cmul(csub(A[k], phi[k]), conjg(a)));
     }
-    // da = conj(A) dA + gamma*eta*conj(phi') dbp
-    const c32 da = cmad(mk(gh, 0.0f), cjmul(fp, dbp), cjmul(A[k], dA));
-    dgamma += c.eta * (phi[k].r * dbp.r + phi[k].i * dbp.i - da.r - theta * da.i);
+    // da = conj(A) dA + conj(phi') dphi with dphi = gt*gh*cz; then through
+    // a = (-gamma*eta, (1 - gamma)*theta*eta).
+    const c32 da = cjmad(fp, cscale(gt * gh, cz), cjmul(A[k], dA));
+    dgamma -= c.eta * fmaf(theta, da.i, da.r);
     float dth = c.eta * (1.0f - gamma) * da.i;
     // controller chain rules (selective_scan_kernel.py:441-460)
     float dbias;
@@ -644,10 +755,11 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
       gg[k] = 0.0f;
     }
     if (p.has_warp) {
-      const float ws = thu[k] * c.inv_theta;  // exp(scale*w) = d theta_u / d theta
-      const float wt = wtk[k];
+      // exp(scale*w) = d theta_u / d theta
+      const float ws = SHARED ? sws[k] : thu[k] * c.inv_theta;
+      const float wt = SHARED ? swt[k] : wtk[k];
       // torch.clamp passes the gradient at both exact edges
-      if (p.bound_warp && !(thu[k] >= c.thlo && thu[k] <= c.thhi)) dth = 0.0f;
+      if (p.bound_warp && !(th_u >= c.thlo && th_u <= c.thhi)) dth = 0.0f;
       gd[k] = dth * theta * p.warp_scale * (1.0f - wt * wt);
       dth *= ws;
     } else {
@@ -660,6 +772,7 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
     }
     tile_bias += dbias;
     tile_theta += dth;
+    RQF_STEP_FENCE();
   }
   r.sum_bias += (double)tile_bias;
   r.sum_theta += (double)tile_theta;
@@ -674,15 +787,16 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
   }
 }
 
-template <bool VEC>
+template <int O, bool VEC>
 __global__ __launch_bounds__(kRowsPerBlock* kWave)
     __attribute__((amdgpu_waves_per_eu(RQF_BWD_WAVES_PER_EU))) void selective_bwd_kernel(
-        const rqf_selective_inputs p, const float* __restrict__ z,
+        const rqf_selective_inputs pin, const float* __restrict__ z,
         const float* __restrict__ entries, int chunk, int nc, const float* __restrict__ gy,
         const float* __restrict__ gx, int truncated, BwdOut o) {
+  const rqf_selective_inputs p = with_options<O>(pin);
   constexpr int K = kBwdK, TILE = kWave * K;
   const int lane = lane_id();
-  const int64_t L = xcd_remap(blockIdx.x, gridDim.x) * kRowsPerBlock + (threadIdx.x >> 6);
+  const int64_t L = xcd_remap(blockIdx.x, gridDim.x) * kRowsPerBlock + wave_id();
   const RowId id = row_id(p, L);
   if (!id.valid) return;
   const Chan c = load_chan(p, id.f);
@@ -704,6 +818,8 @@ __global__ __launch_bounds__(kRowsPerBlock* kWave)
   r.dwr = o.dw ? o.dw + base : nullptr;
   r.ddr = o.ddc ? o.ddc + base : nullptr;
   r.sdd = nullptr;
+  r.swt = nullptr;
+  r.sws = nullptr;
   r.dcarry = mk(0.0f, 0.0f);
   r.Afirst = mk(0.0f, 0.0f);
   r.cfirst = 0.0f;
@@ -712,8 +828,8 @@ __global__ __launch_bounds__(kRowsPerBlock* kWave)
   const int ntiles = (r.T + TILE - 1) / TILE;
   const int full = VEC ? r.T / TILE : 0;
   int tile = ntiles - 1;
-  for (; tile >= full; --tile) bwd_tile<K, VEC, true>(p, c, r, tile * TILE, lane);
-  for (; tile >= 0; --tile) bwd_tile<K, VEC, false>(p, c, r, tile * TILE, lane);
+  for (; tile >= full; --tile) bwd_tile<K, VEC, true, false>(p, c, r, tile * TILE, lane);
+  for (; tile >= 0; --tile) bwd_tile<K, VEC, false, false>(p, c, r, tile * TILE, lane);
   const double sb = wave_sum(r.sum_bias);
   const double st = wave_sum(r.sum_theta);
   if (lane == 0) {
@@ -743,14 +859,24 @@ struct Teams {
   int slots;          // S: upper bound on the number of teams
 };
 
+// Group-sorted channel order and team table, built on the device from the
+// group indices (int64, as the reference's warp_groups buffer).  Groups are
+// staged in LDS; every pass is O(F) or O(F^2 / blockDim) LDS reads.
+constexpr int kBuildLds = 8192;  // channels whose groups fit the LDS stage
 __global__ __launch_bounds__(256) void team_build_kernel(const int64_t* __restrict__ groups,
                                                          int F, int G, int* order, int* first,
                                                          int* count, int* group, int* gteam,
                                                          int* nteams, int* gcount, int* moff) {
+  __shared__ int sg[kBuildLds];
   const int tid = threadIdx.x;
+  const bool staged = F <= kBuildLds;
+  if (staged)
+    for (int f = tid; f < F; f += blockDim.x) sg[f] = groups ? (int)groups[f] : 0;
+  __syncthreads();
+  auto grp = [&](int f) { return staged ? sg[f] : (groups ? (int)groups[f] : 0); };
   for (int g = tid; g < G; g += blockDim.x) {
     int n = 0;
-    for (int f = 0; f < F; ++f) n += groups ? (groups[f] == g) : 1;
+    for (int f = 0; f < F; ++f) n += grp(f) == g;
     gcount[g] = n;
   }
   __syncthreads();
@@ -767,9 +893,9 @@ __global__ __launch_bounds__(256) void team_build_kernel(const int64_t* __restri
   }
   __syncthreads();
   for (int f = tid; f < F; f += blockDim.x) {
-    const int g = groups ? (int)groups[f] : 0;
+    const int g = grp(f);
     int rank = 0;
-    for (int q = 0; q < f; ++q) rank += groups ? (groups[q] == g) : 1;
+    for (int q = 0; q < f; ++q) rank += grp(q) == g;
     order[moff[g] + rank] = f;
   }
   for (int g = tid; g < G; g += blockDim.x) {
@@ -783,17 +909,19 @@ __global__ __launch_bounds__(256) void team_build_kernel(const int64_t* __restri
   }
 }
 
-template <bool VEC>
+template <int O, bool VEC>
 __global__ __launch_bounds__(kTeam* kWave)
     __attribute__((amdgpu_waves_per_eu(RQF_BWD_WAVES_PER_EU))) void selective_bwd_team_kernel(
-        const rqf_selective_inputs p, const float* __restrict__ z,
+        const rqf_selective_inputs pin, const float* __restrict__ z,
         const float* __restrict__ entries, int chunk, int nc, const float* __restrict__ gy,
         const float* __restrict__ gx, int truncated, Teams tm, BwdOut o) {
+  const rqf_selective_inputs p = with_options<O>(pin);
   constexpr int K = kBwdK, TILE = kWave * K;
   static_assert(TILE == kTeam * kWave, "team reduction: one tile element per thread");
   __shared__ float4 s_dd[2][kTeam][kWave];
+  __shared__ float4 s_wt[2][kWave], s_ws[2][kWave];  // staged tanh(warp), exp(scale*tanh)
   const int lane = lane_id();
-  const int w = threadIdx.x >> 6;
+  const int w = wave_id();
   // Logical block -> (batch chunk, team slot, batch element), XCD-contiguous chunks.
   const int64_t bc = batch_chunk(p);
   const int64_t L = xcd_remap(blockIdx.x, gridDim.x);
@@ -825,6 +953,8 @@ __global__ __launch_bounds__(kTeam* kWave)
   r.dwr = o.dw ? o.dw + base : nullptr;
   r.ddr = nullptr;
   r.sdd = nullptr;
+  r.swt = nullptr;
+  r.sws = nullptr;
   r.dcarry = mk(0.0f, 0.0f);
   r.Afirst = mk(0.0f, 0.0f);
   r.cfirst = 0.0f;
@@ -833,16 +963,36 @@ __global__ __launch_bounds__(kTeam* kWave)
   float* ddp = p.has_warp ? o.dd_part + ((int64_t)slot * p.B + b) * r.T : nullptr;
   const int ntiles = (r.T + TILE - 1) / TILE;
   const int full = VEC ? r.T / TILE : 0;
+  // The team's channels share one warp-logit row: thread i stages step i of a
+  // tile (tanh and the frequency factor) into LDS for all four wavefronts.
+  // Tile n+1 (in walk order) is staged during tile n, before that tile's
+  // barrier, so one barrier per tile covers both LDS buffers.
+  const float* dwr = r.dr;
+  float* swt = reinterpret_cast<float*>(&s_wt[0][0]);
+  float* sws = reinterpret_cast<float*>(&s_ws[0][0]);
+  auto stage = [&](int buf, int ts) {
+    const int t = ts + (int)threadIdx.x;
+    const float wt = warp_tanh(p, t < r.T ? dwr[t] : 0.0f);
+    swt[buf * TILE + threadIdx.x] = wt;
+    sws[buf * TILE + threadIdx.x] = warp_factor(p, wt);
+  };
+  if (dwr) {
+    stage(0, (ntiles - 1) * TILE);
+    __syncthreads();
+  }
   int parity = 0;
   for (int tile = ntiles - 1; tile >= 0; --tile) {
     const int t0 = tile * TILE;
+    r.swt = swt + parity * TILE;
+    r.sws = sws + parity * TILE;
     if (ddp) r.sdd = &s_dd[parity][w][0];
     if (active) {
       if (tile >= full)
-        bwd_tile<K, VEC, true>(p, c, r, t0, lane);
+        bwd_tile<K, VEC, true, true>(p, c, r, t0, lane);
       else
-        bwd_tile<K, VEC, false>(p, c, r, t0, lane);
+        bwd_tile<K, VEC, false, true>(p, c, r, t0, lane);
     }
+    if (dwr && tile > 0) stage(parity ^ 1, t0 - TILE);
     if (ddp) {
       __syncthreads();
       const float* sd = reinterpret_cast<const float*>(&s_dd[parity][0][0]);
@@ -850,8 +1000,8 @@ __global__ __launch_bounds__(kTeam* kWave)
       for (int m = 0; m < members; ++m) acc += sd[m * TILE + threadIdx.x];
       const int t = t0 + threadIdx.x;
       if (t < r.T) ddp[t] = acc;
-      parity ^= 1;
     }
+    parity ^= 1;
   }
   if (active) {
     const double sb = wave_sum(r.sum_bias);
@@ -864,16 +1014,33 @@ __global__ __launch_bounds__(kTeam* kWave)
 }
 
 // dd[g, b, t] = sum over the teams of group g (fixed order) of dd_part[team, b, t].
+// VEC: N % 4 == 0 and 16-byte aligned dd; each thread sums one float4.
+template <bool VEC>
 __global__ __launch_bounds__(256) void team_reduce_kernel(const float* __restrict__ dd_part,
                                                           const int* __restrict__ gteam,
                                                           float* __restrict__ dd, int64_t G,
                                                           int64_t N) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= G * N) return;
-  const int64_t g = i / N, n = i - g * N;
-  float acc = 0.0f;
-  for (int s = gteam[g]; s < gteam[g + 1]; ++s) acc += dd_part[(int64_t)s * N + n];
-  dd[i] = acc;
+  if (VEC) {
+    const int64_t n4 = N / 4;
+    if (i >= G * n4) return;
+    const int64_t g = i / n4, n = (i - g * n4) * 4;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int s = gteam[g]; s < gteam[g + 1]; ++s) {
+      const float4 v = ld4(dd_part + (int64_t)s * N + n);
+      acc.x += v.x;
+      acc.y += v.y;
+      acc.z += v.z;
+      acc.w += v.w;
+    }
+    st4(dd + g * N + n, acc);
+  } else {
+    if (i >= G * N) return;
+    const int64_t g = i / N, n = i - g * N;
+    float acc = 0.0f;
+    for (int s = gteam[g]; s < gteam[g + 1]; ++s) acc += dd_part[(int64_t)s * N + n];
+    dd[i] = acc;
+  }
 }
 
 // dd[g, i] = sum over the channels f of group g (ascending f) of ddc[f, i];
@@ -910,20 +1077,26 @@ __global__ __launch_bounds__(256) void group_reduce_kernel(const float* __restri
   }
 }
 
-// dbias[f] = sum_b partial[f*B + b] (fp64, ascending b); same for dtheta.
-__global__ __launch_bounds__(256) void partial_reduce_kernel(const double* __restrict__ partial,
-                                                             float* __restrict__ dbias,
-                                                             float* __restrict__ dtheta,
-                                                             int64_t F, int64_t B) {
-  const int64_t f = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (f >= F) return;
+// dbias[f] = sum_b partial[f*B + b] in fp64, same for dtheta: one wavefront
+// per channel, lane l sums b = l, l+64, ... in order, then a fixed-shape wave
+// reduction (deterministic).
+__global__ __launch_bounds__(kWave) void partial_reduce_kernel(const double* __restrict__ partial,
+                                                               float* __restrict__ dbias,
+                                                               float* __restrict__ dtheta,
+                                                               int64_t F, int64_t B) {
+  const int64_t f = blockIdx.x;
+  const int lane = threadIdx.x;
   double sb = 0.0, st = 0.0;
-  for (int64_t b = 0; b < B; ++b) {
+  for (int64_t b = lane; b < B; b += kWave) {
     sb += partial[f * B + b];
     st += partial[F * B + f * B + b];
   }
-  dbias[f] = (float)sb;
-  dtheta[f] = (float)st;
+  sb = wave_sum(sb);
+  st = wave_sum(st);
+  if (lane == 0) {
+    dbias[f] = (float)sb;
+    dtheta[f] = (float)st;
+  }
 }
 
 // Zero-fill of n 32-bit words (graph-capture safe, unlike a memset node).
@@ -992,15 +1165,43 @@ dim3 row_grid(const rqf_selective_inputs* in) {
   return dim3((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
 }
 
+int options_of(const rqf_selective_inputs* in) {
+  const int o = (in->has_gamma ? kOptGamma : 0) | (in->log_shift ? kOptLogShift : 0) |
+                (in->has_warp ? kOptWarp : 0) | (in->bound_warp ? kOptBound : 0) |
+                (in->has_write ? kOptWrite : 0) | (in->write_sigmoid ? kOptWriteSigmoid : 0) |
+                (in->prospective ? kOptProspective : 0) |
+                (in->gamma_horizon ? kOptGammaHorizon : 0);
+  return normalise_options(o);
+}
+
+// Calls fn(std::integral_constant<int, O>) with O the compiled option set equal
+// to `opts`, or kOptRuntime when none is.
+template <class Fn>
+void with_option_set(int opts, Fn&& fn) {
+  static_assert(sizeof(kOptSets) / sizeof(kOptSets[0]) == 3, "one case per compiled set");
+#ifdef RQF_NO_SPECIALISE
+  opts = kOptRuntime;
+#endif
+  switch (opts) {
+    case kOptSets[0]: fn(std::integral_constant<int, kOptSets[0]>{}); return;
+    case kOptSets[1]: fn(std::integral_constant<int, kOptSets[1]>{}); return;
+    case kOptSets[2]: fn(std::integral_constant<int, kOptSets[2]>{}); return;
+    default: fn(std::integral_constant<int, kOptRuntime>{}); return;
+  }
+}
+
 void launch_fwd(const rqf_selective_inputs* in, const float* z, float* raw, float* act,
                 float* entries, int chunk, int nc, bool vec, hipStream_t s) {
   const dim3 grid = row_grid(in), block(kRowsPerBlock * kWave);
-  if (vec)
-    hipLaunchKernelGGL(selective_fwd_kernel<true>, grid, block, 0, s, *in, z, raw, act, entries,
-                       chunk, nc);
-  else
-    hipLaunchKernelGGL(selective_fwd_kernel<false>, grid, block, 0, s, *in, z, raw, act, entries,
-                       chunk, nc);
+  with_option_set(options_of(in), [&](auto oc) {
+    constexpr int O = decltype(oc)::value;
+    if (vec)
+      hipLaunchKernelGGL((selective_fwd_kernel<O, true>), grid, block, 0, s, *in, z, raw, act,
+                         entries, chunk, nc);
+    else
+      hipLaunchKernelGGL((selective_fwd_kernel<O, false>), grid, block, 0, s, *in, z, raw, act,
+                         entries, chunk, nc);
+  });
 }
 
 constexpr int kBwdTile = kWave * kBwdK;
@@ -1123,26 +1324,33 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
     o.dd_part = in->has_warp ? (float*)(ws + w.dd) : nullptr;
     const int64_t bc = (in->B + kXcds - 1) / kXcds;
     const dim3 grid((unsigned)(kXcds * w.slots * bc)), block(kTeam * kWave);
-    if (vec)
-      hipLaunchKernelGGL(selective_bwd_team_kernel<true>, grid, block, 0, s, *in, z, ent,
-                         ent_chunk, nc, gy, gx, (int)truncated, tm, o);
-    else
-      hipLaunchKernelGGL(selective_bwd_team_kernel<false>, grid, block, 0, s, *in, z, ent,
-                         ent_chunk, nc, gy, gx, (int)truncated, tm, o);
+    with_option_set(options_of(in), [&](auto oc) {
+      constexpr int O = decltype(oc)::value;
+      if (vec)
+        hipLaunchKernelGGL((selective_bwd_team_kernel<O, true>), grid, block, 0, s, *in, z, ent,
+                           ent_chunk, nc, gy, gx, (int)truncated, tm, o);
+      else
+        hipLaunchKernelGGL((selective_bwd_team_kernel<O, false>), grid, block, 0, s, *in, z, ent,
+                           ent_chunk, nc, gy, gx, (int)truncated, tm, o);
+    });
     if (in->has_warp) {
       const int64_t N = in->B * T;
-      hipLaunchKernelGGL(team_reduce_kernel, dim3((unsigned)((in->G * N + 255) / 256)), dim3(256),
-                         0, s, o.dd_part, gteam, dd, in->G, N);
+      if (N % 4 == 0 && aligned16(dd))
+        hipLaunchKernelGGL(team_reduce_kernel<true>, dim3((unsigned)((in->G * N / 4 + 255) / 256)),
+                           dim3(256), 0, s, o.dd_part, gteam, dd, in->G, N);
+      else
+        hipLaunchKernelGGL(team_reduce_kernel<false>, dim3((unsigned)((in->G * N + 255) / 256)),
+                           dim3(256), 0, s, o.dd_part, gteam, dd, in->G, N);
     }
 #else
     o.ddc = in->has_warp ? (float*)(ws + w.dd) : nullptr;
     const dim3 grid = row_grid(in), block(kRowsPerBlock * kWave);
     if (vec)
-      hipLaunchKernelGGL(selective_bwd_kernel<true>, grid, block, 0, s, *in, z, ent, ent_chunk, nc,
-                         gy, gx, (int)truncated, o);
+      hipLaunchKernelGGL((selective_bwd_kernel<kOptRuntime, true>), grid, block, 0, s, *in, z, ent,
+                         ent_chunk, nc, gy, gx, (int)truncated, o);
     else
-      hipLaunchKernelGGL(selective_bwd_kernel<false>, grid, block, 0, s, *in, z, ent, ent_chunk,
-                         nc, gy, gx, (int)truncated, o);
+      hipLaunchKernelGGL((selective_bwd_kernel<kOptRuntime, false>), grid, block, 0, s, *in, z,
+                         ent, ent_chunk, nc, gy, gx, (int)truncated, o);
     if (in->has_warp) {
       const int64_t N = in->B * T;
       hipLaunchKernelGGL(group_reduce_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, s,
@@ -1154,8 +1362,8 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
     if (in->has_warp && dd) zero_words(dd, in->G * in->B * T, s);
   }
   if (in->F > 0)
-    hipLaunchKernelGGL(partial_reduce_kernel, dim3((unsigned)((in->F + 255) / 256)), dim3(256), 0,
-                       s, partial, dbias, dtheta, in->F, in->B);
+    hipLaunchKernelGGL(partial_reduce_kernel, dim3((unsigned)in->F), dim3(kWave), 0, s, partial,
+                       dbias, dtheta, in->F, in->B);
   return launch_status();
 }
 

@@ -91,7 +91,7 @@ __global__ __launch_bounds__(kTiWaves* kWave) void fbt_fwd_kernel(
     const float* __restrict__ z, float* __restrict__ raw, float* __restrict__ act,
     float* __restrict__ carry, int64_t F, int64_t B, int64_t T, int64_t nc) {
   const int lane = lane_id();
-  const int64_t row = (int64_t)blockIdx.x * kTiWaves + (threadIdx.x >> 6);
+  const int64_t row = (int64_t)blockIdx.x * kTiWaves + wave_id();
   if (row >= F * B) return;
   const int64_t f = row / B;
   const c32 a = ldc(c1, f), k0 = ldc(tap0, f), k1 = ldc(tap1, f);
@@ -147,7 +147,7 @@ __global__ __launch_bounds__(kTiWaves* kWave) void fbt_bwd_kernel(
     const float* __restrict__ gout, int mask, float* __restrict__ gz,
     double* __restrict__ partial, int64_t F, int64_t B, int64_t T, int64_t nc) {
   const int lane = lane_id();
-  const int64_t row = (int64_t)blockIdx.x * kTiWaves + (threadIdx.x >> 6);
+  const int64_t row = (int64_t)blockIdx.x * kTiWaves + wave_id();
   if (row >= F * B) return;
   const int64_t f = row / B;
   const c32 a = ldc(c1, f), k0 = ldc(tap0, f), k1 = ldc(tap1, f);

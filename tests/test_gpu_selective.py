@@ -51,7 +51,8 @@ def run_case(F, B, T, case, *, prospective=True, truncated=False, activate=True,
     zt = torch.as_tensor(z.astype(np.complex64), device="cuda")
     dev = lambda a: None if a is None else torch.as_tensor(a.astype(np.complex64), device="cuda")  # noqa: E731
     raw, act, entries = selective_forward(zt, ti, activate, write_raw, chunk)
-    out = selective_backward(zt, ti, entries, dev(gy), dev(gx), activate, truncated, chunk)
+    outs = {"bwd": selective_backward(zt, ti, entries, dev(gy), dev(gx), activate, truncated,
+                                      chunk)}
     raw_o, act_o = oracle.selective_fwd(z, inp)
     ref = oracle.selective_bwd(z, inp, gy, gx, truncated=truncated)
     errs = {}
@@ -69,11 +70,12 @@ def run_case(F, B, T, case, *, prospective=True, truncated=False, activate=True,
     for j in range(1, nc):
         ent_ref[:, j] = rr[:, j * chunk - 1]
     errs["entries"] = relerr(entries, ent_ref)
-    for name, got, want in zip(("dz", "dzw", "dg", "dd", "dw", "dbias", "dtheta"), out, ref):
-        if want is None:
-            assert got is None, name
-        else:
-            errs[name] = relerr(got, want)
+    for tag, out in outs.items():
+        for name, got, want in zip(("dz", "dzw", "dg", "dd", "dw", "dbias", "dtheta"), out, ref):
+            if want is None:
+                assert got is None, name
+            else:
+                errs[f"{tag}.{name}"] = relerr(got, want)
     bad = {k: v for k, v in errs.items() if not v <= PARITY_RTOL}
     assert not bad, bad
     return errs
@@ -174,6 +176,25 @@ def test_numerical_edges(kind, truncated):
     run_case(5, 2, 33, case if kind != "conj" else CASE_LOG, truncated=truncated,
              eta=1000.0 / 0.05 if kind == "collapse" else 0.2, edit=edit,
              conj_cot=kind == "conj", seed=12)
+
+
+@pytest.mark.parametrize("truncated", [False, True])
+def test_irrelevant_option_bits(truncated):
+    """Option bits that the reference only reads under another flag (log link
+    without a gamma head, band bound without a warp head, sigmoid link without
+    a write head, gamma horizon without the prospective tap) change nothing."""
+    print(f"case: irrelevant option bits truncated={truncated}", flush=True)
+    case = dict(gamma=False, write=False, warp="none", log_shift=False, write_sigmoid=True)
+
+    def edit(inp, z):
+        o = list(inp.options)
+        o[3], o[7], o[8], o[11] = True, True, True, True
+        inp.options = tuple(o)
+        # a band the base frequencies violate: a wrong clamp would show
+        inp.theta_minimum[:] = 0.5
+        inp.theta_maximum[:] = 0.6
+
+    run_case(5, 3, 70, case, prospective=False, truncated=truncated, edit=edit, seed=14)
 
 
 def test_long_rows_subset_of_north_star_shape():

@@ -585,6 +585,7 @@ def main():
                               for k, v in per_op.items()},
             "step_frac_of_hbm": round(all_bytes / (scan_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "alg_bytes_step": all_bytes,
+            "alg_bytes_entries": plan.bytes,
         },
     }
     if args.cpu:

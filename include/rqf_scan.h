@@ -144,12 +144,18 @@ typedef struct rqf_selective_inputs {
   const float *write_logits; /* (F,B,T) f32, or NULL */
   const float *bias, *theta, *minimum, *span, *step, *horizon, *theta_minimum,
       *theta_maximum;        /* (F,) f32 */
-  const int64_t *groups;     /* (F,) warp group of each channel, or NULL */
+  const int64_t *groups;     /* (F,) warp group of each channel, each in [0, G), or NULL */
   int32_t has_gamma, has_warp, has_write, log_shift;
   float gamma_scale, warp_scale;
   int32_t prospective, gamma_horizon, write_sigmoid;
   float write_max, write_bias;
   int32_t bound_warp;
+  /* Optional (F,) order in which the forward visits the channels, a
+   * permutation of 0..F-1 that keeps each warp group's channels adjacent
+   * (e.g. a stable argsort of `groups`), so a group's warp-logit rows are
+   * shared in L2 while its channels stream.  NULL visits 0..F-1.  No
+   * reference counterpart: it only changes the schedule, not the results. */
+  const int32_t *order;
 } rqf_selective_inputs;
 
 /* Replaces `_forward[(f*b,)](...)` in `selective_forward`

@@ -37,6 +37,7 @@ class SelectiveInputsStruct(ctypes.Structure):
         ("prospective", _I32), ("gamma_horizon", _I32), ("write_sigmoid", _I32),
         ("write_max", ctypes.c_float), ("write_bias", ctypes.c_float),
         ("bound_warp", _I32),
+        ("order", _P),
     ]
 
 

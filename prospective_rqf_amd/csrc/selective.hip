@@ -328,7 +328,9 @@ __device__ __forceinline__ c32 relu2(c32 v) { return mk(fmaxf(v.r, 0.0f), fmaxf(
 // Inside a chunk rows go channel-major, batch-minor: the bc rows of one
 // channel are adjacent in memory, so the rows a chunk streams concurrently
 // cover few address ranges, and all channels of a batch element stay on one
-// XCD (its L2 keeps the chunk's warp logits).  Logical rows past B are idle.
+// XCD.  Channels are visited in the optional `order` permutation, which keeps
+// a warp group's channels adjacent, so the group's warp-logit rows stay in the
+// XCD's L2 while its channels stream.  Logical rows past B are idle.
 struct RowId {
   int64_t f, b, row;
   bool valid;
@@ -340,8 +342,9 @@ __device__ __forceinline__ RowId row_id(const rqf_selective_inputs& p, int64_t L
   RowId r;
   const int64_t bc = batch_chunk(p), per = p.F * bc;
   const int64_t c = L / per, rem = L - c * per;
-  r.f = rem / bc;
-  r.b = c * bc + (rem - r.f * bc);
+  const int64_t pos = rem / bc;  // channel position in the visiting order
+  r.b = c * bc + (rem - pos * bc);
+  r.f = p.order ? (int64_t)p.order[pos] : pos;  // group-contiguous channel order
   r.valid = c < kXcds && r.b < p.B;
   r.row = r.f * p.B + r.b;
   return r;
@@ -860,21 +863,59 @@ struct Teams {
 };
 
 // Group-sorted channel order and team table, built on the device from the
-// group indices (int64, as the reference's warp_groups buffer).  Groups are
-// staged in LDS; every pass is O(F) or O(F^2 / blockDim) LDS reads.
-constexpr int kBuildLds = 8192;  // channels whose groups fit the LDS stage
+// group indices (int64, as the reference's warp_groups buffer).  Groups,
+// per-group counts and offsets are staged in LDS (F <= kBuildLds and
+// G <= kBuildGroups, else a slower pass over global memory).
+constexpr int kBuildLds = 4096;
+constexpr int kBuildGroups = 1024;
 __global__ __launch_bounds__(256) void team_build_kernel(const int64_t* __restrict__ groups,
                                                          int F, int G, int* order, int* first,
                                                          int* count, int* group, int* gteam,
                                                          int* nteams, int* gcount, int* moff) {
   __shared__ int sg[kBuildLds];
-  const int tid = threadIdx.x;
-  const bool staged = F <= kBuildLds;
-  if (staged)
-    for (int f = tid; f < F; f += blockDim.x) sg[f] = groups ? (int)groups[f] : 0;
-  __syncthreads();
-  auto grp = [&](int f) { return staged ? sg[f] : (groups ? (int)groups[f] : 0); };
-  for (int g = tid; g < G; g += blockDim.x) {
+  __shared__ int s_count[kBuildGroups], s_moff[kBuildGroups], s_gteam[kBuildGroups + 1];
+  const int tid = threadIdx.x, nt = blockDim.x;
+  if (F <= kBuildLds && G <= kBuildGroups) {
+    for (int f = tid; f < F; f += nt) sg[f] = groups ? (int)groups[f] : 0;
+    for (int g = tid; g < G; g += nt) s_count[g] = 0;
+    __syncthreads();
+    for (int f = tid; f < F; f += nt)
+      if ((unsigned)sg[f] < (unsigned)G) atomicAdd(&s_count[sg[f]], 1);
+    __syncthreads();
+    if (tid == 0) {
+      int off = 0, toff = 0;
+      for (int g = 0; g < G; ++g) {
+        s_moff[g] = off;
+        s_gteam[g] = toff;
+        off += s_count[g];
+        toff += (s_count[g] + kTeam - 1) / kTeam;
+      }
+      s_gteam[G] = toff;
+      *nteams = toff;
+    }
+    __syncthreads();
+    for (int f = tid; f < F; f += nt) {
+      const int g = sg[f];
+      int rank = 0;
+      for (int q = 0; q < f; ++q) rank += sg[q] == g;
+      order[s_moff[g] + rank] = f;
+    }
+    for (int g = tid; g <= G; g += nt) gteam[g] = s_gteam[g];
+    for (int g = tid; g < G; g += nt) {
+      const int n = s_count[g], ntm = (n + kTeam - 1) / kTeam;
+      gcount[g] = n;
+      moff[g] = s_moff[g];
+      for (int t = 0; t < ntm; ++t) {
+        const int id = s_gteam[g] + t;
+        first[id] = s_moff[g] + t * kTeam;
+        count[id] = min(kTeam, n - t * kTeam);
+        group[id] = g;
+      }
+    }
+    return;
+  }
+  auto grp = [&](int f) { return groups ? (int)groups[f] : 0; };
+  for (int g = tid; g < G; g += nt) {
     int n = 0;
     for (int f = 0; f < F; ++f) n += grp(f) == g;
     gcount[g] = n;
@@ -892,15 +933,15 @@ __global__ __launch_bounds__(256) void team_build_kernel(const int64_t* __restri
     *nteams = toff;
   }
   __syncthreads();
-  for (int f = tid; f < F; f += blockDim.x) {
+  for (int f = tid; f < F; f += nt) {
     const int g = grp(f);
     int rank = 0;
     for (int q = 0; q < f; ++q) rank += grp(q) == g;
     order[moff[g] + rank] = f;
   }
-  for (int g = tid; g < G; g += blockDim.x) {
-    const int n = gcount[g], nt = (n + kTeam - 1) / kTeam;
-    for (int t = 0; t < nt; ++t) {
+  for (int g = tid; g < G; g += nt) {
+    const int n = gcount[g], ntm = (n + kTeam - 1) / kTeam;
+    for (int t = 0; t < ntm; ++t) {
       const int id = gteam[g] + t;
       first[id] = moff[g] + t * kTeam;
       count[id] = min(kTeam, n - t * kTeam);

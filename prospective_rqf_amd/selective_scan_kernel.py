@@ -27,17 +27,22 @@ def _real_ptr(t: torch.Tensor | None):
 _VALID_GROUPS: dict = {}
 
 
-def _check_groups(groups: torch.Tensor, n_groups: int) -> None:
+def _check_groups(groups: torch.Tensor, n_groups: int) -> torch.Tensor:
     """Warp-group indices must address rows of warp_logits (the kernel reads
-    warp_logits[groups[f]]).  Checked once per tensor version."""
-    key = (groups.data_ptr(), groups._version, groups.numel(), n_groups)
-    if _VALID_GROUPS.get(key):
-        return
+    warp_logits[groups[f]]).  Checked once per tensor version; returns the
+    channel visiting order (stable argsort of the groups, int32) that keeps
+    each group's channels adjacent."""
+    key = (groups.data_ptr(), groups._version, groups.numel(), n_groups, groups.device)
+    order = _VALID_GROUPS.get(key)
+    if order is not None:
+        return order
     if groups.numel() and (int(groups.min()) < 0 or int(groups.max()) >= n_groups):
         raise ValueError(f"groups must index the {n_groups} warp-logit rows")
     if len(_VALID_GROUPS) > 64:
         _VALID_GROUPS.clear()
-    _VALID_GROUPS[key] = True
+    order = torch.argsort(groups, stable=True).to(torch.int32).contiguous()
+    _VALID_GROUPS[key] = order
+    return order
 
 
 def inputs_struct(z: torch.Tensor, inputs) -> tuple[_lib.SelectiveInputsStruct, list]:
@@ -59,13 +64,14 @@ def inputs_struct(z: torch.Tensor, inputs) -> tuple[_lib.SelectiveInputsStruct, 
         if v is not None and tuple(v.shape) != (rows, b, t):
             raise ValueError(f"{name} must have shape {(rows, b, t)}, got {tuple(v.shape)}")
     g = 0
+    order = None
     if dl is not None:
         if dl.dim() != 3 or tuple(dl.shape[1:]) != (b, t):
             raise ValueError(f"warp_logits must have shape (G, {b}, {t}), got {tuple(dl.shape)}")
         g = dl.shape[0]
         if groups is None or groups.shape != (f,):
             raise ValueError("groups must be a (F,) index tensor when the warp head is on")
-        _check_groups(groups, g)
+        order = _check_groups(groups, g)
     for name, v in zip(("bias", "theta", "minimum", "span", "step", "horizon",
                         "theta_minimum", "theta_maximum"), params):
         if v.shape != (f,):
@@ -80,8 +86,9 @@ def inputs_struct(z: torch.Tensor, inputs) -> tuple[_lib.SelectiveInputsStruct, 
         int(bool(o[6])), int(bool(o[7])), int(bool(o[8])),
         float(o[9]), float(o[10]),
         int(bool(o[11])),
+        None if order is None else order.data_ptr(),
     )
-    return s, [gl, dl, wl, groups, *params]
+    return s, [gl, dl, wl, groups, order, *params]
 
 
 def selective_forward(z, inputs, activate, write_raw, chunk):

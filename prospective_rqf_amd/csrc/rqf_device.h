@@ -83,6 +83,14 @@ __device__ __forceinline__ float dpp(float src, float fill) {
                                                     CTRL, ROW_MASK, 0xf, false));
 }
 
+// DPP move with zero fill: a lane whose source lane is out of its row
+// receives 0 (bound_ctrl); every row and bank is written, so no fill value
+// has to be staged in the destination first.
+template <int CTRL>
+__device__ __forceinline__ float dpp0(float src) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(src), CTRL, 0xf, 0xf, true));
+}
+
 // GFX9 DPP controls.
 constexpr int kRowShl1 = 0x101, kRowShl2 = 0x102, kRowShl4 = 0x104, kRowShl8 = 0x108;
 constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
@@ -116,8 +124,13 @@ __device__ __forceinline__ c32 shift_down(c32 v, c32 fill, int lane) {
 // The map received from an earlier lane is applied first.
 template <int CTRL, int ROW_MASK = 0xf>
 __device__ __forceinline__ void fwd_step(c32& P, c32& s) {
-  const c32 lp = mk(dpp<CTRL, ROW_MASK>(P.r, 1.0f), dpp<CTRL, ROW_MASK>(P.i, 0.0f));
-  const c32 ls = mk(dpp<CTRL, ROW_MASK>(s.r, 0.0f), dpp<CTRL, ROW_MASK>(s.i, 0.0f));
+  // Identity (P, s) = (1, 0) for lanes without a source: the zero parts via
+  // bound_ctrl where every row takes part, staged fills where rows are masked.
+  constexpr bool all_rows = ROW_MASK == 0xf;
+  const c32 lp = mk(dpp<CTRL, ROW_MASK>(P.r, 1.0f),
+                    all_rows ? dpp0<CTRL>(P.i) : dpp<CTRL, ROW_MASK>(P.i, 0.0f));
+  const c32 ls = mk(all_rows ? dpp0<CTRL>(s.r) : dpp<CTRL, ROW_MASK>(s.r, 0.0f),
+                    all_rows ? dpp0<CTRL>(s.i) : dpp<CTRL, ROW_MASK>(s.i, 0.0f));
   s = cmad(ls, P, s);
   P = cmul(lp, P);
 }
@@ -137,8 +150,8 @@ __device__ __forceinline__ void wave_scan_fwd(c32& P, c32& s) {
 // from a later lane is applied first (it is closer to the end of time).
 template <int CTRL>
 __device__ __forceinline__ void rev_step(c32& Q, c32& r) {
-  const c32 lq = mk(dpp<CTRL>(Q.r, 1.0f), dpp<CTRL>(Q.i, 0.0f));
-  const c32 lr = mk(dpp<CTRL>(r.r, 0.0f), dpp<CTRL>(r.i, 0.0f));
+  const c32 lq = mk(dpp<CTRL>(Q.r, 1.0f), dpp0<CTRL>(Q.i));
+  const c32 lr = mk(dpp0<CTRL>(r.r), dpp0<CTRL>(r.i));
   r = cmad(Q, lr, r);
   Q = cmul(Q, lq);
 }

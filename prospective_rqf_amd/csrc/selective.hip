@@ -209,8 +209,7 @@ __device__ __forceinline__ float ratio_gamma(const rqf_selective_inputs& p, cons
 // bp z + bn zp = gamma*eta*phi*z + ratio*gamma*A*(z - zp).
 __device__ __forceinline__ void step_coef(const rqf_selective_inputs& p, const Chan& c,
                                           const Ctl& q, c32 zk, c32 zp, c32& A, c32& phi,
-                                          c32& u) {
-  float inv_den;
+                                          c32& u, float& inv_den) {
   zoh(-q.gamma * c.eta, (1.0f - q.gamma) * clamp_theta(p, c, q.theta_u) * c.eta, A, phi,
       inv_den);
   c32 drive = cscale(q.gamma * c.eta, cmul(phi, zk));
@@ -397,7 +396,8 @@ __device__ __forceinline__ void fwd_compute(const rqf_selective_inputs& p, const
   for (int k = 0; k < K; ++k) {
     const Ctl q = controller(p, c, gv[k], dv[k], wv[k]);
     c32 phi;
-    step_coef(p, c, q, zv[k], k ? zv[k - 1] : zp0, A[k], phi, u[k]);
+    float inv_den;
+    step_coef(p, c, q, zv[k], k ? zv[k - 1] : zp0, A[k], phi, u[k], inv_den);
     if (TAIL && tb + k >= T) {
       A[k] = mk(1.0f, 0.0f);
       u[k] = mk(0.0f, 0.0f);
@@ -544,11 +544,14 @@ struct BwdRow {
 // Warp values of the lane's K steps from the team's LDS stage (SHARED).
 template <int K>
 __device__ __forceinline__ void lds_warp(const BwdRow& r, int lane, float (&wt)[K], float (&ws)[K]) {
-  static_assert(K == 4, "one float4 of staged warp values per lane");
-  const float4 a = reinterpret_cast<const float4*>(r.swt)[lane];
-  const float4 b = reinterpret_cast<const float4*>(r.sws)[lane];
-  wt[0] = a.x, wt[1] = a.y, wt[2] = a.z, wt[3] = a.w;
-  ws[0] = b.x, ws[1] = b.y, ws[2] = b.z, ws[3] = b.w;
+  static_assert(K % 4 == 0, "whole float4s of staged warp values per lane");
+#pragma unroll
+  for (int j = 0; j < K / 4; ++j) {
+    const float4 a = reinterpret_cast<const float4*>(r.swt)[lane * (K / 4) + j];
+    const float4 b = reinterpret_cast<const float4*>(r.sws)[lane * (K / 4) + j];
+    wt[4 * j] = a.x, wt[4 * j + 1] = a.y, wt[4 * j + 2] = a.z, wt[4 * j + 3] = a.w;
+    ws[4 * j] = b.x, ws[4 * j + 1] = b.y, ws[4 * j + 2] = b.z, ws[4 * j + 3] = b.w;
+  }
 }
 
 // SHARED: tanh(warp logit) and exp(warp_scale * tanh) of the tile come from
@@ -570,14 +573,14 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
   // Coefficients; kept per step: A, phi, gamma, gate and (unless SHARED)
   // theta_u and tanh(warp logit).
   c32 A[K], phi[K], u[K];
-  float gam[K], thu[K], gate[K], wtk[K];
+  float gam[K], thu[K], gate[K], wtk[K], ivd[K];  // ivd: 1/|a|^2 from the ZOH
   float swt[K], sws[K];
   if (SHARED) lds_warp<K>(r, lane, swt, sws);
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const Ctl q = SHARED ? controller_w(p, c, gv[k], swt[k], sws[k], wv[k])
                          : controller(p, c, gv[k], dv[k], wv[k]);
-    step_coef(p, c, q, zv[k], k ? zv[k - 1] : zp0, A[k], phi[k], u[k]);
+    step_coef(p, c, q, zv[k], k ? zv[k - 1] : zp0, A[k], phi[k], u[k], ivd[k]);
     gam[k] = q.gamma;
     gate[k] = q.gate;
     if (!SHARED) {
@@ -732,7 +735,8 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
         fp = cmadr(a, sr, 0.5f);
       }
     } else {
-      fp = cscale(frcp(den), cmul(csub(A[k], phi[k]), conjg(a)));
+      // 1/|a|^2 as the ZOH formed it (same a, so the same value)
+      fp = cscale(ivd[k], cmul(csub(A[k], phi[k]), conjg(a)));
     }
     // da = conj(A) dA + conj(phi') dphi with dphi = gt*gh*cz; then through
     // a = (-gamma*eta, (1 - gamma)*theta*eta).
@@ -785,8 +789,11 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
   if (r.dwr) store_f<K, VEC, TAIL>(r.dwr, tb, T, gw);
   if (r.ddr) store_f<K, VEC, TAIL>(r.ddr, tb, T, gd);
   if (r.sdd) {
-    static_assert(K == 4, "one float4 of warp gradient per lane");
-    r.sdd[lane] = make_float4(gd[0], gd[1], gd[2], gd[3]);
+    static_assert(K % 4 == 0, "whole float4s of warp gradient per lane");
+#pragma unroll
+    for (int j = 0; j < K / 4; ++j)
+      r.sdd[lane * (K / 4) + j] =
+          make_float4(gd[4 * j], gd[4 * j + 1], gd[4 * j + 2], gd[4 * j + 3]);
   }
 }
 
@@ -957,10 +964,11 @@ __global__ __launch_bounds__(kTeam* kWave)
         const float* __restrict__ entries, int chunk, int nc, const float* __restrict__ gy,
         const float* __restrict__ gx, int truncated, Teams tm, BwdOut o) {
   const rqf_selective_inputs p = with_options<O>(pin);
-  constexpr int K = kBwdK, TILE = kWave * K;
-  static_assert(TILE == kTeam * kWave, "team reduction: one tile element per thread");
-  __shared__ float4 s_dd[2][kTeam][kWave];
-  __shared__ float4 s_wt[2][kWave], s_ws[2][kWave];  // staged tanh(warp), exp(scale*tanh)
+  constexpr int K = kBwdK, TILE = kWave * K, NT = kTeam * kWave;
+  static_assert(TILE % NT == 0, "team staging and reduction: whole tile elements per thread");
+  constexpr int PER = TILE / NT;  // tile elements per thread in the staging and the reduction
+  __shared__ float4 s_dd[2][kTeam][TILE / 4];
+  __shared__ float4 s_wt[2][TILE / 4], s_ws[2][TILE / 4];  // staged tanh(warp), exp(scale*tanh)
   const int lane = lane_id();
   const int w = wave_id();
   // Logical block -> (batch chunk, team slot, batch element), XCD-contiguous chunks.
@@ -1012,10 +1020,13 @@ __global__ __launch_bounds__(kTeam* kWave)
   float* swt = reinterpret_cast<float*>(&s_wt[0][0]);
   float* sws = reinterpret_cast<float*>(&s_ws[0][0]);
   auto stage = [&](int buf, int ts) {
-    const int t = ts + (int)threadIdx.x;
-    const float wt = warp_tanh(p, t < r.T ? dwr[t] : 0.0f);
-    swt[buf * TILE + threadIdx.x] = wt;
-    sws[buf * TILE + threadIdx.x] = warp_factor(p, wt);
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int i = q * NT + (int)threadIdx.x, t = ts + i;
+      const float wt = warp_tanh(p, t < r.T ? dwr[t] : 0.0f);
+      swt[buf * TILE + i] = wt;
+      sws[buf * TILE + i] = warp_factor(p, wt);
+    }
   };
   if (dwr) {
     stage(0, (ntiles - 1) * TILE);
@@ -1037,10 +1048,14 @@ __global__ __launch_bounds__(kTeam* kWave)
     if (ddp) {
       __syncthreads();
       const float* sd = reinterpret_cast<const float*>(&s_dd[parity][0][0]);
-      float acc = 0.0f;
-      for (int m = 0; m < members; ++m) acc += sd[m * TILE + threadIdx.x];
-      const int t = t0 + threadIdx.x;
-      if (t < r.T) ddp[t] = acc;
+#pragma unroll
+      for (int q = 0; q < PER; ++q) {
+        const int i = q * NT + (int)threadIdx.x;
+        float acc = 0.0f;
+        for (int m = 0; m < members; ++m) acc += sd[m * TILE + i];
+        const int t = t0 + i;
+        if (t < r.T) ddp[t] = acc;
+      }
     }
     parity ^= 1;
   }

@@ -5,8 +5,8 @@
 // Two families:
 //
 // FBT (channel-outermost, rows contiguous in time): one wavefront per
-// (channel, batch) row, tiles of 64*8 steps, lane l holding 8 consecutive
-// steps (four float4 loads).  Tile = lane-serial composition -> DPP wave scan
+// (channel, batch) row, tiles of 64*K steps (K = 4), lane l holding K
+// consecutive steps (float4 loads).  Tile = lane-serial composition -> DPP wave scan
 // -> lane-serial replay, as in the selective kernels.  The backward runs the
 // adjoint g[t] = e[t] + conj(c1) g[t+1] the same way in suffix order and
 // keeps raw[t-1] and g[t+1] in registers, so it needs none of the
@@ -28,7 +28,19 @@ using namespace rqf;
 
 namespace {
 
-constexpr int kTiK = 8;
+// Loads of the next tile are issued before the current tile's scan.
+#ifndef RQF_TI_PREFETCH
+#define RQF_TI_PREFETCH 1
+#endif
+
+// Steps per lane.  4 (a 32-byte stretch per lane, 2 KB per wavefront load)
+// streams faster than 8 (64 bytes per lane) on gfx950: wider per-lane
+// stretches make each load instruction's footprint sparser.
+#ifndef RQF_TI_K
+#define RQF_TI_K 4
+#endif
+
+constexpr int kTiK = RQF_TI_K;
 constexpr int kTiTile = kWave * kTiK;
 constexpr int kTiWaves = 4;
 
@@ -42,8 +54,8 @@ __device__ __forceinline__ c32 mask_by(c32 g, c32 raw) {
   return mk(raw.r > 0.0f ? g.r : 0.0f, raw.i > 0.0f ? g.i : 0.0f);
 }
 
-// VEC: T even and 16-byte aligned rows: a lane's 8 steps are all in or all out
-// of range when T % 8 == 0; otherwise the tail uses guarded scalar access.
+// VEC: T even and 16-byte aligned rows: a lane's K steps are all in or all out
+// of range when T % K == 0; otherwise the tail uses guarded scalar access.
 template <bool VEC>
 __device__ __forceinline__ void load8(const float* __restrict__ row, int64_t tb, int64_t T,
                                       c32 (&v)[kTiK]) {
@@ -100,11 +112,22 @@ __global__ __launch_bounds__(kTiWaves* kWave) void fbt_fwd_kernel(
   float* rawr = raw ? raw + 2 * row * T : nullptr;
   float* actr = act ? act + 2 * row * T : nullptr;
   c32 y = mk(0.0f, 0.0f), zlast = mk(0.0f, 0.0f);
+#if RQF_TI_PREFETCH
+  // The next tile's drive is loaded before this tile's scan (software pipeline).
+  c32 znext[kTiK];
+  load8<VEC>(zr, lane * kTiK, T, znext);
+#endif
   for (int64_t t0 = 0, tile = 0; t0 < T; t0 += kTiTile, ++tile) {
     if (carry && lane == 0) stc(carry, row * nc + tile, y);
     const int64_t tb = t0 + lane * kTiK;
     c32 zv[kTiK];
+#if RQF_TI_PREFETCH
+#pragma unroll
+    for (int k = 0; k < kTiK; ++k) zv[k] = znext[k];
+    if (t0 + kTiTile < T) load8<VEC>(zr, tb + kTiTile, T, znext);
+#else
     load8<VEC>(zr, tb, T, zv);
+#endif
     const c32 zp0 = shift_up(zv[kTiK - 1], zlast, lane);
     c32 u[kTiK];
 #pragma unroll
@@ -160,13 +183,32 @@ __global__ __launch_bounds__(kTiWaves* kWave) void fbt_bwd_kernel(
   c32 gcarry = mk(0.0f, 0.0f);
   double s1r = 0, s1i = 0, s0r = 0, s0i = 0, s2r = 0, s2i = 0;
   const int64_t ntiles = (T + kTiTile - 1) / kTiTile;
+#if RQF_TI_PREFETCH
+  // The previous tile's (in walk order: next) drive and cotangent are loaded
+  // before this tile's scans (software pipeline).
+  c32 znext[kTiK], enext[kTiK];
+  load8<VEC>(zr, (ntiles - 1) * kTiTile + lane * kTiK, T, znext);
+  load8<VEC>(gr, (ntiles - 1) * kTiTile + lane * kTiK, T, enext);
+#endif
   for (int64_t tile = ntiles - 1; tile >= 0; --tile) {
     const int64_t t0 = tile * kTiTile;
     const int64_t tb = t0 + lane * kTiK;
     const int cnt = (int)min<int64_t>(max<int64_t>(T - tb, 0), kTiK);
     c32 zv[kTiK], yv[kTiK], ev[kTiK];
+#if RQF_TI_PREFETCH
+#pragma unroll
+    for (int k = 0; k < kTiK; ++k) {
+      zv[k] = znext[k];
+      ev[k] = enext[k];
+    }
+    if (tile > 0) {
+      load8<VEC>(zr, tb - kTiTile, T, znext);
+      load8<VEC>(gr, tb - kTiTile, T, enext);
+    }
+#else
     load8<VEC>(zr, tb, T, zv);
     load8<VEC>(gr, tb, T, ev);
+#endif
     const c32 zprev_tile = t0 > 0 ? ldc(zr, t0 - 1) : mk(0.0f, 0.0f);
     const c32 zp0 = shift_up(zv[kTiK - 1], zprev_tile, lane);
     c32 yp0;

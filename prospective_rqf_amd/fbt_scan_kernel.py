@@ -6,7 +6,7 @@ Mirrors rqf_models/ops/fbt_scan_kernel.py: ``_FBTProspectiveScan`` /
 HIP kernels ``rqf_fbt_*``.
 
 The recompute variant stores only the split-ReLU output plus the state that
-enters every tile of 512 steps, and replays the tile in the backward; its
+enters every tile of 256 steps, and replays the tile in the backward; its
 carry granularity is internal to the autograd context.
 """
 

@@ -53,7 +53,7 @@ def test_library_loads_and_reports_version(built_lib):
     assert b"gfx950" in lib.rqf_version()
     assert lib.rqf_error_string(-2) == b"workspace missing or too small"
     # Pure host-side queries (no device access).
-    assert lib.rqf_fbt_carry_chunks(16000) == 32
+    assert lib.rqf_fbt_carry_chunks(16000) == 63  # one entry state per 256-step tile
     assert lib.rqf_fbt_workspace(128, 32, 16000) >= 6 * 8 * 128 * 32
     assert lib.rqf_btf_scan_workspace(4, 161, 64) > 0
     s = _lib.SelectiveInputsStruct(F=256, B=64, T=16000, G=8, has_warp=1)

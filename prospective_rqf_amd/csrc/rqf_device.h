@@ -120,6 +120,11 @@ __device__ __forceinline__ c32 shift_down(c32 v, c32 fill, int lane) {
   return lane == kWave - 1 ? fill : o;
 }
 
+__device__ __forceinline__ float shift_down(float v, float fill, int lane) {
+  const float o = bperm(v, lane == kWave - 1 ? lane : lane + 1);
+  return lane == kWave - 1 ? fill : o;
+}
+
 // One Hillis-Steele step of the prefix scan of affine maps x -> P x + s.
 // The map received from an earlier lane is applied first.
 template <int CTRL, int ROW_MASK = 0xf>

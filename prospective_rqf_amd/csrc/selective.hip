@@ -51,6 +51,10 @@ using namespace rqf;
 #ifndef RQF_FWD_WAVES_PER_EU
 #define RQF_FWD_WAVES_PER_EU 1
 #endif
+// Forward complex streams through LDS (one contiguous 1 KB per instruction).
+#ifndef RQF_FWD_LDS_IO
+#define RQF_FWD_LDS_IO 1
+#endif
 // Backward form: 1 = teams of channels reduce the warp gradient in LDS;
 // 0 = one wavefront per row, per-channel warp gradient + group pass.
 #ifndef RQF_BWD_TEAMS
@@ -209,9 +213,11 @@ __device__ __forceinline__ float ratio_gamma(const rqf_selective_inputs& p, cons
 // bp z + bn zp = gamma*eta*phi*z + ratio*gamma*A*(z - zp).
 __device__ __forceinline__ void step_coef(const rqf_selective_inputs& p, const Chan& c,
                                           const Ctl& q, c32 zk, c32 zp, c32& A, c32& phi,
-                                          c32& u, float& inv_den) {
-  zoh(-q.gamma * c.eta, (1.0f - q.gamma) * clamp_theta(p, c, q.theta_u) * c.eta, A, phi,
-      inv_den);
+                                          c32& u, float& inv_den, float& ai, float& den) {
+  const float ar = -q.gamma * c.eta;
+  ai = (1.0f - q.gamma) * clamp_theta(p, c, q.theta_u) * c.eta;
+  den = fmaf(ar, ar, ai * ai);
+  zoh(ar, ai, A, phi, inv_den);
   c32 drive = cscale(q.gamma * c.eta, cmul(phi, zk));
   if (p.prospective) drive = cmad(cscale(ratio_gamma(p, c, q.gamma), A), csub(zk, zp), drive);
   u = cscale(q.gate, drive);
@@ -349,6 +355,43 @@ __device__ __forceinline__ RowId row_id(const rqf_selective_inputs& p, int64_t L
   return r;
 }
 
+// Complex tile I/O through a wavefront-private LDS slice (full tiles, VEC).
+// Each global load/store instruction moves one contiguous 1 KB (lane l moves
+// float4 j*64 + l); the lanes then exchange through LDS so that each holds its
+// K consecutive steps.  A direct lane-contiguous access would make every
+// instruction touch 2 KB at half density, which streams measurably slower.
+// The slot swizzle keeps both LDS access patterns free of bank conflicts.
+__device__ __forceinline__ int io_slot(int q) { return q ^ ((q >> 3) & 1); }
+
+template <int K>
+__device__ __forceinline__ void load_c_lds(const float* __restrict__ row, int t0, int lane,
+                                           float4* lds, c32 (&v)[K]) {
+  constexpr int Q = K / 2;  // float4s per lane
+#pragma unroll
+  for (int j = 0; j < Q; ++j) lds[io_slot(j * kWave + lane)] = ld4(row + 2 * t0 + 4 * (j * kWave + lane));
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int j = 0; j < Q; ++j) {
+    const float4 a = lds[io_slot(lane * Q + j)];
+    v[2 * j] = mk(a.x, a.y);
+    v[2 * j + 1] = mk(a.z, a.w);
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
+template <int K>
+__device__ __forceinline__ void store_c_lds(float* __restrict__ row, int t0, int lane, float4* lds,
+                                            const c32 (&v)[K]) {
+  constexpr int Q = K / 2;
+#pragma unroll
+  for (int j = 0; j < Q; ++j)
+    lds[io_slot(lane * Q + j)] = make_float4(v[2 * j].r, v[2 * j].i, v[2 * j + 1].r, v[2 * j + 1].i);
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int j = 0; j < Q; ++j) st4(row + 2 * t0 + 4 * (j * kWave + lane), lds[io_slot(j * kWave + lane)]);
+  __builtin_amdgcn_wave_barrier();
+}
+
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
@@ -360,6 +403,7 @@ struct FwdRow {
   float* rawr;
   float* actr;
   float* ent;
+  float4* io;  // this wavefront's LDS slice for transposed complex I/O (or nullptr)
   int T, chunk;
   c32 y, zlast;
 };
@@ -375,7 +419,10 @@ template <int K, bool VEC, bool TAIL>
 __device__ __forceinline__ void fwd_load(const FwdRow& r, int t0, int lane, FwdIn<K>& in) {
   const int T = r.T;
   const int tb = t0 + lane * K;
-  load_c<K, VEC, TAIL>(r.zr, tb, T, in.zv);
+  if (VEC && !TAIL && RQF_FWD_LDS_IO)
+    load_c_lds<K>(r.zr, t0, lane, r.io, in.zv);
+  else
+    load_c<K, VEC, TAIL>(r.zr, tb, T, in.zv);
   if (r.gr) load_f<K, VEC, TAIL>(r.gr, tb, T, in.gv); else zero(in.gv);
   if (r.wr) load_f<K, VEC, TAIL>(r.wr, tb, T, in.wv); else zero(in.wv);
   if (r.dr) load_f<K, VEC, TAIL>(r.dr, tb, T, in.dv); else zero(in.dv);
@@ -396,8 +443,8 @@ __device__ __forceinline__ void fwd_compute(const rqf_selective_inputs& p, const
   for (int k = 0; k < K; ++k) {
     const Ctl q = controller(p, c, gv[k], dv[k], wv[k]);
     c32 phi;
-    float inv_den;
-    step_coef(p, c, q, zv[k], k ? zv[k - 1] : zp0, A[k], phi, u[k], inv_den);
+    float inv_den, ai, den;
+    step_coef(p, c, q, zv[k], k ? zv[k - 1] : zp0, A[k], phi, u[k], inv_den, ai, den);
     if (TAIL && tb + k >= T) {
       A[k] = mk(1.0f, 0.0f);
       u[k] = mk(0.0f, 0.0f);
@@ -438,11 +485,20 @@ __device__ __forceinline__ void fwd_compute(const rqf_selective_inputs& p, const
       }
     }
   }
-  if (r.rawr) store_c<K, VEC, TAIL>(r.rawr, tb, T, out);
+  constexpr bool lds_io = VEC && !TAIL && RQF_FWD_LDS_IO;
+  if (r.rawr) {
+    if (lds_io)
+      store_c_lds<K>(r.rawr, t0, lane, r.io, out);
+    else
+      store_c<K, VEC, TAIL>(r.rawr, tb, T, out);
+  }
   if (r.actr) {
 #pragma unroll
     for (int k = 0; k < K; ++k) out[k] = relu2(out[k]);
-    store_c<K, VEC, TAIL>(r.actr, tb, T, out);
+    if (lds_io)
+      store_c_lds<K>(r.actr, t0, lane, r.io, out);
+    else
+      store_c<K, VEC, TAIL>(r.actr, tb, T, out);
   }
   r.y = readlane(s, kWave - 1);
   r.zlast = readlane(zv[K - 1], kWave - 1);
@@ -463,6 +519,9 @@ __global__ __launch_bounds__(kRowsPerBlock* kWave)
     float* __restrict__ act, float* __restrict__ entries, int chunk, int nc) {
   constexpr int K = kFwdK, TILE = kWave * K;
   const rqf_selective_inputs p = with_options<O>(pin);
+#if RQF_FWD_LDS_IO
+  __shared__ float4 s_io[kRowsPerBlock][TILE / 2];
+#endif
   const int lane = lane_id();
   const int64_t L = xcd_remap(blockIdx.x, gridDim.x) * kRowsPerBlock + wave_id();
   const RowId id = row_id(p, L);
@@ -479,6 +538,11 @@ __global__ __launch_bounds__(kRowsPerBlock* kWave)
   r.rawr = raw ? raw + 2 * base : nullptr;
   r.actr = act ? act + 2 * base : nullptr;
   r.ent = entries + 2 * id.row * nc;
+#if RQF_FWD_LDS_IO
+  r.io = &s_io[wave_id()][0];
+#else
+  r.io = nullptr;
+#endif
   if (lane == 0) {
     r.ent[0] = 0.0f;
     r.ent[1] = 0.0f;
@@ -556,31 +620,30 @@ __device__ __forceinline__ void lds_warp(const BwdRow& r, int lane, float (&wt)[
 
 // SHARED: tanh(warp logit) and exp(warp_scale * tanh) of the tile come from
 // the team's LDS stage (r.swt, r.sws) instead of per-lane loads and math.
+// zv: the tile's drive; zprev_tile: z[t0 - 1] (0 at t0 = 0).
 template <int K, bool VEC, bool TAIL, bool SHARED>
 __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Chan& c, BwdRow& r,
-                                         int t0, int lane) {
+                                         int t0, int lane, const c32 (&zv)[K], c32 zprev_tile) {
   const int T = r.T;
   const int tb = t0 + lane * K;
-  c32 zv[K];
   float gv[K], wv[K], dv[K];
-  load_c<K, VEC, TAIL>(r.zr, tb, T, zv);
   if (r.gr) load_f<K, VEC, TAIL>(r.gr, tb, T, gv); else zero(gv);
   if (r.wr) load_f<K, VEC, TAIL>(r.wr, tb, T, wv); else zero(wv);
   if (!SHARED && r.dr) load_f<K, VEC, TAIL>(r.dr, tb, T, dv); else zero(dv);
-  const c32 zprev_tile = t0 > 0 ? mk(r.zr[2 * (t0 - 1)], r.zr[2 * (t0 - 1) + 1]) : mk(0.0f, 0.0f);
   const c32 zp0 = shift_up(zv[K - 1], zprev_tile, lane);
 
   // Coefficients; kept per step: A, phi, gamma, gate and (unless SHARED)
   // theta_u and tanh(warp logit).
   c32 A[K], phi[K], u[K];
-  float gam[K], thu[K], gate[K], wtk[K], ivd[K];  // ivd: 1/|a|^2 from the ZOH
+  // ivd = 1/|a|^2, aim = Im a, dsq = |a|^2 of the ZOH exponent a, reused by the VJP
+  float gam[K], thu[K], gate[K], wtk[K], ivd[K], aim[K], dsq[K];
   float swt[K], sws[K];
   if (SHARED) lds_warp<K>(r, lane, swt, sws);
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const Ctl q = SHARED ? controller_w(p, c, gv[k], swt[k], sws[k], wv[k])
                          : controller(p, c, gv[k], dv[k], wv[k]);
-    step_coef(p, c, q, zv[k], k ? zv[k - 1] : zp0, A[k], phi[k], u[k], ivd[k]);
+    step_coef(p, c, q, zv[k], k ? zv[k - 1] : zp0, A[k], phi[k], u[k], ivd[k], aim[k], dsq[k]);
     gam[k] = q.gamma;
     gate[k] = q.gate;
     if (!SHARED) {
@@ -644,7 +707,7 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
   // Lag-tap weight cn = gate*ratio*gamma (gated n = -cn*A) of the lane's first step.
   const float c0 = p.prospective ? gate[0] * ratio_gamma(p, c, gam[0]) : 0.0f;
   const c32 A_lane_next = shift_down(A[0], r.Afirst, lane);
-  const c32 cn_lane_next = shift_down(mk(c0, 0.0f), mk(r.cfirst, 0.0f), lane);
+  const float cn_lane_next = shift_down(c0, r.cfirst, lane);
   r.Afirst = readlane(A[0], 0);
   r.cfirst = readlane(c0, 0);
 
@@ -685,7 +748,7 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
     if (k + 1 < K)
       cn = p.prospective ? gate[k + 1] * ratio_gamma(p, c, gam[k + 1]) : 0.0f;
     else
-      cn = cn_lane_next.r;
+      cn = cn_lane_next;
     const c32 d = r.truncated ? ecot[k] : cjmad(An, dnext, ecot[k]);
     const float gamma = gam[k], gt = gate[k];
     const float rg = p.prospective ? ratio_gamma(p, c, gamma) : 0.0f;
@@ -714,28 +777,21 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
       if (!p.gamma_horizon) dgamma = fmaf(gt * c.horizon, aw, dgamma);  // through rg
       dA = csmad(gt * rg, cw, dA);
     }
-    // phi'(a) = (A - phi)/a, or its series for |a|^2 < 1/64 (cubic below 1e-8);
-    // selective_scan_kernel.py:119-148.
+    // phi'(a) = sum_m (m+1) a^m / (m+2)!  (the reference's series,
+    // selective_scan_kernel.py:119-148), here to degree 4 for |a| < 1/32
+    // (truncation < 1e-10 relative) and (A - phi)/a above, where the
+    // cancellation in A - phi costs at most ~1e-5 relative.
     const float th_u = SHARED ? (p.has_warp ? c.theta * sws[k] : c.theta) : thu[k];
     const float theta = clamp_theta(p, c, th_u);
-    const float ar = -gh, ai = (1.0f - gamma) * theta * c.eta;
-    const float den = fmaf(ar, ar, ai * ai);
-    const c32 a = mk(ar, ai);
+    const c32 a = mk(-gh, aim[k]);
     c32 fp;
-    if (den < 0.015625f) {
-      if (den < 1.0e-8f) {
-        fp = cmadr(a, cmadrr(a, 1.0f / 8.0f, 1.0f / 3.0f), 0.5f);
-      } else {
-        c32 sr = cmadrr(a, 1.0f / 45360.0f, 1.0f / 5760.0f);
-        sr = cmadr(a, sr, 1.0f / 840.0f);
-        sr = cmadr(a, sr, 1.0f / 144.0f);
-        sr = cmadr(a, sr, 1.0f / 30.0f);
-        sr = cmadr(a, sr, 1.0f / 8.0f);
-        sr = cmadr(a, sr, 1.0f / 3.0f);
-        fp = cmadr(a, sr, 0.5f);
-      }
+    if (dsq[k] < 9.765625e-4f) {
+      c32 sr = cmadrr(a, 1.0f / 144.0f, 1.0f / 30.0f);
+      sr = cmadr(a, sr, 1.0f / 8.0f);
+      sr = cmadr(a, sr, 1.0f / 3.0f);
+      fp = cmadr(a, sr, 0.5f);
     } else {
-      // 1/|a|^2 as the ZOH formed it (same a, so the same value)
+      // 1/|a|^2 as the ZOH formed it
       fp = cscale(ivd[k], cmul(csub(A[k], phi[k]), conjg(a)));
     }
     // da = conj(A) dA + conj(phi') dphi with dphi = gt*gh*cz; then through
@@ -838,8 +894,19 @@ __global__ __launch_bounds__(kRowsPerBlock* kWave)
   const int ntiles = (r.T + TILE - 1) / TILE;
   const int full = VEC ? r.T / TILE : 0;
   int tile = ntiles - 1;
-  for (; tile >= full; --tile) bwd_tile<K, VEC, true, false>(p, c, r, tile * TILE, lane);
-  for (; tile >= 0; --tile) bwd_tile<K, VEC, false, false>(p, c, r, tile * TILE, lane);
+  auto zprev = [&](int t0) {
+    return t0 > 0 ? mk(r.zr[2 * (t0 - 1)], r.zr[2 * (t0 - 1) + 1]) : mk(0.0f, 0.0f);
+  };
+  for (; tile >= full; --tile) {
+    c32 zv[K];
+    load_c<K, VEC, true>(r.zr, tile * TILE + lane * K, r.T, zv);
+    bwd_tile<K, VEC, true, false>(p, c, r, tile * TILE, lane, zv, zprev(tile * TILE));
+  }
+  for (; tile >= 0; --tile) {
+    c32 zv[K];
+    load_c<K, VEC, false>(r.zr, tile * TILE + lane * K, r.T, zv);
+    bwd_tile<K, VEC, false, false>(p, c, r, tile * TILE, lane, zv, zprev(tile * TILE));
+  }
   const double sb = wave_sum(r.sum_bias);
   const double st = wave_sum(r.sum_theta);
   if (lane == 0) {
@@ -1039,10 +1106,16 @@ __global__ __launch_bounds__(kTeam* kWave)
     r.sws = sws + parity * TILE;
     if (ddp) r.sdd = &s_dd[parity][w][0];
     if (active) {
-      if (tile >= full)
-        bwd_tile<K, VEC, true, true>(p, c, r, t0, lane);
-      else
-        bwd_tile<K, VEC, false, true>(p, c, r, t0, lane);
+      const c32 zprev_tile =
+          t0 > 0 ? mk(r.zr[2 * (t0 - 1)], r.zr[2 * (t0 - 1) + 1]) : mk(0.0f, 0.0f);
+      c32 zv[K];
+      if (tile >= full) {
+        load_c<K, VEC, true>(r.zr, t0 + lane * K, r.T, zv);
+        bwd_tile<K, VEC, true, true>(p, c, r, t0, lane, zv, zprev_tile);
+      } else {
+        load_c<K, VEC, false>(r.zr, t0 + lane * K, r.T, zv);
+        bwd_tile<K, VEC, false, true>(p, c, r, t0, lane, zv, zprev_tile);
+      }
     }
     if (dwr && tile > 0) stage(parity ^ 1, t0 - TILE);
     if (ddp) {

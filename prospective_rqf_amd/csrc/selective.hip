@@ -922,7 +922,10 @@ __global__ __launch_bounds__(kRowsPerBlock* kWave)
 // barrier per tile with double-buffered LDS), so only one partial per team
 // reaches HBM; a small pass then sums the teams of each group in order.
 // ---------------------------------------------------------------------------
-constexpr int kTeam = kRowsPerBlock;
+#ifndef RQF_TEAM_WAVES
+#define RQF_TEAM_WAVES 4
+#endif
+constexpr int kTeam = RQF_TEAM_WAVES;
 
 // Team table built on the device (no host round trip).  Channels are ordered
 // by (warp group, channel index); a team is up to kTeam consecutive channels
@@ -1032,8 +1035,8 @@ __global__ __launch_bounds__(kTeam* kWave)
         const float* __restrict__ gx, int truncated, Teams tm, BwdOut o) {
   const rqf_selective_inputs p = with_options<O>(pin);
   constexpr int K = kBwdK, TILE = kWave * K, NT = kTeam * kWave;
-  static_assert(TILE % NT == 0, "team staging and reduction: whole tile elements per thread");
-  constexpr int PER = TILE / NT;  // tile elements per thread in the staging and the reduction
+  static_assert(TILE % NT == 0 || NT % TILE == 0, "team staging and reduction: whole tiles");
+  constexpr int PER = TILE >= NT ? TILE / NT : 1;  // tile elements per thread (staging, reduction)
   __shared__ float4 s_dd[2][kTeam][TILE / 4];
   __shared__ float4 s_wt[2][TILE / 4], s_ws[2][TILE / 4];  // staged tanh(warp), exp(scale*tanh)
   const int lane = lane_id();
@@ -1090,6 +1093,7 @@ __global__ __launch_bounds__(kTeam* kWave)
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
       const int i = q * NT + (int)threadIdx.x, t = ts + i;
+      if (NT > TILE && i >= TILE) break;
       const float wt = warp_tanh(p, t < r.T ? dwr[t] : 0.0f);
       swt[buf * TILE + i] = wt;
       sws[buf * TILE + i] = warp_factor(p, wt);
@@ -1124,6 +1128,7 @@ __global__ __launch_bounds__(kTeam* kWave)
 #pragma unroll
       for (int q = 0; q < PER; ++q) {
         const int i = q * NT + (int)threadIdx.x;
+        if (NT > TILE && i >= TILE) break;
         float acc = 0.0f;
         for (int m = 0; m < members; ++m) acc += sd[m * TILE + i];
         const int t = t0 + i;

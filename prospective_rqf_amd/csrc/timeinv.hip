@@ -293,28 +293,35 @@ __global__ __launch_bounds__(kTiWaves* kWave) void fbt_bwd_kernel(
   }
 }
 
-// grad[f] = sum over m of partial[(f*M + m)*6 + j] (fp64, ascending m) for the
-// FBT layout; for BTF tasks ((b*S + s)*F + f) pass stride_f = 1, stride_m = F.
-__global__ __launch_bounds__(256) void coef_reduce_kernel(const double* __restrict__ partial,
-                                                          int64_t F, int64_t M, int64_t stride_f,
-                                                          int64_t stride_m, float* __restrict__ gc1,
-                                                          float* __restrict__ gk0,
-                                                          float* __restrict__ gk1) {
-  const int64_t f = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (f >= F) return;
+// grad[f] = sum over m of partial[6*(f*stride_f + m*stride_m) + j] in fp64:
+// one wavefront per channel, lane l sums m = l, l+64, ... in order, then a
+// fixed-shape wave reduction (deterministic).  FBT layout: stride_f = M,
+// stride_m = 1; BTF tasks ((b*S + s)*F + f): stride_f = 1, stride_m = F.
+__global__ __launch_bounds__(kWave) void coef_reduce_kernel(const double* __restrict__ partial,
+                                                            int64_t F, int64_t M, int64_t stride_f,
+                                                            int64_t stride_m,
+                                                            float* __restrict__ gc1,
+                                                            float* __restrict__ gk0,
+                                                            float* __restrict__ gk1) {
+  const int64_t f = blockIdx.x;
+  const int lane = threadIdx.x;
   double s[6] = {0, 0, 0, 0, 0, 0};
-  for (int64_t m = 0; m < M; ++m) {
+  for (int64_t m = lane; m < M; m += kWave) {
     const double* p = partial + 6 * (f * stride_f + m * stride_m);
 #pragma unroll
     for (int j = 0; j < 6; ++j) s[j] += p[j];
   }
-  gc1[2 * f] = (float)s[0];
-  gc1[2 * f + 1] = (float)s[1];
-  gk0[2 * f] = (float)s[2];
-  gk0[2 * f + 1] = (float)s[3];
-  if (gk1) {
-    gk1[2 * f] = (float)s[4];
-    gk1[2 * f + 1] = (float)s[5];
+#pragma unroll
+  for (int j = 0; j < 6; ++j) s[j] = wave_sum(s[j]);
+  if (lane == 0) {
+    gc1[2 * f] = (float)s[0];
+    gc1[2 * f + 1] = (float)s[1];
+    gk0[2 * f] = (float)s[2];
+    gk0[2 * f + 1] = (float)s[3];
+    if (gk1) {
+      gk1[2 * f] = (float)s[4];
+      gk1[2 * f + 1] = (float)s[5];
+    }
   }
 }
 
@@ -520,10 +527,10 @@ int btf_bwd(const float* c1, const float* k0, const float* k1, const float* x,
     if (sh.S > 1) hipLaunchKernelGGL(btf_bwd_local_kernel, grid, block, 0, s, c1, gout, seg, sh);
     hipLaunchKernelGGL(btf_bwd_final_kernel, grid, block, 0, s, c1, k0, k1, x, states, gout, seg,
                        gx, partial, sh);
-    hipLaunchKernelGGL(coef_reduce_kernel, dim3((unsigned)((F + 255) / 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL(coef_reduce_kernel, dim3((unsigned)F), dim3(kWave), 0, s,
                        partial, F, B * sh.S, (int64_t)1, F, gc1, gk0, gk1);
   } else {
-    hipLaunchKernelGGL(coef_reduce_kernel, dim3((unsigned)((F + 255) / 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL(coef_reduce_kernel, dim3((unsigned)F), dim3(kWave), 0, s,
                        partial, F, (int64_t)0, (int64_t)1, F, gc1, gk0, gk1);
   }
   return launch_status();
@@ -583,10 +590,10 @@ int fbt_bwd(const float* c1, const float* t0, const float* t1, const float* z, c
         hipLaunchKernelGGL((fbt_bwd_kernel<false, false>), grid, block, 0, s, c1, t0, t1, z, raw,
                            carry, gout, mask, gz, partial, F, B, T, nc);
     }
-    hipLaunchKernelGGL(coef_reduce_kernel, dim3((unsigned)((F + 255) / 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL(coef_reduce_kernel, dim3((unsigned)F), dim3(kWave), 0, s,
                        partial, F, B, B, (int64_t)1, gc1, gt0, gt1);
   } else {
-    hipLaunchKernelGGL(coef_reduce_kernel, dim3((unsigned)((F + 255) / 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL(coef_reduce_kernel, dim3((unsigned)F), dim3(kWave), 0, s,
                        partial, F, (int64_t)0, B, (int64_t)1, gc1, gt0, gt1);
   }
   return launch_status();

@@ -203,10 +203,14 @@ def test_long_rows_subset_of_north_star_shape():
     run_case(6, 3, 16000, CASE_ALL, chunk=256, G=2, seed=13)
 
 
+@pytest.mark.parametrize("autocast", [False, True])
 @pytest.mark.parametrize("truncated", [False, True])
-def test_layer_scan_autograd_with_drive_gemm(truncated):
-    """selective_layer_scan (GEMM + kernels) vs float64 autograd of the restatement."""
-    print(f"case: layer scan truncated={truncated}", flush=True)
+def test_layer_scan_autograd_with_drive_gemm(truncated, autocast):
+    """selective_layer_scan (GEMM + kernels) vs float64 autograd of the restatement.
+
+    With an enclosing bf16 autocast region (reference test_selective_cuda.py:263-269)
+    the layer still computes the drive GEMM and the scan in complex64."""
+    print(f"case: layer scan truncated={truncated} autocast={autocast}", flush=True)
     rng = np.random.default_rng(21)
     I, F, B, T = 3, 5, 2, 65
     inp = rounded_to_f32(make_inputs(F, B, T, CASE_ALL, rng, prospective=True, G=2))
@@ -221,7 +225,9 @@ def test_layer_scan_autograd_with_drive_gemm(truncated):
         v.requires_grad_(True)
     xg = torch.as_tensor(x.astype(np.complex64), device="cuda").requires_grad_(True)
     Wg = torch.as_tensor(W.astype(np.complex64), device="cuda").requires_grad_(True)
-    raw, act = selective_layer_scan(xg, Wg, ti, truncated=truncated)
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        raw, act = selective_layer_scan(xg, Wg, ti, truncated=truncated)
+    assert raw.dtype == act.dtype == torch.complex64
     loss = ((torch.as_tensor(cot_raw, dtype=torch.complex64, device="cuda").conj() * raw).real.sum()
             + (torch.as_tensor(cot_act, dtype=torch.complex64, device="cuda").conj() * act).real.sum())
     grads = torch.autograd.grad(loss, [xg, Wg, *leaves])

@@ -230,3 +230,52 @@ def test_collapsed_and_tiny_poles_stay_finite():
         for g in out:
             if g is not None:
                 assert np.all(np.isfinite(g))
+
+
+def test_frequency_band_clamp_and_clipped_gradients():
+    """Global warp with a band bound (reference tests/test_selective_rqf.py:458-503):
+    the effective frequency angle(A) / ((1 - gamma) eta) equals
+    clamp(theta * exp(c tanh d), lo, hi), and a clipped step passes no gradient
+    to the warp logit or to theta."""
+    F, B = 1, 1
+    c = math.log(4.0)
+    lo, hi = 0.3, 1.2
+    theta = math.sqrt(lo * hi)
+    case = dict(gamma=False, write=False, warp="global", log_shift=False, write_sigmoid=True)
+    for d, clipped in ((-2.0, True), (0.1, False), (2.0, True)):
+        inp = make_inputs(F, B, 1, case, np.random.default_rng(0), prospective=False,
+                          warp_scale=c, eta=0.2)
+        inp.bias[:] = 0.2  # gamma (no gamma head: bias is gamma)
+        inp.theta[:] = theta
+        inp.theta_minimum[:] = lo
+        inp.theta_maximum[:] = hi
+        inp.warp_logits[:] = d
+        A, _, _ = oracle.selective_coefficients(inp, F, B, 1)
+        eff = np.angle(A[0, 0, 0]) / ((1 - 0.2) * 0.2)
+        np.testing.assert_allclose(eff, min(max(theta * math.exp(c * math.tanh(d)), lo), hi),
+                                   rtol=1e-13)
+        z = np.array([[[1.0 + 0.5j]]])
+        _, _, _, dd, _, _, dtheta = oracle.selective_bwd(z, inp, np.array([[[0.3 - 1j]]]), None)
+        if clipped:
+            assert dd[0, 0, 0] == 0.0 and dtheta[0] == 0.0
+        else:
+            assert dd[0, 0, 0] != 0.0 and dtheta[0] != 0.0
+
+
+def test_log_shift_gamma_limits():
+    """log_shift link: gamma = exp(bias + c tanh g) reaches exp(bias +- c) at
+    saturated logits (reference tests/test_selective_rqf.py:372-397), read back
+    from the pole radius |A| = exp(-gamma eta)."""
+    F, B, T = 3, 1, 3
+    c = math.log(1.25)
+    case = dict(gamma=True, write=False, warp="none", log_shift=True, write_sigmoid=True)
+    inp = make_inputs(F, B, T, case, np.random.default_rng(1), prospective=False,
+                      gamma_scale=c, eta=0.3)
+    inp.gamma_logits[:, :, 0] = 1000.0
+    inp.gamma_logits[:, :, 1] = -1000.0
+    inp.gamma_logits[:, :, 2] = 0.0
+    A, _, _ = oracle.selective_coefficients(inp, F, B, T)
+    gamma = -np.log(np.abs(A[:, 0, :])) / 0.3
+    np.testing.assert_allclose(gamma[:, 0], np.exp(inp.bias + c), rtol=1e-12)
+    np.testing.assert_allclose(gamma[:, 1], np.exp(inp.bias - c), rtol=1e-12)
+    np.testing.assert_allclose(gamma[:, 2], np.exp(inp.bias), rtol=1e-12)

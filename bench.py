@@ -55,6 +55,8 @@ def _args():
                     help="time steps of the CPU baseline sample (0: the config's default)")
     ap.add_argument("--batch", type=int, default=0,
                     help="override the config's batch size (experiments only)")
+    ap.add_argument("--seq-len", type=int, default=0,
+                    help="override the FBT configs' sequence length (experiments only)")
     ap.add_argument("--act-only", action="store_true",
                     help="config 3 with the act-only contract (no raw output, no gy)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -241,6 +243,9 @@ def plan_fbt(cfg, args, dev):
     if args.batch:
         B = args.batch
         name += f" [batch overridden to {B}]"
+    if args.seq_len:
+        T = args.seq_len
+        name += f" [sequence length overridden to {T}]"
     g = torch.Generator(device=dev).manual_seed(1)
     gcpu = torch.Generator().manual_seed(3)
     state = {}
@@ -550,7 +555,7 @@ def main():
     dom_bytes = plan.bytes[dom]
     achieved = dom_bytes / (per_op[dom] * 1e-3) / 1e9
     all_bytes = sum(plan.bytes.values())
-    traffic = traffic_from_table(f"config{cfg}", entry) if not args.batch else None
+    traffic = traffic_from_table(f"config{cfg}", entry) if not (args.batch or args.seq_len) else None
     result = {
         "metric": METRIC,
         "value": round(value, 3),

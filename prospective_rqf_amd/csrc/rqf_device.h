@@ -184,6 +184,43 @@ __device__ __forceinline__ void wave_scan_rev(c32& Q, c32& r, int lane) {
   rev_cross(Q, r, ((row + 2) & 3) << 4, row < 2);
 }
 
+// Complex tile I/O through a wavefront-private LDS slice (full tiles, VEC).
+// Each global load/store instruction moves one contiguous 1 KB (lane l moves
+// float4 j*64 + l); the lanes then exchange through LDS so that each holds its
+// K consecutive steps.  A direct lane-contiguous access would make every
+// instruction touch 2 KB at half density, which streams measurably slower.
+// The slot swizzle keeps both LDS access patterns free of bank conflicts.
+__device__ __forceinline__ int io_slot(int q) { return q ^ ((q >> 3) & 1); }
+
+template <int K>
+__device__ __forceinline__ void load_c_lds(const float* __restrict__ row, int t0, int lane,
+                                           float4* lds, c32 (&v)[K]) {
+  constexpr int Q = K / 2;  // float4s per lane
+#pragma unroll
+  for (int j = 0; j < Q; ++j) lds[io_slot(j * kWave + lane)] = *reinterpret_cast<const float4*>(row + 2 * t0 + 4 * (j * kWave + lane));
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int j = 0; j < Q; ++j) {
+    const float4 a = lds[io_slot(lane * Q + j)];
+    v[2 * j] = mk(a.x, a.y);
+    v[2 * j + 1] = mk(a.z, a.w);
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
+template <int K>
+__device__ __forceinline__ void store_c_lds(float* __restrict__ row, int t0, int lane, float4* lds,
+                                            const c32 (&v)[K]) {
+  constexpr int Q = K / 2;
+#pragma unroll
+  for (int j = 0; j < Q; ++j)
+    lds[io_slot(lane * Q + j)] = make_float4(v[2 * j].r, v[2 * j].i, v[2 * j + 1].r, v[2 * j + 1].i);
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int j = 0; j < Q; ++j) *reinterpret_cast<float4*>(row + 2 * t0 + 4 * (j * kWave + lane)) = lds[io_slot(j * kWave + lane)];
+  __builtin_amdgcn_wave_barrier();
+}
+
 // Sum of a double over the wave (result valid in every lane).
 __device__ __forceinline__ double wave_sum(double v) {
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);

@@ -355,43 +355,6 @@ __device__ __forceinline__ RowId row_id(const rqf_selective_inputs& p, int64_t L
   return r;
 }
 
-// Complex tile I/O through a wavefront-private LDS slice (full tiles, VEC).
-// Each global load/store instruction moves one contiguous 1 KB (lane l moves
-// float4 j*64 + l); the lanes then exchange through LDS so that each holds its
-// K consecutive steps.  A direct lane-contiguous access would make every
-// instruction touch 2 KB at half density, which streams measurably slower.
-// The slot swizzle keeps both LDS access patterns free of bank conflicts.
-__device__ __forceinline__ int io_slot(int q) { return q ^ ((q >> 3) & 1); }
-
-template <int K>
-__device__ __forceinline__ void load_c_lds(const float* __restrict__ row, int t0, int lane,
-                                           float4* lds, c32 (&v)[K]) {
-  constexpr int Q = K / 2;  // float4s per lane
-#pragma unroll
-  for (int j = 0; j < Q; ++j) lds[io_slot(j * kWave + lane)] = ld4(row + 2 * t0 + 4 * (j * kWave + lane));
-  __builtin_amdgcn_wave_barrier();
-#pragma unroll
-  for (int j = 0; j < Q; ++j) {
-    const float4 a = lds[io_slot(lane * Q + j)];
-    v[2 * j] = mk(a.x, a.y);
-    v[2 * j + 1] = mk(a.z, a.w);
-  }
-  __builtin_amdgcn_wave_barrier();
-}
-
-template <int K>
-__device__ __forceinline__ void store_c_lds(float* __restrict__ row, int t0, int lane, float4* lds,
-                                            const c32 (&v)[K]) {
-  constexpr int Q = K / 2;
-#pragma unroll
-  for (int j = 0; j < Q; ++j)
-    lds[io_slot(lane * Q + j)] = make_float4(v[2 * j].r, v[2 * j].i, v[2 * j + 1].r, v[2 * j + 1].i);
-  __builtin_amdgcn_wave_barrier();
-#pragma unroll
-  for (int j = 0; j < Q; ++j) st4(row + 2 * t0 + 4 * (j * kWave + lane), lds[io_slot(j * kWave + lane)]);
-  __builtin_amdgcn_wave_barrier();
-}
-
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
@@ -1039,6 +1002,11 @@ __global__ __launch_bounds__(kTeam* kWave)
   constexpr int PER = TILE >= NT ? TILE / NT : 1;  // tile elements per thread (staging, reduction)
   __shared__ float4 s_dd[2][kTeam][TILE / 4];
   __shared__ float4 s_wt[2][TILE / 4], s_ws[2][TILE / 4];  // staged tanh(warp), exp(scale*tanh)
+#ifdef RQF_BWD_LDS_RESERVE_KB
+  // Experiment: reserve LDS to cap the number of resident teams per CU.
+  __shared__ float s_reserve[RQF_BWD_LDS_RESERVE_KB * 256];
+  if (p.T < 0) s_reserve[threadIdx.x] = 0.0f;
+#endif
   const int lane = lane_id();
   const int w = wave_id();
   // Logical block -> (batch chunk, team slot, batch element), XCD-contiguous chunks.
@@ -1177,6 +1145,7 @@ __global__ __launch_bounds__(256) void team_reduce_kernel(const float* __restric
   }
 }
 
+#if !RQF_BWD_TEAMS
 // dd[g, i] = sum over the channels f of group g (ascending f) of ddc[f, i];
 // i runs over B*T.  Each thread keeps its G accumulators in LDS.
 constexpr int kReduceGroupsLds = 32;
@@ -1210,6 +1179,7 @@ __global__ __launch_bounds__(256) void group_reduce_kernel(const float* __restri
     }
   }
 }
+#endif
 
 // dbias[f] = sum_b partial[f*B + b] in fp64, same for dtheta: one wavefront
 // per channel, lane l sums b = l, l+64, ... in order, then a fixed-shape wave

@@ -159,6 +159,159 @@ __global__ __launch_bounds__(kTiWaves* kWave) void fbt_fwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Row-block backward.  A block of kRbWaves wavefronts owns one row and walks
+// it in super-tiles of kRbWaves consecutive tiles, wavefront w taking tile w
+// of each, so concurrent wavefronts stream adjacent stretches of the same
+// rows.  When the row stride is a multiple of 2 KB (T a multiple of the tile)
+// the one-row-per-wavefront form's concurrent streams sit at aliased offsets
+// and lose about 3-4%; this form does not (measured at T = 16000, 16128 and
+// 16384), and it replaces that form there.  The forward states of a tile come
+// from its stored entry (REPLAY) or from raw, so only the adjoint needs the
+// block scan: each wavefront scans its tile from a zero carry and publishes
+// the tile's suffix map (Q, r) in LDS; after one barrier every wavefront
+// composes the maps of the tiles after it onto the block's adjoint carry.
+// Map slots are double-buffered, so one barrier per super-tile suffices.
+// ---------------------------------------------------------------------------
+#ifndef RQF_TI_RB_WAVES
+#define RQF_TI_RB_WAVES 4
+#endif
+// 0 disables the row-block backward, 1 selects it for 2 KB-aligned rows.
+#ifndef RQF_TI_ROWBLOCK
+#define RQF_TI_ROWBLOCK 1
+#endif
+constexpr int kRbWaves = RQF_TI_RB_WAVES;
+
+// Super-tiles are walked from the end; wavefront w takes tile w of each.
+template <bool VEC, bool REPLAY>
+__global__ __launch_bounds__(kRbWaves* kWave) void fbt_bwd_rb_kernel(
+    const float* __restrict__ c1, const float* __restrict__ tap0, const float* __restrict__ tap1,
+    const float* __restrict__ z, const float* __restrict__ raw, const float* __restrict__ carry,
+    const float* __restrict__ gout, int mask, float* __restrict__ gz,
+    double* __restrict__ partial, int64_t F, int64_t B, int64_t T, int64_t nc) {
+  __shared__ float4 s_map[2][kRbWaves];
+  __shared__ double s_part[kRbWaves][6];
+  const int lane = lane_id();
+  const int w = wave_id();
+  const int64_t row = blockIdx.x;
+  const int64_t f = row / B;
+  const c32 a = ldc(c1, f), k0 = ldc(tap0, f), k1 = ldc(tap1, f);
+  const c32 ac = conjg(a);
+  const c32 apow = cpow_small(a, kTiK), acpow = conjg(apow);
+  const float* zr = z + 2 * row * T;
+  const float* rr = REPLAY ? nullptr : raw + 2 * row * T;
+  const float* gr = gout + 2 * row * T;
+  float* gzr = gz + 2 * row * T;
+  c32 gcarry = mk(0.0f, 0.0f);  // adjoint entering the super-tile from later times
+  double s1r = 0, s1i = 0, s0r = 0, s0i = 0, s2r = 0, s2i = 0;
+  const int64_t ntiles = (T + kTiTile - 1) / kTiTile;
+  const int64_t nsuper = (ntiles + kRbWaves - 1) / kRbWaves;
+  int parity = 0;
+  for (int64_t sti = nsuper - 1; sti >= 0; --sti) {
+    const int64_t tile = sti * kRbWaves + w;
+    const int64_t t0 = tile * kTiTile;
+    const bool has = t0 < T;
+    const int64_t tb = t0 + lane * kTiK;
+    const int cnt = (int)min<int64_t>(max<int64_t>(T - tb, 0), kTiK);
+    c32 zv[kTiK], yv[kTiK], ev[kTiK];
+    c32 zp0 = mk(0.0f, 0.0f), yp0 = mk(0.0f, 0.0f);
+    c32 Q = mk(1.0f, 0.0f), r = mk(0.0f, 0.0f);
+    if (has) {
+      load8<VEC>(zr, tb, T, zv);
+      load8<VEC>(gr, tb, T, ev);
+      const c32 zprev_tile = t0 > 0 ? ldc(zr, t0 - 1) : mk(0.0f, 0.0f);
+      zp0 = shift_up(zv[kTiK - 1], zprev_tile, lane);
+      if (REPLAY) {
+        c32 u[kTiK];
+#pragma unroll
+        for (int k = 0; k < kTiK; ++k) u[k] = cmad(k1, k ? zv[k - 1] : zp0, cmul(k0, zv[k]));
+        const c32 y0 = ldc(carry, row * nc + tile);
+        c32 s = mk(0.0f, 0.0f);
+#pragma unroll
+        for (int k = 0; k < kTiK; ++k)
+          if (k < cnt) s = cmad(a, s, u[k]);
+        c32 P = cnt == kTiK ? apow : cpow_small(a, cnt);
+        if (lane == 0) s = cmad(P, y0, s);
+        wave_scan_fwd(P, s);
+        c32 yk = shift_up(s, y0, lane);
+        yp0 = yk;
+#pragma unroll
+        for (int k = 0; k < kTiK; ++k) {
+          yk = cmad(a, yk, u[k]);
+          yv[k] = yk;
+        }
+      } else {
+        load8<VEC>(rr, tb, T, yv);
+        const c32 rprev_tile = t0 > 0 ? ldc(rr, t0 - 1) : mk(0.0f, 0.0f);
+        yp0 = shift_up(yv[kTiK - 1], rprev_tile, lane);
+      }
+      if (mask) {
+#pragma unroll
+        for (int k = 0; k < kTiK; ++k) ev[k] = mask_by(ev[k], yv[k]);
+      }
+      // Suffix composition of g -> e + conj(a) g over the lane's valid steps.
+#pragma unroll
+      for (int k = kTiK - 1; k >= 0; --k)
+        if (k < cnt) r = cmad(ac, r, ev[k]);
+      Q = cnt == kTiK ? acpow : conjg(cpow_small(a, cnt));
+      wave_scan_rev(Q, r, lane);  // inclusive suffix over lanes, zero carry
+    }
+    if (lane == 0) s_map[parity][w] = make_float4(Q.r, Q.i, r.r, r.i);
+    __syncthreads();
+    c32 gin = gcarry;  // adjoint entering this tile from its end
+    for (int v = kRbWaves - 1; v > w; --v) {
+      const float4 m = s_map[parity][v];
+      gin = cmad(mk(m.x, m.y), gin, mk(m.z, m.w));
+    }
+    c32 gn = gin;  // the next (earlier) super-tile's carry
+    for (int v = w; v >= 0; --v) {
+      const float4 m = s_map[parity][v];
+      gn = cmad(mk(m.x, m.y), gn, mk(m.z, m.w));
+    }
+    if (has) {
+      c32 gnext = shift_down(cmad(Q, gin, r), gin, lane);
+      c32 go[kTiK];
+      float a1r = 0, a1i = 0, a0r = 0, a0i = 0, a2r = 0, a2i = 0;
+#pragma unroll
+      for (int k = kTiK - 1; k >= 0; --k) {
+        const c32 g = cmad(ac, gnext, ev[k]);
+        go[k] = cjmad(k1, gnext, cjmul(k0, g));
+        const c32 yp = k ? yv[k - 1] : yp0;
+        const c32 zp = k ? zv[k - 1] : zp0;
+        const c32 t1 = cjmul(yp, g), t0c = cjmul(zv[k], g), t2 = cjmul(zp, g);
+        const bool in = k < cnt;
+        a1r += in ? t1.r : 0.0f;
+        a1i += in ? t1.i : 0.0f;
+        a0r += in ? t0c.r : 0.0f;
+        a0i += in ? t0c.i : 0.0f;
+        a2r += in ? t2.r : 0.0f;
+        a2i += in ? t2.i : 0.0f;
+        gnext = g;
+      }
+      store8<VEC>(gzr, tb, T, go);
+      s1r += a1r;
+      s1i += a1i;
+      s0r += a0r;
+      s0i += a0i;
+      s2r += a2r;
+      s2i += a2i;
+    }
+    gcarry = gn;
+    parity ^= 1;
+  }
+  // Per-wavefront sums, then the wavefronts in a fixed order.
+  const double sums[6] = {wave_sum(s1r), wave_sum(s1i), wave_sum(s0r),
+                          wave_sum(s0i), wave_sum(s2r), wave_sum(s2i)};
+  if (lane == 0)
+    for (int j = 0; j < 6; ++j) s_part[w][j] = sums[j];
+  __syncthreads();
+  if (threadIdx.x < 6) {
+    double t = 0.0;
+    for (int v = 0; v < kRbWaves; ++v) t += s_part[v][threadIdx.x];
+    partial[6 * row + threadIdx.x] = t;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // FBT backward.  REPLAY: raw recomputed from the per-tile carry; otherwise raw
 // is read.  MASK: cotangent is on the split-ReLU output.
 // partial: per row, 6 doubles (gc1.re, gc1.im, gk0.re, gk0.im, gk1.re, gk1.im).
@@ -544,8 +697,8 @@ int fbt_fwd(const float* c1, const float* t0, const float* t1, const float* z, f
   if (!c1 || !t0 || !t1 || !z || (!raw && !act)) return RQF_ERR_ARG;
   if (!aligned8(z) || !aligned8(raw) || !aligned8(act) || !aligned8(carry)) return RQF_ERR_ALIGN;
   const int64_t nc = (T + kTiTile - 1) / kTiTile;
-  const dim3 grid((unsigned)((R + kTiWaves - 1) / kTiWaves)), block(kTiWaves * kWave);
   const bool vec = T % 2 == 0 && aligned16(z) && aligned16(raw) && aligned16(act);
+  const dim3 grid((unsigned)((R + kTiWaves - 1) / kTiWaves)), block(kTiWaves * kWave);
   if (vec)
     hipLaunchKernelGGL(fbt_fwd_kernel<true>, grid, block, 0, s, c1, t0, t1, z, raw, act, carry, F,
                        B, T, nc);
@@ -573,9 +726,28 @@ int fbt_bwd(const float* c1, const float* t0, const float* t1, const float* z, c
   const int64_t R = F * B;
   if (R > 0 && T > 0) {
     const int64_t nc = (T + kTiTile - 1) / kTiTile;
-    const dim3 grid((unsigned)((R + kTiWaves - 1) / kTiWaves)), block(kTiWaves * kWave);
     const bool vec = T % 2 == 0 && aligned16(z) && aligned16(raw) && aligned16(gout) && aligned16(gz);
-    if (carry) {
+    const bool rowblock = RQF_TI_ROWBLOCK && T % kTiTile == 0;
+    const dim3 grid = rowblock ? dim3((unsigned)R)
+                               : dim3((unsigned)((R + kTiWaves - 1) / kTiWaves));
+    const dim3 block = rowblock ? dim3(kRbWaves * kWave) : dim3(kTiWaves * kWave);
+    if (rowblock) {
+      if (carry) {
+        if (vec)
+          hipLaunchKernelGGL((fbt_bwd_rb_kernel<true, true>), grid, block, 0, s, c1, t0, t1, z,
+                             raw, carry, gout, mask, gz, partial, F, B, T, nc);
+        else
+          hipLaunchKernelGGL((fbt_bwd_rb_kernel<false, true>), grid, block, 0, s, c1, t0, t1, z,
+                             raw, carry, gout, mask, gz, partial, F, B, T, nc);
+      } else {
+        if (vec)
+          hipLaunchKernelGGL((fbt_bwd_rb_kernel<true, false>), grid, block, 0, s, c1, t0, t1, z,
+                             raw, carry, gout, mask, gz, partial, F, B, T, nc);
+        else
+          hipLaunchKernelGGL((fbt_bwd_rb_kernel<false, false>), grid, block, 0, s, c1, t0, t1, z,
+                             raw, carry, gout, mask, gz, partial, F, B, T, nc);
+      }
+    } else if (carry) {
       if (vec)
         hipLaunchKernelGGL((fbt_bwd_kernel<true, true>), grid, block, 0, s, c1, t0, t1, z, raw,
                            carry, gout, mask, gz, partial, F, B, T, nc);

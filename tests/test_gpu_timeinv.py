@@ -83,7 +83,9 @@ def test_chunked_prospective_matches_oracle(shape):
 
 @pytest.mark.parametrize("variant", ["raw", "act", "recompute"])
 @pytest.mark.parametrize("shape", [(16, 8, 3000), (5, 3, 1023), (4, 2, 512), (3, 2, 513),
-                                   (2, 2, 1), (7, 3, 16000)])
+                                   (2, 2, 1), (7, 3, 16000),
+                                   # T a multiple of the 256-step tile: the row-block backward
+                                   (3, 2, 4096), (5, 2, 1280), (2, 2, 256)])
 def test_fbt_matches_oracle(variant, shape):
     F, B, T = shape
     print(f"case: fbt {variant} {shape}", flush=True)

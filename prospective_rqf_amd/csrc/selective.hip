@@ -34,6 +34,8 @@
 #include "rqf_device.h"
 #include "rqf_scan.h"
 
+#include <algorithm>
+#include <cstdlib>
 #include <initializer_list>
 #include <type_traits>
 
@@ -45,8 +47,10 @@ using namespace rqf;
 #ifndef RQF_SEL_BWD_K
 #define RQF_SEL_BWD_K 4
 #endif
+// Minimum waves per SIMD the backward is compiled for: 3 caps it at 168
+// VGPRs (it needs ~176 unconstrained, without spilling at 168).
 #ifndef RQF_BWD_WAVES_PER_EU
-#define RQF_BWD_WAVES_PER_EU 1
+#define RQF_BWD_WAVES_PER_EU 3
 #endif
 #ifndef RQF_FWD_WAVES_PER_EU
 #define RQF_FWD_WAVES_PER_EU 1
@@ -541,7 +545,8 @@ struct BwdOut {
   float* dg;
   float* dw;
   float* ddc;       // (F, B, T) per-channel warp-logit gradient (per-row kernel)
-  float* dd_part;   // (S, B, T) warp-logit gradient summed over each team (team kernel)
+  float* dd_part;   // (S, B, T) warp-logit gradient summed over each split (team kernel)
+  float* dd;        // (G, B, T) warp-logit gradient (team kernel, groups with one split)
   double* partial;  // (2, F*B): per row sums of d/dbias and d/dtheta
 };
 
@@ -879,16 +884,37 @@ __global__ __launch_bounds__(kRowsPerBlock* kWave)
 }
 
 // ---------------------------------------------------------------------------
-// Backward, team form: a block is a team of up to kTeam wavefronts, one
-// channel each, all of one warp group and one batch element.  Per tile the
-// team sums its warp-logit gradient in LDS (fixed order over channels, one
-// barrier per tile with double-buffered LDS), so only one partial per team
-// reaches HBM; a small pass then sums the teams of each group in order.
+// Backward, team form: a block of kTeam wavefronts owns a split, up to
+// kMaxSplitTeams consecutive teams of one warp group, for one batch element.
+// A team is up to kTeam channels of the group, one per wavefront.  The block
+// walks the row backwards in segments of kSegTiles tiles: it stages the
+// segment's warp tanh and frequency factor in LDS once, then runs each team
+// of the split over the segment in turn, carrying every channel's adjoint
+// state across segments in LDS.  Per tile the team sums its warp-logit
+// gradient in LDS (fixed order over channels, one barrier per tile with
+// double-buffered LDS) and adds it to the segment's group sum, also in LDS
+// and in fixed team order.  A group served by one split writes its gradient
+// row directly; otherwise each split writes a partial row and a small pass
+// sums the splits of the group in order.
 // ---------------------------------------------------------------------------
 #ifndef RQF_TEAM_WAVES
 #define RQF_TEAM_WAVES 4
 #endif
 constexpr int kTeam = RQF_TEAM_WAVES;
+#ifndef RQF_BWD_SEG_TILES
+#define RQF_BWD_SEG_TILES 8
+#endif
+constexpr int kSegTiles = RQF_BWD_SEG_TILES;
+constexpr int kMaxSplitTeams = 16;
+// Teams per split are sized so that the grid holds at least
+// kSplitBlocksPerCu blocks per CU; the environment variable
+// RQF_BWD_SPLIT_TEAMS=<n> fixes it instead (tests and tuning).  Longer splits
+// cut the partial-row traffic but leave fewer, longer blocks: at config 3
+// (8 teams per group and batch element, 3 resident blocks per CU) 2 teams per
+// split measured best (2.77 ms against 2.79 for 1, 2.84 for 3, 3.06 for 4
+// and 2.91 for 8).
+constexpr int kCus = 256;  // MI355X
+constexpr int kSplitBlocksPerCu = 8;
 
 // Team table built on the device (no host round trip).  Channels are ordered
 // by (warp group, channel index); a team is up to kTeam consecutive channels
@@ -899,7 +925,11 @@ struct Teams {
   const int* count;   // (S,) channels in the team
   const int* group;   // (S,) warp group of the team
   const int* nteams;  // (1,) number of teams in use
-  int slots;          // S: upper bound on the number of teams
+  const int* sfirst;  // (S,) first team of each split
+  const int* sn;      // (S,) teams in each split
+  const int* gsplit;  // (G+1,) first split of each group
+  const int* nsplits; // (1,) number of splits in use
+  int slots;          // S: upper bound on the number of teams (and splits)
 };
 
 // Group-sorted channel order and team table, built on the device from the
@@ -908,10 +938,53 @@ struct Teams {
 // G <= kBuildGroups, else a slower pass over global memory).
 constexpr int kBuildLds = 4096;
 constexpr int kBuildGroups = 1024;
+// The team table without LDS staging (F > kBuildLds or G > kBuildGroups).
+__device__ void team_build_global(const int64_t* __restrict__ groups, int F, int G, int* order,
+                                  int* first, int* count, int* group, int* gteam, int* nteams,
+                                  int* gcount, int* moff) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  auto grp = [&](int f) { return groups ? (int)groups[f] : 0; };
+  for (int g = tid; g < G; g += nt) {
+    int n = 0;
+    for (int f = 0; f < F; ++f) n += grp(f) == g;
+    gcount[g] = n;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int off = 0, toff = 0;
+    for (int g = 0; g < G; ++g) {
+      moff[g] = off;
+      gteam[g] = toff;
+      off += gcount[g];
+      toff += (gcount[g] + kTeam - 1) / kTeam;
+    }
+    gteam[G] = toff;
+    *nteams = toff;
+  }
+  __syncthreads();
+  for (int f = tid; f < F; f += nt) {
+    const int g = grp(f);
+    int rank = 0;
+    for (int q = 0; q < f; ++q) rank += grp(q) == g;
+    order[moff[g] + rank] = f;
+  }
+  for (int g = tid; g < G; g += nt) {
+    const int n = gcount[g], ntm = (n + kTeam - 1) / kTeam;
+    for (int t = 0; t < ntm; ++t) {
+      const int id = gteam[g] + t;
+      first[id] = moff[g] + t * kTeam;
+      count[id] = min(kTeam, n - t * kTeam);
+      group[id] = g;
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void team_build_kernel(const int64_t* __restrict__ groups,
-                                                         int F, int G, int* order, int* first,
-                                                         int* count, int* group, int* gteam,
-                                                         int* nteams, int* gcount, int* moff) {
+                                                         int F, int G, int Q, int* order,
+                                                         int* first, int* count, int* group,
+                                                         int* gteam, int* nteams, int* gcount,
+                                                         int* moff, int* sfirst, int* sn,
+                                                         int* gsplit, int* nsplits) {
   __shared__ int sg[kBuildLds];
   __shared__ int s_count[kBuildGroups], s_moff[kBuildGroups], s_gteam[kBuildGroups + 1];
   const int tid = threadIdx.x, nt = blockDim.x;
@@ -952,40 +1025,26 @@ __global__ __launch_bounds__(256) void team_build_kernel(const int64_t* __restri
         group[id] = g;
       }
     }
-    return;
+  } else {
+    team_build_global(groups, F, G, order, first, count, group, gteam, nteams, gcount, moff);
   }
-  auto grp = [&](int f) { return groups ? (int)groups[f] : 0; };
-  for (int g = tid; g < G; g += nt) {
-    int n = 0;
-    for (int f = 0; f < F; ++f) n += grp(f) == g;
-    gcount[g] = n;
-  }
+  // Splits: runs of up to Q consecutive teams of one group.
   __syncthreads();
   if (tid == 0) {
-    int off = 0, toff = 0;
+    int off = 0;
     for (int g = 0; g < G; ++g) {
-      moff[g] = off;
-      gteam[g] = toff;
-      off += gcount[g];
-      toff += (gcount[g] + kTeam - 1) / kTeam;
+      gsplit[g] = off;
+      off += (gteam[g + 1] - gteam[g] + Q - 1) / Q;
     }
-    gteam[G] = toff;
-    *nteams = toff;
+    gsplit[G] = off;
+    *nsplits = off;
   }
   __syncthreads();
-  for (int f = tid; f < F; f += nt) {
-    const int g = grp(f);
-    int rank = 0;
-    for (int q = 0; q < f; ++q) rank += grp(q) == g;
-    order[moff[g] + rank] = f;
-  }
   for (int g = tid; g < G; g += nt) {
-    const int n = gcount[g], ntm = (n + kTeam - 1) / kTeam;
-    for (int t = 0; t < ntm; ++t) {
-      const int id = gteam[g] + t;
-      first[id] = moff[g] + t * kTeam;
-      count[id] = min(kTeam, n - t * kTeam);
-      group[id] = g;
+    const int t0 = gteam[g], ntm = gteam[g + 1] - t0;
+    for (int j = 0; j * Q < ntm; ++j) {
+      sfirst[gsplit[g] + j] = t0 + j * Q;
+      sn[gsplit[g] + j] = min(Q, ntm - j * Q);
     }
   }
 }
@@ -997,11 +1056,16 @@ __global__ __launch_bounds__(kTeam* kWave)
         const float* __restrict__ entries, int chunk, int nc, const float* __restrict__ gy,
         const float* __restrict__ gx, int truncated, Teams tm, BwdOut o) {
   const rqf_selective_inputs p = with_options<O>(pin);
-  constexpr int K = kBwdK, TILE = kWave * K, NT = kTeam * kWave;
+  constexpr int K = kBwdK, TILE = kWave * K, NT = kTeam * kWave, SEG = kSegTiles * TILE;
   static_assert(TILE % NT == 0 || NT % TILE == 0, "team staging and reduction: whole tiles");
-  constexpr int PER = TILE >= NT ? TILE / NT : 1;  // tile elements per thread (staging, reduction)
+  constexpr int PER = TILE >= NT ? TILE / NT : 1;  // tile elements per thread (reduction)
+  constexpr int kChans = kMaxSplitTeams * kTeam;
   __shared__ float4 s_dd[2][kTeam][TILE / 4];
-  __shared__ float4 s_wt[2][TILE / 4], s_ws[2][TILE / 4];  // staged tanh(warp), exp(scale*tanh)
+  __shared__ float4 s_wt[SEG / 4], s_ws[SEG / 4];  // staged tanh(warp), exp(scale*tanh)
+  __shared__ float s_seg[SEG];                     // the segment's group gradient so far
+  __shared__ float4 s_carry[kChans];               // (dcarry, Afirst) of each channel
+  __shared__ float s_cfirst[kChans];
+  __shared__ double s_sum[kChans][2];              // dbias, dtheta sums of finished segments
 #ifdef RQF_BWD_LDS_RESERVE_KB
   // Experiment: reserve LDS to cap the number of resident teams per CU.
   __shared__ float s_reserve[RQF_BWD_LDS_RESERVE_KB * 256];
@@ -1009,103 +1073,155 @@ __global__ __launch_bounds__(kTeam* kWave)
 #endif
   const int lane = lane_id();
   const int w = wave_id();
-  // Logical block -> (batch chunk, team slot, batch element), XCD-contiguous chunks.
+  // Logical block -> (batch chunk, split slot, batch element), XCD-contiguous chunks.
   const int64_t bc = batch_chunk(p);
   const int64_t L = xcd_remap(blockIdx.x, gridDim.x);
   const int64_t per = (int64_t)tm.slots * bc;
   const int64_t ci = L / per, rem = L - ci * per;
   const int slot = (int)(rem / bc);
   const int64_t b = ci * bc + (rem - (int64_t)slot * bc);
-  if (ci >= kXcds || b >= p.B || slot >= *tm.nteams) return;  // block-uniform
-  const int members = tm.count[slot];
-  const bool active = w < members;
-  const int64_t f = tm.order[tm.first[slot] + (active ? w : 0)];
-  const int64_t row = f * p.B + b;
-  const Chan c = load_chan(p, f);
+  if (ci >= kXcds || b >= p.B || slot >= *tm.nsplits) return;  // block-uniform
+  const int team0 = tm.sfirst[slot], nteam = tm.sn[slot];
+  const int g = tm.group[team0];
+  const int T = (int)p.T;
+  const bool warp = p.has_warp;
+  // The group's warp-logit gradient row, or this split's partial row.
+  float* ddrow = nullptr;
+  if (warp)
+    ddrow = tm.gsplit[g + 1] - tm.gsplit[g] == 1 ? o.dd + ((int64_t)g * p.B + b) * T
+                                                 : o.dd_part + ((int64_t)slot * p.B + b) * T;
+  const float* dwr = warp ? p.warp_logits + ((int64_t)g * p.B + b) * T : nullptr;
+  const int ntiles = (T + TILE - 1) / TILE;
+  const int full = VEC ? T / TILE : 0;
+  const int seg_tiles = warp ? kSegTiles : ntiles;  // no warp: one segment
+  const int nseg = (ntiles + seg_tiles - 1) / seg_tiles;
+  float* swt = reinterpret_cast<float*>(&s_wt[0]);
+  float* sws = reinterpret_cast<float*>(&s_ws[0]);
+
   BwdRow r;
-  r.T = (int)p.T;
+  r.T = T;
   r.chunk = chunk;
   r.truncated = truncated;
-  const int64_t base = row * r.T;
-  r.zr = z + 2 * base;
-  r.gr = p.has_gamma ? p.gamma_logits + base : nullptr;
-  r.wr = p.has_write ? p.write_logits + base : nullptr;
-  r.dr = p.has_warp ? p.warp_logits + ((int64_t)tm.group[slot] * p.B + b) * r.T : nullptr;
-  r.gyr = gy ? gy + 2 * base : nullptr;
-  r.gxr = gx ? gx + 2 * base : nullptr;
-  r.ent = entries + 2 * row * nc;
-  r.dzr = o.dz + 2 * base;
-  r.dzwr = o.dzw + 2 * base;
-  r.dgr = o.dg ? o.dg + base : nullptr;
-  r.dwr = o.dw ? o.dw + base : nullptr;
+  r.dr = nullptr;
   r.ddr = nullptr;
   r.sdd = nullptr;
-  r.swt = nullptr;
-  r.sws = nullptr;
-  r.dcarry = mk(0.0f, 0.0f);
-  r.Afirst = mk(0.0f, 0.0f);
-  r.cfirst = 0.0f;
-  r.sum_bias = 0.0;
-  r.sum_theta = 0.0;
-  float* ddp = p.has_warp ? o.dd_part + ((int64_t)slot * p.B + b) * r.T : nullptr;
-  const int ntiles = (r.T + TILE - 1) / TILE;
-  const int full = VEC ? r.T / TILE : 0;
-  // The team's channels share one warp-logit row: thread i stages step i of a
-  // tile (tanh and the frequency factor) into LDS for all four wavefronts.
-  // Tile n+1 (in walk order) is staged during tile n, before that tile's
-  // barrier, so one barrier per tile covers both LDS buffers.
-  const float* dwr = r.dr;
-  float* swt = reinterpret_cast<float*>(&s_wt[0][0]);
-  float* sws = reinterpret_cast<float*>(&s_ws[0][0]);
-  auto stage = [&](int buf, int ts) {
-#pragma unroll
-    for (int q = 0; q < PER; ++q) {
-      const int i = q * NT + (int)threadIdx.x, t = ts + i;
-      if (NT > TILE && i >= TILE) break;
-      const float wt = warp_tanh(p, t < r.T ? dwr[t] : 0.0f);
-      swt[buf * TILE + i] = wt;
-      sws[buf * TILE + i] = warp_factor(p, wt);
-    }
-  };
-  if (dwr) {
-    stage(0, (ntiles - 1) * TILE);
-    __syncthreads();
-  }
+  r.swt = swt;
+  r.sws = sws;
+  Chan c;
+  int64_t row = 0;
+  bool active = false;
+  int members = 0;
   int parity = 0;
-  for (int tile = ntiles - 1; tile >= 0; --tile) {
-    const int t0 = tile * TILE;
-    r.swt = swt + parity * TILE;
-    r.sws = sws + parity * TILE;
-    if (ddp) r.sdd = &s_dd[parity][w][0];
-    if (active) {
-      const c32 zprev_tile =
-          t0 > 0 ? mk(r.zr[2 * (t0 - 1)], r.zr[2 * (t0 - 1) + 1]) : mk(0.0f, 0.0f);
-      c32 zv[K];
-      if (tile >= full) {
-        load_c<K, VEC, true>(r.zr, t0 + lane * K, r.T, zv);
-        bwd_tile<K, VEC, true, true>(p, c, r, t0, lane, zv, zprev_tile);
-      } else {
-        load_c<K, VEC, false>(r.zr, t0 + lane * K, r.T, zv);
-        bwd_tile<K, VEC, false, true>(p, c, r, t0, lane, zv, zprev_tile);
+  for (int sg = nseg - 1; sg >= 0; --sg) {
+    const int tile_lo = sg * seg_tiles, tile_hi = min(ntiles, tile_lo + seg_tiles);
+    const int s0 = tile_lo * TILE;
+    if (warp) {
+      // Stage the segment's warp values for all teams of the split.  The
+      // previous segment's last tile barrier ordered its reads before this.
+      const int n = (tile_hi - tile_lo) * TILE;
+      for (int i = (int)threadIdx.x; i < n; i += NT) {
+        const int t = s0 + i;
+        const float wt = warp_tanh(p, t < T ? dwr[t] : 0.0f);
+        swt[i] = wt;
+        sws[i] = warp_factor(p, wt);
       }
-    }
-    if (dwr && tile > 0) stage(parity ^ 1, t0 - TILE);
-    if (ddp) {
       __syncthreads();
-      const float* sd = reinterpret_cast<const float*>(&s_dd[parity][0][0]);
+    }
+    for (int qi = 0; qi < nteam; ++qi) {
+      const int ch = qi * kTeam + w;
+      if (nteam > 1 || sg == nseg - 1) {
+        // Switch this wavefront to channel w of team qi.
+        const int team = team0 + qi;
+        members = tm.count[team];
+        active = w < members;
+        const int64_t f = tm.order[tm.first[team] + (active ? w : 0)];
+        row = f * p.B + b;
+        c = load_chan(p, f);
+        const int64_t base = row * T;
+        r.zr = z + 2 * base;
+        r.gr = p.has_gamma ? p.gamma_logits + base : nullptr;
+        r.wr = p.has_write ? p.write_logits + base : nullptr;
+        r.gyr = gy ? gy + 2 * base : nullptr;
+        r.gxr = gx ? gx + 2 * base : nullptr;
+        r.ent = entries + 2 * row * nc;
+        r.dzr = o.dz + 2 * base;
+        r.dzwr = o.dzw + 2 * base;
+        r.dgr = o.dg ? o.dg + base : nullptr;
+        r.dwr = o.dw ? o.dw + base : nullptr;
+        r.sum_bias = 0.0;
+        r.sum_theta = 0.0;
+        if (sg == nseg - 1) {
+          r.dcarry = mk(0.0f, 0.0f);
+          r.Afirst = mk(0.0f, 0.0f);
+          r.cfirst = 0.0f;
+        } else {
+          const float4 cs = s_carry[ch];
+          r.dcarry = readlane(mk(cs.x, cs.y), 0);
+          r.Afirst = readlane(mk(cs.z, cs.w), 0);
+          r.cfirst = readlane(s_cfirst[ch], 0);
+        }
+      }
+      for (int tile = tile_hi - 1; tile >= tile_lo; --tile) {
+        const int t0 = tile * TILE;
+        if (warp) {
+          r.swt = swt + (t0 - s0);
+          r.sws = sws + (t0 - s0);
+          r.sdd = &s_dd[parity][w][0];
+        }
+        if (active) {
+          const c32 zprev_tile =
+              t0 > 0 ? mk(r.zr[2 * (t0 - 1)], r.zr[2 * (t0 - 1) + 1]) : mk(0.0f, 0.0f);
+          c32 zv[K];
+          if (tile >= full) {
+            load_c<K, VEC, true>(r.zr, t0 + lane * K, T, zv);
+            bwd_tile<K, VEC, true, true>(p, c, r, t0, lane, zv, zprev_tile);
+          } else {
+            load_c<K, VEC, false>(r.zr, t0 + lane * K, T, zv);
+            bwd_tile<K, VEC, false, true>(p, c, r, t0, lane, zv, zprev_tile);
+          }
+        }
+        if (warp) {
+          __syncthreads();
+          // Thread i owns step i of every tile: the team's sum (fixed channel
+          // order) joins the segment's group sum (fixed team order).
+          const float* sd = reinterpret_cast<const float*>(&s_dd[parity][0][0]);
 #pragma unroll
-      for (int q = 0; q < PER; ++q) {
-        const int i = q * NT + (int)threadIdx.x;
-        if (NT > TILE && i >= TILE) break;
-        float acc = 0.0f;
-        for (int m = 0; m < members; ++m) acc += sd[m * TILE + i];
-        const int t = t0 + i;
-        if (t < r.T) ddp[t] = acc;
+          for (int q = 0; q < PER; ++q) {
+            const int i = q * NT + (int)threadIdx.x;
+            if (NT > TILE && i >= TILE) break;
+            float acc = 0.0f;
+            for (int m = 0; m < members; ++m) acc += sd[m * TILE + i];
+            const int j = t0 - s0 + i, t = t0 + i;
+            if (qi > 0) acc = s_seg[j] + acc;
+            if (qi + 1 < nteam)
+              s_seg[j] = acc;
+            else if (t < T)
+              ddrow[t] = acc;
+          }
+        }
+        parity ^= 1;
+      }
+      if (nteam > 1 && active) {
+        // Park the channel's state until the next segment.
+        const double sb = wave_sum(r.sum_bias);
+        const double st = wave_sum(r.sum_theta);
+        if (lane == 0) {
+          const double pb = sg == nseg - 1 ? 0.0 : s_sum[ch][0];
+          const double pt = sg == nseg - 1 ? 0.0 : s_sum[ch][1];
+          if (sg > 0) {
+            s_carry[ch] = make_float4(r.dcarry.r, r.dcarry.i, r.Afirst.r, r.Afirst.i);
+            s_cfirst[ch] = r.cfirst;
+            s_sum[ch][0] = pb + sb;
+            s_sum[ch][1] = pt + st;
+          } else {
+            o.partial[row] = pb + sb;
+            o.partial[p.F * p.B + row] = pt + st;
+          }
+        }
       }
     }
-    parity ^= 1;
   }
-  if (active) {
+  if (nteam == 1 && active) {
     const double sb = wave_sum(r.sum_bias);
     const double st = wave_sum(r.sum_theta);
     if (lane == 0) {
@@ -1115,11 +1231,12 @@ __global__ __launch_bounds__(kTeam* kWave)
   }
 }
 
-// dd[g, b, t] = sum over the teams of group g (fixed order) of dd_part[team, b, t].
+// dd[g, b, t] = sum over the splits of group g (fixed order) of dd_part[split, b, t],
+// for groups not served by exactly one split (those wrote dd directly).
 // VEC: N % 4 == 0 and 16-byte aligned dd; each thread sums one float4.
 template <bool VEC>
 __global__ __launch_bounds__(256) void team_reduce_kernel(const float* __restrict__ dd_part,
-                                                          const int* __restrict__ gteam,
+                                                          const int* __restrict__ gsplit,
                                                           float* __restrict__ dd, int64_t G,
                                                           int64_t N) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1127,8 +1244,9 @@ __global__ __launch_bounds__(256) void team_reduce_kernel(const float* __restric
     const int64_t n4 = N / 4;
     if (i >= G * n4) return;
     const int64_t g = i / n4, n = (i - g * n4) * 4;
+    if (gsplit[g + 1] - gsplit[g] == 1) return;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int s = gteam[g]; s < gteam[g + 1]; ++s) {
+    for (int s = gsplit[g]; s < gsplit[g + 1]; ++s) {
       const float4 v = ld4(dd_part + (int64_t)s * N + n);
       acc.x += v.x;
       acc.y += v.y;
@@ -1139,8 +1257,9 @@ __global__ __launch_bounds__(256) void team_reduce_kernel(const float* __restric
   } else {
     if (i >= G * N) return;
     const int64_t g = i / N, n = i - g * N;
+    if (gsplit[g + 1] - gsplit[g] == 1) return;
     float acc = 0.0f;
-    for (int s = gteam[g]; s < gteam[g + 1]; ++s) acc += dd_part[(int64_t)s * N + n];
+    for (int s = gsplit[g]; s < gsplit[g + 1]; ++s) acc += dd_part[(int64_t)s * N + n];
     dd[i] = acc;
   }
 }
@@ -1328,25 +1447,41 @@ extern "C" int rqf_selective_fwd(const rqf_selective_inputs* in, const float* z,
 }
 
 namespace {
+// Teams per split of the backward (see the team kernel).
+int split_teams(const rqf_selective_inputs* in) {
+  if (!in->has_warp) return 1;
+  if (const char* e = std::getenv("RQF_BWD_SPLIT_TEAMS")) {
+    const int q = std::atoi(e);
+    if (q > 0) return std::min(q, kMaxSplitTeams);
+  }
+  // Balanced groups assumed: at least kSplitBlocksPerCu blocks per CU.
+  const int64_t teams = (in->F + kTeam - 1) / kTeam;
+  const int64_t q = teams * in->B / (kSplitBlocksPerCu * kCus);
+  return (int)std::max<int64_t>(1, std::min<int64_t>(kMaxSplitTeams, q));
+}
+
 struct SelWs {
   size_t partial, tile_entries, teams, dd, total;
-  int slots, G;
+  int slots, split_slots, Q, G;
 };
 SelWs sel_ws_layout(const rqf_selective_inputs* in, int64_t chunk) {
   SelWs w;
   const int64_t R = in->F * in->B;
   w.G = in->has_warp ? (int)in->G : 1;
-  w.slots = (int)(w.G + (in->F + kTeam - 1) / kTeam);
+  const int teams = (int)((in->F + kTeam - 1) / kTeam);
+  w.slots = w.G + teams;  // teams of all groups <= ceil(F/kTeam) + G
+  w.Q = split_teams(in);
+  w.split_slots = std::min(w.slots, (teams + w.G) / w.Q + w.G);
   w.partial = 0;
   size_t off = round256(sizeof(double) * 2 * (size_t)R);
   w.tile_entries = off;
   if (chunk > kBwdTile)
     off += round256(sizeof(float) * 2 * (size_t)R * ((in->T + kBwdTile - 1) / kBwdTile + 1));
   w.teams = off;
-  off += round256(sizeof(int) * (size_t)(in->F + 3 * w.slots + 3 * w.G + 2));
+  off += round256(sizeof(int) * (size_t)(in->F + 5 * w.slots + 4 * w.G + 4));
   w.dd = off;
 #if RQF_BWD_TEAMS
-  if (in->has_warp) off += round256(sizeof(float) * (size_t)w.slots * in->B * in->T);
+  if (in->has_warp) off += round256(sizeof(float) * (size_t)w.split_slots * in->B * in->T);
 #else
   if (in->has_warp) off += round256(sizeof(float) * (size_t)R * (size_t)in->T);
 #endif
@@ -1405,6 +1540,7 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
     o.dw = in->has_write ? dw : nullptr;
     o.ddc = nullptr;
     o.dd_part = nullptr;
+    o.dd = nullptr;
     o.partial = partial;
 #if RQF_BWD_TEAMS
     int* order = (int*)(ws + w.teams);
@@ -1415,19 +1551,29 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
     int* nteams = gteam + (w.G + 1);
     int* gcount = nteams + 1;
     int* moff = gcount + w.G;
+    int* sfirst = moff + w.G;
+    int* sn = sfirst + w.slots;
+    int* gsplit = sn + w.slots;
+    int* nsplits = gsplit + (w.G + 1);
     hipLaunchKernelGGL(team_build_kernel, dim3(1), dim3(256), 0, s,
-                       in->has_warp ? in->groups : (const int64_t*)nullptr, (int)in->F, w.G,
-                       order, first, count, group, gteam, nteams, gcount, moff);
+                       in->has_warp ? in->groups : (const int64_t*)nullptr, (int)in->F, w.G, w.Q,
+                       order, first, count, group, gteam, nteams, gcount, moff, sfirst, sn,
+                       gsplit, nsplits);
     Teams tm;
     tm.order = order;
     tm.first = first;
     tm.count = count;
     tm.group = group;
     tm.nteams = nteams;
-    tm.slots = w.slots;
+    tm.sfirst = sfirst;
+    tm.sn = sn;
+    tm.gsplit = gsplit;
+    tm.nsplits = nsplits;
+    tm.slots = w.split_slots;
     o.dd_part = in->has_warp ? (float*)(ws + w.dd) : nullptr;
+    o.dd = in->has_warp ? dd : nullptr;
     const int64_t bc = (in->B + kXcds - 1) / kXcds;
-    const dim3 grid((unsigned)(kXcds * w.slots * bc)), block(kTeam * kWave);
+    const dim3 grid((unsigned)(kXcds * w.split_slots * bc)), block(kTeam * kWave);
     with_option_set(options_of(in), [&](auto oc) {
       constexpr int O = decltype(oc)::value;
       if (vec)
@@ -1441,10 +1587,10 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
       const int64_t N = in->B * T;
       if (N % 4 == 0 && aligned16(dd))
         hipLaunchKernelGGL(team_reduce_kernel<true>, dim3((unsigned)((in->G * N / 4 + 255) / 256)),
-                           dim3(256), 0, s, o.dd_part, gteam, dd, in->G, N);
+                           dim3(256), 0, s, o.dd_part, gsplit, dd, in->G, N);
       else
         hipLaunchKernelGGL(team_reduce_kernel<false>, dim3((unsigned)((in->G * N + 255) / 256)),
-                           dim3(256), 0, s, o.dd_part, gteam, dd, in->G, N);
+                           dim3(256), 0, s, o.dd_part, gsplit, dd, in->G, N);
     }
 #else
     o.ddc = in->has_warp ? (float*)(ws + w.dd) : nullptr;

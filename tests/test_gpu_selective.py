@@ -77,6 +77,8 @@ def run_case(F, B, T, case, *, prospective=True, truncated=False, activate=True,
             else:
                 errs[f"{tag}.{name}"] = relerr(got, want)
     bad = {k: v for k, v in errs.items() if not v <= PARITY_RTOL}
+    if bad:
+        print("errors:", {k: f"{v:.3g}" for k, v in errs.items()}, flush=True)
     assert not bad, bad
     return errs
 
@@ -195,6 +197,32 @@ def test_irrelevant_option_bits(truncated):
         inp.theta_maximum[:] = 0.6
 
     run_case(5, 3, 70, case, prospective=False, truncated=truncated, edit=edit, seed=14)
+
+
+@pytest.mark.parametrize("F,B,T,warp,G,split,truncated", [
+    # 2 groups of 10 channels, 3 teams each (last one partial), 3 teams per
+    # split: one split per group, writing the group gradient directly; two
+    # segments of the row, the second partial.
+    (20, 4, 2200, "grouped", 2, 3, False),
+    # global warp, 5 teams, 2 teams per split: splits of 2, 2 and 1 teams,
+    # summed by the split reduction; three segments.
+    (20, 3, 4500, "global", 1, 2, True),
+    (20, 3, 4500, "global", 1, 2, False),
+    # 4 groups of 8 channels, 2 teams each, 16 teams per split: one split
+    # of 2 teams per group.
+    (32, 2, 2100, "grouped", 4, 16, False),
+])
+def test_split_teams_carry_state_across_segments(monkeypatch, F, B, T, warp, G, split, truncated):
+    """Backward blocks that run several teams of a warp group over segmented rows.
+
+    RQF_BWD_SPLIT_TEAMS fixes the teams per block, which the library otherwise
+    sizes from the grid (several teams per block only at large F*B).
+    """
+    print(f"case: split teams F={F} B={B} T={T} warp={warp} split={split} "
+          f"truncated={truncated}", flush=True)
+    monkeypatch.setenv("RQF_BWD_SPLIT_TEAMS", str(split))
+    case = dict(CASE_ALL, warp=warp)
+    run_case(F, B, T, case, chunk=256, G=G, truncated=truncated, seed=F + T)
 
 
 def test_long_rows_subset_of_north_star_shape():

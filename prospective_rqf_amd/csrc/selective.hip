@@ -42,7 +42,7 @@
 using namespace rqf;
 
 #ifndef RQF_SEL_FWD_K
-#define RQF_SEL_FWD_K 4
+#define RQF_SEL_FWD_K 8
 #endif
 #ifndef RQF_SEL_BWD_K
 #define RQF_SEL_BWD_K 4
@@ -395,46 +395,32 @@ __device__ __forceinline__ void fwd_load(const FwdRow& r, int t0, int lane, FwdI
   if (r.dr) load_f<K, VEC, TAIL>(r.dr, tb, T, in.dv); else zero(in.dv);
 }
 
-template <int K, bool VEC, bool TAIL>
-__device__ __forceinline__ void fwd_compute(const rqf_selective_inputs& p, const Chan& c, FwdRow& r,
-                                            int t0, int lane, const FwdIn<K>& in) {
-  const int T = r.T;
+// Per-step coefficients of one tile: A (decay) and u (drive) of each of the
+// lane's K steps.  zlast_tile: z[t0 - 1] (0 at t0 = 0).
+template <int K, bool TAIL>
+__device__ __forceinline__ void fwd_steps(const rqf_selective_inputs& p, const Chan& c, int T,
+                                          int t0, int lane, const FwdIn<K>& in, c32 zlast_tile,
+                                          c32 (&A)[K], c32 (&u)[K]) {
   const int tb = t0 + lane * K;
-  const c32 (&zv)[K] = in.zv;
-  const float (&gv)[K] = in.gv;
-  const float (&wv)[K] = in.wv;
-  const float (&dv)[K] = in.dv;
-  const c32 zp0 = shift_up(zv[K - 1], r.zlast, lane);
-  c32 A[K], u[K];
+  const c32 zp0 = shift_up(in.zv[K - 1], zlast_tile, lane);
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    const Ctl q = controller(p, c, gv[k], dv[k], wv[k]);
+    const Ctl q = controller(p, c, in.gv[k], in.dv[k], in.wv[k]);
     c32 phi;
     float inv_den, ai, den;
-    step_coef(p, c, q, zv[k], k ? zv[k - 1] : zp0, A[k], phi, u[k], inv_den, ai, den);
+    step_coef(p, c, q, in.zv[k], k ? in.zv[k - 1] : zp0, A[k], phi, u[k], inv_den, ai, den);
     if (TAIL && tb + k >= T) {
       A[k] = mk(1.0f, 0.0f);
       u[k] = mk(0.0f, 0.0f);
     }
   }
-  // 1. lane-local composition
-  c32 P = A[0], s = u[0];
-#pragma unroll
-  for (int k = 1; k < K; ++k) {
-    s = cmad(A[k], s, u[k]);
-    P = cmul(A[k], P);
-  }
-  if (lane == 0) s = cmad(P, r.y, s);
-  // 2. wave scan: s becomes the state after the lane's last step
-  wave_scan_fwd(P, s);
-  // 3. replay from the lane's entry state
-  c32 yk = shift_up(s, r.y, lane);
-  c32 out[K];
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    yk = cmad(A[k], yk, u[k]);
-    out[k] = yk;
-  }
+}
+
+// Chunk entry states and the raw / act outputs of one tile.
+template <int K, bool VEC, bool TAIL>
+__device__ __forceinline__ void fwd_emit(const FwdRow& r, int t0, int lane, c32 (&out)[K]) {
+  const int T = r.T;
+  const int tb = t0 + lane * K;
   // Entry states: the state after step t with (t+1) % chunk == 0 enters chunk (t+1)/chunk.
   if (r.chunk >= K) {
     const int t1 = tb + K;
@@ -467,8 +453,34 @@ __device__ __forceinline__ void fwd_compute(const rqf_selective_inputs& p, const
     else
       store_c<K, VEC, TAIL>(r.actr, tb, T, out);
   }
+}
+
+template <int K, bool VEC, bool TAIL>
+__device__ __forceinline__ void fwd_compute(const rqf_selective_inputs& p, const Chan& c, FwdRow& r,
+                                            int t0, int lane, const FwdIn<K>& in) {
+  c32 A[K], u[K];
+  fwd_steps<K, TAIL>(p, c, r.T, t0, lane, in, r.zlast, A, u);
+  // 1. lane-local composition
+  c32 P = A[0], s = u[0];
+#pragma unroll
+  for (int k = 1; k < K; ++k) {
+    s = cmad(A[k], s, u[k]);
+    P = cmul(A[k], P);
+  }
+  if (lane == 0) s = cmad(P, r.y, s);
+  // 2. wave scan: s becomes the state after the lane's last step
+  wave_scan_fwd(P, s);
+  // 3. replay from the lane's entry state
+  c32 yk = shift_up(s, r.y, lane);
+  c32 out[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    yk = cmad(A[k], yk, u[k]);
+    out[k] = yk;
+  }
+  fwd_emit<K, VEC, TAIL>(r, t0, lane, out);
   r.y = readlane(s, kWave - 1);
-  r.zlast = readlane(zv[K - 1], kWave - 1);
+  r.zlast = readlane(in.zv[K - 1], kWave - 1);
 }
 
 template <int K, bool VEC, bool TAIL>
@@ -534,6 +546,119 @@ __global__ __launch_bounds__(kRowsPerBlock* kWave)
   for (int i = 0; i < full; ++i, t0 += TILE) fwd_tile<K, VEC, false>(p, c, r, t0, lane);
 #endif
   for (; t0 < r.T; t0 += TILE) fwd_tile<K, VEC, true>(p, c, r, t0, lane);
+}
+
+// Forward, row-block form: a block of kFwdRbWaves wavefronts owns one row and
+// walks it in super-tiles of kFwdRbWaves consecutive tiles, wavefront w
+// taking tile w of each, so that concurrent wavefronts stream adjacent
+// stretches of the same rows (8 waves x 512 steps = 32 KB of each complex
+// stream per super-tile).  Each wavefront scans its tile from a zero entry
+// and publishes the tile's affine map (P, s) in LDS; after one barrier it
+// composes the maps of the tiles before it onto the block's carry and
+// replays its steps from there.  Map slots are double-buffered, so one
+// barrier per super-tile suffices.  Config 3 forward, measured: 1.746 ms one
+// row per wavefront (K = 4); row blocks of 2 / 4 / 8 / 16 waves: 1.765 /
+// 1.729 / 1.688 / - (K = 4), 8 waves with K = 8: 1.644, 16 waves with K = 8:
+// 1.753, 4 waves with K = 16: 1.701; without the LDS transpose 1.837.
+#ifndef RQF_FWD_ROWBLOCK
+#define RQF_FWD_ROWBLOCK 1
+#endif
+#ifndef RQF_FWD_RB_WAVES
+#define RQF_FWD_RB_WAVES 8
+#endif
+constexpr int kFwdRbWaves = RQF_FWD_RB_WAVES;
+
+template <int O, bool VEC>
+__global__ __launch_bounds__(kFwdRbWaves* kWave)
+    __attribute__((amdgpu_waves_per_eu(RQF_FWD_WAVES_PER_EU))) void selective_fwd_rb_kernel(
+    const rqf_selective_inputs pin, const float* __restrict__ z, float* __restrict__ raw,
+    float* __restrict__ act, float* __restrict__ entries, int chunk, int nc) {
+  constexpr int K = kFwdK, TILE = kWave * K, W = kFwdRbWaves;
+  const rqf_selective_inputs p = with_options<O>(pin);
+#if RQF_FWD_LDS_IO
+  __shared__ float4 s_io[W][TILE / 2];
+#endif
+  __shared__ float4 s_map[2][W];
+  const int lane = lane_id();
+  const int w = wave_id();
+  const RowId id = row_id(p, xcd_remap(blockIdx.x, gridDim.x));
+  if (!id.valid) return;  // the whole block
+  const Chan c = load_chan(p, id.f);
+  FwdRow r;
+  r.T = (int)p.T;
+  r.chunk = chunk;
+  const int T = r.T;
+  const int64_t base = id.row * T;
+  r.zr = z + 2 * base;
+  r.gr = p.has_gamma ? p.gamma_logits + base : nullptr;
+  r.wr = p.has_write ? p.write_logits + base : nullptr;
+  r.dr = p.has_warp ? p.warp_logits + (p.groups[id.f] * p.B + id.b) * T : nullptr;
+  r.rawr = raw ? raw + 2 * base : nullptr;
+  r.actr = act ? act + 2 * base : nullptr;
+  r.ent = entries + 2 * id.row * nc;
+#if RQF_FWD_LDS_IO
+  r.io = &s_io[w][0];
+#else
+  r.io = nullptr;
+#endif
+  if (w == 0 && lane == 0) {
+    r.ent[0] = 0.0f;
+    r.ent[1] = 0.0f;
+  }
+  const int full = VEC ? T / TILE : 0;
+  c32 y = mk(0.0f, 0.0f);  // the row's state entering the super-tile
+  int parity = 0;
+  for (int st0 = 0; st0 < T; st0 += W * TILE) {
+    const int t0 = st0 + w * TILE;
+    const bool has = t0 < T;
+    c32 A[K], u[K];
+    c32 P = mk(1.0f, 0.0f), s = mk(0.0f, 0.0f);
+    if (has) {
+      const c32 zlast = t0 > 0 ? mk(r.zr[2 * (t0 - 1)], r.zr[2 * (t0 - 1) + 1]) : mk(0.0f, 0.0f);
+      FwdIn<K> in;
+      if (t0 / TILE < full) {
+        fwd_load<K, VEC, false>(r, t0, lane, in);
+        fwd_steps<K, false>(p, c, T, t0, lane, in, zlast, A, u);
+      } else {
+        fwd_load<K, VEC, true>(r, t0, lane, in);
+        fwd_steps<K, true>(p, c, T, t0, lane, in, zlast, A, u);
+      }
+      P = A[0];
+      s = u[0];
+#pragma unroll
+      for (int k = 1; k < K; ++k) {
+        s = cmad(A[k], s, u[k]);
+        P = cmul(A[k], P);
+      }
+      wave_scan_fwd(P, s);  // inclusive prefix maps of the tile, zero entry
+      if (lane == kWave - 1) s_map[parity][w] = make_float4(P.r, P.i, s.r, s.i);
+    }
+    __syncthreads();
+    // Entry of this tile and the carry past the super-tile.
+    c32 ye = y, yr = y;
+    for (int v = 0; v < W && st0 + v * TILE < T; ++v) {
+      if (v == w) ye = yr;
+      const float4 m = s_map[parity][v];
+      yr = cmad(mk(m.x, m.y), yr, mk(m.z, m.w));
+    }
+    if (has) {
+      const c32 pex = shift_up(P, mk(1.0f, 0.0f), lane);
+      const c32 sex = shift_up(s, mk(0.0f, 0.0f), lane);
+      c32 yk = cmad(pex, ye, sex);
+      c32 out[K];
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        yk = cmad(A[k], yk, u[k]);
+        out[k] = yk;
+      }
+      if (t0 / TILE < full)
+        fwd_emit<K, VEC, false>(r, t0, lane, out);
+      else
+        fwd_emit<K, VEC, true>(r, t0, lane, out);
+    }
+    y = yr;
+    parity ^= 1;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1415,6 +1540,20 @@ void with_option_set(int opts, Fn&& fn) {
 
 void launch_fwd(const rqf_selective_inputs* in, const float* z, float* raw, float* act,
                 float* entries, int chunk, int nc, bool vec, hipStream_t s) {
+  if (RQF_FWD_ROWBLOCK) {
+    const dim3 grid((unsigned)(kXcds * in->F * ((in->B + kXcds - 1) / kXcds)));
+    const dim3 block(kFwdRbWaves * kWave);
+    with_option_set(options_of(in), [&](auto oc) {
+      constexpr int O = decltype(oc)::value;
+      if (vec)
+        hipLaunchKernelGGL((selective_fwd_rb_kernel<O, true>), grid, block, 0, s, *in, z, raw,
+                           act, entries, chunk, nc);
+      else
+        hipLaunchKernelGGL((selective_fwd_rb_kernel<O, false>), grid, block, 0, s, *in, z, raw,
+                           act, entries, chunk, nc);
+    });
+    return;
+  }
   const dim3 grid = row_grid(in), block(kRowsPerBlock * kWave);
   with_option_set(options_of(in), [&](auto oc) {
     constexpr int O = decltype(oc)::value;

@@ -159,27 +159,202 @@ __global__ __launch_bounds__(kTiWaves* kWave) void fbt_fwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// FBT forward, row-block form: a block of kTfWaves wavefronts owns one row and
+// walks it in super-tiles of kTfWaves tiles of kTfTile steps (kTfK per lane),
+// wavefront w taking tile w of each, so that concurrent wavefronts stream
+// adjacent stretches of the same rows.  Each wavefront scans its tile from a
+// zero entry and publishes the tile's map (P, s) in LDS; after one barrier it
+// composes the maps of the tiles before it onto the block's carry and replays
+// from there.  Full tiles move through a wavefront-private LDS slice (one
+// contiguous 1 KB per global instruction).  Entry carries stay at the
+// backward's kTiTile granularity.
+// ---------------------------------------------------------------------------
+#ifndef RQF_TI_FWD_RB
+#define RQF_TI_FWD_RB 1
+#endif
+#ifndef RQF_TI_FWD_K
+#define RQF_TI_FWD_K 8
+#endif
+#ifndef RQF_TI_FWD_RB_WAVES
+#define RQF_TI_FWD_RB_WAVES 8
+#endif
+constexpr int kTfK = RQF_TI_FWD_K, kTfTile = kWave * kTfK, kTfWaves = RQF_TI_FWD_RB_WAVES;
+static_assert(kTfTile % kTiTile == 0, "forward tiles hold whole carry tiles");
+
+template <bool VEC>
+__global__ __launch_bounds__(kTfWaves* kWave) void fbt_fwd_rb_kernel(
+    const float* __restrict__ c1, const float* __restrict__ tap0, const float* __restrict__ tap1,
+    const float* __restrict__ z, float* __restrict__ raw, float* __restrict__ act,
+    float* __restrict__ carry, int64_t F, int64_t B, int64_t T, int64_t nc) {
+  constexpr int K = kTfK, W = kTfWaves;
+  __shared__ float4 s_io[W][kTfTile / 2];
+  __shared__ float4 s_map[2][W];  // (P, s) of each wavefront's tile
+  const int lane = lane_id();
+  const int w = wave_id();
+  float4* io = &s_io[w][0];
+  const int64_t row = blockIdx.x;
+  const int64_t f = row / B;
+  const c32 a = ldc(c1, f), k0 = ldc(tap0, f), k1 = ldc(tap1, f);
+  const c32 apow = cpow_small(a, K);
+  const float* zr = z + 2 * row * T;
+  float* rawr = raw ? raw + 2 * row * T : nullptr;
+  float* actr = act ? act + 2 * row * T : nullptr;
+  c32 y = mk(0.0f, 0.0f);  // the row's state entering the super-tile
+  int parity = 0;
+  for (int64_t st0 = 0; st0 < T; st0 += (int64_t)W * kTfTile) {
+    const int64_t t0 = st0 + (int64_t)w * kTfTile;
+    const bool has = t0 < T;
+    const bool full = VEC && t0 + kTfTile <= T;
+    const int64_t tb = t0 + lane * K;
+    c32 u[K];
+    c32 P = mk(1.0f, 0.0f), s = mk(0.0f, 0.0f);
+    if (has) {
+      c32 zv[K];
+      if (full) {
+        load_c_lds<K>(zr, (int)t0, lane, io, zv);
+      } else {
+#pragma unroll
+        for (int k = 0; k < K; ++k) zv[k] = (tb + k < T) ? ldc(zr, tb + k) : mk(0.0f, 0.0f);
+      }
+      const c32 zlast = t0 > 0 ? ldc(zr, t0 - 1) : mk(0.0f, 0.0f);
+      const c32 zp0 = shift_up(zv[K - 1], zlast, lane);
+#pragma unroll
+      for (int k = 0; k < K; ++k) u[k] = cmad(k1, k ? zv[k - 1] : zp0, cmul(k0, zv[k]));
+      const int cnt = (int)min<int64_t>(max<int64_t>(T - tb, 0), K);
+#pragma unroll
+      for (int k = 0; k < K; ++k)
+        if (k < cnt) s = cmad(a, s, u[k]);
+      P = cnt == K ? apow : cpow_small(a, cnt);
+      wave_scan_fwd(P, s);  // inclusive prefix maps of the tile, zero entry
+      if (lane == kWave - 1) s_map[parity][w] = make_float4(P.r, P.i, s.r, s.i);
+    }
+    __syncthreads();
+    c32 ye = y, yr = y;
+    for (int v = 0; v < W && st0 + (int64_t)v * kTfTile < T; ++v) {
+      if (v == w) ye = yr;
+      const float4 m = s_map[parity][v];
+      yr = cmad(mk(m.x, m.y), yr, mk(m.z, m.w));
+    }
+    if (has) {
+      const c32 pex = shift_up(P, mk(1.0f, 0.0f), lane);
+      const c32 sex = shift_up(s, mk(0.0f, 0.0f), lane);
+      c32 yk = cmad(pex, ye, sex);
+      c32 out[K];
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        yk = cmad(a, yk, u[k]);
+        out[k] = yk;
+      }
+      if (carry) {
+        // Carry tiles of kTiTile steps: the state entering each one.
+        const int64_t c0 = t0 / kTiTile;
+        if (lane == 0) stc(carry, row * nc + c0, ye);
+        constexpr int kLanesPerCarry = kTiTile / K;
+        if (lane % kLanesPerCarry == kLanesPerCarry - 1 && lane != kWave - 1) {
+          const int64_t ci = c0 + (lane + 1) / kLanesPerCarry;
+          if (ci * kTiTile < T) stc(carry, row * nc + ci, out[K - 1]);
+        }
+      }
+      if (rawr) {
+        if (full) {
+          store_c_lds<K>(rawr, (int)t0, lane, io, out);
+        } else {
+#pragma unroll
+          for (int k = 0; k < K; ++k)
+            if (tb + k < T) stc(rawr, tb + k, out[k]);
+        }
+      }
+      if (actr) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) out[k] = relu2(out[k]);
+        if (full) {
+          store_c_lds<K>(actr, (int)t0, lane, io, out);
+        } else {
+#pragma unroll
+          for (int k = 0; k < K; ++k)
+            if (tb + k < T) stc(actr, tb + k, out[k]);
+        }
+      }
+    }
+    y = yr;
+    parity ^= 1;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Row-block backward.  A block of kRbWaves wavefronts owns one row and walks
-// it in super-tiles of kRbWaves consecutive tiles, wavefront w taking tile w
-// of each, so concurrent wavefronts stream adjacent stretches of the same
-// rows.  When the row stride is a multiple of 2 KB (T a multiple of the tile)
-// the one-row-per-wavefront form's concurrent streams sit at aliased offsets
-// and lose about 3-4%; this form does not (measured at T = 16000, 16128 and
-// 16384), and it replaces that form there.  The forward states of a tile come
-// from its stored entry (REPLAY) or from raw, so only the adjoint needs the
-// block scan: each wavefront scans its tile from a zero carry and publishes
-// the tile's suffix map (Q, r) in LDS; after one barrier every wavefront
-// composes the maps of the tiles after it onto the block's adjoint carry.
-// Map slots are double-buffered, so one barrier per super-tile suffices.
+// it in super-tiles of kRbWaves consecutive tiles of kTbTile steps (kTbK per
+// lane), wavefront w taking tile w of each, so concurrent wavefronts stream
+// adjacent stretches of the same rows; full tiles move through a
+// wavefront-private LDS slice (one contiguous 1 KB per global instruction).
+// When the row stride is a multiple of 2 KB (T a multiple of kTiTile) the
+// one-row-per-wavefront form's concurrent streams sit at aliased offsets and
+// lose 3-4%; there this form is faster (config 5 backward: 0.353 ms one row
+// per wavefront, 0.341 with 4 waves x 256-step tiles, 0.330 with 4 waves x
+// 512-step tiles through LDS, 0.390 with 8 waves x 512 steps through LDS).  On
+// unaligned rows the per-row form stays ahead (config 2: 0.353 against 0.359)
+// and is kept.  The forward states of a tile come from its stored entry
+// (REPLAY) or from raw, so only the adjoint needs the block scan: each
+// wavefront scans its tile from a zero carry and publishes the tile's suffix
+// map (Q, r) in LDS; after one barrier every wavefront composes the maps of
+// the tiles after it onto the block's adjoint carry.  Map slots are
+// double-buffered, so one barrier per super-tile suffices.
 // ---------------------------------------------------------------------------
 #ifndef RQF_TI_RB_WAVES
 #define RQF_TI_RB_WAVES 4
 #endif
-// 0 disables the row-block backward, 1 selects it for 2 KB-aligned rows.
+// 0 disables the row-block backward, 1 selects it for 2 KB-aligned rows,
+// 2 for all rows (experiments).
 #ifndef RQF_TI_ROWBLOCK
 #define RQF_TI_ROWBLOCK 1
 #endif
+#ifndef RQF_TI_BWD_K
+#define RQF_TI_BWD_K 8
+#endif
+#ifndef RQF_TI_BWD_LDS_IO
+#define RQF_TI_BWD_LDS_IO 1
+#endif
+constexpr int kTbK = RQF_TI_BWD_K, kTbTile = kWave * kTbK;
+static_assert(kTbTile % kTiTile == 0, "backward tiles start on carry tiles");
 constexpr int kRbWaves = RQF_TI_RB_WAVES;
+
+// Super-tiles are walked from the end; wavefront w takes tile w of each.
+// Complex tile of K steps per lane: full tiles through the wavefront's LDS
+// slice (RQF_TI_BWD_LDS_IO) or as lane-contiguous float4s, partial tiles
+// element by element.
+template <int K>
+__device__ __forceinline__ void ld_tile(const float* __restrict__ row, int64_t t0, int64_t tb,
+                                        int64_t T, int lane, bool full, float4* io, c32 (&v)[K]) {
+  if (full && RQF_TI_BWD_LDS_IO) {
+    load_c_lds<K>(row, (int)t0, lane, io, v);
+  } else if (full) {
+#pragma unroll
+    for (int j = 0; j < K / 2; ++j) {
+      const float4 q = *reinterpret_cast<const float4*>(row + 2 * tb + 4 * j);
+      v[2 * j] = mk(q.x, q.y);
+      v[2 * j + 1] = mk(q.z, q.w);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < K; ++k) v[k] = (tb + k < T) ? ldc(row, tb + k) : mk(0.0f, 0.0f);
+  }
+}
+template <int K>
+__device__ __forceinline__ void st_tile(float* __restrict__ row, int64_t t0, int64_t tb, int64_t T,
+                                        int lane, bool full, float4* io, const c32 (&v)[K]) {
+  if (full && RQF_TI_BWD_LDS_IO) {
+    store_c_lds<K>(row, (int)t0, lane, io, v);
+  } else if (full) {
+#pragma unroll
+    for (int j = 0; j < K / 2; ++j)
+      *reinterpret_cast<float4*>(row + 2 * tb + 4 * j) =
+          make_float4(v[2 * j].r, v[2 * j].i, v[2 * j + 1].r, v[2 * j + 1].i);
+  } else {
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (tb + k < T) stc(row, tb + k, v[k]);
+  }
+}
 
 // Super-tiles are walked from the end; wavefront w takes tile w of each.
 template <bool VEC, bool REPLAY>
@@ -188,77 +363,87 @@ __global__ __launch_bounds__(kRbWaves* kWave) void fbt_bwd_rb_kernel(
     const float* __restrict__ z, const float* __restrict__ raw, const float* __restrict__ carry,
     const float* __restrict__ gout, int mask, float* __restrict__ gz,
     double* __restrict__ partial, int64_t F, int64_t B, int64_t T, int64_t nc) {
-  __shared__ float4 s_map[2][kRbWaves];
-  __shared__ double s_part[kRbWaves][6];
+  constexpr int K = kTbK, TILE = kTbTile, W = kRbWaves;
+  __shared__ float4 s_map[2][W];
+  __shared__ double s_part[W][6];
+#if RQF_TI_BWD_LDS_IO
+  __shared__ float4 s_io[W][TILE / 2];
+#endif
   const int lane = lane_id();
   const int w = wave_id();
+#if RQF_TI_BWD_LDS_IO
+  float4* io = &s_io[w][0];
+#else
+  float4* io = nullptr;
+#endif
   const int64_t row = blockIdx.x;
   const int64_t f = row / B;
   const c32 a = ldc(c1, f), k0 = ldc(tap0, f), k1 = ldc(tap1, f);
   const c32 ac = conjg(a);
-  const c32 apow = cpow_small(a, kTiK), acpow = conjg(apow);
+  const c32 apow = cpow_small(a, K), acpow = conjg(apow);
   const float* zr = z + 2 * row * T;
   const float* rr = REPLAY ? nullptr : raw + 2 * row * T;
   const float* gr = gout + 2 * row * T;
   float* gzr = gz + 2 * row * T;
   c32 gcarry = mk(0.0f, 0.0f);  // adjoint entering the super-tile from later times
   double s1r = 0, s1i = 0, s0r = 0, s0i = 0, s2r = 0, s2i = 0;
-  const int64_t ntiles = (T + kTiTile - 1) / kTiTile;
-  const int64_t nsuper = (ntiles + kRbWaves - 1) / kRbWaves;
+  const int64_t ntiles = (T + TILE - 1) / TILE;
+  const int64_t nsuper = (ntiles + W - 1) / W;
   int parity = 0;
   for (int64_t sti = nsuper - 1; sti >= 0; --sti) {
-    const int64_t tile = sti * kRbWaves + w;
-    const int64_t t0 = tile * kTiTile;
+    const int64_t tile = sti * W + w;
+    const int64_t t0 = tile * TILE;
     const bool has = t0 < T;
-    const int64_t tb = t0 + lane * kTiK;
-    const int cnt = (int)min<int64_t>(max<int64_t>(T - tb, 0), kTiK);
-    c32 zv[kTiK], yv[kTiK], ev[kTiK];
+    const bool full = VEC && t0 + TILE <= T;
+    const int64_t tb = t0 + lane * K;
+    const int cnt = (int)min<int64_t>(max<int64_t>(T - tb, 0), K);
+    c32 zv[K], yv[K], ev[K];
     c32 zp0 = mk(0.0f, 0.0f), yp0 = mk(0.0f, 0.0f);
     c32 Q = mk(1.0f, 0.0f), r = mk(0.0f, 0.0f);
     if (has) {
-      load8<VEC>(zr, tb, T, zv);
-      load8<VEC>(gr, tb, T, ev);
+      ld_tile<K>(zr, t0, tb, T, lane, full, io, zv);
+      ld_tile<K>(gr, t0, tb, T, lane, full, io, ev);
       const c32 zprev_tile = t0 > 0 ? ldc(zr, t0 - 1) : mk(0.0f, 0.0f);
-      zp0 = shift_up(zv[kTiK - 1], zprev_tile, lane);
+      zp0 = shift_up(zv[K - 1], zprev_tile, lane);
       if (REPLAY) {
-        c32 u[kTiK];
+        c32 u[K];
 #pragma unroll
-        for (int k = 0; k < kTiK; ++k) u[k] = cmad(k1, k ? zv[k - 1] : zp0, cmul(k0, zv[k]));
-        const c32 y0 = ldc(carry, row * nc + tile);
+        for (int k = 0; k < K; ++k) u[k] = cmad(k1, k ? zv[k - 1] : zp0, cmul(k0, zv[k]));
+        const c32 y0 = ldc(carry, row * nc + t0 / kTiTile);  // carries every kTiTile steps
         c32 s = mk(0.0f, 0.0f);
 #pragma unroll
-        for (int k = 0; k < kTiK; ++k)
+        for (int k = 0; k < K; ++k)
           if (k < cnt) s = cmad(a, s, u[k]);
-        c32 P = cnt == kTiK ? apow : cpow_small(a, cnt);
+        c32 P = cnt == K ? apow : cpow_small(a, cnt);
         if (lane == 0) s = cmad(P, y0, s);
         wave_scan_fwd(P, s);
         c32 yk = shift_up(s, y0, lane);
         yp0 = yk;
 #pragma unroll
-        for (int k = 0; k < kTiK; ++k) {
+        for (int k = 0; k < K; ++k) {
           yk = cmad(a, yk, u[k]);
           yv[k] = yk;
         }
       } else {
-        load8<VEC>(rr, tb, T, yv);
+        ld_tile<K>(rr, t0, tb, T, lane, full, io, yv);
         const c32 rprev_tile = t0 > 0 ? ldc(rr, t0 - 1) : mk(0.0f, 0.0f);
-        yp0 = shift_up(yv[kTiK - 1], rprev_tile, lane);
+        yp0 = shift_up(yv[K - 1], rprev_tile, lane);
       }
       if (mask) {
 #pragma unroll
-        for (int k = 0; k < kTiK; ++k) ev[k] = mask_by(ev[k], yv[k]);
+        for (int k = 0; k < K; ++k) ev[k] = mask_by(ev[k], yv[k]);
       }
       // Suffix composition of g -> e + conj(a) g over the lane's valid steps.
 #pragma unroll
-      for (int k = kTiK - 1; k >= 0; --k)
+      for (int k = K - 1; k >= 0; --k)
         if (k < cnt) r = cmad(ac, r, ev[k]);
-      Q = cnt == kTiK ? acpow : conjg(cpow_small(a, cnt));
+      Q = cnt == K ? acpow : conjg(cpow_small(a, cnt));
       wave_scan_rev(Q, r, lane);  // inclusive suffix over lanes, zero carry
     }
     if (lane == 0) s_map[parity][w] = make_float4(Q.r, Q.i, r.r, r.i);
     __syncthreads();
     c32 gin = gcarry;  // adjoint entering this tile from its end
-    for (int v = kRbWaves - 1; v > w; --v) {
+    for (int v = W - 1; v > w; --v) {
       const float4 m = s_map[parity][v];
       gin = cmad(mk(m.x, m.y), gin, mk(m.z, m.w));
     }
@@ -269,10 +454,10 @@ __global__ __launch_bounds__(kRbWaves* kWave) void fbt_bwd_rb_kernel(
     }
     if (has) {
       c32 gnext = shift_down(cmad(Q, gin, r), gin, lane);
-      c32 go[kTiK];
+      c32 go[K];
       float a1r = 0, a1i = 0, a0r = 0, a0i = 0, a2r = 0, a2i = 0;
 #pragma unroll
-      for (int k = kTiK - 1; k >= 0; --k) {
+      for (int k = K - 1; k >= 0; --k) {
         const c32 g = cmad(ac, gnext, ev[k]);
         go[k] = cjmad(k1, gnext, cjmul(k0, g));
         const c32 yp = k ? yv[k - 1] : yp0;
@@ -287,7 +472,7 @@ __global__ __launch_bounds__(kRbWaves* kWave) void fbt_bwd_rb_kernel(
         a2i += in ? t2.i : 0.0f;
         gnext = g;
       }
-      store8<VEC>(gzr, tb, T, go);
+      st_tile<K>(gzr, t0, tb, T, lane, full, io, go);
       s1r += a1r;
       s1i += a1i;
       s0r += a0r;
@@ -306,7 +491,7 @@ __global__ __launch_bounds__(kRbWaves* kWave) void fbt_bwd_rb_kernel(
   __syncthreads();
   if (threadIdx.x < 6) {
     double t = 0.0;
-    for (int v = 0; v < kRbWaves; ++v) t += s_part[v][threadIdx.x];
+    for (int v = 0; v < W; ++v) t += s_part[v][threadIdx.x];
     partial[6 * row + threadIdx.x] = t;
   }
 }
@@ -698,6 +883,16 @@ int fbt_fwd(const float* c1, const float* t0, const float* t1, const float* z, f
   if (!aligned8(z) || !aligned8(raw) || !aligned8(act) || !aligned8(carry)) return RQF_ERR_ALIGN;
   const int64_t nc = (T + kTiTile - 1) / kTiTile;
   const bool vec = T % 2 == 0 && aligned16(z) && aligned16(raw) && aligned16(act);
+  if (RQF_TI_FWD_RB) {
+    const dim3 grid((unsigned)R), block(kTfWaves * kWave);
+    if (vec)
+      hipLaunchKernelGGL(fbt_fwd_rb_kernel<true>, grid, block, 0, s, c1, t0, t1, z, raw, act, carry,
+                         F, B, T, nc);
+    else
+      hipLaunchKernelGGL(fbt_fwd_rb_kernel<false>, grid, block, 0, s, c1, t0, t1, z, raw, act,
+                         carry, F, B, T, nc);
+    return launch_status();
+  }
   const dim3 grid((unsigned)((R + kTiWaves - 1) / kTiWaves)), block(kTiWaves * kWave);
   if (vec)
     hipLaunchKernelGGL(fbt_fwd_kernel<true>, grid, block, 0, s, c1, t0, t1, z, raw, act, carry, F,
@@ -727,7 +922,7 @@ int fbt_bwd(const float* c1, const float* t0, const float* t1, const float* z, c
   if (R > 0 && T > 0) {
     const int64_t nc = (T + kTiTile - 1) / kTiTile;
     const bool vec = T % 2 == 0 && aligned16(z) && aligned16(raw) && aligned16(gout) && aligned16(gz);
-    const bool rowblock = RQF_TI_ROWBLOCK && T % kTiTile == 0;
+    const bool rowblock = RQF_TI_ROWBLOCK == 2 || (RQF_TI_ROWBLOCK == 1 && T % kTiTile == 0);
     const dim3 grid = rowblock ? dim3((unsigned)R)
                                : dim3((unsigned)((R + kTiWaves - 1) / kTiWaves));
     const dim3 block = rowblock ? dim3(kRbWaves * kWave) : dim3(kTiWaves * kWave);

@@ -206,7 +206,7 @@ def plan_selective(cfg, args, dev):
         nbytes[f"rqf_selective_fwd[L{li}]"] = fb
         nbytes[f"rqf_selective_bwd[L{li}]"] = bb
     kernels = {
-        "rqf_selective_fwd": "selective_fwd_kernel",
+        "rqf_selective_fwd": "selective_fwd_rb_kernel",
         "rqf_selective_bwd": ("team_build_kernel + selective_bwd_team_kernel + "
                               "team_reduce_kernel + partial_reduce_kernel"),
     }
@@ -282,8 +282,9 @@ def plan_fbt(cfg, args, dev):
     for li in range(L):
         nbytes[f"rqf_fbt_recompute_fwd[L{li}]"] = fb
         nbytes[f"rqf_fbt_recompute_bwd[L{li}]"] = bb
-    kernels = {"rqf_fbt_recompute_fwd": "fbt_fwd_kernel",
-               "rqf_fbt_recompute_bwd": "fbt_bwd_kernel<replay> + coef_reduce_kernel"}
+    kernels = {"rqf_fbt_recompute_fwd": "fbt_fwd_rb_kernel",
+               "rqf_fbt_recompute_bwd": ("fbt_bwd_rb_kernel<replay> (T % 256 == 0) or "
+                                         "fbt_bwd_kernel<replay>, + coef_reduce_kernel")}
     config = {"workload": name, "F": F, "B": B, "T": T, "layers": L,
               "contract": "split-ReLU output, per-tile carries; gy cotangent, full BPTT"}
     cpu_steps = args.cpu_steps or (1000 if cfg == 2 else 500)

@@ -48,7 +48,9 @@ def _args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5, 6, 7],
+                    help="1-5: BASELINE.json configs; 6: multi-oscillator C-weighted scan; "
+                         "7: fused |y| readout scan")
     ap.add_argument("--cpu-baseline", dest="cpu", action="store_true", default=True)
     ap.add_argument("--no-cpu-baseline", dest="cpu", action="store_false")
     ap.add_argument("--cpu-steps", type=int, default=0,
@@ -56,7 +58,7 @@ def _args():
     ap.add_argument("--batch", type=int, default=0,
                     help="override the config's batch size (experiments only)")
     ap.add_argument("--seq-len", type=int, default=0,
-                    help="override the FBT configs' sequence length (experiments only)")
+                    help="override the config's sequence length (experiments only)")
     ap.add_argument("--act-only", action="store_true",
                     help="config 3 with the act-only contract (no raw output, no gy)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -151,6 +153,9 @@ def plan_selective(cfg, args, dev):
     if args.batch:
         B = args.batch
         name += f" [batch overridden to {B}]"
+    if args.seq_len:
+        T = args.seq_len
+        name += f" [sequence length overridden to {T}]"
     chunk = 256
     g = torch.Generator(device=dev).manual_seed(1)
     state = {}
@@ -349,6 +354,77 @@ def plan_chunked(cfg, args, dev):
     return Plan(name, config, N * L, (state, ops), nbytes, kernels, cpu, config["contract"])
 
 
+def plan_multi_osc(cfg, args, dev):
+    """Config 6: RQF-S4-style multi-oscillator scan (N = 4 oscillators per filter,
+    complex C-weights), fwd + bwd.  Config 7: the fused |y| readout
+    (``sequential_scan_abs``) of a single-oscillator scan on real input, forward
+    only (an inference path).  Both on the raw-waveform shape of config 2."""
+    import torch
+
+    from prospective_rqf_amd import multi_osc_scan as mo
+    from prospective_rqf_amd import workloads
+
+    B, T, F = 32, 16000, 128
+    N = 4 if cfg == 6 else 1
+    if args.batch:
+        B = args.batch
+    if args.seq_len:
+        T = args.seq_len
+    g = torch.Generator().manual_seed(6)
+    r = 0.9 + 0.0999 * torch.rand(F * N, generator=g, dtype=torch.float64)
+    ph = math.pi * torch.rand(F * N, generator=g, dtype=torch.float64)
+    c1 = torch.polar(r, ph)
+    a = torch.log(c1)
+    c2 = (-a.real * (c1 - 1) / a).to(torch.complex64).to(dev)  # ZOH gain with a = log C1
+    c1 = c1.to(torch.complex64).to(dev)
+    cw = torch.randn(F * N, 2, generator=g).to(dev)
+    wave = workloads.raw_waveform(B, T, samp=16000.0, generator=g)  # (B, T)
+    gain = torch.randn(F, generator=g)
+    state = {}
+    if cfg == 6:
+        name = ("multi-oscillator C-weighted scan, N=4 oscillators x 128 filters, "
+                "B=32 T=16000, complex input (config 6)")
+        state["u"] = (wave[:, :, None] * gain).to(torch.complex64).to(dev)
+        state["gy"] = workloads.randn_c64(B, T, F, generator=g).to(dev)
+
+        def fwd(st):
+            st["y"] = mo._sequential_scan_multi_osc_forward_raw(c1, c2, st["u"], cw[:, 0],
+                                                                cw[:, 1], N)
+
+        def bwd(st):
+            st["grads"] = mo._sequential_scan_multi_osc_backward_raw(c1, c2, st["u"], cw,
+                                                                     st["gy"], N)
+
+        ops = [("rqf_multi_osc_fwd", fwd), ("rqf_multi_osc_bwd", bwd)]
+        elems = B * T * F
+        nbytes = {"rqf_multi_osc_fwd": 16 * elems, "rqf_multi_osc_bwd": 24 * elems}
+        kernels = {"rqf_multi_osc_fwd": "mosc_fwd_local + mosc_carry + mosc_fwd_final",
+                   "rqf_multi_osc_bwd": ("mosc_fwd_local + mosc_carry + mosc_bwd_local + "
+                                         "mosc_carry + mosc_bwd_final + mosc_coef_reduce")}
+        contract = "complex u in, complex y out; grad_u + grad_C1/C2/c_weights"
+    else:
+        name = ("fused |y| readout: single-oscillator scan on real input, 128 filters, "
+                "B=32 T=16000, forward only (config 7)")
+        state["u"] = (wave[:, :, None] * gain).to(torch.float32).to(dev)
+
+        def fwd(st):
+            st["y"] = mo._sequential_scan_real_forward_abs_raw_block_f(c1, c2, st["u"])
+
+        ops = [("rqf_multi_osc_fwd[abs]", fwd)]
+        elems = B * T * F
+        nbytes = {"rqf_multi_osc_fwd[abs]": 8 * elems}
+        kernels = {"rqf_multi_osc_fwd": "mosc_fwd_local + mosc_carry + mosc_fwd_final<abs>"}
+        contract = "real u in, |y| real out, no autograd"
+    config = {"workload": name, "F": F, "B": B, "T": T, "oscillators": N, "layers": 1,
+              "contract": contract}
+
+    def cpu():
+        return cpu_baseline_multi_osc(F, N, B, args.cpu_steps or 500, c1.cpu(), c2.cpu(),
+                                      cw.cpu(), absolute=cfg == 7)
+
+    return Plan(name, config, elems, (state, ops), nbytes, kernels, cpu, contract)
+
+
 # ---------------------------------------------------------------------------
 # CPU baselines: fp32 PyTorch restatement of the reference CPU path
 # ---------------------------------------------------------------------------
@@ -472,6 +548,47 @@ def cpu_baseline_timeinv(F, B, steps, L, *, prospective, coef, btf=None):
     }
 
 
+def cpu_baseline_multi_osc(F, N, B, steps, c1, c2, cw, *, absolute):
+    """The reference's unfused CPU path for the multi-oscillator scan: expand the
+    input over the oscillators, `_sequential_scan_cpu`, C-weighted sum
+    (block.py:599-630, 766-785); fwd + autograd bwd, or |y| forward only."""
+    import torch
+
+    from oracle import torch_ref
+    from prospective_rqf_amd import workloads
+
+    threads = _cpu_threads()
+    g = torch.Generator().manual_seed(2)
+    u = workloads.randn_c64(B, steps, F, generator=g)
+    cot = workloads.randn_c64(B, steps, F, generator=g)
+    cwc = torch.view_as_complex(cw.contiguous())
+
+    def run():
+        uu = u.clone().requires_grad_(not absolute)
+        cc = c1.clone().requires_grad_(not absolute)
+        x = torch_ref.sequential_scan(cc, c2, uu.repeat_interleave(N, dim=-1))
+        y = (x.view(B, steps, F, N) * cwc.view(F, N)).sum(-1) if N > 1 else x
+        if absolute:
+            y.abs()
+        else:
+            (cot.conj() * y).real.sum().backward()
+
+    with torch.set_grad_enabled(not absolute):
+        t = _median_time(run)
+    what = ("expand + _sequential_scan_cpu + C-weighted sum, fwd + autograd bwd" if not absolute
+            else "_sequential_scan_cpu(...).abs(), forward")
+    return {
+        "value": F * B * steps / t / 1e9,
+        "unit": "Gelem/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"fp32 PyTorch restatement of {what} (oracle/torch_ref.py), (B,T,F) layout, "
+                   f"N={N} oscillators, F={F} B={B} T={steps} (T reduced), median of 3 after 1 "
+                   f"warm-up; torch threads={threads}, os.cpu_count()={os.cpu_count()}, "
+                   f"cpu={_cpu_model()}"),
+    }
+
+
 # ---------------------------------------------------------------------------
 # Traffic table (rocprofv3 FETCH_SIZE / WRITE_SIZE, committed under profiles/)
 # ---------------------------------------------------------------------------
@@ -518,6 +635,8 @@ def main():
         plan = plan_selective(cfg, args, dev)
     elif cfg in (2, 5):
         plan = plan_fbt(cfg, args, dev)
+    elif cfg in (6, 7):
+        plan = plan_multi_osc(cfg, args, dev)
     else:
         plan = plan_chunked(cfg, args, dev)
     state, ops = plan.ops

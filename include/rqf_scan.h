@@ -89,6 +89,42 @@ int rqf_chunked_prospective_bwd(const float *c1, const float *tap0, const float 
                                 rqf_stream_t stream);
 
 /* ------------------------------------------------------------------------ *
+ * Multi-oscillator scans with C-weight reduction, and the |y| readout       *
+ * (BTF layout).  N oscillators per filter f (1 <= N <= 8), index f*N + n:   *
+ *   x_n[t] = C1_n*x_n[t-1] + C2_n*u[t]                                      *
+ *   y[t]   = sum_n cw_n*x_n[t]          (cw NULL: y = x_0, requires N = 1)  *
+ * c1, c2, cw: (F*N,) complex (cw is the reference's real (F*N, 2) view).    *
+ * u: (B,T,F) complex, or real when u_real != 0.                            *
+ * ------------------------------------------------------------------------ */
+
+/* Workspace bytes of rqf_multi_osc_fwd (backward = 0) or _bwd (backward = 1);
+ * 0 for N outside [1, 8]. */
+size_t rqf_multi_osc_workspace(int64_t B, int64_t T, int64_t F, int64_t N, int32_t backward);
+
+/* Replaces `_sequential_scan_multi_osc_kernel[grid](...)` with EPILOGUE 0 / 1
+ * (rqf_models/ops/triton_scan_kernel.py:1991-2015 and its abs and real-input
+ * twins, :2019-2087, :2688-2760), and, with cw NULL and N = 1, the fused |y|
+ * scan of `sequential_scan_abs` (rqf_models/ops/scan.py:381-432).
+ * out: (B,T,F) complex, or real |y| when out_abs != 0. */
+int rqf_multi_osc_fwd(const float *c1, const float *c2, const float *cw, const float *u,
+                      int32_t u_real, float *out, int32_t out_abs, int64_t B, int64_t T,
+                      int64_t F, int64_t N, void *workspace, size_t workspace_bytes,
+                      rqf_stream_t stream);
+
+/* Replaces `_sequential_scan_multi_osc_backward_kernel[grid](...)` and its
+ * real-input twin (rqf_models/ops/triton_scan_kernel.py:2370-2404, :2880):
+ *   d_n[t] = conj(C1_n) d_n[t+1] + conj(cw_n) grad_out[t]
+ *   grad_u = sum_n conj(C2_n) d_n (real part for real u),
+ *   grad_c1_n = sum d_n[t] conj(x_n[t-1]), grad_c2_n = sum d_n conj(u),
+ *   grad_cw_n = sum grad_out conj(x_n)   (each (F*N,) complex, overwritten).
+ * Any of grad_u / grad_c1 / grad_c2 / grad_cw may be NULL (not computed). */
+int rqf_multi_osc_bwd(const float *c1, const float *c2, const float *cw, const float *u,
+                      int32_t u_real, const float *grad_out, float *grad_u, float *grad_c1,
+                      float *grad_c2, float *grad_cw, int64_t B, int64_t T, int64_t F,
+                      int64_t N, void *workspace, size_t workspace_bytes,
+                      rqf_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
  * Two-tap prospective scans in channel-outermost FBT layout.               *
  *   raw[t] = C1*raw[t-1] + tap0*z[t] + tap1*z[t-1]                          *
  *   act    = relu(Re raw) + i relu(Im raw)                                  *

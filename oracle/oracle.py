@@ -102,6 +102,41 @@ def twotap_bwd(c1, k0, k1, x, y, gy, layout=BTF, mask_act=False):
 
 
 # --------------------------------------------------------------------------
+# multi-oscillator scan with C-weight reduction (BTF)
+# --------------------------------------------------------------------------
+
+
+def mosc_fwd(c1, c2, cw, u, num_osc):
+    """``(y, |y|)`` of x_n[t] = c1_n x_n[t-1] + c2_n u[t], y = sum_n cw_n x_n
+    (``cw=None``: y = x_0 with one oscillator).  ``u`` is (B,T,F)."""
+    u = _c(u)
+    B, T, F = u.shape
+    c1, c2 = _c(c1), _c(c2)
+    cw = None if cw is None else _c(cw)
+    y = np.empty_like(u)
+    yabs = np.empty(u.shape, np.float64)
+    lib().orc_mosc_fwd(ctypes.c_int64(B), ctypes.c_int64(T), ctypes.c_int64(F),
+                       ctypes.c_int64(num_osc), _p(c1), _p(c2), _p(cw), _p(u), _p(y), _p(yabs))
+    return y, yabs
+
+
+def mosc_bwd(c1, c2, cw, u, gy, num_osc):
+    """Adjoint of :func:`mosc_fwd`: ``(gu, gc1, gc2, gcw)`` (gu complex (B,T,F);
+    the coefficient gradients (F*N,) complex)."""
+    u, gy = _c(u), _c(gy)
+    B, T, F = u.shape
+    c1, c2, cw = _c(c1), _c(c2), _c(cw)
+    gu = np.empty_like(u)
+    gc1 = np.empty(F * num_osc, np.complex128)
+    gc2 = np.empty_like(gc1)
+    gcw = np.empty_like(gc1)
+    lib().orc_mosc_bwd(ctypes.c_int64(B), ctypes.c_int64(T), ctypes.c_int64(F),
+                       ctypes.c_int64(num_osc), _p(c1), _p(c2), _p(cw), _p(u), _p(gy), _p(gu),
+                       _p(gc1), _p(gc2), _p(gcw))
+    return gu, gc1, gc2, gcw
+
+
+# --------------------------------------------------------------------------
 # selective scan
 # --------------------------------------------------------------------------
 

@@ -15,6 +15,14 @@
  *       (rqf_models/ops/fbt_scan_kernel.py:130-146), including the split-ReLU
  *       mask convention relu'(0) = 0 (fbt_scan_kernel.py:180-185).
  *
+ *   multi-oscillator scan with C-weight reduction (BTF)
+ *     - x_n[t] = C1_n x_n[t-1] + C2_n u[t], y[t] = sum_n cw_n x_n[t]:
+ *       `_sequential_scan_multi_osc_kernel` (rqf_models/ops/triton_scan_kernel.py:1826-1940),
+ *       the same as the expand -> scan -> C-weighted sum of
+ *       `_scan_standard_fallback` / `_c_weighted_sum` (rqf_models/backbones/rqf/block.py:599-630)
+ *     - adjoint and gradients of `_sequential_scan_multi_osc_backward_kernel`
+ *       (triton_scan_kernel.py:2089-2279)
+ *
  *   selective scan
  *     - coefficients: `selective_coefficients` (rqf_models/ops/selective_scan.py:26-68)
  *     - recurrence:   `reference_layer_scan`   (rqf_models/ops/selective_scan.py:71-104)
@@ -115,6 +123,78 @@ void orc_twotap_bwd(int layout, int64_t B, int64_t T, int64_t F, const double *c
             acc(gk0, f, s0);
             if (gk1) acc(gk1, f, sk1);
         }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Multi-oscillator scan with C-weight reduction (BTF layout)                */
+/* ------------------------------------------------------------------------ */
+
+/* N oscillators per filter f, coefficient index f*N + n:
+ *   x_n[t] = c1_n x_n[t-1] + c2_n u[t],   y[t] = sum_n cw_n x_n[t]
+ * cw NULL means y = x_0 (N = 1).  u, y: (B,T,F) complex; yabs (nullable)
+ * receives |y|; y may be NULL when only yabs is wanted. */
+void orc_mosc_fwd(int64_t B, int64_t T, int64_t F, int64_t N, const double *c1,
+                  const double *c2, const double *cw, const double *u, double *y,
+                  double *yabs) {
+    cd *x = calloc((size_t)N, sizeof(cd));
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t f = 0; f < F; ++f) {
+            for (int64_t n = 0; n < N; ++n) x[n] = 0;
+            for (int64_t t = 0; t < T; ++t) {
+                int64_t i = (b * T + t) * F + f;
+                cd ut = ld(u, i), out = 0;
+                for (int64_t n = 0; n < N; ++n) {
+                    x[n] = ld(c1, f * N + n) * x[n] + ld(c2, f * N + n) * ut;
+                    out += cw ? ld(cw, f * N + n) * x[n] : (n == 0 ? x[0] : 0);
+                }
+                if (y) st(y, i, out);
+                if (yabs) yabs[i] = cabs(out);
+            }
+        }
+    free(x);
+}
+
+/* Adjoint of orc_mosc_fwd (cw required) for the cotangent gy on y:
+ *   d_n[t] = conj(c1_n) d_n[t+1] + conj(cw_n) gy[t]
+ *   gu[t]  = sum_n conj(c2_n) d_n[t]
+ *   gc1_n  = sum_{b,t} d_n[t] conj(x_n[t-1]),  gc2_n = sum d_n[t] conj(u[t]),
+ *   gcw_n  = sum gy[t] conj(x_n[t])
+ * Forward states are recomputed and kept per row (T*N complex). */
+void orc_mosc_bwd(int64_t B, int64_t T, int64_t F, int64_t N, const double *c1,
+                  const double *c2, const double *cw, const double *u, const double *gy,
+                  double *gu, double *gc1, double *gc2, double *gcw) {
+    memset(gc1, 0, sizeof(double) * 2 * F * N);
+    memset(gc2, 0, sizeof(double) * 2 * F * N);
+    memset(gcw, 0, sizeof(double) * 2 * F * N);
+    cd *xs = malloc(sizeof(cd) * (size_t)(T * N + 1));
+    cd *d = calloc((size_t)N, sizeof(cd));
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t f = 0; f < F; ++f) {
+            for (int64_t n = 0; n < N; ++n) {
+                cd x = 0;
+                for (int64_t t = 0; t < T; ++t) {
+                    x = ld(c1, f * N + n) * x + ld(c2, f * N + n) * ld(u, (b * T + t) * F + f);
+                    xs[t * N + n] = x;
+                }
+                d[n] = 0;
+            }
+            for (int64_t t = T - 1; t >= 0; --t) {
+                int64_t i = (b * T + t) * F + f;
+                cd g = ld(gy, i), ut = ld(u, i), gsum = 0;
+                for (int64_t n = 0; n < N; ++n) {
+                    int64_t k = f * N + n;
+                    d[n] = conj(ld(c1, k)) * d[n] + conj(ld(cw, k)) * g;
+                    gsum += conj(ld(c2, k)) * d[n];
+                    cd xprev = t ? xs[(t - 1) * N + n] : 0;
+                    acc(gc1, k, d[n] * conj(xprev));
+                    acc(gc2, k, d[n] * conj(ut));
+                    acc(gcw, k, g * conj(xs[t * N + n]));
+                }
+                st(gu, i, gsum);
+            }
+        }
+    free(d);
+    free(xs);
 }
 
 /* ------------------------------------------------------------------------ */

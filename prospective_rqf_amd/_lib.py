@@ -52,6 +52,12 @@ SIGNATURES = {
         ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
     "rqf_chunked_prospective_bwd": (
         ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
+    "rqf_multi_osc_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I32]),
+    "rqf_multi_osc_fwd": (
+        ctypes.c_int, [_P, _P, _P, _P, _I32, _P, _I32, _I64, _I64, _I64, _I64, _P, _SZ, _P]),
+    "rqf_multi_osc_bwd": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _SZ, _P]),
     "rqf_fbt_carry_chunks": (_I64, [_I64]),
     "rqf_fbt_workspace": (_SZ, [_I64, _I64, _I64]),
     "rqf_fbt_prospective_fwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),

@@ -4,11 +4,12 @@
 //
 // Two families:
 //
-// FBT (channel-outermost, rows contiguous in time): one wavefront per
-// (channel, batch) row, tiles of 64*K steps (K = 4), lane l holding K
-// consecutive steps (float4 loads).  Tile = lane-serial composition -> DPP wave scan
-// -> lane-serial replay, as in the selective kernels.  The backward runs the
-// adjoint g[t] = e[t] + conj(c1) g[t+1] the same way in suffix order and
+// FBT (channel-outermost, rows contiguous in time): tiles of 64*K steps, lane
+// l holding K consecutive steps.  Tile = lane-serial composition -> DPP wave
+// scan -> lane-serial replay, as in the selective kernels.  The forward runs
+// row blocks (8 wavefronts per row, K = 8); the backward runs one row per
+// wavefront (K = 4), or row blocks on 2 KB-aligned rows.  The backward runs
+// the adjoint g[t] = e[t] + conj(c1) g[t+1] the same way in suffix order and
 // keeps raw[t-1] and g[t+1] in registers, so it needs none of the
 // reference's divisions by c1 (fbt_scan_kernel.py:157-160, 518-521).
 //
@@ -33,9 +34,11 @@ namespace {
 #define RQF_TI_PREFETCH 1
 #endif
 
-// Steps per lane.  4 (a 32-byte stretch per lane, 2 KB per wavefront load)
-// streams faster than 8 (64 bytes per lane) on gfx950: wider per-lane
-// stretches make each load instruction's footprint sparser.
+// Steps per lane of the one-row-per-wavefront kernels.  4 (a 32-byte stretch
+// per lane, 2 KB per wavefront load) streams faster than 8 (64 bytes per
+// lane) on gfx950: wider per-lane stretches make each load instruction's
+// footprint sparser.  (The row-block kernels move full tiles through LDS, one
+// contiguous 1 KB per instruction, and use K = 8.)
 #ifndef RQF_TI_K
 #define RQF_TI_K 4
 #endif

@@ -1,8 +1,9 @@
 """Dispatch surface of the time-invariant scans, honouring the reference's flags.
 
 Mirrors rqf_models/ops/scan.py: the import-time flags (:38-70),
-``sequential_scan`` (:290-378) and ``parallel_scan`` (:435-529) for the
-scalar (``B is None``) case that the chunked kernel serves.
+``sequential_scan`` (:290-378), ``sequential_scan_abs`` (:381-432) and
+``parallel_scan`` (:435-529) for the scalar (``B is None``) case that the
+HIP kernels serve.
 
 Flags (read at import, like the reference):
   ORGANICS_SCAN_BACKEND=chunked|sequential  -> ``_SCAN_BACKEND``, ``_USE_CHUNKED``
@@ -73,6 +74,37 @@ def sequential_scan(C1, C2, u, B=None):
     """x[n] = C1 x[n-1] + C2 u[n] on (batch, time, filters) -> complex64."""
     _require_served(u, B)
     return _triton_chunked_scan(*_prepare(C1, C2, u))
+
+
+def sequential_scan_abs(C1, C2, u, B=None):
+    """``|sequential_scan(C1, C2, u)|`` as real (batch, time, filters) (scan.py:381-432).
+
+    Without autograd the magnitude is fused into the scan's output store
+    (``rqf_multi_osc_fwd`` with one oscillator and no C-weights), reading a
+    real ``u`` as real.  When any input requires grad the reference composes
+    ``sequential_scan(...).abs()``, and so does this.
+    """
+    _require_served(u, B)
+    needs_grad = torch.is_grad_enabled() and (u.requires_grad or C1.requires_grad
+                                              or C2.requires_grad)
+    if needs_grad:
+        return sequential_scan(C1, C2, u).abs()
+    from prospective_rqf_amd.multi_osc_scan import (
+        _sequential_scan_forward_abs_raw_block_f,
+        _sequential_scan_real_forward_abs_raw_block_f,
+    )
+
+    if not C1.is_complex():
+        C1 = C1.to(torch.cfloat)
+    if not C2.is_complex():
+        C2 = C2.to(torch.cfloat)
+    _, _, in_filters = u.shape
+    num_filters = C1.shape[0]
+    if in_filters == 1 and num_filters > 1:
+        u = u.expand(-1, -1, num_filters).contiguous()
+    if u.is_complex():
+        return _sequential_scan_forward_abs_raw_block_f(C1, C2, u)
+    return _sequential_scan_real_forward_abs_raw_block_f(C1, C2, u)
 
 
 def parallel_scan(C1, C2, u, B=None):

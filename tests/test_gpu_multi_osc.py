@@ -1,0 +1,170 @@
+"""GPU parity of the multi-oscillator scans and the fused |y| readout.
+
+Compares ``rqf_multi_osc_fwd`` / ``rqf_multi_osc_bwd`` (through the reference's
+Python names) with the fp64 oracle, for complex and real inputs, one to eight
+oscillators, segment edges (T below, at and above the 256-step segment bound)
+and the autograd boundaries, including the ``needs_input_grad`` gating the
+reference's kernels implement (triton_scan_kernel.py:2280-2410).  Bar:
+normwise max relative error <= 1e-4 per output and gradient tensor.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from prospective_rqf_amd import multi_osc_scan as mo
+from prospective_rqf_amd import scan as hip_scan
+from tests.helpers import PARITY_RTOL, crandn, relerr
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+
+
+def _c64(a):
+    return np.asarray(a, dtype=np.complex64).astype(np.complex128)
+
+
+def _problem(rng, B, T, F, N, real):
+    c1 = _c64(rng.uniform(0.7, 0.995, F * N) * np.exp(1j * rng.uniform(0, 2 * np.pi, F * N)))
+    c2 = _c64(0.5 * crandn(rng, F * N))
+    cw = _c64(crandn(rng, F * N))
+    u = rng.standard_normal((B, T, F)) if real else crandn(rng, B, T, F)
+    u = np.asarray(u, np.float32).astype(np.float64) if real else _c64(u)
+    return c1, c2, cw, u
+
+
+def _t(a, grad=False):
+    if np.iscomplexobj(a):
+        t = torch.as_tensor(a.astype(np.complex64), device="cuda")
+    else:
+        t = torch.as_tensor(a.astype(np.float32), device="cuda")
+    return t.requires_grad_(grad)
+
+
+def _cw_param(cw, grad=False):
+    return torch.as_tensor(np.stack([cw.real, cw.imag], -1).astype(np.float32),
+                           device="cuda").requires_grad_(grad)
+
+
+SHAPES = [(2, 1, 5), (2, 37, 3), (3, 256, 4), (2, 257, 3), (1, 1000, 2), (4, 3000, 64),
+          (2, 600, 130)]
+
+
+@pytest.mark.parametrize("real", [False, True])
+@pytest.mark.parametrize("N", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_multi_osc_forward_backward(shape, N, real):
+    B, T, F = shape
+    print(f"case: multi-osc {shape} N={N} real={real}", flush=True)
+    rng = np.random.default_rng(B * 1000 + T * 10 + F + N)
+    c1, c2, cw, u = _problem(rng, B, T, F, N, real)
+    gy = _c64(crandn(rng, B, T, F))
+    y_ref, yabs_ref = oracle.mosc_fwd(c1, c2, cw, u, N)
+    gu_ref, gc1_ref, gc2_ref, gcw_ref = oracle.mosc_bwd(c1, c2, cw, u, gy, N)
+    C1, C2, U, CW = _t(c1, True), _t(c2, True), _t(u, True), _cw_param(cw, True)
+    fn = mo._triton_sequential_scan_multi_osc_real if real else mo._triton_sequential_scan_multi_osc
+    y = fn(C1, C2, U, CW, N)
+    assert y.dtype == torch.complex64 and y.shape == (B, T, F)
+    y.backward(_t(gy))
+    gcw_got = CW.grad[:, 0].double() + 1j * CW.grad[:, 1].double()
+    errs = {"y": relerr(y, y_ref), "gc1": relerr(C1.grad, gc1_ref),
+            "gc2": relerr(C2.grad, gc2_ref), "gcw": relerr(gcw_got.cpu(), gcw_ref),
+            "gu": relerr(U.grad, gu_ref.real if real else gu_ref)}
+    assert U.grad.dtype == U.dtype
+    with torch.no_grad():
+        if real:
+            yabs = mo._sequential_scan_multi_osc_real_forward_abs_raw(C1, C2, U, CW, N)
+        else:
+            yabs = mo._sequential_scan_multi_osc_forward_abs_raw(C1, C2, U, CW[:, 0], CW[:, 1], N)
+    assert yabs.dtype == torch.float32
+    errs["|y|"] = relerr(yabs, yabs_ref)
+    bad = {k: v for k, v in errs.items() if not v <= PARITY_RTOL}
+    assert not bad, errs
+
+
+def test_needs_input_grad_gating_and_parallel_alias():
+    rng = np.random.default_rng(5)
+    B, T, F, N = 2, 300, 6, 4
+    c1, c2, cw, u = _problem(rng, B, T, F, N, False)
+    gy = _c64(crandn(rng, B, T, F))
+    gu_ref, gc1_ref, gc2_ref, gcw_ref = oracle.mosc_bwd(c1, c2, cw, u, gy, N)
+    # frozen recurrence: only u and the C-weights need gradients
+    C1, C2, U, CW = _t(c1), _t(c2), _t(u, True), _cw_param(cw, True)
+    y = mo._triton_parallel_scan_multi_osc(C1, C2, U, CW, N)
+    y.backward(_t(gy))
+    assert C1.grad is None and C2.grad is None
+    assert relerr(U.grad, gu_ref) <= PARITY_RTOL
+    gcw_got = CW.grad[:, 0].double() + 1j * CW.grad[:, 1].double()
+    assert relerr(gcw_got.cpu(), gcw_ref) <= PARITY_RTOL
+    # raw backward with only grad_C1 requested
+    g = mo._sequential_scan_multi_osc_backward_raw(_t(c1), _t(c2), _t(u), _cw_param(cw), _t(gy),
+                                                   N, compute_grad_C2=False, compute_grad_u=False,
+                                                   compute_grad_cw=False)
+    assert g[1] is None and g[2] is None and g[3] is None
+    assert relerr(g[0], gc1_ref) <= PARITY_RTOL
+    assert mo._sequential_scan_multi_osc_backward_raw(
+        _t(c1), _t(c2), _t(u), _cw_param(cw), _t(gy), N, compute_grad_C1=False,
+        compute_grad_C2=False, compute_grad_u=False, compute_grad_cw=False) == (None,) * 4
+
+
+def test_forward_raw_names_match_the_autograd_path():
+    rng = np.random.default_rng(9)
+    B, T, F, N = 2, 500, 8, 2
+    c1, c2, cw, u = _problem(rng, B, T, F, N, False)
+    y_ref, _ = oracle.mosc_fwd(c1, c2, cw, u, N)
+    CW = _cw_param(cw)
+    y = mo._sequential_scan_multi_osc_forward_raw(_t(c1), _t(c2), _t(u), CW[:, 0], CW[:, 1], N)
+    assert relerr(y, y_ref) <= PARITY_RTOL
+    c1r, c2r, cwr, ur = _problem(rng, B, T, F, N, True)
+    yr_ref, _ = oracle.mosc_fwd(c1r, c2r, cwr, ur, N)
+    yr = mo._sequential_scan_multi_osc_real_forward_raw(_t(c1r), _t(c2r), _t(ur),
+                                                        _cw_param(cwr), N)
+    assert relerr(yr, yr_ref) <= PARITY_RTOL
+
+
+@pytest.mark.parametrize("real", [False, True])
+@pytest.mark.parametrize("in_f", [1, 16])
+def test_sequential_scan_abs(real, in_f):
+    rng = np.random.default_rng(11 + in_f)
+    B, T, F = 3, 2000, 16
+    c1 = _c64(rng.uniform(0.8, 0.999, F) * np.exp(1j * rng.uniform(0, np.pi, F)))
+    c2 = _c64(0.3 * crandn(rng, F))
+    u = rng.standard_normal((B, T, in_f)) if real else crandn(rng, B, T, in_f)
+    u = np.asarray(u, np.float32).astype(np.float64) if real else _c64(u)
+    ue = np.broadcast_to(u, (B, T, F))
+    want = np.abs(oracle.twotap_fwd(c1, c2, None, ue.astype(np.complex128)))
+    with torch.no_grad():
+        got = hip_scan.sequential_scan_abs(_t(c1), _t(c2), _t(u))
+    assert got.dtype == torch.float32 and got.shape == (B, T, F)
+    assert relerr(got, want) <= PARITY_RTOL
+    # with autograd the reference composes sequential_scan(...).abs()
+    U = _t(u, True)
+    got_g = hip_scan.sequential_scan_abs(_t(c1), _t(c2), U)
+    assert got_g.requires_grad and relerr(got_g, want) <= PARITY_RTOL
+
+
+def test_rejects_unsupported_oscillator_counts_and_host_tensors():
+    u = torch.zeros(1, 4, 2, dtype=torch.complex64, device="cuda")
+    c = torch.zeros(2 * 9, dtype=torch.complex64, device="cuda")
+    cw = torch.zeros(2 * 9, 2, device="cuda")
+    with pytest.raises(ValueError):
+        mo._triton_sequential_scan_multi_osc(c, c, u, cw, 9)
+    with pytest.raises(RuntimeError):
+        mo._triton_sequential_scan_multi_osc(c.cpu()[:4], c.cpu()[:4], u.cpu(), cw.cpu()[:4], 2)
+
+
+def test_empty_batch_and_time():
+    c = torch.ones(6, dtype=torch.complex64, device="cuda")
+    cw = torch.ones(6, 2, device="cuda", requires_grad=True)
+    C1 = c.clone().requires_grad_(True)
+    u = torch.zeros(0, 5, 3, dtype=torch.complex64, device="cuda", requires_grad=True)
+    y = mo._triton_sequential_scan_multi_osc(C1, c, u, cw, 2)
+    assert y.shape == (0, 5, 3)
+    y.sum().abs().backward()
+    assert torch.all(C1.grad == 0) and torch.all(cw.grad == 0)

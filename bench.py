@@ -59,6 +59,10 @@ def _args():
                     help="override the config's batch size (experiments only)")
     ap.add_argument("--seq-len", type=int, default=0,
                     help="override the config's sequence length (experiments only)")
+    ap.add_argument("--stack", choices=["none", "fused", "unfused"], default="none",
+                    help="configs 3 and 5: include the encoder's residual add (h = out + h) in "
+                         "each layer's forward, fused into the scan's stores or as a separate "
+                         "pass (the reference's pure.py:486-496, 530-534)")
     ap.add_argument("--act-only", action="store_true",
                     help="config 3 with the act-only contract (no raw output, no gy)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -192,9 +196,22 @@ def plan_selective(cfg, args, dev):
         state[f"gx{li}"] = _cn(g, dev, F, B, T) if activate else None
 
     ops, nbytes = [], {}
+    stack = args.stack if cfg == 3 else "none"
+    if stack != "none":
+        for li in range(len(layer_inputs)):
+            state[f"h{li}"] = _cn(g, dev, F, B, T)  # the layer input the skip adds
     for li, (inputs, write_raw, activate) in enumerate(layer_inputs):
         def fwd(st, li=li, inputs=inputs, write_raw=write_raw, activate=activate):
-            st[f"out{li}"] = selective_forward(st[f"z{li}"], inputs, activate, write_raw, chunk)
+            if stack == "fused":
+                st[f"out{li}"] = selective_forward(st[f"z{li}"], inputs, activate, write_raw,
+                                                   chunk, skip=st[f"h{li}"])
+            else:
+                out = selective_forward(st[f"z{li}"], inputs, activate, write_raw, chunk)
+                if stack == "unfused":  # source = raw + h; h = act + h
+                    h = st[f"h{li}"]
+                    out = (None if out[0] is None else out[0] + h,
+                           None if out[1] is None else out[1] + h, out[2])
+                st[f"out{li}"] = out
 
         ops.append((f"rqf_selective_fwd[L{li}]", fwd))
     for li in reversed(range(len(layer_inputs))):
@@ -208,13 +225,15 @@ def plan_selective(cfg, args, dev):
         ops.append((f"rqf_selective_bwd[L{li}]", bwd))
     for li, (_, write_raw, activate) in enumerate(layer_inputs):
         fb, bb = selective_bytes(F, B, T, G, chunk, write_raw=write_raw, activate=activate)
-        nbytes[f"rqf_selective_fwd[L{li}]"] = fb
+        nbytes[f"rqf_selective_fwd[L{li}]"] = fb + (8 * F * B * T if stack != "none" else 0)
         nbytes[f"rqf_selective_bwd[L{li}]"] = bb
     kernels = {
         "rqf_selective_fwd": "selective_fwd_rb_kernel",
         "rqf_selective_bwd": ("team_build_kernel + selective_bwd_team_kernel + "
                               "team_reduce_kernel + partial_reduce_kernel"),
     }
+    if stack != "none":
+        contract += f"; encoder residual add (raw + h, act + h) {stack}"
     config = {"workload": name, "F": F, "B": B, "T": T, "G": G, "layers": len(layers),
               "chunk": chunk, "contract": contract}
     cpu_steps = args.cpu_steps or (200 if cfg == 3 else 100)
@@ -271,9 +290,20 @@ def plan_fbt(cfg, args, dev):
         state[f"gy{li}"] = _cn(g, dev, F, B, T)
 
     ops = []
+    stack = args.stack if cfg == 5 else "none"
+    if stack != "none":
+        for li in range(L):
+            state[f"h{li}"] = _cn(g, dev, F, B, T)  # the layer input the skip adds
     for li in range(L):
         def fwd(st, li=li):
-            st[f"out{li}"] = fbt_recompute_forward_raw(*coefs[li], st[f"x{li}"])
+            if stack == "fused":
+                st[f"out{li}"] = fbt_recompute_forward_raw(*coefs[li], st[f"x{li}"],
+                                                           skip=st[f"h{li}"])
+            else:
+                act, carry, saved = fbt_recompute_forward_raw(*coefs[li], st[f"x{li}"])
+                if stack == "unfused":  # h = out + h
+                    act = act + st[f"h{li}"]
+                st[f"out{li}"] = (act, carry, saved)
 
         ops.append((f"rqf_fbt_recompute_fwd[L{li}]", fwd))
     for li in reversed(range(L)):
@@ -283,6 +313,8 @@ def plan_fbt(cfg, args, dev):
 
         ops.append((f"rqf_fbt_recompute_bwd[L{li}]", bwd))
     fb, bb = fbt_recompute_bytes(F, B, T)
+    if stack != "none":
+        fb += 8 * F * B * T
     nbytes = {}
     for li in range(L):
         nbytes[f"rqf_fbt_recompute_fwd[L{li}]"] = fb
@@ -290,8 +322,10 @@ def plan_fbt(cfg, args, dev):
     kernels = {"rqf_fbt_recompute_fwd": "fbt_fwd_rb_kernel",
                "rqf_fbt_recompute_bwd": ("fbt_bwd_rb_kernel<replay> (T % 256 == 0) or "
                                          "fbt_bwd_kernel<replay>, + coef_reduce_kernel")}
-    config = {"workload": name, "F": F, "B": B, "T": T, "layers": L,
-              "contract": "split-ReLU output, per-tile carries; gy cotangent, full BPTT"}
+    contract = "split-ReLU output, per-tile carries; gy cotangent, full BPTT"
+    if stack != "none":
+        contract += f"; encoder residual add (act + h) {stack}"
+    config = {"workload": name, "F": F, "B": B, "T": T, "layers": L, "contract": contract}
     cpu_steps = args.cpu_steps or (1000 if cfg == 2 else 500)
 
     def cpu():
@@ -675,7 +709,8 @@ def main():
     dom_bytes = plan.bytes[dom]
     achieved = dom_bytes / (per_op[dom] * 1e-3) / 1e9
     all_bytes = sum(plan.bytes.values())
-    traffic = traffic_from_table(f"config{cfg}", entry) if not (args.batch or args.seq_len) else None
+    traffic = (traffic_from_table(f"config{cfg}", entry)
+               if not (args.batch or args.seq_len or args.stack != "none") else None)
     result = {
         "metric": METRIC,
         "value": round(value, 3),

@@ -157,6 +157,17 @@ int rqf_fbt_recompute_fwd(const float *c1, const float *tap0, const float *tap1,
                           const float *z, float *act, float *carry, int64_t F, int64_t B,
                           int64_t T, rqf_stream_t stream);
 
+/* rqf_fbt_recompute_fwd with the encoder's residual connection fused into the
+ * output store: act = split-ReLU(raw) + skip, skip (F,B,T) complex (the
+ * layer input).  Replaces the block call plus the separate skip add of
+ * `PureRQFEncoder._forward_fbt_stack` (rqf_models/backbones/rqf/pure.py:
+ * 530-534).  The carries are the scan's own states, so
+ * rqf_fbt_recompute_bwd applies unchanged (the skip's gradient is the
+ * identity). */
+int rqf_fbt_recompute_skip_fwd(const float *c1, const float *tap0, const float *tap1,
+                               const float *z, const float *skip, float *act, float *carry,
+                               int64_t F, int64_t B, int64_t T, rqf_stream_t stream);
+
 /* Replaces `_fbt_recompute_backward_kernel[grid](...)`
  * (rqf_models/ops/fbt_scan_kernel.py:653-669). */
 int rqf_fbt_recompute_bwd(const float *c1, const float *tap0, const float *tap1,
@@ -201,6 +212,18 @@ typedef struct rqf_selective_inputs {
  * chunk: positive power of two. */
 int rqf_selective_fwd(const rqf_selective_inputs *in, const float *z, int64_t chunk,
                       float *raw, float *act, float *entries, rqf_stream_t stream);
+
+/* rqf_selective_fwd with the encoder's residual connection fused into the
+ * output stores: raw = state + skip and act = split-ReLU(state) + skip, skip
+ * (F,B,T) complex (the layer input).  Replaces the block call plus the two
+ * skip adds `source = raw + h`, `h = out + h` of
+ * `PureRQFEncoder._forward_selective_stack`
+ * (rqf_models/backbones/rqf/pure.py:486-496).  entries hold the scan's own
+ * states, so rqf_selective_bwd applies unchanged (the skip's gradient is the
+ * identity). */
+int rqf_selective_skip_fwd(const rqf_selective_inputs *in, const float *z, int64_t chunk,
+                           const float *skip, float *raw, float *act, float *entries,
+                           rqf_stream_t stream);
 
 size_t rqf_selective_bwd_workspace(const rqf_selective_inputs *in, int64_t chunk);
 

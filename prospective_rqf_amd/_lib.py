@@ -65,9 +65,12 @@ SIGNATURES = {
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
     "rqf_fbt_recompute_fwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
+    "rqf_fbt_recompute_skip_fwd": (
+        ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "rqf_fbt_recompute_bwd": (
         ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
     "rqf_selective_fwd": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P]),
+    "rqf_selective_skip_fwd": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P, _P]),
     "rqf_selective_bwd_workspace": (_SZ, [_P, _I64]),
     "rqf_selective_bwd": (
         ctypes.c_int,

@@ -369,6 +369,7 @@ struct FwdRow {
   const float* dr;
   float* rawr;
   float* actr;
+  const float* skr;  // residual added to both outputs (the layer input), or nullptr
   float* ent;
   float4* io;  // this wavefront's LDS slice for transposed complex I/O (or nullptr)
   int T, chunk;
@@ -439,15 +440,25 @@ __device__ __forceinline__ void fwd_emit(const FwdRow& r, int t0, int lane, c32 
     }
   }
   constexpr bool lds_io = VEC && !TAIL && RQF_FWD_LDS_IO;
-  if (r.rawr) {
+  c32 sk[K];
+  if (r.skr) {
     if (lds_io)
-      store_c_lds<K>(r.rawr, t0, lane, r.io, out);
+      load_c_lds<K>(r.skr, t0, lane, r.io, sk);
     else
-      store_c<K, VEC, TAIL>(r.rawr, tb, T, out);
+      load_c<K, VEC, TAIL>(r.skr, tb, T, sk);
+  }
+  if (r.rawr) {
+    c32 o[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) o[k] = r.skr ? cadd(out[k], sk[k]) : out[k];
+    if (lds_io)
+      store_c_lds<K>(r.rawr, t0, lane, r.io, o);
+    else
+      store_c<K, VEC, TAIL>(r.rawr, tb, T, o);
   }
   if (r.actr) {
 #pragma unroll
-    for (int k = 0; k < K; ++k) out[k] = relu2(out[k]);
+    for (int k = 0; k < K; ++k) out[k] = r.skr ? cadd(relu2(out[k]), sk[k]) : relu2(out[k]);
     if (lds_io)
       store_c_lds<K>(r.actr, t0, lane, r.io, out);
     else
@@ -494,8 +505,9 @@ __device__ __forceinline__ void fwd_tile(const rqf_selective_inputs& p, const Ch
 template <int O, bool VEC>
 __global__ __launch_bounds__(kRowsPerBlock* kWave)
     __attribute__((amdgpu_waves_per_eu(RQF_FWD_WAVES_PER_EU))) void selective_fwd_kernel(
-    const rqf_selective_inputs pin, const float* __restrict__ z, float* __restrict__ raw,
-    float* __restrict__ act, float* __restrict__ entries, int chunk, int nc) {
+    const rqf_selective_inputs pin, const float* __restrict__ z, const float* __restrict__ skip,
+    float* __restrict__ raw, float* __restrict__ act, float* __restrict__ entries, int chunk,
+    int nc) {
   constexpr int K = kFwdK, TILE = kWave * K;
   const rqf_selective_inputs p = with_options<O>(pin);
 #if RQF_FWD_LDS_IO
@@ -516,6 +528,7 @@ __global__ __launch_bounds__(kRowsPerBlock* kWave)
   r.dr = p.has_warp ? p.warp_logits + (p.groups[id.f] * p.B + id.b) * r.T : nullptr;
   r.rawr = raw ? raw + 2 * base : nullptr;
   r.actr = act ? act + 2 * base : nullptr;
+  r.skr = skip ? skip + 2 * base : nullptr;
   r.ent = entries + 2 * id.row * nc;
 #if RQF_FWD_LDS_IO
   r.io = &s_io[wave_id()][0];
@@ -571,8 +584,9 @@ constexpr int kFwdRbWaves = RQF_FWD_RB_WAVES;
 template <int O, bool VEC>
 __global__ __launch_bounds__(kFwdRbWaves* kWave)
     __attribute__((amdgpu_waves_per_eu(RQF_FWD_WAVES_PER_EU))) void selective_fwd_rb_kernel(
-    const rqf_selective_inputs pin, const float* __restrict__ z, float* __restrict__ raw,
-    float* __restrict__ act, float* __restrict__ entries, int chunk, int nc) {
+    const rqf_selective_inputs pin, const float* __restrict__ z, const float* __restrict__ skip,
+    float* __restrict__ raw, float* __restrict__ act, float* __restrict__ entries, int chunk,
+    int nc) {
   constexpr int K = kFwdK, TILE = kWave * K, W = kFwdRbWaves;
   const rqf_selective_inputs p = with_options<O>(pin);
 #if RQF_FWD_LDS_IO
@@ -595,6 +609,7 @@ __global__ __launch_bounds__(kFwdRbWaves* kWave)
   r.dr = p.has_warp ? p.warp_logits + (p.groups[id.f] * p.B + id.b) * T : nullptr;
   r.rawr = raw ? raw + 2 * base : nullptr;
   r.actr = act ? act + 2 * base : nullptr;
+  r.skr = skip ? skip + 2 * base : nullptr;
   r.ent = entries + 2 * id.row * nc;
 #if RQF_FWD_LDS_IO
   r.io = &s_io[w][0];
@@ -1538,19 +1553,19 @@ void with_option_set(int opts, Fn&& fn) {
   }
 }
 
-void launch_fwd(const rqf_selective_inputs* in, const float* z, float* raw, float* act,
-                float* entries, int chunk, int nc, bool vec, hipStream_t s) {
+void launch_fwd(const rqf_selective_inputs* in, const float* z, const float* skip, float* raw,
+                float* act, float* entries, int chunk, int nc, bool vec, hipStream_t s) {
   if (RQF_FWD_ROWBLOCK) {
     const dim3 grid((unsigned)(kXcds * in->F * ((in->B + kXcds - 1) / kXcds)));
     const dim3 block(kFwdRbWaves * kWave);
     with_option_set(options_of(in), [&](auto oc) {
       constexpr int O = decltype(oc)::value;
       if (vec)
-        hipLaunchKernelGGL((selective_fwd_rb_kernel<O, true>), grid, block, 0, s, *in, z, raw,
-                           act, entries, chunk, nc);
+        hipLaunchKernelGGL((selective_fwd_rb_kernel<O, true>), grid, block, 0, s, *in, z, skip,
+                           raw, act, entries, chunk, nc);
       else
-        hipLaunchKernelGGL((selective_fwd_rb_kernel<O, false>), grid, block, 0, s, *in, z, raw,
-                           act, entries, chunk, nc);
+        hipLaunchKernelGGL((selective_fwd_rb_kernel<O, false>), grid, block, 0, s, *in, z, skip,
+                           raw, act, entries, chunk, nc);
     });
     return;
   }
@@ -1558,11 +1573,11 @@ void launch_fwd(const rqf_selective_inputs* in, const float* z, float* raw, floa
   with_option_set(options_of(in), [&](auto oc) {
     constexpr int O = decltype(oc)::value;
     if (vec)
-      hipLaunchKernelGGL((selective_fwd_kernel<O, true>), grid, block, 0, s, *in, z, raw, act,
-                         entries, chunk, nc);
+      hipLaunchKernelGGL((selective_fwd_kernel<O, true>), grid, block, 0, s, *in, z, skip, raw,
+                         act, entries, chunk, nc);
     else
-      hipLaunchKernelGGL((selective_fwd_kernel<O, false>), grid, block, 0, s, *in, z, raw, act,
-                         entries, chunk, nc);
+      hipLaunchKernelGGL((selective_fwd_kernel<O, false>), grid, block, 0, s, *in, z, skip, raw,
+                         act, entries, chunk, nc);
   });
 }
 
@@ -1570,19 +1585,34 @@ constexpr int kBwdTile = kWave * kBwdK;
 
 }  // namespace
 
-extern "C" int rqf_selective_fwd(const rqf_selective_inputs* in, const float* z, int64_t chunk,
-                                 float* raw, float* act, float* entries, rqf_stream_t stream) {
+namespace {
+int selective_fwd(const rqf_selective_inputs* in, const float* z, int64_t chunk, const float* skip,
+                  float* raw, float* act, float* entries, rqf_stream_t stream) {
   if (!in || in->F < 0 || in->B < 0 || in->T < 0 || !pow2(chunk)) return RQF_ERR_ARG;
   const int64_t R = in->F * in->B;
   if (R == 0 || in->T == 0) return RQF_OK;
   int st = check_inputs(in);
   if (st) return st;
   if (!z || !entries || (!raw && !act)) return RQF_ERR_ARG;
-  if (!aligned8(z) || !aligned8(raw) || !aligned8(act) || !aligned8(entries)) return RQF_ERR_ALIGN;
+  if (!aligned8(z) || !aligned8(skip) || !aligned8(raw) || !aligned8(act) || !aligned8(entries))
+    return RQF_ERR_ALIGN;
   const int nc = (int)((in->T + chunk - 1) / chunk);
-  launch_fwd(in, z, raw, act, entries, chunk_int(chunk), nc, vec_ok(in, {z, raw, act}),
-             (hipStream_t)stream);
+  launch_fwd(in, z, skip, raw, act, entries, chunk_int(chunk), nc,
+             vec_ok(in, {z, skip, raw, act}), (hipStream_t)stream);
   return launch_status();
+}
+}  // namespace
+
+extern "C" int rqf_selective_fwd(const rqf_selective_inputs* in, const float* z, int64_t chunk,
+                                 float* raw, float* act, float* entries, rqf_stream_t stream) {
+  return selective_fwd(in, z, chunk, nullptr, raw, act, entries, stream);
+}
+
+extern "C" int rqf_selective_skip_fwd(const rqf_selective_inputs* in, const float* z,
+                                      int64_t chunk, const float* skip, float* raw, float* act,
+                                      float* entries, rqf_stream_t stream) {
+  if (!skip && in && in->F * in->B * in->T > 0) return RQF_ERR_ARG;
+  return selective_fwd(in, z, chunk, skip, raw, act, entries, stream);
 }
 
 namespace {
@@ -1669,7 +1699,7 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
       float* te = (float*)(ws + w.tile_entries);
       ent_chunk = kBwdTile;
       nc = (int)((T + kBwdTile - 1) / kBwdTile);
-      launch_fwd(in, z, nullptr, nullptr, te, ent_chunk, nc, vec, s);
+      launch_fwd(in, z, nullptr, nullptr, nullptr, te, ent_chunk, nc, vec, s);
       ent = te;
     }
     BwdOut o;

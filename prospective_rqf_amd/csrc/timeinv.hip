@@ -184,11 +184,14 @@ __global__ __launch_bounds__(kTiWaves* kWave) void fbt_fwd_kernel(
 constexpr int kTfK = RQF_TI_FWD_K, kTfTile = kWave * kTfK, kTfWaves = RQF_TI_FWD_RB_WAVES;
 static_assert(kTfTile % kTiTile == 0, "forward tiles hold whole carry tiles");
 
+// skip (nullable, FBT like z): added to the act output (a residual connection
+// around the layer); raw and the carries stay the scan's own states.
 template <bool VEC>
 __global__ __launch_bounds__(kTfWaves* kWave) void fbt_fwd_rb_kernel(
     const float* __restrict__ c1, const float* __restrict__ tap0, const float* __restrict__ tap1,
-    const float* __restrict__ z, float* __restrict__ raw, float* __restrict__ act,
-    float* __restrict__ carry, int64_t F, int64_t B, int64_t T, int64_t nc) {
+    const float* __restrict__ z, const float* __restrict__ skip, float* __restrict__ raw,
+    float* __restrict__ act, float* __restrict__ carry, int64_t F, int64_t B, int64_t T,
+    int64_t nc) {
   constexpr int K = kTfK, W = kTfWaves;
   __shared__ float4 s_io[W][kTfTile / 2];
   __shared__ float4 s_map[2][W];  // (P, s) of each wavefront's tile
@@ -202,6 +205,7 @@ __global__ __launch_bounds__(kTfWaves* kWave) void fbt_fwd_rb_kernel(
   const float* zr = z + 2 * row * T;
   float* rawr = raw ? raw + 2 * row * T : nullptr;
   float* actr = act ? act + 2 * row * T : nullptr;
+  const float* skr = skip ? skip + 2 * row * T : nullptr;
   c32 y = mk(0.0f, 0.0f);  // the row's state entering the super-tile
   int parity = 0;
   for (int64_t st0 = 0; st0 < T; st0 += (int64_t)W * kTfTile) {
@@ -270,6 +274,17 @@ __global__ __launch_bounds__(kTfWaves* kWave) void fbt_fwd_rb_kernel(
       if (actr) {
 #pragma unroll
         for (int k = 0; k < K; ++k) out[k] = relu2(out[k]);
+        if (skr) {
+          c32 sk[K];
+          if (full) {
+            load_c_lds<K>(skr, (int)t0, lane, io, sk);
+          } else {
+#pragma unroll
+            for (int k = 0; k < K; ++k) sk[k] = (tb + k < T) ? ldc(skr, tb + k) : mk(0.0f, 0.0f);
+          }
+#pragma unroll
+          for (int k = 0; k < K; ++k) out[k] = cadd(out[k], sk[k]);
+        }
         if (full) {
           store_c_lds<K>(actr, (int)t0, lane, io, out);
         } else {
@@ -877,22 +892,27 @@ int btf_bwd(const float* c1, const float* k0, const float* k1, const float* x,
   return launch_status();
 }
 
-int fbt_fwd(const float* c1, const float* t0, const float* t1, const float* z, float* raw,
-            float* act, float* carry, int64_t F, int64_t B, int64_t T, hipStream_t s) {
+int fbt_fwd(const float* c1, const float* t0, const float* t1, const float* z, const float* skip,
+            float* raw, float* act, float* carry, int64_t F, int64_t B, int64_t T,
+            hipStream_t s) {
   if (F < 0 || B < 0 || T < 0) return RQF_ERR_ARG;
   const int64_t R = F * B;
   if (R == 0 || T == 0) return RQF_OK;
   if (!c1 || !t0 || !t1 || !z || (!raw && !act)) return RQF_ERR_ARG;
-  if (!aligned8(z) || !aligned8(raw) || !aligned8(act) || !aligned8(carry)) return RQF_ERR_ALIGN;
+  if (!aligned8(z) || !aligned8(skip) || !aligned8(raw) || !aligned8(act) || !aligned8(carry))
+    return RQF_ERR_ALIGN;
+  if (skip && !act) return RQF_ERR_ARG;
   const int64_t nc = (T + kTiTile - 1) / kTiTile;
-  const bool vec = T % 2 == 0 && aligned16(z) && aligned16(raw) && aligned16(act);
+  const bool vec =
+      T % 2 == 0 && aligned16(z) && aligned16(skip) && aligned16(raw) && aligned16(act);
+  if (!RQF_TI_FWD_RB && skip) return RQF_ERR_ARG;  // the per-row forward has no skip input
   if (RQF_TI_FWD_RB) {
     const dim3 grid((unsigned)R), block(kTfWaves * kWave);
     if (vec)
-      hipLaunchKernelGGL(fbt_fwd_rb_kernel<true>, grid, block, 0, s, c1, t0, t1, z, raw, act, carry,
+      hipLaunchKernelGGL(fbt_fwd_rb_kernel<true>, grid, block, 0, s, c1, t0, t1, z, skip, raw, act, carry,
                          F, B, T, nc);
     else
-      hipLaunchKernelGGL(fbt_fwd_rb_kernel<false>, grid, block, 0, s, c1, t0, t1, z, raw, act,
+      hipLaunchKernelGGL(fbt_fwd_rb_kernel<false>, grid, block, 0, s, c1, t0, t1, z, skip, raw, act,
                          carry, F, B, T, nc);
     return launch_status();
   }
@@ -1021,7 +1041,7 @@ extern "C" int rqf_fbt_prospective_fwd(const float* c1, const float* tap0, const
                                        const float* z, float* raw, float* act, int64_t F,
                                        int64_t B, int64_t T, rqf_stream_t stream) {
   if (!raw && F * B * T > 0) return RQF_ERR_ARG;
-  return fbt_fwd(c1, tap0, tap1, z, raw, act, nullptr, F, B, T, (hipStream_t)stream);
+  return fbt_fwd(c1, tap0, tap1, z, nullptr, raw, act, nullptr, F, B, T, (hipStream_t)stream);
 }
 
 extern "C" int rqf_fbt_prospective_bwd(const float* c1, const float* tap0, const float* tap1,
@@ -1038,7 +1058,15 @@ extern "C" int rqf_fbt_recompute_fwd(const float* c1, const float* tap0, const f
                                      const float* z, float* act, float* carry, int64_t F,
                                      int64_t B, int64_t T, rqf_stream_t stream) {
   if ((!act || !carry) && F * B * T > 0) return RQF_ERR_ARG;
-  return fbt_fwd(c1, tap0, tap1, z, nullptr, act, carry, F, B, T, (hipStream_t)stream);
+  return fbt_fwd(c1, tap0, tap1, z, nullptr, nullptr, act, carry, F, B, T, (hipStream_t)stream);
+}
+
+extern "C" int rqf_fbt_recompute_skip_fwd(const float* c1, const float* tap0, const float* tap1,
+                                          const float* z, const float* skip, float* act,
+                                          float* carry, int64_t F, int64_t B, int64_t T,
+                                          rqf_stream_t stream) {
+  if ((!act || !carry || !skip) && F * B * T > 0) return RQF_ERR_ARG;
+  return fbt_fwd(c1, tap0, tap1, z, skip, nullptr, act, carry, F, B, T, (hipStream_t)stream);
 }
 
 extern "C" int rqf_fbt_recompute_bwd(const float* c1, const float* tap0, const float* tap1,

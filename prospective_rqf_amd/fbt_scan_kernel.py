@@ -86,22 +86,34 @@ def fbt_prospective_scan(C1, tap0, tap1, x_fbt, fuse_act=False):
     return _FBTProspectiveScan.apply(C1, tap0, tap1, x_fbt, fuse_act)
 
 
-def fbt_recompute_forward_raw(C1, tap0, tap1, x):
-    """Kernel-only forward of :func:`fbt_recompute_scan`: ``(act, carry, coefs)``."""
+def fbt_recompute_forward_raw(C1, tap0, tap1, x, skip=None):
+    """Kernel-only forward of :func:`fbt_recompute_scan`: ``(act, carry, coefs)``.
+
+    ``skip`` (optional, same shape as ``x``) is added to ``act`` in the
+    kernel's output store: the encoder's residual connection
+    (pure.py:530-534) without a separate pass."""
     x = _c64(x)
-    _lib.require_device(x)
+    _lib.require_device(x, skip)
     filters, batch, time = x.shape
     C1, tap0, tap1 = _coefs(C1, tap0, tap1, filters)
+    if skip is not None:
+        if skip.shape != x.shape:
+            raise ValueError(f"skip must have the drive's shape {tuple(x.shape)}, "
+                             f"got {tuple(skip.shape)}")
+        skip = _c64(skip)
     lib = _lib.load()
     nchunks = lib.rqf_fbt_carry_chunks(time)
     act = torch.empty_like(x)
     carry = torch.empty((filters * batch, max(nchunks, 1)), dtype=torch.complex64, device=x.device)
-    _lib.check(
-        lib.rqf_fbt_recompute_fwd(
+    if skip is None:
+        rc = lib.rqf_fbt_recompute_fwd(
             _lib.ptr(C1), _lib.ptr(tap0), _lib.ptr(tap1), _lib.ptr(x), _lib.ptr(act),
-            _lib.ptr(carry), filters, batch, time, _lib.stream_of(x)),
-        "rqf_fbt_recompute_fwd",
-    )
+            _lib.ptr(carry), filters, batch, time, _lib.stream_of(x))
+    else:
+        rc = lib.rqf_fbt_recompute_skip_fwd(
+            _lib.ptr(C1), _lib.ptr(tap0), _lib.ptr(tap1), _lib.ptr(x), _lib.ptr(skip),
+            _lib.ptr(act), _lib.ptr(carry), filters, batch, time, _lib.stream_of(x))
+    _lib.check(rc, "rqf_fbt_recompute_fwd")
     return act, carry, (C1, tap0, tap1, x)
 
 
@@ -128,18 +140,24 @@ class _FBTRecompute(torch.autograd.Function):
     """Split-ReLU prospective scan that replays the raw state in the backward."""
 
     @staticmethod
-    def forward(ctx, C1, tap0, tap1, x_fbt):
-        act, carry, (C1, tap0, tap1, x) = fbt_recompute_forward_raw(C1, tap0, tap1, x_fbt)
+    def forward(ctx, C1, tap0, tap1, x_fbt, skip=None):
+        act, carry, (C1, tap0, tap1, x) = fbt_recompute_forward_raw(C1, tap0, tap1, x_fbt, skip)
         ctx.save_for_backward(C1, tap0, tap1, x, carry)
+        ctx.has_skip = skip is not None
         return act
 
     @staticmethod
     @once_differentiable
     def backward(ctx, grad_output):
         C1, tap0, tap1, x, carry = ctx.saved_tensors
-        return fbt_recompute_backward_raw(C1, tap0, tap1, x, carry, grad_output)
+        grads = fbt_recompute_backward_raw(C1, tap0, tap1, x, carry, grad_output)
+        # act = split-ReLU(scan) + skip: the skip's gradient is the cotangent itself.
+        return (*grads, grad_output if ctx.has_skip else None)
 
 
-def fbt_recompute_scan(C1, tap0, tap1, x_fbt):
-    """Split-ReLU prospective scan; stores the output plus per-tile entry states."""
-    return _FBTRecompute.apply(C1, tap0, tap1, x_fbt)
+def fbt_recompute_scan(C1, tap0, tap1, x_fbt, skip=None):
+    """Split-ReLU prospective scan; stores the output plus per-tile entry states.
+
+    With ``skip`` (the layer input, same shape) the result is
+    ``split-ReLU(scan) + skip``, the residual add fused into the kernel."""
+    return _FBTRecompute.apply(C1, tap0, tap1, x_fbt, skip)

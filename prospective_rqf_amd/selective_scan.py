@@ -51,15 +51,16 @@ class _SelectiveLayerScan(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, weight, *args):
-        *tensors, options, truncated, activate, write_raw, chunk = args
+        *tensors, options, truncated, activate, write_raw, chunk, skip = args
         inputs = SelectiveScanInputs(*tensors, options)
         f_in, batch, time = x.shape
         with torch.autocast(x.device.type, enabled=False):
             z = (weight @ x.reshape(f_in, batch * time)).reshape(-1, batch, time)
-        raw, act, entries = selective_forward(z, inputs, activate, write_raw, chunk)
+        raw, act, entries = selective_forward(z, inputs, activate, write_raw, chunk,
+                                              skip=x if skip else None)
         ctx.save_for_backward(x, weight, z, entries, *tensors)
         ctx.options, ctx.truncated = options, truncated
-        ctx.activate, ctx.chunk = activate, chunk
+        ctx.activate, ctx.chunk, ctx.skip = activate, chunk, skip
         ctx.set_materialize_grads(False)
         return raw, act
 
@@ -75,7 +76,12 @@ class _SelectiveLayerScan(torch.autograd.Function):
         with torch.autocast(x.device.type, enabled=False):
             dx = (weight.mH @ dx_drive.reshape(weight.shape[0], -1)).reshape_as(x)
             dweight = dw_drive.reshape(weight.shape[0], -1) @ x.reshape(f_in, -1).mH
-        grads = (dx, dweight, dg, dd, dw, dbias, dtheta) + (None,) * 12
+        if ctx.skip:
+            # raw + x and act + x: the skip passes both cotangents to x.
+            for g in (grad_raw, grad_act):
+                if g is not None:
+                    dx = dx + g
+        grads = (dx, dweight, dg, dd, dw, dbias, dtheta) + (None,) * 13
         return tuple(g if need else None for g, need in zip(grads, ctx.needs_input_grad))
 
 
@@ -104,15 +110,22 @@ def selective_layer_scan(
     write_raw: bool = True,
     use_kernel: bool = True,
     chunk: int | None = None,
+    skip: bool = False,
 ) -> tuple[Tensor | None, Tensor | None]:
     """Complex ``(I,B,T)`` selective layer on the HIP kernels.
 
     Same signature, validation and return convention as the reference.  Inputs
     the kernels cannot serve raise ``RuntimeError``: the caller's reference
     path handles them.
+
+    ``skip=True`` (not in the reference's signature) returns ``(raw + x,
+    act + x)``: the encoder's residual connection (pure.py:486-496), added in
+    the kernel's output stores.  It needs a square ``weight``.
     """
     if not activate and not write_raw:
         raise ValueError("selective scan requires at least one output")
+    if skip and weight.shape[0] != x.shape[0]:
+        raise ValueError("skip needs as many output channels as input channels")
     if not eligible(x, weight, inputs, use_kernel):
         raise RuntimeError(
             "selective_layer_scan: input not eligible for the HIP kernels (needs complex64 "
@@ -125,5 +138,6 @@ def selective_layer_scan(
         raise ValueError("chunk must be a positive power of two")
     tensors = [v.contiguous() if isinstance(v, Tensor) else v for v in inputs[:-1]]
     return _SelectiveLayerScan.apply(
-        x.contiguous(), weight, *tensors, inputs.options, truncated, activate, write_raw, chunk
+        x.contiguous(), weight, *tensors, inputs.options, truncated, activate, write_raw, chunk,
+        bool(skip)
     )

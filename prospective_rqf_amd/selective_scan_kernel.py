@@ -91,16 +91,24 @@ def inputs_struct(z: torch.Tensor, inputs) -> tuple[_lib.SelectiveInputsStruct, 
     return s, [gl, dl, wl, groups, order, *params]
 
 
-def selective_forward(z, inputs, activate, write_raw, chunk):
+def selective_forward(z, inputs, activate, write_raw, chunk, skip=None):
     """Fused forward: returns ``(raw|None, act|None, entries)``.
 
     z: (F,B,T) complex64 drive.  entries: (F*B, ceil(T/chunk)) complex64 state
-    entering each chunk (consumed by :func:`selective_backward`).
+    entering each chunk (consumed by :func:`selective_backward`).  ``skip``
+    (optional, like z) is added to both outputs in the kernel's stores: the
+    encoder's residual connection (pure.py:486-496) without separate passes;
+    entries stay the scan's own states.
     """
-    _lib.require_device(z)
+    _lib.require_device(z, skip)
     if z.dtype != torch.complex64:
         raise TypeError("selective_forward expects a complex64 drive")
     z = z.resolve_conj().contiguous()
+    if skip is not None:
+        if skip.shape != z.shape:
+            raise ValueError(f"skip must have the drive's shape {tuple(z.shape)}, "
+                             f"got {tuple(skip.shape)}")
+        skip = skip.to(torch.complex64).resolve_conj().contiguous()
     f, b, t = z.shape
     nc = -(-t // chunk)
     raw = torch.empty_like(z) if write_raw else None
@@ -108,11 +116,14 @@ def selective_forward(z, inputs, activate, write_raw, chunk):
     entries = torch.empty((f * b, nc), dtype=z.dtype, device=z.device)
     s, keep = inputs_struct(z, inputs)
     lib = _lib.load()
-    _lib.check(
-        lib.rqf_selective_fwd(ctypes.byref(s), _real_ptr(z), chunk, _real_ptr(raw),
-                              _real_ptr(act), _real_ptr(entries), _lib.stream_of(z)),
-        "rqf_selective_fwd",
-    )
+    if skip is None:
+        rc = lib.rqf_selective_fwd(ctypes.byref(s), _real_ptr(z), chunk, _real_ptr(raw),
+                                   _real_ptr(act), _real_ptr(entries), _lib.stream_of(z))
+    else:
+        rc = lib.rqf_selective_skip_fwd(ctypes.byref(s), _real_ptr(z), chunk, _real_ptr(skip),
+                                        _real_ptr(raw), _real_ptr(act), _real_ptr(entries),
+                                        _lib.stream_of(z))
+    _lib.check(rc, "rqf_selective_fwd")
     del keep
     return raw, act, entries
 

@@ -53,15 +53,6 @@ __device__ __forceinline__ void stc(float* p, int64_t i, c32 v) {
   p[2 * i] = v.r;
   p[2 * i + 1] = v.i;
 }
-__device__ __forceinline__ c32 cpow_int(c32 a, int64_t n) {
-  c32 r = mk(1.0f, 0.0f);
-  while (n > 0) {
-    if (n & 1) r = cmul(r, a);
-    a = cmul(a, a);
-    n >>= 1;
-  }
-  return r;
-}
 
 struct MoscShape {
   int64_t B, T, F, S, L, tasks;
@@ -139,24 +130,26 @@ __global__ __launch_bounds__(256) void mosc_carry_kernel(const float* __restrict
   const int n = (int)(bn % NP);
   const int64_t b = bn / NP;
   const c32 a = n < sh.N ? ldc(c1, f * sh.N + n) : mk(0.0f, 0.0f);
-  c32 e = mk(0.0f, 0.0f);
+  // Powers and the fold in fp64: a float32 power is off by ~L ulp, a bias that
+  // every hop of a long-memory channel would repeat.
+  c64d e = mkd(0.0, 0.0);
   if (!ADJ) {
-    const c32 aL = cpow_int(a, sh.L);
+    const c64d aL = dpow(widen(a), sh.L);
     for (int64_t s = 0; s < sh.S; ++s) {
       const int64_t i = seg_idx(sh, b, s, n, f, NP);
       const c32 v = ldc(seg, i);
-      stc(seg, i, e);
-      e = cmad(aL, e, v);
+      stc(seg, i, narrow(e));
+      e = dmad(aL, e, widen(v));
     }
   } else {
-    const c32 ac = conjg(a);
-    const c32 acL = cpow_int(ac, sh.L);
-    const c32 acLast = cpow_int(ac, sh.T - (sh.S - 1) * sh.L);
+    const c64d ac = dconj(widen(a));
+    const c64d acL = dpow(ac, sh.L);
+    const c64d acLast = dpow(ac, sh.T - (sh.S - 1) * sh.L);
     for (int64_t s = sh.S - 1; s >= 0; --s) {
       const int64_t i = seg_idx(sh, b, s, n, f, NP);
       const c32 v = ldc(seg, i);
-      stc(seg, i, e);
-      e = cmad(s == sh.S - 1 ? acLast : acL, e, v);
+      stc(seg, i, narrow(e));
+      e = dmad(s == sh.S - 1 ? acLast : acL, e, widen(v));
     }
   }
 }

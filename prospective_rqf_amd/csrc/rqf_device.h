@@ -63,6 +63,48 @@ __device__ __forceinline__ c32 cmadrr(c32 a, float s, float c) { return mk(fmaf(
 // Re(conj(a) b)
 __device__ __forceinline__ float cdot(c32 a, c32 b) { return fmaf(a.r, b.r, a.i * b.i); }
 
+// ---------------------------------------------------------------------------
+// Complex fp64, for the few per-channel quantities whose float32 rounding
+// would compound: powers a^n of the transition coefficient and the carry
+// chains that apply them.  Binary powering squares its running factor, which
+// doubles that factor's relative error at each step, so a^n evaluated in
+// float32 is off by ~n ulp -- one systematic error per channel that every
+// carry hop then repeats.  With |a| near 1 (trained filters reach
+// |a| = 0.9996, a memory of ~2800 steps) a hop chain covers many hops and the
+// coefficient gradients, sums of products of long-memory states, pick the
+// bias up coherently.  In fp64 the power is exact to float32 precision once
+// rounded.
+// ---------------------------------------------------------------------------
+struct c64d {
+  double r, i;
+};
+__device__ __forceinline__ c64d mkd(double r, double i) {
+  c64d v;
+  v.r = r;
+  v.i = i;
+  return v;
+}
+__device__ __forceinline__ c64d widen(c32 a) { return mkd(a.r, a.i); }
+__device__ __forceinline__ c32 narrow(c64d a) { return mk((float)a.r, (float)a.i); }
+__device__ __forceinline__ c64d dconj(c64d a) { return mkd(a.r, -a.i); }
+__device__ __forceinline__ c64d dmul(c64d a, c64d b) {
+  return mkd(fma(a.r, b.r, -a.i * b.i), fma(a.r, b.i, a.i * b.r));
+}
+// a*b + c
+__device__ __forceinline__ c64d dmad(c64d a, c64d b, c64d c) {
+  return mkd(fma(a.r, b.r, fma(-a.i, b.i, c.r)), fma(a.r, b.i, fma(a.i, b.r, c.i)));
+}
+// a^n, n >= 0, by binary powering in fp64.
+__device__ __forceinline__ c64d dpow(c64d a, int64_t n) {
+  c64d r = mkd(1.0, 0.0);
+  while (n > 0) {
+    if (n & 1) r = dmul(r, a);
+    a = dmul(a, a);
+    n >>= 1;
+  }
+  return r;
+}
+
 // Index of this wavefront within its block, as a wave-uniform (scalar) value:
 // the compiler cannot prove threadIdx.x >> 6 uniform, and everything derived
 // from a divergent value (row pointers, per-channel parameters) would occupy
@@ -182,6 +224,102 @@ __device__ __forceinline__ void wave_scan_rev(c32& Q, c32& r, int lane) {
   const int row = lane >> 4;
   rev_cross(Q, r, ((row + 1) & 3) << 4, row < 3);
   rev_cross(Q, r, ((row + 2) & 3) << 4, row < 2);
+}
+
+// ---------------------------------------------------------------------------
+// Scans of a time-invariant recurrence.  Every lane applies the same map power
+// A = a^K (K steps per lane; steps past the end of the row run with zero input,
+// which changes nothing any valid step reads), so the map covering lanes i..j
+// is A^(j-i+1) and the scans only propagate the offsets: at each step a lane
+// adds its partner's offset times A^(lanes it already covers).  Those powers
+// come from ScanPow, each rounded once from fp64, instead of the products of
+// products the general scans form (a squaring doubles its factor's relative
+// error, so A^64 composed in float32 is off by ~64 ulp of A -- a per-channel
+// bias that every tile hop repeats).  Two DPP moves and one complex product per
+// step fewer than the general scans.
+// ---------------------------------------------------------------------------
+struct ScanPow {
+  c32 p[4];      // A^(2^j), j = 0..3: the in-row steps (wave-uniform)
+  c32 row, row2; // per lane: the powers of the two cross-row steps
+};
+// Cross-row powers of the adjoint's suffix scan, whose map power is conj(A);
+// its in-row powers are the conjugates of ScanPow::p.
+struct RevPow {
+  c32 row, row2;
+};
+// A wave-uniform value, marked as such.  (The compiler drops the readfirstlane
+// when it already knows the value uniform and keeps the value in a VGPR; an
+// inline-asm v_readfirstlane_b32 into an SGPR was measured to give wrong
+// results here, so the builtin is kept.)
+__device__ __forceinline__ float uniform(float v) {
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+__device__ __forceinline__ c32 uniform(c32 v) { return mk(uniform(v.r), uniform(v.i)); }
+
+// Powers for wave_scan_fwd_pow: lane i covers lanes 16*(i/16)..i before the
+// first cross-row step and 32*(i/32)..i before the second.
+__device__ __forceinline__ ScanPow scan_pow_fwd(c64d A, int lane) {
+  ScanPow s;
+  c64d q = A;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    s.p[j] = uniform(narrow(q));
+    q = dmul(q, q);
+  }
+  s.row = narrow(dpow(A, (lane & 15) + 1));
+  s.row2 = narrow(dpow(A, (lane & 31) + 1));
+  return s;
+}
+// Cross-row powers for wave_scan_rev_pow (A as for scan_pow_fwd): lane i covers
+// lanes i..16*(i/16)+15 before the first cross-row step and i..16*(i/16)+31
+// before the second.
+__device__ __forceinline__ RevPow scan_pow_rev(c64d A, int lane) {
+  const c64d Ac = dconj(A);
+  RevPow s;
+  s.row = narrow(dpow(Ac, 16 - (lane & 15)));
+  s.row2 = narrow(dpow(Ac, 32 - (lane & 15)));
+  return s;
+}
+
+// In-row step: the power is wave-uniform, so the partner multiplies its own
+// offset by it and the DPP move folds into the add.  CONJ: the power is conj(p).
+template <int CTRL, bool CONJ = false>
+__device__ __forceinline__ void step_upow(c32& s, c32 p) {
+  const c32 t = CONJ ? cjmul(p, s) : cmul(s, p);
+  s = mk(s.r + dpp0<CTRL>(t.r), s.i + dpp0<CTRL>(t.i));
+}
+// Cross-row step: the power depends on the receiving lane.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void fwd_step_lpow(c32& s, c32 p) {
+  const c32 ls = mk(dpp<CTRL, ROW_MASK>(s.r, 0.0f), dpp<CTRL, ROW_MASK>(s.i, 0.0f));
+  s = cmad(ls, p, s);
+}
+// Inclusive prefix scan of the offsets: lane i ends with the offset of the
+// composition of lanes 0..i (its power is A^(i+1)).
+__device__ __forceinline__ void wave_scan_fwd_pow(c32& s, const ScanPow& pw) {
+  step_upow<kRowShr1>(s, pw.p[0]);
+  step_upow<kRowShr2>(s, pw.p[1]);
+  step_upow<kRowShr4>(s, pw.p[2]);
+  step_upow<kRowShr8>(s, pw.p[3]);
+  fwd_step_lpow<kRowBcast15, 0xa>(s, pw.row);
+  fwd_step_lpow<kRowBcast31, 0xc>(s, pw.row2);
+}
+
+// Inclusive suffix scan of the offsets of maps with power conj(A): lane i ends
+// with the offset of the composition of lanes i..63 (its power is conj(A)^(64-i)).
+__device__ __forceinline__ void wave_scan_rev_pow(c32& r, const ScanPow& pw, const RevPow& rv,
+                                                  int lane) {
+  step_upow<kRowShl1, true>(r, pw.p[0]);
+  step_upow<kRowShl2, true>(r, pw.p[1]);
+  step_upow<kRowShl4, true>(r, pw.p[2]);
+  step_upow<kRowShl8, true>(r, pw.p[3]);
+  const int row = lane >> 4;
+  c32 lr = mk(bperm(r.r, ((row + 1) & 3) << 4), bperm(r.i, ((row + 1) & 3) << 4));
+  if (row >= 3) lr = mk(0.0f, 0.0f);
+  r = cmad(rv.row, lr, r);
+  lr = mk(bperm(r.r, ((row + 2) & 3) << 4), bperm(r.i, ((row + 2) & 3) << 4));
+  if (row >= 2) lr = mk(0.0f, 0.0f);
+  r = cmad(rv.row2, lr, r);
 }
 
 // Complex tile I/O through a wavefront-private LDS slice (full tiles, VEC).

@@ -89,13 +89,6 @@ __device__ __forceinline__ void store8(float* __restrict__ row, int64_t tb, int6
   }
 }
 
-// a^n for small n >= 0 (uniform or per lane).
-__device__ __forceinline__ c32 cpow_small(c32 a, int n) {
-  c32 r = mk(1.0f, 0.0f);
-  for (int k = 0; k < n; ++k) r = cmul(r, a);
-  return r;
-}
-
 // ---------------------------------------------------------------------------
 // FBT forward: raw (optional), split-ReLU act (optional), entry carry per tile
 // (optional).
@@ -110,7 +103,7 @@ __global__ __launch_bounds__(kTiWaves* kWave) void fbt_fwd_kernel(
   if (row >= F * B) return;
   const int64_t f = row / B;
   const c32 a = ldc(c1, f), k0 = ldc(tap0, f), k1 = ldc(tap1, f);
-  c32 apow = cpow_small(a, kTiK);  // composition of a full lane
+  const ScanPow pw = scan_pow_fwd(dpow(widen(a), kTiK), lane);
   const float* zr = z + 2 * row * T;
   float* rawr = raw ? raw + 2 * row * T : nullptr;
   float* actr = act ? act + 2 * row * T : nullptr;
@@ -135,14 +128,11 @@ __global__ __launch_bounds__(kTiWaves* kWave) void fbt_fwd_kernel(
     c32 u[kTiK];
 #pragma unroll
     for (int k = 0; k < kTiK; ++k) u[k] = cmad(k1, k ? zv[k - 1] : zp0, cmul(k0, zv[k]));
-    const int cnt = (int)min<int64_t>(max<int64_t>(T - tb, 0), kTiK);
     c32 s = mk(0.0f, 0.0f);
 #pragma unroll
-    for (int k = 0; k < kTiK; ++k)
-      if (k < cnt) s = cmad(a, s, u[k]);
-    c32 P = cnt == kTiK ? apow : cpow_small(a, cnt);
-    if (lane == 0) s = cmad(P, y, s);
-    wave_scan_fwd(P, s);
+    for (int k = 0; k < kTiK; ++k) s = cmad(a, s, u[k]);
+    if (lane == 0) s = cmad(pw.p[0], y, s);
+    wave_scan_fwd_pow(s, pw);
     c32 yk = shift_up(s, y, lane);
     c32 out[kTiK];
 #pragma unroll
@@ -194,14 +184,17 @@ __global__ __launch_bounds__(kTfWaves* kWave) void fbt_fwd_rb_kernel(
     int64_t nc) {
   constexpr int K = kTfK, W = kTfWaves;
   __shared__ float4 s_io[W][kTfTile / 2];
-  __shared__ float4 s_map[2][W];  // (P, s) of each wavefront's tile
+  __shared__ float2 s_map[2][W];  // offset of each wavefront's tile map (its power is ptile)
   const int lane = lane_id();
   const int w = wave_id();
   float4* io = &s_io[w][0];
   const int64_t row = blockIdx.x;
   const int64_t f = row / B;
   const c32 a = ldc(c1, f), k0 = ldc(tap0, f), k1 = ldc(tap1, f);
-  const c32 apow = cpow_small(a, K);
+  const c64d A = dpow(widen(a), K);
+  const ScanPow pw = scan_pow_fwd(A, lane);
+  const c32 pex = narrow(dpow(A, lane));          // power of the lanes before this one
+  const c32 ptile = uniform(narrow(dpow(A, kWave)));  // a tile's map
   const float* zr = z + 2 * row * T;
   float* rawr = raw ? raw + 2 * row * T : nullptr;
   float* actr = act ? act + 2 * row * T : nullptr;
@@ -214,7 +207,7 @@ __global__ __launch_bounds__(kTfWaves* kWave) void fbt_fwd_rb_kernel(
     const bool full = VEC && t0 + kTfTile <= T;
     const int64_t tb = t0 + lane * K;
     c32 u[K];
-    c32 P = mk(1.0f, 0.0f), s = mk(0.0f, 0.0f);
+    c32 s = mk(0.0f, 0.0f);
     if (has) {
       c32 zv[K];
       if (full) {
@@ -227,23 +220,19 @@ __global__ __launch_bounds__(kTfWaves* kWave) void fbt_fwd_rb_kernel(
       const c32 zp0 = shift_up(zv[K - 1], zlast, lane);
 #pragma unroll
       for (int k = 0; k < K; ++k) u[k] = cmad(k1, k ? zv[k - 1] : zp0, cmul(k0, zv[k]));
-      const int cnt = (int)min<int64_t>(max<int64_t>(T - tb, 0), K);
 #pragma unroll
-      for (int k = 0; k < K; ++k)
-        if (k < cnt) s = cmad(a, s, u[k]);
-      P = cnt == K ? apow : cpow_small(a, cnt);
-      wave_scan_fwd(P, s);  // inclusive prefix maps of the tile, zero entry
-      if (lane == kWave - 1) s_map[parity][w] = make_float4(P.r, P.i, s.r, s.i);
+      for (int k = 0; k < K; ++k) s = cmad(a, s, u[k]);
+      wave_scan_fwd_pow(s, pw);  // inclusive prefix offsets of the tile, zero entry
+      if (lane == kWave - 1) s_map[parity][w] = make_float2(s.r, s.i);
     }
     __syncthreads();
     c32 ye = y, yr = y;
     for (int v = 0; v < W && st0 + (int64_t)v * kTfTile < T; ++v) {
       if (v == w) ye = yr;
-      const float4 m = s_map[parity][v];
-      yr = cmad(mk(m.x, m.y), yr, mk(m.z, m.w));
+      const float2 m = s_map[parity][v];
+      yr = cmad(ptile, yr, mk(m.x, m.y));
     }
     if (has) {
-      const c32 pex = shift_up(P, mk(1.0f, 0.0f), lane);
       const c32 sex = shift_up(s, mk(0.0f, 0.0f), lane);
       c32 yk = cmad(pex, ye, sex);
       c32 out[K];
@@ -382,7 +371,7 @@ __global__ __launch_bounds__(kRbWaves* kWave) void fbt_bwd_rb_kernel(
     const float* __restrict__ gout, int mask, float* __restrict__ gz,
     double* __restrict__ partial, int64_t F, int64_t B, int64_t T, int64_t nc) {
   constexpr int K = kTbK, TILE = kTbTile, W = kRbWaves;
-  __shared__ float4 s_map[2][W];
+  __shared__ float2 s_map[2][W];  // offset of each wavefront's tile suffix map (power ptile)
   __shared__ double s_part[W][6];
 #if RQF_TI_BWD_LDS_IO
   __shared__ float4 s_io[W][TILE / 2];
@@ -398,7 +387,11 @@ __global__ __launch_bounds__(kRbWaves* kWave) void fbt_bwd_rb_kernel(
   const int64_t f = row / B;
   const c32 a = ldc(c1, f), k0 = ldc(tap0, f), k1 = ldc(tap1, f);
   const c32 ac = conjg(a);
-  const c32 apow = cpow_small(a, K), acpow = conjg(apow);
+  const c64d A = dpow(widen(a), K), Ac = dconj(A);
+  const ScanPow pf = scan_pow_fwd(A, lane);  // the replay's forward scan; in-row adjoint powers
+  const RevPow pr = scan_pow_rev(A, lane);
+  const c32 psfx = narrow(dpow(Ac, kWave - lane));     // this lane and the ones after it
+  const c32 ptile = uniform(narrow(dpow(Ac, kWave)));  // a whole tile
   const float* zr = z + 2 * row * T;
   const float* rr = REPLAY ? nullptr : raw + 2 * row * T;
   const float* gr = gout + 2 * row * T;
@@ -417,7 +410,7 @@ __global__ __launch_bounds__(kRbWaves* kWave) void fbt_bwd_rb_kernel(
     const int cnt = (int)min<int64_t>(max<int64_t>(T - tb, 0), K);
     c32 zv[K], yv[K], ev[K];
     c32 zp0 = mk(0.0f, 0.0f), yp0 = mk(0.0f, 0.0f);
-    c32 Q = mk(1.0f, 0.0f), r = mk(0.0f, 0.0f);
+    c32 r = mk(0.0f, 0.0f);
     if (has) {
       ld_tile<K>(zr, t0, tb, T, lane, full, io, zv);
       ld_tile<K>(gr, t0, tb, T, lane, full, io, ev);
@@ -430,11 +423,9 @@ __global__ __launch_bounds__(kRbWaves* kWave) void fbt_bwd_rb_kernel(
         const c32 y0 = ldc(carry, row * nc + t0 / kTiTile);  // carries every kTiTile steps
         c32 s = mk(0.0f, 0.0f);
 #pragma unroll
-        for (int k = 0; k < K; ++k)
-          if (k < cnt) s = cmad(a, s, u[k]);
-        c32 P = cnt == K ? apow : cpow_small(a, cnt);
-        if (lane == 0) s = cmad(P, y0, s);
-        wave_scan_fwd(P, s);
+        for (int k = 0; k < K; ++k) s = cmad(a, s, u[k]);
+        if (lane == 0) s = cmad(pf.p[0], y0, s);
+        wave_scan_fwd_pow(s, pf);
         c32 yk = shift_up(s, y0, lane);
         yp0 = yk;
 #pragma unroll
@@ -451,27 +442,28 @@ __global__ __launch_bounds__(kRbWaves* kWave) void fbt_bwd_rb_kernel(
 #pragma unroll
         for (int k = 0; k < K; ++k) ev[k] = mask_by(ev[k], yv[k]);
       }
-      // Suffix composition of g -> e + conj(a) g over the lane's valid steps.
+      // Suffix composition of g -> e + conj(a) g over the lane's steps (zero
+      // cotangent past the end of the row).
 #pragma unroll
-      for (int k = K - 1; k >= 0; --k)
-        if (k < cnt) r = cmad(ac, r, ev[k]);
-      Q = cnt == K ? acpow : conjg(cpow_small(a, cnt));
-      wave_scan_rev(Q, r, lane);  // inclusive suffix over lanes, zero carry
+      for (int k = K - 1; k >= 0; --k) r = cmad(ac, r, ev[k]);
+      wave_scan_rev_pow(r, pf, pr, lane);  // inclusive suffix over lanes, zero carry
     }
-    if (lane == 0) s_map[parity][w] = make_float4(Q.r, Q.i, r.r, r.i);
+    // Tiles past the end publish a zero offset; they only occur in the first
+    // super-tile walked, whose carry is zero, so the tile power applies alike.
+    if (lane == 0) s_map[parity][w] = make_float2(r.r, r.i);
     __syncthreads();
     c32 gin = gcarry;  // adjoint entering this tile from its end
     for (int v = W - 1; v > w; --v) {
-      const float4 m = s_map[parity][v];
-      gin = cmad(mk(m.x, m.y), gin, mk(m.z, m.w));
+      const float2 m = s_map[parity][v];
+      gin = cmad(ptile, gin, mk(m.x, m.y));
     }
     c32 gn = gin;  // the next (earlier) super-tile's carry
     for (int v = w; v >= 0; --v) {
-      const float4 m = s_map[parity][v];
-      gn = cmad(mk(m.x, m.y), gn, mk(m.z, m.w));
+      const float2 m = s_map[parity][v];
+      gn = cmad(ptile, gn, mk(m.x, m.y));
     }
     if (has) {
-      c32 gnext = shift_down(cmad(Q, gin, r), gin, lane);
+      c32 gnext = shift_down(cmad(psfx, gin, r), gin, lane);
       c32 go[K];
       float a1r = 0, a1i = 0, a0r = 0, a0i = 0, a2r = 0, a2i = 0;
 #pragma unroll
@@ -531,7 +523,9 @@ __global__ __launch_bounds__(kTiWaves* kWave) void fbt_bwd_kernel(
   const int64_t f = row / B;
   const c32 a = ldc(c1, f), k0 = ldc(tap0, f), k1 = ldc(tap1, f);
   const c32 ac = conjg(a);
-  const c32 apow = cpow_small(a, kTiK), acpow = conjg(apow);
+  const c64d A = dpow(widen(a), kTiK);
+  const ScanPow pf = scan_pow_fwd(A, lane);  // the replay's forward scan; in-row adjoint powers
+  const RevPow pr = scan_pow_rev(A, lane);
   const float* zr = z + 2 * row * T;
   const float* rr = REPLAY ? nullptr : raw + 2 * row * T;
   const float* gr = gout + 2 * row * T;
@@ -575,11 +569,9 @@ __global__ __launch_bounds__(kTiWaves* kWave) void fbt_bwd_kernel(
       const c32 y0 = ldc(carry, row * nc + tile);
       c32 s = mk(0.0f, 0.0f);
 #pragma unroll
-      for (int k = 0; k < kTiK; ++k)
-        if (k < cnt) s = cmad(a, s, u[k]);
-      c32 P = cnt == kTiK ? apow : cpow_small(a, cnt);
-      if (lane == 0) s = cmad(P, y0, s);
-      wave_scan_fwd(P, s);
+      for (int k = 0; k < kTiK; ++k) s = cmad(a, s, u[k]);
+      if (lane == 0) s = cmad(pf.p[0], y0, s);
+      wave_scan_fwd_pow(s, pf);
       c32 yk = shift_up(s, y0, lane);
       yp0 = yk;
 #pragma unroll
@@ -596,14 +588,13 @@ __global__ __launch_bounds__(kTiWaves* kWave) void fbt_bwd_kernel(
 #pragma unroll
       for (int k = 0; k < kTiK; ++k) ev[k] = mask_by(ev[k], yv[k]);
     }
-    // Suffix composition of g -> e + conj(a) g over the lane's valid steps.
+    // Suffix composition of g -> e + conj(a) g over the lane's steps (zero
+    // cotangent past the end of the row).
     c32 r = mk(0.0f, 0.0f);
 #pragma unroll
-    for (int k = kTiK - 1; k >= 0; --k)
-      if (k < cnt) r = cmad(ac, r, ev[k]);
-    c32 Q = cnt == kTiK ? acpow : conjg(cpow_small(a, cnt));
-    if (lane == kWave - 1) r = cmad(Q, gcarry, r);
-    wave_scan_rev(Q, r, lane);
+    for (int k = kTiK - 1; k >= 0; --k) r = cmad(ac, r, ev[k]);
+    if (lane == kWave - 1) r = cjmad(pf.p[0], gcarry, r);
+    wave_scan_rev_pow(r, pf, pr, lane);
     c32 gnext = shift_down(r, gcarry, lane);
     gcarry = readlane(r, 0);
     c32 go[kTiK];
@@ -689,15 +680,6 @@ struct BtfShape {
   int64_t B, T, F, S, L;
 };
 
-__device__ __forceinline__ c32 cpow_int(c32 a, int64_t n) {
-  c32 r = mk(1.0f, 0.0f);
-  while (n > 0) {
-    if (n & 1) r = cmul(r, a);
-    a = cmul(a, a);
-    n >>= 1;
-  }
-  return r;
-}
 
 // Phase 1 of the forward: segment end states from a zero entry.
 __global__ __launch_bounds__(256) void btf_fwd_local_kernel(
@@ -731,9 +713,11 @@ __global__ __launch_bounds__(256) void btf_fwd_final_kernel(
   const int64_t f = task % sh.F, bs = task / sh.F, seg = bs % sh.S, b = bs / sh.S;
   const c32 a = ldc(c1, f), k0 = ldc(k0p, f), k1 = k1p ? ldc(k1p, f) : mk(0.0f, 0.0f);
   c32 y = mk(0.0f, 0.0f);
-  if (seg > 0) {
-    const c32 aL = cpow_int(a, sh.L);
-    for (int64_t s = 0; s < seg; ++s) y = cmad(aL, y, ldc(seg_end, (b * sh.S + s) * sh.F + f));
+  if (seg > 0) {  // entry state: the earlier segments' end states, folded in fp64
+    const c64d aL = dpow(widen(a), sh.L);
+    c64d e = mkd(0.0, 0.0);
+    for (int64_t s = 0; s < seg; ++s) e = dmad(aL, e, widen(ldc(seg_end, (b * sh.S + s) * sh.F + f)));
+    y = narrow(e);
   }
   const int64_t t_beg = seg * sh.L, t_end = min(sh.T, t_beg + sh.L);
   const float* xb = x + 2 * (b * sh.T * sh.F + f);
@@ -779,9 +763,12 @@ __global__ __launch_bounds__(256) void btf_bwd_final_kernel(
   const c32 a = ldc(c1, f), k0 = ldc(k0p, f), k1 = k1p ? ldc(k1p, f) : mk(0.0f, 0.0f);
   const c32 ac = conjg(a);
   c32 gnext = mk(0.0f, 0.0f);
-  if (seg + 1 < sh.S) {
-    const c32 acL = conjg(cpow_int(a, sh.L));
-    for (int64_t s = sh.S - 1; s > seg; --s) gnext = cmad(acL, gnext, ldc(seg_beg, (b * sh.S + s) * sh.F + f));
+  if (seg + 1 < sh.S) {  // adjoint entering from the later segments, folded in fp64
+    const c64d acL = dconj(dpow(widen(a), sh.L));
+    c64d e = mkd(0.0, 0.0);
+    for (int64_t s = sh.S - 1; s > seg; --s)
+      e = dmad(acL, e, widen(ldc(seg_beg, (b * sh.S + s) * sh.F + f)));
+    gnext = narrow(e);
   }
   const int64_t t_beg = seg * sh.L, t_end = min(sh.T, t_beg + sh.L);
   const int64_t base = b * sh.T * sh.F + f;

@@ -1,7 +1,12 @@
 """Numerics helpers shared by the tests."""
 
+import json
+import os
+
 import numpy as np
 import torch
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 
 # Parity bar: normwise max relative error of each output / gradient tensor
 # against the fp64 oracle (north star: 1e-4 in fp32).
@@ -33,3 +38,56 @@ def to_np(t):
 
 def crandn(rng, *shape):
     return rng.standard_normal(shape) + 1j * rng.standard_normal(shape)
+
+
+def load_checkpoint_params():
+    """(records, arrays) of tests/golden/checkpoint_params.{json,npz}: one record per
+    packaged checkpoint, per-channel RQF leaves flattened over (checkpoint, block)."""
+    with open(os.path.join(GOLDEN, "checkpoint_params.json")) as f:
+        records = json.load(f)
+    arrays = np.load(os.path.join(GOLDEN, "checkpoint_params.npz"))
+    return records, {k: arrays[k] for k in arrays.files}
+
+
+def block_params(rec, arrays, block):
+    """RQFParams of block ``block`` of checkpoint record ``rec``."""
+    from prospective_rqf_amd.coefficients import RQFParams
+
+    off, n = rec["blocks"][block]
+    t = lambda k: torch.from_numpy(arrays[k][off:off + n].astype(np.float64))  # noqa: E731
+    return RQFParams(log_tau=t("log_tau"), dt=rec["dt"], discretization=rec["discretization"],
+                     clamp_gamma=rec["clamp_gamma"], gamma_param=t("gamma_param"),
+                     freq_param=t("freq_param"), min_gamma=t("min_gamma"),
+                     max_gamma=t("max_gamma"), min_freq=t("min_freq"), max_freq=t("max_freq"))
+
+
+def block_coefficients(rec, arrays, block):
+    """The complex64 coefficients block ``block`` feeds its scan, as complex128 numpy:
+    (C1, tap0, tap1) for prospective models, (C1, C2, None) otherwise."""
+    from prospective_rqf_amd.coefficients import compute_coefficients, compute_two_tap_coefficients
+
+    p = block_params(rec, arrays, block)
+    if rec["prospective"]:
+        c = compute_two_tap_coefficients(p, True, rec["prospective_mode"], rec["prospective_tau"])
+    else:
+        c = compute_coefficients(p) + (None,)
+    return tuple(None if v is None else v.numpy().astype(np.complex128) for v in c)
+
+
+def cotangent_off_relu_kink(y_ref, gy, band=1e-4):
+    """Zero the cotangent where the split-ReLU mask is decided by rounding.
+
+    A masked backward (Re/Im of the cotangent pass where Re/Im of the raw state is
+    > 0) is discontinuous in the state.  Where the fp64 state lies within float32
+    rounding of zero, the kernel (whose recompute backward re-derives the state by
+    replay) and the oracle may decide differently, and one such element moves a
+    near-cancelling gradient like grad_z by up to ~10% normwise.  Zeroing the
+    cotangent's component wherever the state's component lies within
+    ``band * max|y_ref|`` of zero makes the result independent of those decisions
+    while every other element still tests the kernel.  Returns (gy', count)."""
+    y = np.asarray(y_ref)
+    g = np.array(gy, dtype=np.complex128, copy=True)
+    lim = band * (float(np.max(np.abs(y))) if y.size else 0.0)
+    near_re, near_im = np.abs(y.real) <= lim, np.abs(y.imag) <= lim
+    g = np.where(near_re, 0.0, g.real) + 1j * np.where(near_im, 0.0, g.imag)
+    return g, int(near_re.sum() + near_im.sum())

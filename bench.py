@@ -63,6 +63,13 @@ def _args():
                     help="configs 3 and 5: include the encoder's residual add (h = out + h) in "
                          "each layer's forward, fused into the scan's stores or as a separate "
                          "pass (the reference's pure.py:486-496, 530-534)")
+    ap.add_argument("--layer", choices=["scan", "split", "single"], default="scan",
+                    help="config 3: 'split'/'single' time the whole selective layer, adding the "
+                         "selector projection (selective.py:205-217) and the drive GEMM "
+                         "(selective_scan.py:117-118) forward, and their backward GEMMs "
+                         "(selective_scan.py:144-146, selective.py:86-97) with the weight "
+                         "gradients as split-K batched GEMMs ('split') or as the reference's "
+                         "single GEMMs ('single')")
     ap.add_argument("--act-only", action="store_true",
                     help="config 3 with the act-only contract (no raw output, no gy)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -170,7 +177,15 @@ def plan_selective(cfg, args, dev):
             write_max=2.0, gamma_scale=math.log(1.25), warp_scale=log_scale, prospective=True,
             samp=samp, tau=tau, seq_duration=seq, device=dev, seed=li)
         layer_inputs.append((inputs, write_raw, activate))
-    if cfg == 3:
+    layer = args.layer if cfg == 3 else "scan"
+    if layer != "scan":
+        # Layer input x (D = F, square layer), drive weight W and the selector heads
+        # Ws (gamma F, warp G, write F rows) over v = [Re x; Im x].  The heads' output
+        # replaces the synthetic logits, at the same N(0, 1) scale.
+        state["x"] = _cn(g, dev, F, B * T)
+        state["W"] = _cn(g, dev, F, F) / math.sqrt(2 * F)
+        state["Ws"] = torch.randn(2 * F + G, 2 * F, generator=g, device=dev) / math.sqrt(2 * F)
+    elif cfg == 3:
         state["z0"] = _cn(g, dev, F, B, T)
     else:
         # Token-copy drive: one-hot tokens (16 markers in the first T-16 steps,
@@ -196,6 +211,37 @@ def plan_selective(cfg, args, dev):
         state[f"gx{li}"] = _cn(g, dev, F, B, T) if activate else None
 
     ops, nbytes = [], {}
+    if layer != "scan":
+        from prospective_rqf_amd.projection import weight_grad
+
+        inputs0 = layer_inputs[0][0]
+
+        def proj_fwd(st):
+            x = st["x"]
+            v = torch.cat((x.real, x.imag), 0)  # the controller's source features
+            lg, ld, lw = (st["Ws"] @ v).split((F, G, F))
+            st["v"] = v
+            st["inputs0"] = inputs0._replace(gamma_logits=lg.reshape(F, B, T),
+                                             warp_logits=ld.reshape(G, B, T),
+                                             write_logits=lw.reshape(F, B, T))
+            st["z0"] = (st["W"] @ x).reshape(F, B, T)
+
+        def proj_bwd(st):
+            dz, dzw, dg, dd, dw = st["grads0"][:5]
+            glog = torch.cat((dg, dd, dw), 0).reshape(2 * F + G, B * T)
+            dv = st["Ws"].T @ glog
+            x, v = st["x"], st.pop("v")
+            dx = st["W"].mH @ dz.reshape(F, B * T) + torch.complex(dv[:F], dv[F:])
+            if layer == "split":
+                dW = weight_grad(dzw.reshape(F, B * T), x)
+                dWs = weight_grad(glog, v)
+            else:
+                dW = dzw.reshape(F, B * T) @ x.mH
+                dWs = glog @ v.T
+            st["layer_grads"] = (dx, dW, dWs)
+
+        ops.append(("proj_fwd[L0]", proj_fwd))
+        nbytes["proj_fwd[L0]"] = 0
     stack = args.stack if cfg == 3 else "none"
     if stack != "none":
         for li in range(len(layer_inputs)):
@@ -206,7 +252,8 @@ def plan_selective(cfg, args, dev):
                 st[f"out{li}"] = selective_forward(st[f"z{li}"], inputs, activate, write_raw,
                                                    chunk, skip=st[f"h{li}"])
             else:
-                out = selective_forward(st[f"z{li}"], inputs, activate, write_raw, chunk)
+                inp = st.get(f"inputs{li}", inputs)
+                out = selective_forward(st[f"z{li}"], inp, activate, write_raw, chunk)
                 if stack == "unfused":  # source = raw + h; h = act + h
                     h = st[f"h{li}"]
                     out = (None if out[0] is None else out[0] + h,
@@ -219,10 +266,14 @@ def plan_selective(cfg, args, dev):
 
         def bwd(st, li=li, inputs=inputs, activate=activate):
             entries = st.pop(f"out{li}")[2]
-            st[f"grads{li}"] = selective_backward(st[f"z{li}"], inputs, entries, st[f"gy{li}"],
+            inp = st.get(f"inputs{li}", inputs)
+            st[f"grads{li}"] = selective_backward(st[f"z{li}"], inp, entries, st[f"gy{li}"],
                                                   st[f"gx{li}"], activate, False, chunk)
 
         ops.append((f"rqf_selective_bwd[L{li}]", bwd))
+    if layer != "scan":
+        ops.append(("proj_bwd[L0]", proj_bwd))
+        nbytes["proj_bwd[L0]"] = 0
     for li, (_, write_raw, activate) in enumerate(layer_inputs):
         fb, bb = selective_bytes(F, B, T, G, chunk, write_raw=write_raw, activate=activate)
         nbytes[f"rqf_selective_fwd[L{li}]"] = fb + (8 * F * B * T if stack != "none" else 0)
@@ -234,6 +285,10 @@ def plan_selective(cfg, args, dev):
     }
     if stack != "none":
         contract += f"; encoder residual add (raw + h, act + h) {stack}"
+    if layer != "scan":
+        contract += (f"; whole layer: selector projection and drive GEMM (fp32), weight "
+                     f"gradients as {'split-K batched' if layer == 'split' else 'single'} GEMMs")
+        name += f" [whole layer, {layer} weight gradients]"
     config = {"workload": name, "F": F, "B": B, "T": T, "G": G, "layers": len(layers),
               "chunk": chunk, "contract": contract}
     cpu_steps = args.cpu_steps or (200 if cfg == 3 else 100)
@@ -702,9 +757,11 @@ def main():
               for i, (name, _) in enumerate(ops)}
     scan_ms = sum(per_op.values())
     fwd_ms = sum(v for k, v in per_op.items() if "_fwd" in k)
+    proj_ms = {k: v for k, v in per_op.items() if k.startswith("proj_")}
     bwd_ms = scan_ms - fwd_ms
     value = plan.elems / (scan_ms * 1e-3) / 1e9
-    dom = max(per_op, key=per_op.get)
+    scan_ops = {k: v for k, v in per_op.items() if not k.startswith("proj_")}
+    dom = max(scan_ops, key=scan_ops.get)
     entry = dom.split("[")[0]
     dom_bytes = plan.bytes[dom]
     achieved = dom_bytes / (per_op[dom] * 1e-3) / 1e9
@@ -748,6 +805,9 @@ def main():
             "alg_bytes_entries": plan.bytes,
         },
     }
+    if proj_ms:
+        result["detail"]["projection_ms"] = {k: round(v, 4) for k, v in proj_ms.items()}
+        result["detail"]["scan_only_ms"] = round(scan_ms - sum(proj_ms.values()), 4)
     if args.cpu:
         result["cpu_baseline"] = plan.cpu()
     print(json.dumps(result), flush=True)

@@ -20,6 +20,7 @@ import torch
 from torch import Tensor
 
 from prospective_rqf_amd import _lib
+from prospective_rqf_amd.projection import weight_grad
 from prospective_rqf_amd.selective_scan_kernel import selective_backward, selective_forward
 
 
@@ -75,7 +76,9 @@ class _SelectiveLayerScan(torch.autograd.Function):
         f_in = x.shape[0]
         with torch.autocast(x.device.type, enabled=False):
             dx = (weight.mH @ dx_drive.reshape(weight.shape[0], -1)).reshape_as(x)
-            dweight = dw_drive.reshape(weight.shape[0], -1) @ x.reshape(f_in, -1).mH
+            # The reference's single GEMM here (dw_drive @ x.mH) reduces over
+            # batch*time into (out, in) and runs at ~2.4 TFLOP/s on MI355X.
+            dweight = weight_grad(dw_drive.reshape(weight.shape[0], -1), x.reshape(f_in, -1))
         if ctx.skip:
             # raw + x and act + x: the skip passes both cotangents to x.
             for g in (grad_raw, grad_act):

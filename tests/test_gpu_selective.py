@@ -231,16 +231,18 @@ def test_long_rows_subset_of_north_star_shape():
     run_case(6, 3, 16000, CASE_ALL, chunk=256, G=2, seed=13)
 
 
-@pytest.mark.parametrize("autocast", [False, True])
+@pytest.mark.parametrize("autocast,shape", [(False, (3, 5, 2, 65)), (True, (3, 5, 2, 65)),
+                                            (False, (3, 5, 1, 4501))])
 @pytest.mark.parametrize("truncated", [False, True])
-def test_layer_scan_autograd_with_drive_gemm(truncated, autocast):
+def test_layer_scan_autograd_with_drive_gemm(truncated, autocast, shape):
     """selective_layer_scan (GEMM + kernels) vs float64 autograd of the restatement.
 
     With an enclosing bf16 autocast region (reference test_selective_cuda.py:263-269)
-    the layer still computes the drive GEMM and the scan in complex64."""
-    print(f"case: layer scan truncated={truncated} autocast={autocast}", flush=True)
+    the layer still computes the drive GEMM and the scan in complex64.  B*T = 4501
+    takes the split weight gradient (4 batched GEMMs and a one-column remainder)."""
+    print(f"case: layer scan truncated={truncated} autocast={autocast} shape={shape}", flush=True)
     rng = np.random.default_rng(21)
-    I, F, B, T = 3, 5, 2, 65
+    I, F, B, T = shape
     inp = rounded_to_f32(make_inputs(F, B, T, CASE_ALL, rng, prospective=True, G=2))
     x = _c64(crandn(rng, I, B, T))
     W = _c64(0.5 * crandn(rng, F, I))

@@ -63,13 +63,15 @@ def _args():
                     help="configs 3 and 5: include the encoder's residual add (h = out + h) in "
                          "each layer's forward, fused into the scan's stores or as a separate "
                          "pass (the reference's pure.py:486-496, 530-534)")
-    ap.add_argument("--layer", choices=["scan", "split", "single"], default="scan",
+    ap.add_argument("--layer", choices=["scan", "fused", "split", "single"], default="scan",
                     help="config 3: 'split'/'single' time the whole selective layer, adding the "
                          "selector projection (selective.py:205-217) and the drive GEMM "
                          "(selective_scan.py:117-118) forward, and their backward GEMMs "
                          "(selective_scan.py:144-146, selective.py:86-97) with the weight "
                          "gradients as split-K batched GEMMs ('split') or as the reference's "
-                         "single GEMMs ('single')")
+                         "single GEMMs ('single'); 'fused' runs the forward and the input "
+                         "gradient as one MFMA GEMM each (csrc/proj.hip) with split-K weight "
+                         "gradients")
     ap.add_argument("--act-only", action="store_true",
                     help="config 3 with the act-only contract (no raw output, no gy)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -212,25 +214,38 @@ def plan_selective(cfg, args, dev):
 
     ops, nbytes = [], {}
     if layer != "scan":
-        from prospective_rqf_amd.projection import weight_grad
+        from prospective_rqf_amd.projection import fused_dx, fused_forward, stacked, weight_grad
 
         inputs0 = layer_inputs[0][0]
 
         def proj_fwd(st):
             x = st["x"]
-            v = torch.cat((x.real, x.imag), 0)  # the controller's source features
-            lg, ld, lw = (st["Ws"] @ v).split((F, G, F))
-            st["v"] = v
+            if layer == "fused":
+                z, logits = fused_forward(x, st["W"], st["Ws"])
+                lg, ld, lw = logits.split((F, G, F))
+            else:
+                v = torch.cat((x.real, x.imag), 0)  # the controller's source features
+                lg, ld, lw = (st["Ws"] @ v).split((F, G, F))
+                st["v"] = v
+                z = st["W"] @ x
             st["inputs0"] = inputs0._replace(gamma_logits=lg.reshape(F, B, T),
                                              warp_logits=ld.reshape(G, B, T),
                                              write_logits=lw.reshape(F, B, T))
-            st["z0"] = (st["W"] @ x).reshape(F, B, T)
+            st["z0"] = z.reshape(F, B, T)
 
         def proj_bwd(st):
             dz, dzw, dg, dd, dw = st["grads0"][:5]
-            glog = torch.cat((dg, dd, dw), 0).reshape(2 * F + G, B * T)
+            n = B * T
+            x = st["x"]
+            if layer == "fused":
+                dx = fused_dx(dz.reshape(F, n), [dg, dd, dw], st["W"], st["Ws"])
+                glog = stacked([dg, dd, dw])  # one buffer: no copy
+                v = torch.cat((x.real, x.imag), 0)
+                st["layer_grads"] = (dx, weight_grad(dzw.reshape(F, n), x), weight_grad(glog, v))
+                return
+            glog = stacked([dg, dd, dw])
             dv = st["Ws"].T @ glog
-            x, v = st["x"], st.pop("v")
+            v = st.pop("v")
             dx = st["W"].mH @ dz.reshape(F, B * T) + torch.complex(dv[:F], dv[F:])
             if layer == "split":
                 dW = weight_grad(dzw.reshape(F, B * T), x)
@@ -286,8 +301,10 @@ def plan_selective(cfg, args, dev):
     if stack != "none":
         contract += f"; encoder residual add (raw + h, act + h) {stack}"
     if layer != "scan":
+        how = {"fused": "fused MFMA projections, split-K", "split": "split-K batched",
+               "single": "single"}[layer]
         contract += (f"; whole layer: selector projection and drive GEMM (fp32), weight "
-                     f"gradients as {'split-K batched' if layer == 'split' else 'single'} GEMMs")
+                     f"gradients as {how} GEMMs")
         name += f" [whole layer, {layer} weight gradients]"
     config = {"workload": name, "F": F, "B": B, "T": T, "G": G, "layers": len(layers),
               "chunk": chunk, "contract": contract}

@@ -240,6 +240,43 @@ int rqf_selective_bwd(const rqf_selective_inputs *in, const float *z, const floa
                       size_t workspace_bytes, rqf_stream_t stream);
 
 /* ------------------------------------------------------------------------ *
+ * Projection GEMM of a selective layer on MFMA, fp32:                       *
+ *   C (M x N) = A (M x K) . B (K x N).                                      *
+ * It has no single reference counterpart. With the drive and selector       *
+ * weights stacked in A it replaces two reference GEMMs and the copy         *
+ * between them:                                                             *
+ *   - z = weight @ x (rqf_models/ops/selective_scan.py:117-118);            *
+ *   - the logits (weights @ v).split(sizes) over                            *
+ *     v = cat(x.real, x.imag) (rqf_models/backbones/rqf/selective.py:205-217). *
+ * With their adjoints stacked it computes dx = weight.mH @ dz               *
+ * (selective_scan.py:144) plus the selector's weights.T @ grad              *
+ * (selective.py:96) in one pass.                                            *
+ *   weights: (k_pad, m_pad) fp32, k-major (m contiguous), zero padded;      *
+ *            k_pad a multiple of 16, m_pad a multiple of 128.               *
+ *   B: b_cplx_rows complex64 rows of n (complex row d is K rows 2d, 2d+1:   *
+ *      real and imaginary part), then b_real_rows fp32 rows of n.           *
+ *   C: out_cplx_rows complex64 rows (rows 2f, 2f+1 of C), then              *
+ *      out_real_rows fp32 rows of n.                                        *
+ * Returns RQF_ERR_ARG when 2*b_cplx_rows + b_real_rows > k_pad or           *
+ * 2*out_cplx_rows + out_real_rows > m_pad.                                  *
+ * ------------------------------------------------------------------------ */
+typedef struct rqf_proj_gemm_args {
+  const float *weights;
+  int64_t k_pad, m_pad;
+  const float *b_cplx;
+  int64_t b_cplx_rows;
+  const float *b_real;
+  int64_t b_real_rows;
+  int64_t n;
+  float *out_cplx;
+  int64_t out_cplx_rows;
+  float *out_real;
+  int64_t out_real_rows;
+} rqf_proj_gemm_args;
+
+int rqf_proj_gemm(const rqf_proj_gemm_args *args, rqf_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
  * Self-test of the wave-level scan primitives (no reference counterpart):   *
  * in: 64 lanes x 4 complex (P, s) affine maps; out: inclusive prefix (fwd)  *
  * and suffix (rev) compositions.                                            *

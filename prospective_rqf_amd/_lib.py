@@ -41,7 +41,21 @@ class SelectiveInputsStruct(ctypes.Structure):
     ]
 
 
+class ProjGemmArgs(ctypes.Structure):
+    """ctypes image of ``rqf_proj_gemm_args``."""
+
+    _fields_ = [
+        ("weights", _P), ("k_pad", _I64), ("m_pad", _I64),
+        ("b_cplx", _P), ("b_cplx_rows", _I64),
+        ("b_real", _P), ("b_real_rows", _I64),
+        ("n", _I64),
+        ("out_cplx", _P), ("out_cplx_rows", _I64),
+        ("out_real", _P), ("out_real_rows", _I64),
+    ]
+
+
 SIGNATURES = {
+    "rqf_proj_gemm": (ctypes.c_int, [_P, _P]),
     "rqf_version": (ctypes.c_char_p, []),
     "rqf_error_string": (ctypes.c_char_p, [ctypes.c_int]),
     "rqf_btf_scan_workspace": (_SZ, [_I64, _I64, _I64]),

@@ -1,0 +1,361 @@
+// proj.hip -- the selective layer's projection GEMMs on MFMA (fp32).
+//
+// C (M x N) = A (M x K) . B (K x N), in fp32 with fp32 accumulation
+// (v_mfma_f32_32x32x2_f32), where
+//   * A is a small weight matrix packed on the host as (k_pad, m_pad), k-major
+//     with m contiguous, zero padded to the tile sizes;
+//   * B is gathered from a complex (rows, N) array -- complex row d gives K rows
+//     2d (real part) and 2d+1 (imaginary part) -- followed by a real (rows, N)
+//     array, so the interleaved complex input needs no [Re; Im] copy;
+//   * C is scattered to a complex (rows, N) array -- rows 2f and 2f+1 are the
+//     real and imaginary parts of complex row f -- followed by a real (rows, N)
+//     array.
+// With the drive and selector weights stacked in A, one pass over the layer
+// input gives both z = W x and the logits Ws [Re x; Im x]
+// (rqf_models/ops/selective_scan.py:117-118, rqf_models/backbones/rqf/
+// selective.py:205-217); with their adjoints stacked, one pass over dz and the
+// logit gradients gives dx (selective_scan.py:144, selective.py:96).
+//
+// Tiles: a 256-thread block computes a 128 x 128 tile of C in four 64 x 64
+// wavefront tiles of 2 x 2 MFMA 32 x 32 blocks, walking K in stages of 16
+// through double-buffered LDS (one barrier per stage).  Blocks are numbered so
+// that the M tiles of one N tile run on one XCD and share its L2 copy of B.
+//
+// Measured at H = 256, B*T = 1.02M: 98 TFLOP/s forward, 96 for dx, 62% of the
+// fp32 MFMA peak.  The library GEMMs it replaces run at 105-135 TFLOP/s, so
+// despite saving the [Re; Im] copy and the add passes it is 5-8% slower than
+// them.  Each k-step waits for its two LDS fragment reads before four MFMAs;
+// tile shape, prefetch depth and occupancy variants all land at 90-100.
+#include "rqf_device.h"
+#include "rqf_scan.h"
+
+using namespace rqf;
+
+namespace {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// Wavefront tile: RQF_PROJ_TM x RQF_PROJ_TN blocks of 32 x 32; the block is
+// 2 x 2 wavefronts.
+#ifndef RQF_PROJ_TM
+#define RQF_PROJ_TM 2
+#endif
+#ifndef RQF_PROJ_TN
+#define RQF_PROJ_TN 2
+#endif
+constexpr int kTM = RQF_PROJ_TM, kTN = RQF_PROJ_TN;
+// 1: read all of a stage's MFMA operands from LDS before its MFMAs.
+#ifndef RQF_PROJ_ALLFRAGS
+#define RQF_PROJ_ALLFRAGS 0
+#endif
+// Stages the global loads run ahead of the MFMAs (1 or 2).
+#ifndef RQF_PROJ_PREFETCH
+#define RQF_PROJ_PREFETCH 1
+#endif
+// Occupancy (waves per SIMD) the register allocator is held to; 0 = no hint.
+// Fused forward at H = 256, B*T = 1.02M: 98 TFLOP/s unhinted (3 waves), 97 held
+// to 3, 82 at 2 waves; 2-stage prefetch 90.
+#ifndef RQF_PROJ_WAVES
+#define RQF_PROJ_WAVES 0
+#endif
+constexpr int kPM = 64 * kTM, kPN = 64 * kTN, kPK = 16, kPThreads = 256, kPXcds = 8;
+// The host pads the weights' M to a multiple of 128 whatever the tile.
+constexpr int kPMPad = 128;
+static_assert(kPM % kPMPad == 0 || kPMPad % kPM == 0, "M tiles cover the padded weights");
+
+// Blocks are dealt round-robin over the XCDs; give each XCD a contiguous range
+// of tile ids.
+__device__ __forceinline__ int64_t proj_xcd_order(int64_t P, int64_t n) {
+  const int64_t x = P % kPXcds, j = P / kPXcds, q = n / kPXcds, r = n % kPXcds;
+  return x * q + (x < r ? x : r) + j;
+}
+
+// Real B row j (0-based after the complex rows), or null past the last row.
+__device__ __forceinline__ const float* real_row(const rqf_proj_gemm_args& g, int64_t j) {
+  return j < g.b_real_rows ? g.b_real + j * g.n : nullptr;
+}
+
+// Two consecutive columns n, n+1 of B rows k (x, y) and k+1 (z, w); zero past
+// the ends.  VEC: N is even, so n < N implies n + 1 < N and the complex pair
+// is one aligned float4.
+template <bool VEC>
+__device__ __forceinline__ float4 load_b_pair(const rqf_proj_gemm_args& g, int64_t k, int64_t n) {
+  float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (n >= g.n) return v;
+  const int64_t kc = 2 * g.b_cplx_rows;
+  if (k < kc) {
+    const float* p = g.b_cplx + 2 * ((k >> 1) * g.n + n);
+    if (VEC) {
+      const float4 q = *reinterpret_cast<const float4*>(p);  // re n, im n, re n+1, im n+1
+      v = make_float4(q.x, q.z, q.y, q.w);
+    } else {
+      v.x = p[0];
+      v.z = p[1];
+      if (n + 1 < g.n) {
+        v.y = p[2];
+        v.w = p[3];
+      }
+    }
+    return v;
+  }
+  const float* r0 = real_row(g, k - kc);
+  const float* r1 = real_row(g, k + 1 - kc);
+  if (VEC) {
+    if (r0) {
+      const float2 q = *reinterpret_cast<const float2*>(r0 + n);
+      v.x = q.x;
+      v.y = q.y;
+    }
+    if (r1) {
+      const float2 q = *reinterpret_cast<const float2*>(r1 + n);
+      v.z = q.x;
+      v.w = q.y;
+    }
+  } else {
+    const bool n1 = n + 1 < g.n;
+    if (r0) {
+      v.x = r0[n];
+      if (n1) v.y = r0[n + 1];
+    }
+    if (r1) {
+      v.z = r1[n];
+      if (n1) v.w = r1[n + 1];
+    }
+  }
+  return v;
+}
+
+// FAST: N even (and at least 2), 16-byte aligned complex rows, 8-byte aligned
+// real rows, and 2 * b_cplx_rows a multiple of the K stage.
+template <bool VEC, bool FAST>
+__global__ __launch_bounds__(kPThreads)
+#if RQF_PROJ_WAVES
+__attribute__((amdgpu_waves_per_eu(RQF_PROJ_WAVES)))
+#endif
+void proj_gemm_kernel(const rqf_proj_gemm_args g,
+                                                              int64_t m_tiles, int64_t tiles) {
+  __shared__ float s_a[2][kPK][kPM];
+  __shared__ float s_b[2][kPK][kPN];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid >> 6;
+  const int64_t id = proj_xcd_order(blockIdx.x, tiles);
+  const int64_t m0 = (id % m_tiles) * kPM, n0 = (id / m_tiles) * kPN;
+  const int wm = (w & 1) * (kPM / 2), wn = (w >> 1) * (kPN / 2);
+  // Staging: an A stage is 16 rows of kPM/4 float4s; a B stage is 8 row pairs of
+  // kPN/2 column pairs.
+  constexpr int kA4 = kPM / 4, kB2 = kPN / 2;
+  constexpr int kRa = kPK * kA4 / kPThreads, kRb = (kPK / 2) * kB2 / kPThreads;
+  struct Slot {
+    float4 a[kRa], b[kRb];
+  };
+  // Per-thread B offsets of the fast path (column clamped to N - 2).
+  int64_t b_off[kRb], b_col[kRb];
+  int b_pair[kRb];
+#pragma unroll
+  for (int r = 0; r < kRb; ++r) {
+    const int idx = tid + r * kPThreads;
+    const int64_t n = n0 + 2 * (idx % kB2);
+    b_pair[r] = idx / kB2;
+    b_col[r] = n < g.n - 2 ? n : g.n - 2;
+    b_off[r] = b_pair[r] * g.n + b_col[r];
+  }
+  // Rows of the padded weights past m_pad: the last M tile of a 256-row tile
+  // over 128-padded weights reads nothing there.
+  auto fetch = [&](int64_t kt, Slot& sl) {
+    float4 (&ra)[kRa] = sl.a;
+    float4 (&rb)[kRb] = sl.b;
+#pragma unroll
+    for (int r = 0; r < kRa; ++r) {
+      const int idx = tid + r * kPThreads;
+      const int64_t krow = kt * kPK + idx / kA4, mcol = m0 + 4 * (idx % kA4);
+      if (kPM <= kPMPad || mcol < g.m_pad)
+        ra[r] = *reinterpret_cast<const float4*>(g.weights + krow * g.m_pad + mcol);
+      else
+        ra[r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    const int64_t k0 = kt * kPK, kc = 2 * g.b_cplx_rows;
+    if (FAST) {
+      // Every stage is all complex or all real rows (2 * b_cplx_rows is a multiple
+      // of the stage).  Rows past the end and columns past N are clamped to the
+      // last ones: the padded weights are zero there, and columns past N are
+      // never stored, so the values read only need to be finite.
+      if (k0 < kc) {
+#pragma unroll
+        for (int r = 0; r < kRb; ++r) {
+          const float4 q = *reinterpret_cast<const float4*>(
+              g.b_cplx + 2 * ((k0 >> 1) * g.n + b_off[r]));
+          rb[r] = make_float4(q.x, q.z, q.y, q.w);
+        }
+      } else if (g.b_real_rows > 0) {
+#pragma unroll
+        for (int r = 0; r < kRb; ++r) {
+          const int64_t j = k0 - kc + 2 * b_pair[r];
+          const int64_t last = g.b_real_rows - 1;
+          const float* base = g.b_real + b_col[r];
+          const float2 a = *reinterpret_cast<const float2*>(base + (j < last ? j : last) * g.n);
+          const float2 b =
+              *reinterpret_cast<const float2*>(base + (j + 1 < last ? j + 1 : last) * g.n);
+          rb[r] = make_float4(a.x, a.y, b.x, b.y);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < kRb; ++r) rb[r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < kRb; ++r) {
+        const int idx = tid + r * kPThreads;
+        rb[r] = load_b_pair<VEC>(g, k0 + 2 * (idx / kB2), n0 + 2 * (idx % kB2));
+      }
+    }
+  };
+  auto stage = [&](int buf, const Slot& sl) {
+    const float4 (&ra)[kRa] = sl.a;
+    const float4 (&rb)[kRb] = sl.b;
+#pragma unroll
+    for (int r = 0; r < kRa; ++r) {
+      const int idx = tid + r * kPThreads;
+      *reinterpret_cast<float4*>(&s_a[buf][idx / kA4][4 * (idx % kA4)]) = ra[r];
+    }
+#pragma unroll
+    for (int r = 0; r < kRb; ++r) {
+      const int idx = tid + r * kPThreads;
+      const int p = idx / kB2, q = idx % kB2;
+      *reinterpret_cast<float2*>(&s_b[buf][2 * p][2 * q]) = make_float2(rb[r].x, rb[r].y);
+      *reinterpret_cast<float2*>(&s_b[buf][2 * p + 1][2 * q]) = make_float2(rb[r].z, rb[r].w);
+    }
+  };
+  v16f acc[kTM][kTN];
+#pragma unroll
+  for (int i = 0; i < kTM; ++i)
+#pragma unroll
+    for (int j = 0; j < kTN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+  // A wavefront whose rows all lie past the output rows computes nothing (the
+  // stacked forward has 2F + 2F + G rows, 1032 at H = 256, padded to 1152); it
+  // still loads and waits at the barriers with its block.
+  const int64_t mtot = 2 * g.out_cplx_rows + g.out_real_rows;
+  const bool live = m0 + wm < mtot;
+
+  const int64_t ktiles = g.k_pad / kPK;
+  // While stage kt is computed from one LDS buffer, the next stage's global
+  // loads are in flight into registers and go to the other buffer after it
+  // (RQF_PROJ_PREFETCH 2: stage kt + 2 is fetched and kt + 1, fetched one stage
+  // earlier, is written).
+  Slot s0, s1;
+  fetch(0, s0);
+  stage(0, s0);
+  if (RQF_PROJ_PREFETCH == 2 && ktiles > 1) fetch(1, s1);
+  __syncthreads();
+  const int kr = lane >> 5, col = lane & 31;
+  // The operand fragments of k-step kk + 1 are read from LDS while the MFMAs of
+  // step kk run (two fragment slots).
+  auto frags = [&](int buf, int kk, float (&af)[kTM], float (&bf)[kTN]) {
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) af[i] = s_a[buf][2 * kk + kr][wm + 32 * i + col];
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) bf[j] = s_b[buf][2 * kk + kr][wn + 32 * j + col];
+  };
+  auto step = [&](int64_t kt, int buf, Slot& into, const Slot& from) {
+    if (RQF_PROJ_PREFETCH == 2) {
+      if (kt + 2 < ktiles) fetch(kt + 2, into);
+    } else if (kt + 1 < ktiles) {
+      fetch(kt + 1, into);
+    }
+    if (live) {
+#if RQF_PROJ_ALLFRAGS
+      // All of the stage's fragments first; the MFMAs then wait for them in order.
+      float af[kPK / 2][kTM], bf[kPK / 2][kTN];
+#pragma unroll
+      for (int kk = 0; kk < kPK / 2; ++kk) frags(buf, kk, af[kk], bf[kk]);
+#pragma unroll
+      for (int kk = 0; kk < kPK / 2; ++kk)
+#pragma unroll
+        for (int i = 0; i < kTM; ++i)
+#pragma unroll
+          for (int j = 0; j < kTN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[kk][i], bf[kk][j], acc[i][j], 0,
+                                                             0, 0);
+#else
+      float af[2][kTM], bf[2][kTN];
+      frags(buf, 0, af[0], bf[0]);
+#pragma unroll
+      for (int kk = 0; kk < kPK / 2; ++kk) {
+        if (kk + 1 < kPK / 2) frags(buf, kk + 1, af[(kk + 1) & 1], bf[(kk + 1) & 1]);
+#pragma unroll
+        for (int i = 0; i < kTM; ++i)
+#pragma unroll
+          for (int j = 0; j < kTN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[kk & 1][i], bf[kk & 1][j],
+                                                             acc[i][j], 0, 0, 0);
+      }
+#endif
+    }
+    if (kt + 1 < ktiles) stage(buf ^ 1, RQF_PROJ_PREFETCH == 2 ? from : into);
+    __syncthreads();
+  };
+  for (int64_t kt = 0; kt < ktiles; kt += 2) {
+    step(kt, 0, s0, s1);
+    if (kt + 1 < ktiles) step(kt + 1, 1, s1, s0);
+  }
+
+  // Lane l holds C[8*(v/4) + 4*(l/32) + v%4][l%32] of each 32 x 32 block.
+  const int64_t mc = 2 * g.out_cplx_rows;
+#pragma unroll
+  for (int i = 0; i < kTM; ++i)
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+      const int64_t n = n0 + wn + 32 * j + col;
+      if (n >= g.n) continue;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t m = m0 + wm + 32 * i + 8 * (v >> 2) + 4 * kr + (v & 3);
+        if (m < mc) {
+          if ((v & 1) == 0)  // rows m (even) and m + 1: one complex value
+            *reinterpret_cast<float2*>(g.out_cplx + 2 * ((m >> 1) * g.n + n)) =
+                make_float2(acc[i][j][v], acc[i][j][v + 1]);
+        } else if (m < mtot) {
+          g.out_real[(m - mc) * g.n + n] = acc[i][j][v];
+        }
+      }
+    }
+}
+
+inline bool aligned(const void* p, uintptr_t a) { return p == nullptr || ((uintptr_t)p & (a - 1)) == 0; }
+
+}  // namespace
+
+extern "C" int rqf_proj_gemm(const rqf_proj_gemm_args* args, rqf_stream_t stream) {
+  if (!args) return RQF_ERR_ARG;
+  const rqf_proj_gemm_args& g = *args;
+  if (g.n < 0 || g.k_pad < 0 || g.m_pad < 0 || g.b_cplx_rows < 0 || g.out_cplx_rows < 0 ||
+      g.out_real_rows < 0)
+    return RQF_ERR_ARG;
+  if (g.b_real_rows < 0 || (g.b_real_rows > 0 && !g.b_real)) return RQF_ERR_ARG;
+  const int64_t k = 2 * g.b_cplx_rows + g.b_real_rows, m = 2 * g.out_cplx_rows + g.out_real_rows;
+  if (g.k_pad % kPK || g.m_pad % kPMPad || k > g.k_pad || m > g.m_pad) return RQF_ERR_ARG;
+  if (g.n == 0 || m == 0) return RQF_OK;
+  if (!g.weights || (g.b_cplx_rows && !g.b_cplx) || (g.out_cplx_rows && !g.out_cplx) ||
+      (g.out_real_rows && !g.out_real))
+    return RQF_ERR_ARG;
+  if (!aligned(g.weights, 16) || !aligned(g.b_cplx, 8) || !aligned(g.out_cplx, 8) ||
+      !aligned(g.out_real, 4))
+    return RQF_ERR_ALIGN;
+  const bool vec = g.n % 2 == 0 && aligned(g.b_cplx, 16) && aligned(g.b_real, 8);
+  const int64_t m_tiles = (g.m_pad + kPM - 1) / kPM, n_tiles = (g.n + kPN - 1) / kPN;
+  const int64_t tiles = m_tiles * n_tiles;
+  if (tiles > 0x7fffffff) return RQF_ERR_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  const bool fast = vec && g.n >= 2 && (2 * g.b_cplx_rows) % kPK == 0;
+  if (fast)
+    hipLaunchKernelGGL((proj_gemm_kernel<true, true>), dim3((unsigned)tiles), dim3(kPThreads), 0,
+                       s, g, m_tiles, tiles);
+  else if (vec)
+    hipLaunchKernelGGL((proj_gemm_kernel<true, false>), dim3((unsigned)tiles), dim3(kPThreads),
+                       0, s, g, m_tiles, tiles);
+  else
+    hipLaunchKernelGGL((proj_gemm_kernel<false, false>), dim3((unsigned)tiles), dim3(kPThreads),
+                       0, s, g, m_tiles, tiles);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? RQF_OK : (int)err;
+}

@@ -139,10 +139,14 @@ def selective_backward(z, inputs, entries, gy, gx, activate, truncated, chunk):
     o = inputs.options
     dz = torch.empty_like(z)
     dzw = torch.empty_like(z) if truncated else dz
-    dg = torch.empty((f, b, t), dtype=torch.float32, device=z.device) if o[0] else None
-    dw = torch.empty((f, b, t), dtype=torch.float32, device=z.device) if o[2] else None
     s, keep = inputs_struct(z, inputs)
-    dd = torch.empty((s.G, b, t), dtype=torch.float32, device=z.device) if o[1] else None
+    # The head gradients are consecutive row ranges of one buffer, in the
+    # selector's head order (gamma, warp, write; selective.py:211-217), so the
+    # projection backward reads them as one (rows, B*T) matrix without a copy.
+    rows = (f if o[0] else 0, s.G if o[1] else 0, f if o[2] else 0)
+    heads = torch.empty((sum(rows), b, t), dtype=torch.float32, device=z.device)
+    dg, dd, dw = (heads[a:a + r] if r and o[i] else None
+                  for i, (a, r) in enumerate(zip((0, rows[0], rows[0] + rows[1]), rows)))
     dbias = torch.empty(f, dtype=torch.float32, device=z.device)
     dtheta = torch.empty(f, dtype=torch.float32, device=z.device)
     gy = None if gy is None else gy.resolve_conj().to(torch.complex64).contiguous()

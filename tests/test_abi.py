@@ -71,27 +71,28 @@ def test_struct_layout_matches_header():
     assert ctypes.sizeof(s) == 32 + 12 * 8 + 56
 
 
-def test_struct_layout_matches_c_compiler(tmp_path):
-    """offsetof() of every rqf_selective_inputs field, as gcc lays out the
-    header, equals the ctypes image's offsets."""
+@pytest.mark.parametrize("cname,image", [("rqf_selective_inputs", "SelectiveInputsStruct"),
+                                         ("rqf_proj_gemm_args", "ProjGemmArgs")])
+def test_struct_layout_matches_c_compiler(tmp_path, cname, image):
+    """offsetof() of every field of the header's struct, as gcc lays it out,
+    equals the ctypes image's offsets."""
     import shutil
     import subprocess
 
     if shutil.which("gcc") is None:
         pytest.skip("gcc not available")
-    fields = [name for name, _ in _lib.SelectiveInputsStruct._fields_]
+    s = getattr(_lib, image)
+    fields = [name for name, _ in s._fields_]
     src = tmp_path / "offsets.c"
     src.write_text(
         '#include <stddef.h>\n#include <stdio.h>\n#include "rqf_scan.h"\nint main(void) {\n'
-        + "".join(f'  printf("{f} %zu\\n", offsetof(rqf_selective_inputs, {f}));\n'
-                  for f in fields)
-        + '  printf("sizeof %zu\\n", sizeof(rqf_selective_inputs));\n  return 0;\n}\n')
+        + "".join(f'  printf("{f} %zu\\n", offsetof({cname}, {f}));\n' for f in fields)
+        + f'  printf("sizeof %zu\\n", sizeof({cname}));\n  return 0;\n}}\n')
     exe = tmp_path / "offsets"
     subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)],
                    check=True)
     got = dict(line.split() for line in subprocess.run(
         [str(exe)], check=True, capture_output=True, text=True).stdout.splitlines())
-    s = _lib.SelectiveInputsStruct
     for f in fields:
         assert int(got[f]) == getattr(s, f).offset, f
     assert int(got["sizeof"]) == ctypes.sizeof(s)

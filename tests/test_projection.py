@@ -104,3 +104,29 @@ def test_split_projection_matches_reference_semantics(sizes):
     loss2.backward()
     assert torch.allclose(v.grad, v2.grad, rtol=1e-12, atol=1e-12)
     assert torch.allclose(Ws.grad, W2.grad, rtol=1e-12, atol=1e-9)
+
+
+def test_stacked_reads_consecutive_blocks_in_place():
+    from prospective_rqf_amd.projection import stacked
+
+    buf = torch.arange(2 * 7 * 5, dtype=torch.float32).reshape(7, 2, 5)  # (rows, B, T)
+    a, b, c = buf[:3], buf[3:4], buf[4:]
+    s = stacked([a, b, c])
+    assert s.data_ptr() == buf.data_ptr() and s.shape == (7, 10)
+    assert torch.equal(s, buf.reshape(7, 10))
+    # Not consecutive: a copy with the same values.
+    s2 = stacked([c, a])
+    assert s2.data_ptr() != buf.data_ptr()
+    assert torch.equal(s2, torch.cat([c.reshape(3, 10), a.reshape(3, 10)]))
+    assert stacked([None, buf[:0]]) is None
+
+
+def test_stacked_does_not_join_separate_allocations():
+    from prospective_rqf_amd.projection import stacked
+
+    # Two tensors that happen to be adjacent in memory but have separate storages.
+    big = torch.zeros(10, 4)
+    a = big[:3].clone()
+    b = torch.ones(2, 4)
+    s = stacked([a, b])
+    assert s.shape == (5, 4) and torch.equal(s, torch.cat([a, b]))

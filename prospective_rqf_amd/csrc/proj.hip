@@ -24,8 +24,12 @@
 // Measured at H = 256, B*T = 1.02M: 98 TFLOP/s forward, 96 for dx, 62% of the
 // fp32 MFMA peak.  The library GEMMs it replaces run at 105-135 TFLOP/s, so
 // despite saving the [Re; Im] copy and the add passes it is 5-8% slower than
-// them.  Each k-step waits for its two LDS fragment reads before four MFMAs;
-// tile shape, prefetch depth and occupancy variants all land at 90-100.
+// them.  Variants measured and dropped (forward, TFLOP/s):
+// - wavefront tiles 2x4, 4x2, 4x4 (occupancy 1): 68-78;
+// - all of a stage's fragments read before its MFMAs (occupancy 2): 82;
+// - loads two stages ahead: 90;
+// - tiles row-major with a stage's K values contiguous, so one ds_read_b128
+//   brings four k-steps (two LDS waits per stage): 91.
 #include "rqf_device.h"
 #include "rqf_scan.h"
 
@@ -44,19 +48,11 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 #define RQF_PROJ_TN 2
 #endif
 constexpr int kTM = RQF_PROJ_TM, kTN = RQF_PROJ_TN;
-// 1: read all of a stage's MFMA operands from LDS before its MFMAs.
-#ifndef RQF_PROJ_ALLFRAGS
-#define RQF_PROJ_ALLFRAGS 0
-#endif
-// Stages the global loads run ahead of the MFMAs (1 or 2).
-#ifndef RQF_PROJ_PREFETCH
-#define RQF_PROJ_PREFETCH 1
-#endif
-// Occupancy (waves per SIMD) the register allocator is held to; 0 = no hint.
-// Fused forward at H = 256, B*T = 1.02M: 98 TFLOP/s unhinted (3 waves), 97 held
-// to 3, 82 at 2 waves; 2-stage prefetch 90.
+// Occupancy (waves per SIMD) the register allocator is held to; 0 = no hint
+// (which leaves this kernel at 2 waves: 64 accumulator AGPRs + 112 VGPRs; held
+// to 3 it keeps the accumulators in VGPRs, 125 in all).
 #ifndef RQF_PROJ_WAVES
-#define RQF_PROJ_WAVES 0
+#define RQF_PROJ_WAVES 3
 #endif
 constexpr int kPM = 64 * kTM, kPN = 64 * kTN, kPK = 16, kPThreads = 256, kPXcds = 8;
 // The host pads the weights' M to a multiple of 128 whatever the tile.
@@ -239,13 +235,10 @@ void proj_gemm_kernel(const rqf_proj_gemm_args g,
 
   const int64_t ktiles = g.k_pad / kPK;
   // While stage kt is computed from one LDS buffer, the next stage's global
-  // loads are in flight into registers and go to the other buffer after it
-  // (RQF_PROJ_PREFETCH 2: stage kt + 2 is fetched and kt + 1, fetched one stage
-  // earlier, is written).
-  Slot s0, s1;
-  fetch(0, s0);
-  stage(0, s0);
-  if (RQF_PROJ_PREFETCH == 2 && ktiles > 1) fetch(1, s1);
+  // loads are in flight into registers and go to the other buffer after it.
+  Slot sl;
+  fetch(0, sl);
+  stage(0, sl);
   __syncthreads();
   const int kr = lane >> 5, col = lane & 31;
   // The operand fragments of k-step kk + 1 are read from LDS while the MFMAs of
@@ -256,27 +249,10 @@ void proj_gemm_kernel(const rqf_proj_gemm_args g,
 #pragma unroll
     for (int j = 0; j < kTN; ++j) bf[j] = s_b[buf][2 * kk + kr][wn + 32 * j + col];
   };
-  auto step = [&](int64_t kt, int buf, Slot& into, const Slot& from) {
-    if (RQF_PROJ_PREFETCH == 2) {
-      if (kt + 2 < ktiles) fetch(kt + 2, into);
-    } else if (kt + 1 < ktiles) {
-      fetch(kt + 1, into);
-    }
+  for (int64_t kt = 0; kt < ktiles; ++kt) {
+    const int buf = (int)(kt & 1);
+    if (kt + 1 < ktiles) fetch(kt + 1, sl);
     if (live) {
-#if RQF_PROJ_ALLFRAGS
-      // All of the stage's fragments first; the MFMAs then wait for them in order.
-      float af[kPK / 2][kTM], bf[kPK / 2][kTN];
-#pragma unroll
-      for (int kk = 0; kk < kPK / 2; ++kk) frags(buf, kk, af[kk], bf[kk]);
-#pragma unroll
-      for (int kk = 0; kk < kPK / 2; ++kk)
-#pragma unroll
-        for (int i = 0; i < kTM; ++i)
-#pragma unroll
-          for (int j = 0; j < kTN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[kk][i], bf[kk][j], acc[i][j], 0,
-                                                             0, 0);
-#else
       float af[2][kTM], bf[2][kTN];
       frags(buf, 0, af[0], bf[0]);
 #pragma unroll
@@ -289,14 +265,9 @@ void proj_gemm_kernel(const rqf_proj_gemm_args g,
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[kk & 1][i], bf[kk & 1][j],
                                                              acc[i][j], 0, 0, 0);
       }
-#endif
     }
-    if (kt + 1 < ktiles) stage(buf ^ 1, RQF_PROJ_PREFETCH == 2 ? from : into);
+    if (kt + 1 < ktiles) stage(buf ^ 1, sl);
     __syncthreads();
-  };
-  for (int64_t kt = 0; kt < ktiles; kt += 2) {
-    step(kt, 0, s0, s1);
-    if (kt + 1 < ktiles) step(kt + 1, 1, s1, s0);
   }
 
   // Lane l holds C[8*(v/4) + 4*(l/32) + v%4][l%32] of each 32 x 32 block.

@@ -72,6 +72,12 @@ def _args():
                          "single GEMMs ('single'); 'fused' runs the forward and the input "
                          "gradient as one MFMA GEMM each (csrc/proj.hip) with split-K weight "
                          "gradients")
+    ap.add_argument("--readout", choices=["none", "fused", "reference"], default="none",
+                    help="configs 2 and 5: add the per-timestep [Re; Im] MLP readout "
+                         "(train.py:74-136, hidden 256, 10 classes, per-step logits and their "
+                         "backward) on the last layer's output: 'fused' runs "
+                         "readout.complex_readout on the (F, B, T) features, 'reference' the "
+                         "reference's permute + cat + Linear + ReLU + Linear")
     ap.add_argument("--act-only", action="store_true",
                     help="config 3 with the act-only contract (no raw output, no gy)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -384,6 +390,38 @@ def plan_fbt(cfg, args, dev):
             st[f"grads{li}"] = fbt_recompute_backward_raw(c1, t0, t1, x, carry, st[f"gy{li}"])
 
         ops.append((f"rqf_fbt_recompute_bwd[L{li}]", bwd))
+    if args.readout != "none":
+        from prospective_rqf_amd.readout import complex_readout
+
+        H, C = 256, 10
+        gw = torch.Generator(device=dev).manual_seed(7)
+        w1 = (torch.randn(H, 2 * F, generator=gw, device=dev) / math.sqrt(2 * F)).requires_grad_(True)
+        b1 = torch.zeros(H, device=dev, requires_grad=True)
+        w2 = (torch.randn(C, H, generator=gw, device=dev) * 1e-3).requires_grad_(True)
+        b2 = torch.zeros(C, device=dev, requires_grad=True)
+        l1, l2 = torch.nn.Linear(2 * F, H).to(dev), torch.nn.Linear(H, C).to(dev)
+        with torch.no_grad():
+            l1.weight.copy_(w1), l1.bias.copy_(b1), l2.weight.copy_(w2), l2.bias.copy_(b2)
+        state["readout_cot"] = torch.randn(B, T, C, generator=gw, device=dev)
+        last = L - 1
+
+        def ro_fwd(st):
+            feats = st[f"out{last}"][0].detach().requires_grad_(True)
+            if args.readout == "fused":
+                logits = complex_readout(feats, w1, b1, w2, b2, pool=False)
+            else:  # the FBT stack's exit copy (pure.py:536), then train.py:130-132
+                f = feats.permute(1, 2, 0).contiguous()
+                x = torch.cat([f.real, f.imag], dim=-1).reshape(B * T, 2 * F)
+                logits = l2(torch.relu(l1(x))).reshape(B, T, C)
+            st["readout"] = (feats, logits)
+
+        def ro_bwd(st):
+            feats, logits = st.pop("readout")
+            logits.backward(st["readout_cot"])
+            st["grads_readout"] = feats.grad
+
+        ops.insert(L, ("readout_fwd", ro_fwd))
+        ops.append(("readout_bwd", ro_bwd))
     fb, bb = fbt_recompute_bytes(F, B, T)
     if stack != "none":
         fb += 8 * F * B * T
@@ -391,12 +429,17 @@ def plan_fbt(cfg, args, dev):
     for li in range(L):
         nbytes[f"rqf_fbt_recompute_fwd[L{li}]"] = fb
         nbytes[f"rqf_fbt_recompute_bwd[L{li}]"] = bb
+    if args.readout != "none":
+        nbytes["readout_fwd"] = nbytes["readout_bwd"] = 0
     kernels = {"rqf_fbt_recompute_fwd": "fbt_fwd_rb_kernel",
                "rqf_fbt_recompute_bwd": ("fbt_bwd_rb_kernel<replay> (T % 256 == 0) or "
                                          "fbt_bwd_kernel<replay>, + coef_reduce_kernel")}
     contract = "split-ReLU output, per-tile carries; gy cotangent, full BPTT"
     if stack != "none":
         contract += f"; encoder residual add (act + h) {stack}"
+    if args.readout != "none":
+        contract += f"; per-timestep [Re; Im] MLP readout (hidden 256, 10 classes), {args.readout}"
+        name += f" [+ readout, {args.readout}]"
     config = {"workload": name, "F": F, "B": B, "T": T, "layers": L, "contract": contract}
     cpu_steps = args.cpu_steps or (1000 if cfg == 2 else 500)
 
@@ -774,10 +817,10 @@ def main():
               for i, (name, _) in enumerate(ops)}
     scan_ms = sum(per_op.values())
     fwd_ms = sum(v for k, v in per_op.items() if "_fwd" in k)
-    proj_ms = {k: v for k, v in per_op.items() if k.startswith("proj_")}
+    proj_ms = {k: v for k, v in per_op.items() if k.startswith(("proj_", "readout_"))}
     bwd_ms = scan_ms - fwd_ms
     value = plan.elems / (scan_ms * 1e-3) / 1e9
-    scan_ops = {k: v for k, v in per_op.items() if not k.startswith("proj_")}
+    scan_ops = {k: v for k, v in per_op.items() if not k.startswith(("proj_", "readout_"))}
     dom = max(scan_ops, key=scan_ops.get)
     entry = dom.split("[")[0]
     dom_bytes = plan.bytes[dom]
@@ -823,7 +866,7 @@ def main():
         },
     }
     if proj_ms:
-        result["detail"]["projection_ms"] = {k: round(v, 4) for k, v in proj_ms.items()}
+        result["detail"]["outside_scan_ms"] = {k: round(v, 4) for k, v in proj_ms.items()}
         result["detail"]["scan_only_ms"] = round(scan_ms - sum(proj_ms.values()), 4)
     if args.cpu:
         result["cpu_baseline"] = plan.cpu()

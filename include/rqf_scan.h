@@ -257,6 +257,9 @@ int rqf_selective_bwd(const rqf_selective_inputs *in, const float *z, const floa
  *      real and imaginary part), then b_real_rows fp32 rows of n.           *
  *   C: out_cplx_rows complex64 rows (rows 2f, 2f+1 of C), then              *
  *      out_real_rows fp32 rows of n.                                        *
+ *   The real rows may take a bias and a ReLU (a Linear + ReLU layer on the  *
+ *   stacked [Re; Im] of complex features: the per-timestep readout,         *
+ *   train.py:74-136).                                                       *
  * Returns RQF_ERR_ARG when 2*b_cplx_rows + b_real_rows > k_pad or           *
  * 2*out_cplx_rows + out_real_rows > m_pad.                                  *
  * ------------------------------------------------------------------------ */
@@ -272,6 +275,8 @@ typedef struct rqf_proj_gemm_args {
   int64_t out_cplx_rows;
   float *out_real;
   int64_t out_real_rows;
+  const float *out_real_bias; /* out_real_rows biases added to the real rows, or NULL */
+  int64_t out_real_relu;      /* nonzero: max(0, .) on the real rows after the bias */
 } rqf_proj_gemm_args;
 
 int rqf_proj_gemm(const rqf_proj_gemm_args *args, rqf_stream_t stream);

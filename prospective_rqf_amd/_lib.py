@@ -51,6 +51,7 @@ class ProjGemmArgs(ctypes.Structure):
         ("n", _I64),
         ("out_cplx", _P), ("out_cplx_rows", _I64),
         ("out_real", _P), ("out_real_rows", _I64),
+        ("out_real_bias", _P), ("out_real_relu", _I64),
     ]
 
 

@@ -286,7 +286,10 @@ void proj_gemm_kernel(const rqf_proj_gemm_args g,
             *reinterpret_cast<float2*>(g.out_cplx + 2 * ((m >> 1) * g.n + n)) =
                 make_float2(acc[i][j][v], acc[i][j][v + 1]);
         } else if (m < mtot) {
-          g.out_real[(m - mc) * g.n + n] = acc[i][j][v];
+          float o = acc[i][j][v];
+          if (g.out_real_bias) o += g.out_real_bias[m - mc];
+          if (g.out_real_relu) o = fmaxf(o, 0.0f);
+          g.out_real[(m - mc) * g.n + n] = o;
         }
       }
     }

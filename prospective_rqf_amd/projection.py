@@ -169,7 +169,8 @@ def pack_dx(weight: Tensor, heads: Tensor | None) -> Tensor:
 
 
 def _proj_gemm(packed: Tensor, b_cplx: Tensor | None, b_real: Tensor | None, n: int,
-               out_cplx_rows: int, out_real_rows: int, device):
+               out_cplx_rows: int, out_real_rows: int, device, bias: Tensor | None = None,
+               relu: bool = False):
     from prospective_rqf_amd import _lib
 
     lib = _lib.load()
@@ -188,6 +189,8 @@ def _proj_gemm(packed: Tensor, b_cplx: Tensor | None, b_real: Tensor | None, n: 
     a.out_cplx_rows = out_cplx_rows
     a.out_real = 0 if out_r is None else out_r.data_ptr()
     a.out_real_rows = out_real_rows
+    a.out_real_bias = 0 if bias is None else bias.data_ptr()
+    a.out_real_relu = int(bool(relu))
     _lib.check(lib.rqf_proj_gemm(ctypes.byref(a), _lib.stream_of(packed)), "rqf_proj_gemm")
     return out_c, out_r
 

@@ -130,3 +130,54 @@ def test_stacked_does_not_join_separate_allocations():
     b = torch.ones(2, 4)
     s = stacked([a, b])
     assert s.shape == (5, 4) and torch.equal(s, torch.cat([a, b]))
+
+
+def _kernel_emulation(packed, b_cplx, b_real, out_cplx_rows, out_real_rows):
+    """What rqf_proj_gemm computes, in fp64 on the CPU: B rows from the interleaved
+    complex rows then the real rows, C = A B, C rows scattered to complex then real."""
+    rows = []
+    if b_cplx is not None:
+        rows.append(torch.view_as_real(b_cplx.to(torch.complex128)).permute(0, 2, 1)
+                    .reshape(-1, b_cplx.shape[1]))
+    if b_real is not None:
+        rows.append(b_real.double())
+    b = torch.cat(rows, 0)
+    a = packed.double()[:b.shape[0]].T  # (m_pad, K)
+    c = a @ b
+    zc = None
+    if out_cplx_rows:
+        pairs = c[:2 * out_cplx_rows].reshape(out_cplx_rows, 2, -1)
+        zc = torch.complex(pairs[:, 0], pairs[:, 1])
+    return zc, c[2 * out_cplx_rows:2 * out_cplx_rows + out_real_rows]
+
+
+def test_packed_weights_give_the_reference_products():
+    from prospective_rqf_amd.projection import pack_dx, pack_forward
+    from prospective_rqf_amd.readout import pack_feature_grad, pack_hidden
+
+    gen = torch.Generator().manual_seed(11)
+    F, D, ml, N = 5, 3, 7, 13
+    W = _rand((F, D), True, gen)
+    Ws = torch.randn(ml, 2 * D, generator=gen)
+    x = _rand((D, N), True, gen)
+    x64, W64, Ws64 = x.to(torch.complex128), W.to(torch.complex128), Ws.double()
+    v = torch.cat((x64.real, x64.imag), 0)
+    z, lg = _kernel_emulation(pack_forward(W, Ws), x, None, F, ml)
+    assert torch.allclose(z, W64 @ x64, atol=1e-9) and torch.allclose(lg, Ws64 @ v, atol=1e-9)
+    dz = _rand((F, N), True, gen)
+    g = torch.randn(ml, N, generator=gen)
+    dx, _ = _kernel_emulation(pack_dx(W, Ws), dz, g, D, 0)
+    dv = Ws64.T @ g.double()
+    want = W64.mH @ dz.to(torch.complex128) + torch.complex(dv[:D], dv[D:])
+    assert torch.allclose(dx, want, atol=1e-9)
+    # Readout: hidden = W1 [Re f; Im f]; the feature gradient W1^T dh as complex rows.
+    H = 4
+    w1 = torch.randn(H, 2 * F, generator=gen)
+    f = _rand((F, N), True, gen)
+    _, hid = _kernel_emulation(pack_hidden(w1), f, None, 0, H)
+    f64 = f.to(torch.complex128)
+    assert torch.allclose(hid, w1.double() @ torch.cat((f64.real, f64.imag), 0), atol=1e-9)
+    dh = torch.randn(H, N, generator=gen)
+    df, _ = _kernel_emulation(pack_feature_grad(w1), None, dh, F, 0)
+    dfv = w1.double().T @ dh.double()
+    assert torch.allclose(df, torch.complex(dfv[:F], dfv[F:]), atol=1e-9)

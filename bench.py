@@ -548,8 +548,8 @@ def plan_multi_osc(cfg, args, dev):
         elems = B * T * F
         nbytes = {"rqf_multi_osc_fwd": 16 * elems, "rqf_multi_osc_bwd": 24 * elems}
         kernels = {"rqf_multi_osc_fwd": "mosc_fwd_local + mosc_carry + mosc_fwd_final",
-                   "rqf_multi_osc_bwd": ("mosc_fwd_local + mosc_carry + mosc_bwd_local + "
-                                         "mosc_carry + mosc_bwd_final + mosc_coef_reduce")}
+                   "rqf_multi_osc_bwd": ("mosc_bwd_local + mosc_carry + mosc_bwd_final + "
+                                         "mosc_coef_reduce")}
         contract = "complex u in, complex y out; grad_u + grad_C1/C2/c_weights"
     else:
         name = ("fused |y| readout: single-oscillator scan on real input, 128 filters, "

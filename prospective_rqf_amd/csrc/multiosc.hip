@@ -16,12 +16,24 @@
 // NP oscillators (N padded to a power of two; padded oscillators have zero
 // coefficients) in registers over its segment.  Segments are joined by a
 // carry pass per (batch, oscillator, filter) over the segments (three-phase
-// scan).  The backward runs the adjoint the same way.  For the coefficient
-// gradients, which pair the adjoint at t with the state at t-1, it writes
-// checkpoints of the forward state every LC steps during a forward sweep of
-// the segment, then walks the segment's LC-step chunks backwards, recomputing
-// each chunk's states into registers from its checkpoint.  No division by C1
-// and no per-step state tensor are needed.
+// scan).
+//
+// The scanned state is w_n = x_n / C2_n, i.e. w_n[t] = C1_n w_n[t-1] + u[t],
+// with C2_n applied at the output: y = sum_n (cw_n C2_n) w_n.  No division
+// happens; C2 = 0 is fine.
+//
+// Backward.  The adjoint e_n[t] = conj(C1_n) e_n[t+1] + grad_out[t] runs as a
+// reverse three-phase scan (local pass, carry, final pass); grad_u is
+// sum_n conj(cw_n C2_n) e_n.  The reference's coefficient sums pair the
+// adjoint at t with the state at t-1, which a reverse sweep does not have.
+// Exchanging the order of summation pairs them with u instead
+// (mosc_coef_reduce_kernel): against e_n for grad_C2 and grad_cw, and against
+// f_n, the derivative of e_n's recurrence with respect to conj(C1_n), for
+// grad_C1.  f_n is itself a reverse recurrence, f_n[t] = conj(C1_n) f_n[t+1] +
+// e_n[t+1], carried between segments with e_n.  So the final pass reads
+// grad_out and u once and produces grad_u and all three sums, with no forward
+// state, no checkpoints and no per-step state tensor (the reference keeps
+// every state in a (B*F, T, N) scratch tensor).
 //
 // Coefficient gradients are reduced deterministically: per-task fp32 partial
 // sums over at most kMoscMaxSeg steps, then an ordered fp64 reduction per
@@ -39,14 +51,6 @@ constexpr int kMoscMaxOsc = 8;     // oscillators per filter (N <= 8)
 constexpr int kMoscMaxSeg = 256;   // steps per segment, at most
 constexpr int kMoscMinSeg = 16;    // steps per segment, at least (when T allows)
 constexpr int64_t kMoscLanes = 65536;  // target number of tasks
-// Backward register chunk: kMoscChunk / NP steps (at least 2) of all NP
-// oscillator states are recomputed into registers per checkpoint.  Config 6
-// (N = 4) backward: 1.34 ms with 8, 1.49 with 16, 1.34 with 32 (206 VGPRs
-// against 110).
-#ifndef RQF_MOSC_CHUNK
-#define RQF_MOSC_CHUNK 8
-#endif
-constexpr int kMoscChunk = RQF_MOSC_CHUNK;
 
 __device__ __forceinline__ c32 ldc(const float* p, int64_t i) { return mk(p[2 * i], p[2 * i + 1]); }
 __device__ __forceinline__ void stc(float* p, int64_t i, c32 v) {
@@ -56,7 +60,7 @@ __device__ __forceinline__ void stc(float* p, int64_t i, c32 v) {
 
 struct MoscShape {
   int64_t B, T, F, S, L, tasks;
-  int N, LC, NCH;
+  int N;
 };
 
 template <bool REAL>
@@ -91,39 +95,50 @@ __device__ __forceinline__ int64_t seg_idx(const MoscShape& sh, int64_t b, int64
   return ((b * sh.S + s) * NP + n) * sh.F + f;
 }
 
+// One step of the scanned state w_n[t] = C1_n w_n[t-1] + u[t].
+template <bool REAL>
+__device__ __forceinline__ c32 step_w(c32 a, c32 w, c32 ut) {
+  return REAL ? cmadr(a, w, ut.r) : cmad(a, w, ut);
+}
+
 // Phase 1 of the forward: each segment's end states from a zero entry.
 template <int NP, bool REAL>
 __global__ __launch_bounds__(256) void mosc_fwd_local_kernel(const float* __restrict__ c1,
-                                                             const float* __restrict__ c2,
                                                              const float* __restrict__ u,
                                                              float* __restrict__ seg,
                                                              MoscShape sh) {
   const int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (task >= sh.tasks) return;
   const Task k = task_of(sh, task);
-  c32 a[NP], g[NP], x[NP];
+  c32 a[NP], w[NP];
   load_osc<NP>(c1, k.f, sh.N, a);
-  load_osc<NP>(c2, k.f, sh.N, g);
 #pragma unroll
-  for (int n = 0; n < NP; ++n) x[n] = mk(0.0f, 0.0f);
+  for (int n = 0; n < NP; ++n) w[n] = mk(0.0f, 0.0f);
   const int64_t base = k.b * sh.T * sh.F + k.f;
 #pragma unroll 8
   for (int64_t t = k.tb; t < k.te; ++t) {
     const c32 ut = load_u<REAL>(u, base + t * sh.F);
 #pragma unroll
-    for (int n = 0; n < NP; ++n) x[n] = cmad(a[n], x[n], cmul(g[n], ut));
+    for (int n = 0; n < NP; ++n) w[n] = step_w<REAL>(a[n], w[n], ut);
   }
 #pragma unroll
-  for (int n = 0; n < NP; ++n) stc(seg, seg_idx(sh, k.b, k.s, n, k.f, NP), x[n]);
+  for (int n = 0; n < NP; ++n) stc(seg, seg_idx(sh, k.b, k.s, n, k.f, NP), w[n]);
 }
 
 // Phase 2: exclusive fold over the segments, in place, per (b, n, f).
-//   forward: entry[s+1] = C1^L entry[s] + end[s]                (entry[0] = 0)
-//   adjoint: exit[s-1] = conj(C1)^len(s) exit[s] + start[s]     (exit[S-1] = 0)
-// where exit[s] is the adjoint entering segment s from its end.
-template <int NP, bool ADJ>
+//   forward: w_in[s+1] = C1^L w_in[s] + w_end[s]                    (w_in[0] = 0)
+//   adjoint: the pair (e, f) entering segment s from its end,
+//            e_out[s-1] = P e_out[s] + e_start[s]
+//            f_out[s-1] = P f_out[s] + len(s) P' e_out[s] + f_start[s]   (TAN)
+//            with P = conj(C1)^len(s), P' = conj(C1)^(len(s)-1), and zero
+//            at s = S-1.
+// len(s) steps of zero input take (e, f) to (P e, P f + len P' e), by
+// induction on the adjoint step (see mosc_bwd_final_kernel).
+template <int NP, bool ADJ, bool TAN>
 __global__ __launch_bounds__(256) void mosc_carry_kernel(const float* __restrict__ c1,
-                                                         float* __restrict__ seg, MoscShape sh) {
+                                                         float* __restrict__ seg,
+                                                         float* __restrict__ segf,
+                                                         MoscShape sh) {
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= sh.B * NP * sh.F) return;
   const int64_t f = id % sh.F, bn = id / sh.F;
@@ -143,19 +158,45 @@ __global__ __launch_bounds__(256) void mosc_carry_kernel(const float* __restrict
     }
   } else {
     const c64d ac = dconj(widen(a));
-    const c64d acL = dpow(ac, sh.L);
-    const c64d acLast = dpow(ac, sh.T - (sh.S - 1) * sh.L);
+    const int64_t lenLast = sh.T - (sh.S - 1) * sh.L;
+    const c64d p1 = sh.L > 1 ? dpow(ac, sh.L - 1) : mkd(1.0, 0.0);
+    const c64d p1Last = lenLast > 1 ? dpow(ac, lenLast - 1) : mkd(1.0, 0.0);
+    const c64d p = dmul(p1, ac), pLast = dmul(p1Last, ac);
+    const c64d q = mkd(p1.r * (double)sh.L, p1.i * (double)sh.L);
+    const c64d qLast = mkd(p1Last.r * (double)lenLast, p1Last.i * (double)lenLast);
+    c64d ef = mkd(0.0, 0.0);
     for (int64_t s = sh.S - 1; s >= 0; --s) {
+      const bool last = s == sh.S - 1;
       const int64_t i = seg_idx(sh, b, s, n, f, NP);
       const c32 v = ldc(seg, i);
       stc(seg, i, narrow(e));
-      e = dmad(s == sh.S - 1 ? acLast : acL, e, widen(v));
+      if (TAN) {
+        const c32 vf = ldc(segf, i);
+        stc(segf, i, narrow(ef));
+        ef = dmad(last ? pLast : p, ef, dmad(last ? qLast : q, e, widen(vf)));
+      }
+      e = dmad(last ? pLast : p, e, widen(v));
     }
   }
 }
 
+// Output weights of the scanned state: y = sum_n (cw_n C2_n) w_n, or C2_0 w_0
+// without C-weights.
+template <int NP, bool CW>
+__device__ __forceinline__ void load_out_weights(const float* __restrict__ c2,
+                                                 const float* __restrict__ cw, int64_t f, int N,
+                                                 c32 (&h)[NP]) {
+  load_osc<NP>(c2, f, N, h);
+  if (CW) {
+    c32 w[NP];
+    load_osc<NP>(cw, f, N, w);
+#pragma unroll
+    for (int n = 0; n < NP; ++n) h[n] = cmul(w[n], h[n]);
+  }
+}
+
 // Phase 3 of the forward: rescan each segment from its entry state and write
-// y = sum_n cw_n x_n (CW) or x_0, as complex or as |y| (ABS).
+// y = sum_n cw_n C2_n w_n (CW) or C2_0 w_0, as complex or as |y| (ABS).
 template <int NP, bool REAL, bool CW, bool ABS>
 __global__ __launch_bounds__(256) void mosc_fwd_final_kernel(
     const float* __restrict__ c1, const float* __restrict__ c2, const float* __restrict__ cw,
@@ -164,12 +205,11 @@ __global__ __launch_bounds__(256) void mosc_fwd_final_kernel(
   const int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (task >= sh.tasks) return;
   const Task k = task_of(sh, task);
-  c32 a[NP], g[NP], w[NP], x[NP];
+  c32 a[NP], h[NP], w[NP];
   load_osc<NP>(c1, k.f, sh.N, a);
-  load_osc<NP>(c2, k.f, sh.N, g);
-  if (CW) load_osc<NP>(cw, k.f, sh.N, w);
+  load_out_weights<NP, CW>(c2, cw, k.f, sh.N, h);
 #pragma unroll
-  for (int n = 0; n < NP; ++n) x[n] = ldc(seg, seg_idx(sh, k.b, k.s, n, k.f, NP));
+  for (int n = 0; n < NP; ++n) w[n] = ldc(seg, seg_idx(sh, k.b, k.s, n, k.f, NP));
   const int64_t base = k.b * sh.T * sh.F + k.f;
 #pragma unroll 8
   for (int64_t t = k.tb; t < k.te; ++t) {
@@ -178,8 +218,8 @@ __global__ __launch_bounds__(256) void mosc_fwd_final_kernel(
     c32 y = mk(0.0f, 0.0f);
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
-      x[n] = cmad(a[n], x[n], cmul(g[n], ut));
-      y = CW ? cmad(w[n], x[n], y) : (n == 0 ? x[0] : y);
+      w[n] = step_w<REAL>(a[n], w[n], ut);
+      if (CW || n == 0) y = cmad(h[n], w[n], y);
     }
     if (ABS)
       out[e] = sqrtf(fmaf(y.r, y.r, y.i * y.i));
@@ -188,161 +228,144 @@ __global__ __launch_bounds__(256) void mosc_fwd_final_kernel(
   }
 }
 
-// Phase 1 of the backward: each segment's adjoint at its first step from a
-// zero adjoint after its last step; the scan input is conj(cw_n) gy[t].
-template <int NP>
+// One reverse step of the adjoint pair (see mosc_bwd_final_kernel).
+template <bool TAN>
+__device__ __forceinline__ void step_adj(c32 a, c32& e, c32& f, c32 gt) {
+  if (TAN) f = cjmad(a, f, e);
+  e = cjmad(a, e, gt);
+}
+
+// Phase 1 of the backward: each segment's adjoint pair at its first step from
+// a zero pair after its last step.
+template <int NP, bool TAN>
 __global__ __launch_bounds__(256) void mosc_bwd_local_kernel(const float* __restrict__ c1,
-                                                             const float* __restrict__ cw,
                                                              const float* __restrict__ gy,
                                                              float* __restrict__ segb,
+                                                             float* __restrict__ segf,
                                                              MoscShape sh) {
   const int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (task >= sh.tasks) return;
   const Task k = task_of(sh, task);
-  c32 a[NP], w[NP], d[NP];
+  c32 a[NP], d[NP], f[NP];
   load_osc<NP>(c1, k.f, sh.N, a);
-  load_osc<NP>(cw, k.f, sh.N, w);
 #pragma unroll
-  for (int n = 0; n < NP; ++n) d[n] = mk(0.0f, 0.0f);
+  for (int n = 0; n < NP; ++n) d[n] = f[n] = mk(0.0f, 0.0f);
   const int64_t base = k.b * sh.T * sh.F + k.f;
 #pragma unroll 8
   for (int64_t t = k.te - 1; t >= k.tb; --t) {
     const c32 gt = ldc(gy, base + t * sh.F);
 #pragma unroll
-    for (int n = 0; n < NP; ++n) d[n] = cjmad(a[n], d[n], cjmul(w[n], gt));
+    for (int n = 0; n < NP; ++n) step_adj<TAN>(a[n], d[n], f[n], gt);
   }
 #pragma unroll
-  for (int n = 0; n < NP; ++n) stc(segb, seg_idx(sh, k.b, k.s, n, k.f, NP), d[n]);
+  for (int n = 0; n < NP; ++n) {
+    const int64_t i = seg_idx(sh, k.b, k.s, n, k.f, NP);
+    stc(segb, i, d[n]);
+    if (TAN) stc(segf, i, f[n]);
+  }
 }
 
-// Phase 3 of the backward.  Per task: forward sweep writing a checkpoint of
-// the states every LC steps; then the chunks in reverse, each recomputing its
-// LC states into registers and running the adjoint over them:
-//   d_n[t]     = conj(C1_n) d_n[t+1] + conj(cw_n) gy[t]
-//   grad_u[t]  = sum_n conj(C2_n) d_n[t]          (real u: its real part)
-//   grad_C1_n += d_n[t] conj(x_n[t-1]),  grad_C2_n += d_n[t] conj(u[t]),
-//   grad_cw_n += gy[t] conj(x_n[t])
-// Partial sums per task go to part[(n*6 + j)*tasks + task].
-template <int NP, bool REAL>
+// Phase 3 of the backward, from each segment's exit pair, for t descending:
+//   f_n[t]    = conj(C1_n) f_n[t+1] + e_n[t+1]                  (TAN)
+//   e_n[t]    = conj(C1_n) e_n[t+1] + gy[t]
+//   grad_u[t] = sum_n conj(cw_n C2_n) e_n[t]   (GU; real u: its real part)
+//   Q_n += e_n[t] conj(u[t]),  R_n += f_n[t] conj(u[t])         (TAN)
+// e_n is the reference's adjoint d_n without its conj(cw_n) factor, and
+// f_n[t] = sum_{s>t} conj(C1_n)^(s-1-t) e_n[s], the derivative of e_n's
+// recurrence with respect to conj(C1_n).  Partial sums go to
+// part[(n*4 + j)*tasks + task] (j: Re Q, Im Q, Re R, Im R).
+template <int NP, bool REAL, bool TAN, bool GU>
 __global__ __launch_bounds__(256) void mosc_bwd_final_kernel(
     const float* __restrict__ c1, const float* __restrict__ c2, const float* __restrict__ cw,
-    const float* __restrict__ u, const float* __restrict__ gy, const float* __restrict__ seg,
-    const float* __restrict__ segb, float* __restrict__ ckpt, float* __restrict__ gu,
-    float* __restrict__ part, MoscShape sh) {
-  constexpr int LC = kMoscChunk / NP > 2 ? kMoscChunk / NP : 2;
+    const float* __restrict__ u, const float* __restrict__ gy, const float* __restrict__ segb,
+    const float* __restrict__ segf, float* __restrict__ gu, float* __restrict__ part,
+    MoscShape sh) {
   const int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (task >= sh.tasks) return;
   const Task k = task_of(sh, task);
-  c32 a[NP], g[NP], w[NP], x[NP], d[NP];
+  c32 a[NP], h[NP], d[NP], f[NP], q[NP], r[NP];
   load_osc<NP>(c1, k.f, sh.N, a);
-  load_osc<NP>(c2, k.f, sh.N, g);
-  load_osc<NP>(cw, k.f, sh.N, w);
+  if (GU) load_out_weights<NP, true>(c2, cw, k.f, sh.N, h);
+#pragma unroll
+  for (int n = 0; n < NP; ++n) {
+    const int64_t i = seg_idx(sh, k.b, k.s, n, k.f, NP);
+    d[n] = ldc(segb, i);
+    f[n] = TAN ? ldc(segf, i) : mk(0.0f, 0.0f);
+    q[n] = r[n] = mk(0.0f, 0.0f);
+  }
   const int64_t base = k.b * sh.T * sh.F + k.f;
-  // Forward sweep: checkpoint the state entering every chunk.
+#pragma unroll 8
+  for (int64_t t = k.te - 1; t >= k.tb; --t) {
+    const int64_t e = base + t * sh.F;
+    const c32 gt = ldc(gy, e);
+    const c32 ut = TAN ? load_u<REAL>(u, e) : mk(0.0f, 0.0f);
+    c32 g = mk(0.0f, 0.0f);
 #pragma unroll
-  for (int n = 0; n < NP; ++n) x[n] = ldc(seg, seg_idx(sh, k.b, k.s, n, k.f, NP));
-  const int nch = (int)((k.te - k.tb + LC - 1) / LC);
-  for (int c = 0; c < nch; ++c) {
-#pragma unroll
-    for (int n = 0; n < NP; ++n) stc(ckpt, ((int64_t)c * NP + n) * sh.tasks + task, x[n]);
-    if (c + 1 == nch) break;
-    const int64_t t0 = k.tb + (int64_t)c * LC;
-#pragma unroll
-    for (int j = 0; j < LC; ++j) {
-      const c32 ut = load_u<REAL>(u, base + (t0 + j) * sh.F);
-#pragma unroll
-      for (int n = 0; n < NP; ++n) x[n] = cmad(a[n], x[n], cmul(g[n], ut));
-    }
-  }
-  // Reverse over the chunks.
-#pragma unroll
-  for (int n = 0; n < NP; ++n) d[n] = ldc(segb, seg_idx(sh, k.b, k.s, n, k.f, NP));
-  float acc[NP][6];
-#pragma unroll
-  for (int n = 0; n < NP; ++n)
-#pragma unroll
-    for (int j = 0; j < 6; ++j) acc[n][j] = 0.0f;
-  for (int c = nch - 1; c >= 0; --c) {
-    const int64_t t0 = k.tb + (int64_t)c * LC;
-    const int cnt = (int)min<int64_t>(LC, k.te - t0);
-    c32 x0[NP], xs[LC][NP];
-#pragma unroll
-    for (int n = 0; n < NP; ++n) x0[n] = ldc(ckpt, ((int64_t)c * NP + n) * sh.tasks + task);
-#pragma unroll
-    for (int j = 0; j < LC; ++j) {
-      const c32 ut = j < cnt ? load_u<REAL>(u, base + (t0 + j) * sh.F) : mk(0.0f, 0.0f);
-#pragma unroll
-      for (int n = 0; n < NP; ++n)
-        xs[j][n] = cmad(a[n], j ? xs[j - 1][n] : x0[n], cmul(g[n], ut));
-    }
-#pragma unroll
-    for (int j = LC - 1; j >= 0; --j) {
-      if (j >= cnt) continue;
-      const int64_t e = base + (t0 + j) * sh.F;
-      const c32 gt = ldc(gy, e);
-      const c32 ut = load_u<REAL>(u, e);  // re-read: cache-resident from the chunk's replay
-      c32 gsum = mk(0.0f, 0.0f);
-#pragma unroll
-      for (int n = 0; n < NP; ++n) {
-        d[n] = cjmad(a[n], d[n], cjmul(w[n], gt));
-        gsum = cjmad(g[n], d[n], gsum);
-        const c32 xp = j ? xs[j - 1][n] : x0[n];
-        const c32 s1 = cjmul(xp, d[n]);     // d conj(x[t-1])
-        const c32 s2 = cjmul(ut, d[n]);     // d conj(u[t])
-        const c32 s3 = cjmul(xs[j][n], gt); // gy conj(x[t])
-        acc[n][0] += s1.r;
-        acc[n][1] += s1.i;
-        acc[n][2] += s2.r;
-        acc[n][3] += s2.i;
-        acc[n][4] += s3.r;
-        acc[n][5] += s3.i;
-      }
-      if (gu) {
-        if (REAL)
-          gu[e] = gsum.r;
-        else
-          stc(gu, e, gsum);
+    for (int n = 0; n < NP; ++n) {
+      step_adj<TAN>(a[n], d[n], f[n], gt);
+      if (GU) g = cjmad(h[n], d[n], g);
+      if (TAN) {
+        if (REAL) {
+          q[n] = csmad(ut.r, d[n], q[n]);
+          r[n] = csmad(ut.r, f[n], r[n]);
+        } else {
+          q[n] = cjmad(ut, d[n], q[n]);
+          r[n] = cjmad(ut, f[n], r[n]);
+        }
       }
     }
+    if (GU) {
+      if (REAL)
+        gu[e] = g.r;
+      else
+        stc(gu, e, g);
+    }
   }
+  if (TAN) {
 #pragma unroll
-  for (int n = 0; n < NP; ++n)
-#pragma unroll
-    for (int j = 0; j < 6; ++j) part[((int64_t)n * 6 + j) * sh.tasks + task] = acc[n][j];
+    for (int n = 0; n < NP; ++n) {
+      float* p = part + (int64_t)n * 4 * sh.tasks + task;
+      p[0] = q[n].r;
+      p[sh.tasks] = q[n].i;
+      p[2 * sh.tasks] = r[n].r;
+      p[3 * sh.tasks] = r[n].i;
+    }
+  }
 }
 
 // grad_C1, grad_C2, grad_cw of oscillator n of filter f: one wavefront per
-// (f, n < N) sums the B*S task partials in a fixed order in fp64.
-__global__ __launch_bounds__(64) void mosc_coef_reduce_kernel(const float* __restrict__ part,
-                                                              MoscShape sh, int NP,
-                                                              float* __restrict__ gc1,
-                                                              float* __restrict__ gc2,
-                                                              float* __restrict__ gcw) {
+// (f, n < N) sums the B*S task partials of Q and R in a fixed order in fp64,
+// then
+//   grad_C1 = conj(cw C2) R,   grad_C2 = conj(cw) Q,   grad_cw = conj(C2) Q.
+// These are the reference's sums, with x_n = C2_n w_n and d_n = conj(cw_n) e_n
+// and the order of summation exchanged (u[r] enters w_n[t] with C1^(t-r)):
+//   sum_t d_n[t] conj(u[t])     = conj(cw_n) sum_t e_n[t] conj(u[t])
+//   sum_t gy[t] conj(x_n[t])    = conj(C2_n) sum_r conj(u[r]) sum_{t>=r} conj(C1)^(t-r) gy[t]
+//                               = conj(C2_n) sum_r e_n[r] conj(u[r])
+//   sum_t d_n[t] conj(x_n[t-1]) = conj(cw_n C2_n) sum_r conj(u[r]) sum_{t>r} conj(C1)^(t-1-r) e_n[t]
+//                               = conj(cw_n C2_n) sum_r f_n[r] conj(u[r]).
+__global__ __launch_bounds__(64) void mosc_coef_reduce_kernel(
+    const float* __restrict__ part, const float* __restrict__ c2, const float* __restrict__ cw,
+    MoscShape sh, int NP, float* __restrict__ gc1, float* __restrict__ gc2,
+    float* __restrict__ gcw) {
   const int64_t fn = blockIdx.x;  // f*N + n
   const int64_t f = fn / sh.N;
   const int n = (int)(fn - f * sh.N);
   const int lane = threadIdx.x;
   const int64_t M = sh.B * sh.S;
-  double s[6] = {0, 0, 0, 0, 0, 0};
+  double s[4] = {0, 0, 0, 0};
   for (int64_t m = lane; m < M; m += kWave) {
 #pragma unroll
-    for (int j = 0; j < 6; ++j) s[j] += part[((int64_t)n * 6 + j) * sh.tasks + m * sh.F + f];
+    for (int j = 0; j < 4; ++j) s[j] += part[((int64_t)n * 4 + j) * sh.tasks + m * sh.F + f];
   }
 #pragma unroll
-  for (int j = 0; j < 6; ++j) s[j] = wave_sum(s[j]);
+  for (int j = 0; j < 4; ++j) s[j] = wave_sum(s[j]);
   if (lane == 0) {
-    if (gc1) {
-      gc1[2 * fn] = (float)s[0];
-      gc1[2 * fn + 1] = (float)s[1];
-    }
-    if (gc2) {
-      gc2[2 * fn] = (float)s[2];
-      gc2[2 * fn + 1] = (float)s[3];
-    }
-    if (gcw) {
-      gcw[2 * fn] = (float)s[4];
-      gcw[2 * fn + 1] = (float)s[5];
-    }
+    const c64d q = mkd(s[0], s[1]), r = mkd(s[2], s[3]);
+    const c64d g2 = dconj(widen(ldc(c2, fn))), gw = dconj(widen(ldc(cw, fn)));
+    if (gc1) stc(gc1, fn, narrow(dmul(dmul(gw, g2), r)));
+    if (gc2) stc(gc2, fn, narrow(dmul(gw, q)));
+    if (gcw) stc(gcw, fn, narrow(dmul(g2, q)));
   }
 }
 
@@ -367,8 +390,6 @@ MoscShape mosc_shape(int64_t B, int64_t T, int64_t F, int N) {
   sh.T = T;
   sh.F = F;
   sh.N = N;
-  const int NP = pad_osc(N);
-  sh.LC = kMoscChunk / NP > 2 ? kMoscChunk / NP : 2;
   const int64_t lanes = std::max<int64_t>(B * F, 1);
   int64_t S = (kMoscLanes + lanes - 1) / lanes;
   S = std::min<int64_t>(S, std::max<int64_t>(T / kMoscMinSeg, 1));
@@ -377,27 +398,30 @@ MoscShape mosc_shape(int64_t B, int64_t T, int64_t F, int N) {
   sh.L = T > 0 ? (T + S - 1) / S : 1;
   sh.S = T > 0 ? (T + sh.L - 1) / sh.L : 1;
   sh.tasks = B * sh.S * F;
-  sh.NCH = (int)((sh.L + sh.LC - 1) / sh.LC);
   return sh;
 }
 
+// Segment states of one kind: (b, s, n, f) complex.
+size_t mosc_states(const MoscShape& sh) {
+  return round256((size_t)(sh.B * sh.S * pad_osc(sh.N) * sh.F) * 8);
+}
+
+// Workspace: forward, the w entries; backward, the adjoint pair's entries and
+// the per-task partial sums.
 struct MoscWs {
-  size_t seg, segb, ckpt, part, total;
+  size_t seg, segf, part, total;
 };
 MoscWs mosc_ws(const MoscShape& sh, bool backward) {
-  const int NP = pad_osc(sh.N);
-  const size_t states = (size_t)(sh.B * sh.S * NP * sh.F) * 8;
+  const size_t states = mosc_states(sh);
   MoscWs w;
-  size_t off = 0;
-  w.seg = off;
-  off += round256(states);
-  w.segb = off;
-  if (backward) off += round256(states);
-  w.ckpt = off;
-  if (backward) off += round256((size_t)sh.tasks * sh.NCH * NP * 8);
-  w.part = off;
-  if (backward) off += round256((size_t)sh.tasks * NP * 6 * 4);
-  w.total = off;
+  w.seg = 0;
+  if (!backward) {
+    w.segf = w.part = w.total = states;
+    return w;
+  }
+  w.segf = states;
+  w.part = 2 * states;
+  w.total = w.part + round256((size_t)sh.tasks * pad_osc(sh.N) * 4 * 4);
   return w;
 }
 
@@ -414,6 +438,20 @@ int with_np(int N, Fn&& fn) {
 
 bool bad_shape(int64_t B, int64_t T, int64_t F, int64_t N) {
   return B < 0 || T < 0 || F < 0 || N < 1 || N > kMoscMaxOsc;
+}
+
+// Phases 1-3 of the backward, for the gradients requested (tan: the
+// coefficient sums; gu: grad_u).
+template <int NP, bool REAL, bool TAN, bool GU>
+void launch_bwd(const float* c1, const float* c2, const float* cw, const float* u,
+                const float* gy, float* segb, float* segf, float* gu, float* part,
+                const MoscShape& sh, hipStream_t s) {
+  const dim3 block(256), grid((unsigned)((sh.tasks + 255) / 256));
+  const dim3 cgrid((unsigned)((sh.B * NP * sh.F + 255) / 256));
+  hipLaunchKernelGGL((mosc_bwd_local_kernel<NP, TAN>), grid, block, 0, s, c1, gy, segb, segf, sh);
+  hipLaunchKernelGGL((mosc_carry_kernel<NP, true, TAN>), cgrid, block, 0, s, c1, segb, segf, sh);
+  hipLaunchKernelGGL((mosc_bwd_final_kernel<NP, REAL, TAN, GU>), grid, block, 0, s, c1, c2, cw,
+                     u, gy, segb, segf, gu, part, sh);
 }
 
 }  // namespace
@@ -447,10 +485,11 @@ extern "C" int rqf_multi_osc_fwd(const float* c1, const float* c2, const float* 
   const int rc = with_np((int)N, [&](auto npc) {
     constexpr int NP = decltype(npc)::value;
     if (u_real)
-      hipLaunchKernelGGL((mosc_fwd_local_kernel<NP, true>), grid, block, 0, s, c1, c2, u, seg, sh);
+      hipLaunchKernelGGL((mosc_fwd_local_kernel<NP, true>), grid, block, 0, s, c1, u, seg, sh);
     else
-      hipLaunchKernelGGL((mosc_fwd_local_kernel<NP, false>), grid, block, 0, s, c1, c2, u, seg, sh);
-    hipLaunchKernelGGL((mosc_carry_kernel<NP, false>), cgrid, block, 0, s, c1, seg, sh);
+      hipLaunchKernelGGL((mosc_fwd_local_kernel<NP, false>), grid, block, 0, s, c1, u, seg, sh);
+    hipLaunchKernelGGL((mosc_carry_kernel<NP, false, false>), cgrid, block, 0, s, c1, seg,
+                       nullptr, sh);
     const bool has_cw = cw != nullptr;
     if (u_real) {
       if (has_cw && out_abs)
@@ -492,40 +531,39 @@ extern "C" int rqf_multi_osc_bwd(const float* c1, const float* c2, const float* 
   const MoscWs w = mosc_ws(sh, true);
   if (w.total && (!workspace || workspace_bytes < w.total)) return RQF_ERR_WORKSPACE;
   char* ws = (char*)workspace;
-  float* seg = (float*)(ws + w.seg);
-  float* segb = (float*)(ws + w.segb);
-  float* ckpt = (float*)(ws + w.ckpt);
+  float* segb = (float*)(ws + w.seg);
+  float* segf = (float*)(ws + w.segf);
   float* part = (float*)(ws + w.part);
+  const bool coefs = grad_c1 || grad_c2 || grad_cw;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 block(256), grid((unsigned)((sh.tasks + 255) / 256));
-  const int64_t carriers = B * pad_osc((int)N) * F;
-  const dim3 cgrid((unsigned)((carriers + 255) / 256));
-  const bool work = B * T > 0;
   const int rc = with_np((int)N, [&](auto npc) {
     constexpr int NP = decltype(npc)::value;
-    if (!work) return;
-    if (u_real)
-      hipLaunchKernelGGL((mosc_fwd_local_kernel<NP, true>), grid, block, 0, s, c1, c2, u, seg, sh);
-    else
-      hipLaunchKernelGGL((mosc_fwd_local_kernel<NP, false>), grid, block, 0, s, c1, c2, u, seg, sh);
-    hipLaunchKernelGGL((mosc_carry_kernel<NP, false>), cgrid, block, 0, s, c1, seg, sh);
-    hipLaunchKernelGGL((mosc_bwd_local_kernel<NP>), grid, block, 0, s, c1, cw, grad_out, segb, sh);
-    hipLaunchKernelGGL((mosc_carry_kernel<NP, true>), cgrid, block, 0, s, c1, segb, sh);
-    if (u_real)
-      hipLaunchKernelGGL((mosc_bwd_final_kernel<NP, true>), grid, block, 0, s, c1, c2, cw, u,
-                         grad_out, seg, segb, ckpt, grad_u, part, sh);
-    else
-      hipLaunchKernelGGL((mosc_bwd_final_kernel<NP, false>), grid, block, 0, s, c1, c2, cw, u,
-                         grad_out, seg, segb, ckpt, grad_u, part, sh);
+    if (B * T == 0 || (!coefs && !grad_u)) return;
+    if (u_real) {
+      if (coefs && grad_u)
+        launch_bwd<NP, true, true, true>(c1, c2, cw, u, grad_out, segb, segf, grad_u, part, sh, s);
+      else if (coefs)
+        launch_bwd<NP, true, true, false>(c1, c2, cw, u, grad_out, segb, segf, grad_u, part, sh, s);
+      else
+        launch_bwd<NP, true, false, true>(c1, c2, cw, u, grad_out, segb, segf, grad_u, part, sh, s);
+    } else {
+      if (coefs && grad_u)
+        launch_bwd<NP, false, true, true>(c1, c2, cw, u, grad_out, segb, segf, grad_u, part, sh, s);
+      else if (coefs)
+        launch_bwd<NP, false, true, false>(c1, c2, cw, u, grad_out, segb, segf, grad_u, part, sh, s);
+      else
+        launch_bwd<NP, false, false, true>(c1, c2, cw, u, grad_out, segb, segf, grad_u, part, sh, s);
+    }
   });
   if (rc) return rc;
-  MoscShape rs = sh;
-  if (!work) {
-    rs.B = 0;  // no partial rows: the reduction writes zeros
-    rs.S = 0;
-  }
-  if (grad_c1 || grad_c2 || grad_cw)
+  if (coefs) {
+    MoscShape rs = sh;
+    if (B * T == 0) {
+      rs.B = 0;  // no partial rows: the reduction writes zeros
+      rs.S = 0;
+    }
     hipLaunchKernelGGL(mosc_coef_reduce_kernel, dim3((unsigned)(F * N)), dim3(kWave), 0, s,
-                       part, rs, pad_osc((int)N), grad_c1, grad_c2, grad_cw);
+                       part, c2, cw, rs, pad_osc((int)N), grad_c1, grad_c2, grad_cw);
+  }
   return launch_status();
 }

@@ -27,8 +27,11 @@ The kernels are ``rqf_multi_osc_fwd`` / ``rqf_multi_osc_bwd`` of librqf_hip.so
 conj(x[t-1])``, ``grad_C2 = sum d conj(u)``, ``grad_u = sum_n conj(C2_n) d_n``
 (its real part for real ``u``) and ``grad_c_weights = (Re, Im) of
 sum grad_y conj(x_n)``, with ``d_n[t] = conj(C1_n) d_n[t+1] + conj(cw_n)
-grad_y[t]``.  Unlike the reference, the coefficient gradients are reduced in
-a fixed order (no atomics), so repeated calls agree bit for bit.
+grad_y[t]``.  The kernels evaluate all three coefficient sums in the
+adjoint's reverse sweep, against ``u``, after exchanging the order of
+summation (same values; no forward state and no per-step state tensor).  Unlike the reference, the
+coefficient gradients are reduced in a fixed order (no atomics), so repeated
+calls agree bit for bit.
 """
 
 from __future__ import annotations
@@ -159,7 +162,7 @@ class _SequentialScanMultiOscFunction(torch.autograd.Function):
     """Autograd boundary of the fused multi-oscillator scan (complex ``u``).
 
     Saves only (C1, C2, u, c_weights), as the reference does; the backward
-    recomputes the oscillator states.
+    needs no forward state.
     """
 
     @staticmethod

@@ -113,6 +113,66 @@ def test_needs_input_grad_gating_and_parallel_alias():
         compute_grad_C2=False, compute_grad_u=False, compute_grad_cw=False) == (None,) * 4
 
 
+@pytest.mark.parametrize("real", [False, True])
+@pytest.mark.parametrize("shape,N", [((2, 37, 3), 3), ((3, 2000, 40), 4), ((2, 600, 130), 8)])
+def test_gradient_subsets_launch_their_own_variants(shape, N, real):
+    """grad_u alone skips the adjoint's C1 tangent and the coefficient sums;
+    the coefficient gradients alone skip grad_u.  Each variant runs the same
+    arithmetic on what it computes: bit-identical to the full call, which is
+    checked against the oracle."""
+    B, T, F = shape
+    print(f"case: multi-osc gradient subsets {shape} N={N} real={real}", flush=True)
+    rng = np.random.default_rng(T + N)
+    c1, c2, cw, u = _problem(rng, B, T, F, N, real)
+    gy = _c64(crandn(rng, B, T, F))
+    gu_ref, gc1_ref, gc2_ref, gcw_ref = oracle.mosc_bwd(c1, c2, cw, u, gy, N)
+    if real:
+        gu_ref = gu_ref.real
+    C1, C2, U, CW, GY = _t(c1), _t(c2), _t(u), _cw_param(cw), _t(gy)
+    full = mo._backward(C1, C2, U, CW, GY, N, real=real)
+    want = (gc1_ref, gc2_ref, gu_ref, gcw_ref)
+    for i, name in enumerate(("gc1", "gc2", "gu", "gcw")):
+        got = full[i]
+        if name == "gcw":
+            got = got[:, 0].double() + 1j * got[:, 1].double()
+        assert relerr(got, want[i]) <= PARITY_RTOL, name
+    only_u = mo._backward(C1, C2, U, CW, GY, N, real=real, compute_grad_C1=False,
+                          compute_grad_C2=False, compute_grad_cw=False)
+    assert only_u[0] is None and only_u[1] is None and only_u[3] is None
+    assert torch.equal(only_u[2], full[2])
+    coefs = mo._backward(C1, C2, U, CW, GY, N, real=real, compute_grad_u=False)
+    assert coefs[2] is None
+    for i in (0, 1, 3):
+        assert torch.equal(coefs[i], full[i])
+
+
+def test_long_memory_filters_at_full_length():
+    """Trained-filter magnitudes (|C1| up to 0.9996, ~2500-step memory) over
+    T = 16000: the adjoint's C1 tangent grows like t |C1|^t, the regime where float32
+    sums are least forgiving."""
+    B, T, F, N = 2, 16000, 8, 4
+    print(f"case: multi-osc long memory B={B} T={T} F={F} N={N}", flush=True)
+    rng = np.random.default_rng(16000)
+    r = np.concatenate([np.full(F * N // 2, 0.9996), rng.uniform(0.99, 0.9995, F * N // 2)])
+    c1 = _c64(r * np.exp(1j * rng.uniform(-0.2, 0.2, F * N)))
+    c2 = _c64(0.02 * crandn(rng, F * N))
+    cw = _c64(crandn(rng, F * N))
+    u = _c64(crandn(rng, B, T, F))
+    gy = _c64(crandn(rng, B, T, F))
+    y_ref, _ = oracle.mosc_fwd(c1, c2, cw, u, N)
+    gu_ref, gc1_ref, gc2_ref, gcw_ref = oracle.mosc_bwd(c1, c2, cw, u, gy, N)
+    C1, C2, U, CW = _t(c1, True), _t(c2, True), _t(u, True), _cw_param(cw, True)
+    y = mo._triton_sequential_scan_multi_osc(C1, C2, U, CW, N)
+    y.backward(_t(gy))
+    gcw_got = CW.grad[:, 0].double() + 1j * CW.grad[:, 1].double()
+    errs = {"y": relerr(y, y_ref), "gc1": relerr(C1.grad, gc1_ref),
+            "gc2": relerr(C2.grad, gc2_ref), "gcw": relerr(gcw_got.cpu(), gcw_ref),
+            "gu": relerr(U.grad, gu_ref)}
+    print("  " + " ".join(f"{k} {v:.1e}" for k, v in errs.items()), flush=True)
+    bad = {k: v for k, v in errs.items() if not v <= PARITY_RTOL}
+    assert not bad, errs
+
+
 def test_forward_raw_names_match_the_autograd_path():
     rng = np.random.default_rng(9)
     B, T, F, N = 2, 500, 8, 2

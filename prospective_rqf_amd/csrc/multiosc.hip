@@ -51,6 +51,18 @@ constexpr int kMoscMaxOsc = 8;     // oscillators per filter (N <= 8)
 constexpr int kMoscMaxSeg = 256;   // steps per segment, at most
 constexpr int kMoscMinSeg = 16;    // steps per segment, at least (when T allows)
 constexpr int64_t kMoscLanes = 65536;  // target number of tasks
+// Steps per streamed chunk (see stream_steps).  Config 6 (B=32 T=16000 F=128,
+// N=4) fwd+bwd on one MI355X: 70.1 Gelem/s with one load in flight per wave,
+// 71.6 with 8-step chunks, 71.0 with 16, 69.8 with 32 for the local passes
+// (the final passes' 16-step chunks reach 153 VGPRs).
+#ifndef RQF_MOSC_STREAM
+#define RQF_MOSC_STREAM 8
+#endif
+#ifndef RQF_MOSC_STREAM_FINAL
+#define RQF_MOSC_STREAM_FINAL 8
+#endif
+constexpr int kStream = RQF_MOSC_STREAM;
+constexpr int kStreamFinal = RQF_MOSC_STREAM_FINAL;
 
 __device__ __forceinline__ c32 ldc(const float* p, int64_t i) { return mk(p[2 * i], p[2 * i + 1]); }
 __device__ __forceinline__ void stc(float* p, int64_t i, c32 v) {
@@ -95,6 +107,37 @@ __device__ __forceinline__ int64_t seg_idx(const MoscShape& sh, int64_t b, int64
   return ((b * sh.S + s) * NP + n) * sh.F + f;
 }
 
+// Walks a task's steps t = tb..te-1 (FWD) or te-1..tb in chunks of CH:
+// load(j, t) fills chunk slot j for step t, step(j, t) consumes it.  All the
+// loads of a chunk issue before any of its steps computes.  Left to itself the
+// scheduler sinks each load next to its use (load, wait, compute, next load),
+// which keeps one load in flight per wave and runs the pass at memory latency
+// rather than bandwidth.  The last, partial chunk loads every slot too (slots
+// past the segment re-read its last step, so every address stays inside it)
+// and computes only its valid steps: stepping the tail one load at a time
+// would cost a full memory latency per step.
+template <int CH, bool FWD, class Load, class Step>
+__device__ __forceinline__ void stream_steps(int64_t tb, int64_t te, Load&& load, Step&& step) {
+  int64_t t = FWD ? tb : te - 1;
+  const int64_t full = (te - tb) / CH;
+  for (int64_t c = 0; c < full; ++c) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j) load(j, FWD ? t + j : t - j);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < CH; ++j) step(j, FWD ? t + j : t - j);
+    t += FWD ? CH : -CH;
+  }
+  const int rem = (int)(te - tb - full * CH);
+  if (rem == 0) return;
+#pragma unroll
+  for (int j = 0; j < CH; ++j) load(j, FWD ? min(t + j, te - 1) : max(t - j, tb));
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < CH; ++j)
+    if (j < rem) step(j, FWD ? t + j : t - j);
+}
+
 // One step of the scanned state w_n[t] = C1_n w_n[t-1] + u[t].
 template <bool REAL>
 __device__ __forceinline__ c32 step_w(c32 a, c32 w, c32 ut) {
@@ -115,12 +158,13 @@ __global__ __launch_bounds__(256) void mosc_fwd_local_kernel(const float* __rest
 #pragma unroll
   for (int n = 0; n < NP; ++n) w[n] = mk(0.0f, 0.0f);
   const int64_t base = k.b * sh.T * sh.F + k.f;
-#pragma unroll 8
-  for (int64_t t = k.tb; t < k.te; ++t) {
-    const c32 ut = load_u<REAL>(u, base + t * sh.F);
+  c32 ub[kStream];
+  stream_steps<kStream, true>(
+      k.tb, k.te, [&](int j, int64_t t) { ub[j] = load_u<REAL>(u, base + t * sh.F); },
+      [&](int j, int64_t) {
 #pragma unroll
-    for (int n = 0; n < NP; ++n) w[n] = step_w<REAL>(a[n], w[n], ut);
-  }
+        for (int n = 0; n < NP; ++n) w[n] = step_w<REAL>(a[n], w[n], ub[j]);
+      });
 #pragma unroll
   for (int n = 0; n < NP; ++n) stc(seg, seg_idx(sh, k.b, k.s, n, k.f, NP), w[n]);
 }
@@ -211,21 +255,22 @@ __global__ __launch_bounds__(256) void mosc_fwd_final_kernel(
 #pragma unroll
   for (int n = 0; n < NP; ++n) w[n] = ldc(seg, seg_idx(sh, k.b, k.s, n, k.f, NP));
   const int64_t base = k.b * sh.T * sh.F + k.f;
-#pragma unroll 8
-  for (int64_t t = k.tb; t < k.te; ++t) {
-    const int64_t e = base + t * sh.F;
-    const c32 ut = load_u<REAL>(u, e);
-    c32 y = mk(0.0f, 0.0f);
+  c32 ub[kStreamFinal];
+  stream_steps<kStreamFinal, true>(
+      k.tb, k.te, [&](int j, int64_t t) { ub[j] = load_u<REAL>(u, base + t * sh.F); },
+      [&](int j, int64_t t) {
+        c32 y = mk(0.0f, 0.0f);
 #pragma unroll
-    for (int n = 0; n < NP; ++n) {
-      w[n] = step_w<REAL>(a[n], w[n], ut);
-      if (CW || n == 0) y = cmad(h[n], w[n], y);
-    }
-    if (ABS)
-      out[e] = sqrtf(fmaf(y.r, y.r, y.i * y.i));
-    else
-      stc(out, e, y);
-  }
+        for (int n = 0; n < NP; ++n) {
+          w[n] = step_w<REAL>(a[n], w[n], ub[j]);
+          if (CW || n == 0) y = cmad(h[n], w[n], y);
+        }
+        const int64_t e = base + t * sh.F;
+        if (ABS)
+          out[e] = sqrtf(fmaf(y.r, y.r, y.i * y.i));
+        else
+          stc(out, e, y);
+      });
 }
 
 // One reverse step of the adjoint pair (see mosc_bwd_final_kernel).
@@ -251,12 +296,13 @@ __global__ __launch_bounds__(256) void mosc_bwd_local_kernel(const float* __rest
 #pragma unroll
   for (int n = 0; n < NP; ++n) d[n] = f[n] = mk(0.0f, 0.0f);
   const int64_t base = k.b * sh.T * sh.F + k.f;
-#pragma unroll 8
-  for (int64_t t = k.te - 1; t >= k.tb; --t) {
-    const c32 gt = ldc(gy, base + t * sh.F);
+  c32 gb[kStream];
+  stream_steps<kStream, false>(
+      k.tb, k.te, [&](int j, int64_t t) { gb[j] = ldc(gy, base + t * sh.F); },
+      [&](int j, int64_t) {
 #pragma unroll
-    for (int n = 0; n < NP; ++n) step_adj<TAN>(a[n], d[n], f[n], gt);
-  }
+        for (int n = 0; n < NP; ++n) step_adj<TAN>(a[n], d[n], f[n], gb[j]);
+      });
 #pragma unroll
   for (int n = 0; n < NP; ++n) {
     const int64_t i = seg_idx(sh, k.b, k.s, n, k.f, NP);
@@ -294,33 +340,37 @@ __global__ __launch_bounds__(256) void mosc_bwd_final_kernel(
     q[n] = r[n] = mk(0.0f, 0.0f);
   }
   const int64_t base = k.b * sh.T * sh.F + k.f;
-#pragma unroll 8
-  for (int64_t t = k.te - 1; t >= k.tb; --t) {
-    const int64_t e = base + t * sh.F;
-    const c32 gt = ldc(gy, e);
-    const c32 ut = TAN ? load_u<REAL>(u, e) : mk(0.0f, 0.0f);
-    c32 g = mk(0.0f, 0.0f);
+  c32 gb[kStreamFinal], ub[kStreamFinal];
+  stream_steps<kStreamFinal, false>(
+      k.tb, k.te,
+      [&](int j, int64_t t) {
+        gb[j] = ldc(gy, base + t * sh.F);
+        if (TAN) ub[j] = load_u<REAL>(u, base + t * sh.F);
+      },
+      [&](int j, int64_t t) {
+        c32 g = mk(0.0f, 0.0f);
 #pragma unroll
-    for (int n = 0; n < NP; ++n) {
-      step_adj<TAN>(a[n], d[n], f[n], gt);
-      if (GU) g = cjmad(h[n], d[n], g);
-      if (TAN) {
-        if (REAL) {
-          q[n] = csmad(ut.r, d[n], q[n]);
-          r[n] = csmad(ut.r, f[n], r[n]);
-        } else {
-          q[n] = cjmad(ut, d[n], q[n]);
-          r[n] = cjmad(ut, f[n], r[n]);
+        for (int n = 0; n < NP; ++n) {
+          step_adj<TAN>(a[n], d[n], f[n], gb[j]);
+          if (GU) g = cjmad(h[n], d[n], g);
+          if (TAN) {
+            if (REAL) {
+              q[n] = csmad(ub[j].r, d[n], q[n]);
+              r[n] = csmad(ub[j].r, f[n], r[n]);
+            } else {
+              q[n] = cjmad(ub[j], d[n], q[n]);
+              r[n] = cjmad(ub[j], f[n], r[n]);
+            }
+          }
         }
-      }
-    }
-    if (GU) {
-      if (REAL)
-        gu[e] = g.r;
-      else
-        stc(gu, e, g);
-    }
-  }
+        if (GU) {
+          const int64_t e = base + t * sh.F;
+          if (REAL)
+            gu[e] = g.r;
+          else
+            stc(gu, e, g);
+        }
+      });
   if (TAN) {
 #pragma unroll
     for (int n = 0; n < NP; ++n) {

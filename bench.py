@@ -549,7 +549,7 @@ def plan_multi_osc(cfg, args, dev):
         nbytes = {"rqf_multi_osc_fwd": 16 * elems, "rqf_multi_osc_bwd": 24 * elems}
         kernels = {"rqf_multi_osc_fwd": "mosc_fwd_local + mosc_carry + mosc_fwd_final",
                    "rqf_multi_osc_bwd": ("mosc_bwd_local + mosc_carry + mosc_bwd_final + "
-                                         "mosc_coef_reduce")}
+                                         "mosc_coef_stage1 + mosc_coef_stage2")}
         contract = "complex u in, complex y out; grad_u + grad_C1/C2/c_weights"
     else:
         name = ("fused |y| readout: single-oscillator scan on real input, 128 filters, "

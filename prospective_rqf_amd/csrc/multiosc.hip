@@ -27,7 +27,7 @@
 // sum_n conj(cw_n C2_n) e_n.  The reference's coefficient sums pair the
 // adjoint at t with the state at t-1, which a reverse sweep does not have.
 // Exchanging the order of summation pairs them with u instead
-// (mosc_coef_reduce_kernel): against e_n for grad_C2 and grad_cw, and against
+// (mosc_coef_stage2_kernel): against e_n for grad_C2 and grad_cw, and against
 // f_n, the derivative of e_n's recurrence with respect to conj(C1_n), for
 // grad_C1.  f_n is itself a reverse recurrence, f_n[t] = conj(C1_n) f_n[t+1] +
 // e_n[t+1], carried between segments with e_n.  So the final pass reads
@@ -383,9 +383,36 @@ __global__ __launch_bounds__(256) void mosc_bwd_final_kernel(
   }
 }
 
-// grad_C1, grad_C2, grad_cw of oscillator n of filter f: one wavefront per
-// (f, n < N) sums the B*S task partials of Q and R in a fixed order in fp64,
-// then
+// Coefficient-gradient reduction, stage 1: partial sums over a run of task
+// rows m in [m0, m1) (m = b*S + s), in fp64, in m order.  Thread i covers
+// (nj, f) = (i / F, i % F) of the 4*NP*F sums, so a wavefront reads
+// consecutive f of one row; the loads of 16 rows issue together.
+__global__ __launch_bounds__(256) void mosc_coef_stage1_kernel(const float* __restrict__ part,
+                                                               MoscShape sh, int NP, int64_t run,
+                                                               double* __restrict__ s1) {
+  const int64_t n_sums = (int64_t)4 * NP * sh.F;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_sums) return;
+  const int64_t c = blockIdx.y;
+  const int64_t nj = i / sh.F, f = i - nj * sh.F;
+  const int64_t M = sh.B * sh.S;
+  const int64_t m0 = c * run, m1 = min(M, m0 + run);
+  const float* p = part + nj * sh.tasks + f;
+  double acc = 0.0;
+  for (int64_t m = m0; m < m1; m += 16) {
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = m + k < m1 ? p[(m + k) * sh.F] : 0.0f;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) acc += v[k];
+  }
+  s1[c * n_sums + i] = acc;
+}
+
+// Stage 2: grad_C1, grad_C2, grad_cw of oscillator n of filter f (one
+// wavefront per f*N + n) from the stage-1 sums of Q and R (lane l adds chunks
+// l, l+64, ..., then a fixed-shape wave sum), then
 //   grad_C1 = conj(cw C2) R,   grad_C2 = conj(cw) Q,   grad_cw = conj(C2) Q.
 // These are the reference's sums, with x_n = C2_n w_n and d_n = conj(cw_n) e_n
 // and the order of summation exchanged (u[r] enters w_n[t] with C1^(t-r)):
@@ -394,19 +421,19 @@ __global__ __launch_bounds__(256) void mosc_bwd_final_kernel(
 //                               = conj(C2_n) sum_r e_n[r] conj(u[r])
 //   sum_t d_n[t] conj(x_n[t-1]) = conj(cw_n C2_n) sum_r conj(u[r]) sum_{t>r} conj(C1)^(t-1-r) e_n[t]
 //                               = conj(cw_n C2_n) sum_r f_n[r] conj(u[r]).
-__global__ __launch_bounds__(64) void mosc_coef_reduce_kernel(
-    const float* __restrict__ part, const float* __restrict__ c2, const float* __restrict__ cw,
-    MoscShape sh, int NP, float* __restrict__ gc1, float* __restrict__ gc2,
-    float* __restrict__ gcw) {
-  const int64_t fn = blockIdx.x;  // f*N + n
+__global__ __launch_bounds__(kWave) void mosc_coef_stage2_kernel(
+    const double* __restrict__ s1, int64_t chunks, const float* __restrict__ c2,
+    const float* __restrict__ cw, MoscShape sh, int NP, float* __restrict__ gc1,
+    float* __restrict__ gc2, float* __restrict__ gcw) {
+  const int64_t fn = blockIdx.x;  // f*N + n: one wavefront each
   const int64_t f = fn / sh.N;
   const int n = (int)(fn - f * sh.N);
   const int lane = threadIdx.x;
-  const int64_t M = sh.B * sh.S;
+  const int64_t n_sums = (int64_t)4 * NP * sh.F;
   double s[4] = {0, 0, 0, 0};
-  for (int64_t m = lane; m < M; m += kWave) {
+  for (int64_t c = lane; c < chunks; c += kWave) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) s[j] += part[((int64_t)n * 4 + j) * sh.tasks + m * sh.F + f];
+    for (int j = 0; j < 4; ++j) s[j] += s1[c * n_sums + ((int64_t)n * 4 + j) * sh.F + f];
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) s[j] = wave_sum(s[j]);
@@ -459,19 +486,27 @@ size_t mosc_states(const MoscShape& sh) {
 // Workspace: forward, the w entries; backward, the adjoint pair's entries and
 // the per-task partial sums.
 struct MoscWs {
-  size_t seg, segf, part, total;
+  size_t seg, segf, part, s1, total;
 };
+// Rows of task partials per stage-1 chunk of the coefficient reduction, and
+// the number of chunks.
+constexpr int64_t kCoefRun = 16;
+int64_t coef_run(const MoscShape&) { return kCoefRun; }
+int64_t coef_chunks(const MoscShape& sh) {
+  return std::max<int64_t>((sh.B * sh.S + coef_run(sh) - 1) / coef_run(sh), 1);
+}
 MoscWs mosc_ws(const MoscShape& sh, bool backward) {
   const size_t states = mosc_states(sh);
   MoscWs w;
   w.seg = 0;
   if (!backward) {
-    w.segf = w.part = w.total = states;
+    w.segf = w.part = w.s1 = w.total = states;
     return w;
   }
   w.segf = states;
   w.part = 2 * states;
-  w.total = w.part + round256((size_t)sh.tasks * pad_osc(sh.N) * 4 * 4);
+  w.s1 = w.part + round256((size_t)sh.tasks * pad_osc(sh.N) * 4 * 4);
+  w.total = w.s1 + round256((size_t)coef_chunks(sh) * 4 * pad_osc(sh.N) * sh.F * 8);
   return w;
 }
 
@@ -612,8 +647,14 @@ extern "C" int rqf_multi_osc_bwd(const float* c1, const float* c2, const float* 
       rs.B = 0;  // no partial rows: the reduction writes zeros
       rs.S = 0;
     }
-    hipLaunchKernelGGL(mosc_coef_reduce_kernel, dim3((unsigned)(F * N)), dim3(kWave), 0, s,
-                       part, c2, cw, rs, pad_osc((int)N), grad_c1, grad_c2, grad_cw);
+    const int NP = pad_osc((int)N);
+    const int64_t chunks = coef_chunks(sh), n_sums = (int64_t)4 * NP * F;
+    double* s1 = (double*)(ws + w.s1);
+    hipLaunchKernelGGL(mosc_coef_stage1_kernel,
+                       dim3((unsigned)((n_sums + 255) / 256), (unsigned)chunks), dim3(256), 0, s,
+                       part, rs, NP, coef_run(sh), s1);
+    hipLaunchKernelGGL(mosc_coef_stage2_kernel, dim3((unsigned)(F * N)), dim3(kWave), 0, s, s1,
+                       chunks, c2, cw, rs, NP, grad_c1, grad_c2, grad_cw);
   }
   return launch_status();
 }

@@ -78,6 +78,10 @@ def _args():
                          "backward) on the last layer's output: 'fused' runs "
                          "readout.complex_readout on the (F, B, T) features, 'reference' the "
                          "reference's permute + cat + Linear + ReLU + Linear")
+    ap.add_argument("--layout", choices=["fbt", "btf"], default="fbt",
+                    help="config 2: 'btf' runs the same workload on (batch, time, filters) "
+                         "tensors through the chunked prospective scan (the layout RQF-S4 "
+                         "and the non-FBT Pure RQF cells use, block.py:690-733)")
     ap.add_argument("--act-only", action="store_true",
                     help="config 3 with the act-only contract (no raw output, no gy)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -449,6 +453,57 @@ def plan_fbt(cfg, args, dev):
     return Plan(name, config, F * B * T * L, (state, ops), nbytes, kernels, cpu, config["contract"])
 
 
+def plan_chunked_raw(cfg, args, dev):
+    """Config 2's workload on (B, T, F) tensors: the chunked two-tap prospective
+    scan (rqf_chunked_prospective_fwd / _bwd), whose backward takes the
+    forward's output as the reference's autograd context saves it."""
+    import torch
+
+    from prospective_rqf_amd import workloads
+    from prospective_rqf_amd.chunked_scan_kernel import (
+        _chunked_prospective_backward_raw,
+        _chunked_prospective_forward_raw,
+    )
+
+    F, B, T = 128, 32, 16000
+    coef = dict(samp=16000.0, tau=5.0 / 16000.0, seq_duration=1.0)
+    name = ("non-selective two-tap scan B=32 T=16000 H=128 on (B,T,F) tensors: chunked "
+            "prospective scan (config 2, --layout btf)")
+    if args.batch:
+        B = args.batch
+        name += f" [batch overridden to {B}]"
+    if args.seq_len:
+        T = args.seq_len
+        name += f" [sequence length overridden to {T}]"
+    g = torch.Generator(device=dev).manual_seed(1)
+    gcpu = torch.Generator().manual_seed(3)
+    c1, t0, t1 = workloads.static_two_tap(F, seed=0, device=dev, **coef)
+    u = workloads.raw_waveform(B, T, samp=16000.0, generator=gcpu).to(dev)  # (B, T)
+    state = {"x": (u[:, :, None].to(torch.complex64) * _cn(g, dev, F)).contiguous(),
+             "gy": _cn(g, dev, B, T, F)}
+
+    def fwd(st):
+        st["out"] = _chunked_prospective_forward_raw(c1, t0, t1, st["x"])
+
+    def bwd(st):
+        st["grads"] = _chunked_prospective_backward_raw(c1, t0, t1, st["x"], st.pop("out"),
+                                                        st["gy"])
+
+    ops = [("rqf_chunked_prospective_fwd", fwd), ("rqf_chunked_prospective_bwd", bwd)]
+    N = B * T * F
+    nbytes = {"rqf_chunked_prospective_fwd": 16 * N, "rqf_chunked_prospective_bwd": 32 * N}
+    kernels = {"rqf_chunked_prospective_fwd": "btf_fwd_local + btf_fwd_final",
+               "rqf_chunked_prospective_bwd": "btf_bwd_local + btf_bwd_final + coef_reduce_kernel"}
+    config = {"workload": name, "F": F, "B": B, "T": T, "layers": 1,
+              "contract": "(B,T,F) two-tap scan; x in, y out; backward reads x, y and gy, "
+                          "writes grad_x; full BPTT"}
+
+    def cpu():
+        return cpu_baseline_timeinv(F, B, args.cpu_steps or 1000, 1, prospective=True, coef=coef)
+
+    return Plan(name, config, N, (state, ops), nbytes, kernels, cpu, config["contract"])
+
+
 def plan_chunked(cfg, args, dev):
     import torch
 
@@ -782,6 +837,8 @@ def main():
     cfg = args.config
     if cfg in (3, 4):
         plan = plan_selective(cfg, args, dev)
+    elif cfg == 2 and args.layout == "btf":
+        plan = plan_chunked_raw(cfg, args, dev)
     elif cfg in (2, 5):
         plan = plan_fbt(cfg, args, dev)
     elif cfg in (6, 7):

@@ -125,6 +125,29 @@ def _chunked_prospective_forward_raw(C1, tap0, tap1, x):
     return out
 
 
+def _chunked_prospective_backward_raw(C1, tap0, tap1, x, states, grad_output):
+    """``(grad_C1, grad_tap0, grad_tap1, grad_x)`` of the two-tap scan, from the
+    forward's output ``states`` (the tensor the reference's autograd context
+    saves)."""
+    C1, tap0, tap1, x, states, grad_output = (
+        _c64(t) for t in (C1, tap0, tap1, x, states, grad_output))
+    _lib.require_device(C1, tap0, tap1, x, states, grad_output)
+    B, T, F = x.shape
+    grad_x = torch.empty_like(x)
+    gc1 = torch.empty(F, dtype=torch.complex64, device=x.device)
+    gt0 = torch.empty_like(gc1)
+    gt1 = torch.empty_like(gc1)
+    ws, n = _ws(B, T, F, x.device)
+    _lib.check(
+        _lib.load().rqf_chunked_prospective_bwd(
+            _lib.ptr(C1), _lib.ptr(tap0), _lib.ptr(tap1), _lib.ptr(x), _lib.ptr(states),
+            _lib.ptr(grad_output), _lib.ptr(grad_x), _lib.ptr(gc1), _lib.ptr(gt0),
+            _lib.ptr(gt1), B, T, F, _lib.ptr(ws), n, _lib.stream_of(x)),
+        "rqf_chunked_prospective_bwd",
+    )
+    return gc1, gt0, gt1, grad_x
+
+
 class _ChunkedProspectiveScanFunction(torch.autograd.Function):
     """x_out[n] = C1 x_out[n-1] + tap0 x[n] + tap1 x[n-1], drive fused."""
 
@@ -139,21 +162,7 @@ class _ChunkedProspectiveScanFunction(torch.autograd.Function):
     @once_differentiable
     def backward(ctx, grad_output):
         C1, tap0, tap1, x, states = ctx.saved_tensors
-        grad_output = _c64(grad_output)
-        B, T, F = x.shape
-        grad_x = torch.empty_like(x)
-        gc1 = torch.empty(F, dtype=torch.complex64, device=x.device)
-        gt0 = torch.empty_like(gc1)
-        gt1 = torch.empty_like(gc1)
-        ws, n = _ws(B, T, F, x.device)
-        _lib.check(
-            _lib.load().rqf_chunked_prospective_bwd(
-                _lib.ptr(C1), _lib.ptr(tap0), _lib.ptr(tap1), _lib.ptr(x), _lib.ptr(states),
-                _lib.ptr(grad_output), _lib.ptr(grad_x), _lib.ptr(gc1), _lib.ptr(gt0),
-                _lib.ptr(gt1), B, T, F, _lib.ptr(ws), n, _lib.stream_of(x)),
-            "rqf_chunked_prospective_bwd",
-        )
-        return gc1, gt0, gt1, grad_x
+        return _chunked_prospective_backward_raw(C1, tap0, tap1, x, states, grad_output)
 
 
 def _triton_chunked_scan_prospective(C1, tap0, tap1, x):

@@ -364,6 +364,37 @@ __device__ __forceinline__ void store_c_lds(float* __restrict__ row, int t0, int
   __builtin_amdgcn_wave_barrier();
 }
 
+// Walks a task's steps t = tb..te-1 (FWD) or te-1..tb in chunks of CH:
+// load(j, t) fills chunk slot j for step t, step(j, t) consumes it.  All the
+// loads of a chunk issue before any of its steps computes.  Left to itself the
+// scheduler sinks each load next to its use (load, wait, compute, next load),
+// which keeps one load in flight per wave and runs the pass at memory latency
+// rather than bandwidth.  The last, partial chunk loads every slot too (slots
+// past the segment re-read its last step, so every address stays inside it)
+// and computes only its valid steps: stepping the tail one load at a time
+// would cost a full memory latency per step.
+template <int CH, bool FWD, class Load, class Step>
+__device__ __forceinline__ void stream_steps(int64_t tb, int64_t te, Load&& load, Step&& step) {
+  int64_t t = FWD ? tb : te - 1;
+  const int64_t full = (te - tb) / CH;
+  for (int64_t c = 0; c < full; ++c) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j) load(j, FWD ? t + j : t - j);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < CH; ++j) step(j, FWD ? t + j : t - j);
+    t += FWD ? CH : -CH;
+  }
+  const int rem = (int)(te - tb - full * CH);
+  if (rem == 0) return;
+#pragma unroll
+  for (int j = 0; j < CH; ++j) load(j, FWD ? min(t + j, te - 1) : max(t - j, tb));
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < CH; ++j)
+    if (j < rem) step(j, FWD ? t + j : t - j);
+}
+
 // Sum of a double over the wave (result valid in every lane).
 __device__ __forceinline__ double wave_sum(double v) {
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);

@@ -128,7 +128,10 @@ def _chunked_prospective_forward_raw(C1, tap0, tap1, x):
 def _chunked_prospective_backward_raw(C1, tap0, tap1, x, states, grad_output):
     """``(grad_C1, grad_tap0, grad_tap1, grad_x)`` of the two-tap scan, from the
     forward's output ``states`` (the tensor the reference's autograd context
-    saves)."""
+    saves).  The reference's ``_ChunkedProspectiveScanFunction.backward``
+    (chunked_scan_kernel.py:490-504) computes the same with a chunked adjoint
+    scan and five pointwise passes; here one three-phase scan
+    (``rqf_chunked_prospective_bwd``) produces grad_x and the three sums."""
     C1, tap0, tap1, x, states, grad_output = (
         _c64(t) for t in (C1, tap0, tap1, x, states, grad_output))
     _lib.require_device(C1, tap0, tap1, x, states, grad_output)

@@ -491,11 +491,13 @@ def plan_chunked_raw(cfg, args, dev):
 
     ops = [("rqf_chunked_prospective_fwd", fwd), ("rqf_chunked_prospective_bwd", bwd)]
     N = B * T * F
-    nbytes = {"rqf_chunked_prospective_fwd": 16 * N, "rqf_chunked_prospective_bwd": 32 * N}
+    # The backward's contract reads x and gy and writes grad_x; the saved output
+    # it is handed is not needed (grad_C1 comes from x, csrc/timeinv.hip).
+    nbytes = {"rqf_chunked_prospective_fwd": 16 * N, "rqf_chunked_prospective_bwd": 24 * N}
     kernels = {"rqf_chunked_prospective_fwd": "btf_fwd_local + btf_fwd_final",
                "rqf_chunked_prospective_bwd": "btf_bwd_local + btf_bwd_final + coef_reduce_kernel"}
     config = {"workload": name, "F": F, "B": B, "T": T, "layers": 1,
-              "contract": "(B,T,F) two-tap scan; x in, y out; backward reads x, y and gy, "
+              "contract": "(B,T,F) two-tap scan; x in, y out; backward reads x and gy, "
                           "writes grad_x; full BPTT"}
 
     def cpu():

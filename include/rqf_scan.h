@@ -65,7 +65,10 @@ int rqf_chunked_scan_fwd(const float *c1, const float *c2, const float *u, float
 
 /* Replaces `_chunked_scan_backward_kernel[grid](...)`
  * (rqf_models/ops/chunked_scan_kernel.py:286-299): grad_u = conj(C2) g,
- * grad_C1 = sum conj(x[t-1]) g, grad_C2 = sum conj(u) g. */
+ * grad_C1 = sum conj(x[t-1]) g, grad_C2 = sum conj(u) g, where x is the
+ * forward's output.  grad_C1 is evaluated with the order of summation
+ * exchanged, from u, so `states` (the saved output the reference passes) is
+ * accepted but not read and may be NULL. */
 int rqf_chunked_scan_bwd(const float *c1, const float *c2, const float *u,
                          const float *states, const float *grad_out, float *grad_u,
                          float *grad_c1, float *grad_c2, int64_t B, int64_t T, int64_t F,
@@ -80,7 +83,8 @@ int rqf_chunked_prospective_fwd(const float *c1, const float *tap0, const float 
 
 /* Replaces `_ChunkedProspectiveScanFunction.backward`
  * (rqf_models/ops/chunked_scan_kernel.py:491-503): the chunked adjoint plus
- * its PyTorch finisher, fused: grad_x = conj(tap0) g[t] + conj(tap1) g[t+1]. */
+ * its PyTorch finisher, fused: grad_x = conj(tap0) g[t] + conj(tap1) g[t+1].
+ * As in rqf_chunked_scan_bwd, `states` is accepted but not read (may be NULL). */
 int rqf_chunked_prospective_bwd(const float *c1, const float *tap0, const float *tap1,
                                 const float *x, const float *states, const float *grad_out,
                                 float *grad_x, float *grad_c1, float *grad_tap0,

@@ -753,11 +753,12 @@ __global__ __launch_bounds__(256) void btf_fwd_final_kernel(
       });
 }
 
-// Phase 1 of the backward: adjoint at each segment's first step from a zero
-// carry after the segment.
+// Phase 1 of the backward: the adjoint pair (g, h) at each segment's first
+// step from a zero pair after the segment (see btf_bwd_final_kernel).
 __global__ __launch_bounds__(256) void btf_bwd_local_kernel(const float* __restrict__ c1,
                                                             const float* __restrict__ gout,
                                                             float* __restrict__ seg_beg,
+                                                            float* __restrict__ seg_h,
                                                             BtfShape sh) {
   const int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (task >= sh.B * sh.S * sh.F) return;
@@ -765,55 +766,76 @@ __global__ __launch_bounds__(256) void btf_bwd_local_kernel(const float* __restr
   const c32 ac = conjg(ldc(c1, f));
   const int64_t t_beg = seg * sh.L, t_end = min(sh.T, t_beg + sh.L);
   const float* gb = gout + 2 * (b * sh.T * sh.F + f);
-  c32 g = mk(0.0f, 0.0f);
+  c32 g = mk(0.0f, 0.0f), h = mk(0.0f, 0.0f);
   c32 gbuf[kBtfStream];
   stream_steps<kBtfStream, false>(
       t_beg, t_end, [&](int j, int64_t t) { gbuf[j] = ldc(gb, t * sh.F); },
-      [&](int j, int64_t) { g = cmad(ac, g, gbuf[j]); });
+      [&](int j, int64_t) {
+        h = cmad(ac, h, g);
+        g = cmad(ac, g, gbuf[j]);
+      });
   stc(seg_beg, task, g);
+  stc(seg_h, task, h);
 }
 
 // Phase 2 of the backward: carry from the later segments, reverse serial
-// pass, grad_x and per-task coefficient partial sums.
+// pass, grad_x and per-task coefficient partial sums.  For t descending:
+//   g[t] = conj(C1) g[t+1] + gy[t]              (the adjoint of the drive)
+//   h[t] = conj(C1) h[t+1] + g[t+1]
+//   grad_x[t] = conj(tap0) g[t] + conj(tap1) g[t+1]
+//   sums: conj(d[t]) h[t] (grad_C1), conj(x[t]) g[t] (tap0), conj(x[t-1]) g[t] (tap1)
+// with the drive d[t] = tap0 x[t] + tap1 x[t-1].  The reference's grad_C1 is
+// sum_t g[t] conj(y[t-1]) over the saved states y; exchanging the order of
+// summation (y[t-1] = sum_{r<t} C1^(t-1-r) d[r]) gives sum_r conj(d[r]) h[r],
+// since h[r] = sum_{t>r} conj(C1)^(t-1-r) g[t].  So the pass reads gy and x
+// only, not the saved states.  len steps of zero input take (g, h) to
+// (P g, P h + len P' g), P = conj(C1)^len, P' = conj(C1)^(len-1); only full
+// segments carry (the last one starts from zero).
 __global__ __launch_bounds__(256) void btf_bwd_final_kernel(
     const float* __restrict__ c1, const float* __restrict__ k0p, const float* __restrict__ k1p,
-    const float* __restrict__ x, const float* __restrict__ states, const float* __restrict__ gout,
-    const float* __restrict__ seg_beg, float* __restrict__ gx, double* __restrict__ partial,
-    BtfShape sh) {
+    const float* __restrict__ x, const float* __restrict__ gout,
+    const float* __restrict__ seg_beg, const float* __restrict__ seg_h, float* __restrict__ gx,
+    double* __restrict__ partial, BtfShape sh) {
   const int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (task >= sh.B * sh.S * sh.F) return;
   const int64_t f = task % sh.F, bs = task / sh.F, seg = bs % sh.S, b = bs / sh.S;
   const c32 a = ldc(c1, f), k0 = ldc(k0p, f), k1 = k1p ? ldc(k1p, f) : mk(0.0f, 0.0f);
   const c32 ac = conjg(a);
-  c32 gnext = mk(0.0f, 0.0f);
-  if (seg + 1 < sh.S) {  // adjoint entering from the later segments, folded in fp64
-    const c64d acL = dconj(dpow(widen(a), sh.L));
-    c64d e = mkd(0.0, 0.0);
-    for (int64_t s = sh.S - 1; s > seg; --s)
-      e = dmad(acL, e, widen(ldc(seg_beg, (b * sh.S + s) * sh.F + f)));
+  c32 gnext = mk(0.0f, 0.0f), hnext = mk(0.0f, 0.0f);
+  if (seg + 1 < sh.S) {  // the pair entering from the later segments, folded in fp64
+    const c64d p1 = sh.L > 1 ? dconj(dpow(widen(a), sh.L - 1)) : mkd(1.0, 0.0);
+    const c64d pL = dmul(p1, widen(ac));
+    const c64d q = mkd(p1.r * (double)sh.L, p1.i * (double)sh.L);
+    c64d e = mkd(0.0, 0.0), eh = mkd(0.0, 0.0);
+    for (int64_t s = sh.S - 1; s > seg; --s) {
+      const int64_t i = (b * sh.S + s) * sh.F + f;
+      eh = dmad(pL, eh, dmad(q, e, widen(ldc(seg_h, i))));
+      e = dmad(pL, e, widen(ldc(seg_beg, i)));
+    }
     gnext = narrow(e);
+    hnext = narrow(eh);
   }
   const int64_t t_beg = seg * sh.L, t_end = min(sh.T, t_beg + sh.L);
   const int64_t base = b * sh.T * sh.F + f;
   const float* xb = x + 2 * base;
-  const float* yb = states + 2 * base;
   const float* gb = gout + 2 * base;
   float* gxb = gx + 2 * base;
   double s1r = 0, s1i = 0, s0r = 0, s0i = 0, s2r = 0, s2i = 0;
   // x[t] of each step is the x[t-1] the step after it (in time) loaded.
   c32 xt = ldc(xb, (t_end - 1) * sh.F);
-  c32 gbuf[kBtfStream], xpbuf[kBtfStream], ypbuf[kBtfStream];
+  c32 gbuf[kBtfStream], xpbuf[kBtfStream];
   stream_steps<kBtfStream, false>(
       t_beg, t_end,
       [&](int j, int64_t t) {
         gbuf[j] = ldc(gb, t * sh.F);
         xpbuf[j] = t > 0 ? ldc(xb, (t - 1) * sh.F) : mk(0.0f, 0.0f);
-        ypbuf[j] = t > 0 ? ldc(yb, (t - 1) * sh.F) : mk(0.0f, 0.0f);
       },
       [&](int j, int64_t t) {
+        const c32 h = cmad(ac, hnext, gnext);
         const c32 g = cmad(ac, gnext, gbuf[j]);
         stc(gxb, t * sh.F, cjmad(k1, gnext, cjmul(k0, g)));
-        const c32 t1 = cjmul(ypbuf[j], g), t0c = cjmul(xt, g), t2 = cjmul(xpbuf[j], g);
+        const c32 d = cmad(k1, xpbuf[j], cmul(k0, xt));
+        const c32 t1 = cjmul(d, h), t0c = cjmul(xt, g), t2 = cjmul(xpbuf[j], g);
         s1r += t1.r;
         s1i += t1.i;
         s0r += t0c.r;
@@ -821,6 +843,7 @@ __global__ __launch_bounds__(256) void btf_bwd_final_kernel(
         s2r += t2.r;
         s2i += t2.i;
         gnext = g;
+        hnext = h;
         xt = xpbuf[j];
       });
   double* o = partial + 6 * task;
@@ -864,7 +887,7 @@ size_t btf_ws(int64_t B, int64_t T, int64_t F) {
   const BtfShape fw = btf_shape(B, T, F, kBtfLanesFwd), bw = btf_shape(B, T, F, kBtfLanesBwd);
   const size_t tf = (size_t)(B * fw.S * F), tb = (size_t)(B * bw.S * F);
   return std::max(round256(sizeof(float) * 2 * tf),
-                  round256(sizeof(float) * 2 * tb) + round256(sizeof(double) * 6 * tb));
+                  2 * round256(sizeof(float) * 2 * tb) + round256(sizeof(double) * 6 * tb));
 }
 
 int btf_fwd(const float* c1, const float* k0, const float* k1, const float* x, float* out,
@@ -891,18 +914,22 @@ int btf_bwd(const float* c1, const float* k0, const float* k1, const float* x,
   if (B < 0 || T < 0 || F < 0) return RQF_ERR_ARG;
   if (F == 0) return RQF_OK;
   if (!c1 || !k0 || !gc1 || !gk0 || (k1 && !gk1)) return RQF_ERR_ARG;
-  if (B * T > 0 && (!x || !states || !gout || !gx)) return RQF_ERR_ARG;
+  (void)states;  // grad_C1 comes from x (see btf_bwd_final_kernel)
+  if (B * T > 0 && (!x || !gout || !gx)) return RQF_ERR_ARG;
   if (!aligned8(x) || !aligned8(states) || !aligned8(gout) || !aligned8(gx)) return RQF_ERR_ALIGN;
   const size_t need = btf_ws(B, T, F);
   if (need && (!ws || ws_bytes < need)) return RQF_ERR_WORKSPACE;
   const BtfShape sh = btf_shape(B, T, F, kBtfLanesBwd);
   const int64_t tasks = B * sh.S * F;
+  const size_t seg_bytes = round256(sizeof(float) * 2 * (size_t)tasks);
   float* seg = (float*)ws;
-  double* partial = (double*)((char*)ws + round256(sizeof(float) * 2 * (size_t)tasks));
+  float* seg_h = (float*)((char*)ws + seg_bytes);
+  double* partial = (double*)((char*)ws + 2 * seg_bytes);
   if (tasks > 0 && T > 0) {
     const dim3 grid((unsigned)((tasks + 255) / 256)), block(256);
-    if (sh.S > 1) hipLaunchKernelGGL(btf_bwd_local_kernel, grid, block, 0, s, c1, gout, seg, sh);
-    hipLaunchKernelGGL(btf_bwd_final_kernel, grid, block, 0, s, c1, k0, k1, x, states, gout, seg,
+    if (sh.S > 1)
+      hipLaunchKernelGGL(btf_bwd_local_kernel, grid, block, 0, s, c1, gout, seg, seg_h, sh);
+    hipLaunchKernelGGL(btf_bwd_final_kernel, grid, block, 0, s, c1, k0, k1, x, gout, seg, seg_h,
                        gx, partial, sh);
     hipLaunchKernelGGL(coef_reduce_kernel, dim3((unsigned)F), dim3(kWave), 0, s,
                        partial, F, B * sh.S, (int64_t)1, F, gc1, gk0, gk1);

@@ -211,6 +211,9 @@ def test_irrelevant_option_bits(truncated):
     # 4 groups of 8 channels, 2 teams each, 16 teams per split: one split
     # of 2 teams per group.
     (32, 2, 2100, "grouped", 4, 16, False),
+    # 150 channels in 5 groups interleaved in f order: the team build orders
+    # them over three 64-channel chunks (the last partial).
+    (150, 2, 1100, "grouped", 5, 2, False),
 ])
 def test_split_teams_carry_state_across_segments(monkeypatch, F, B, T, warp, G, split, truncated):
     """Backward blocks that run several teams of a warp group over segmented rows.

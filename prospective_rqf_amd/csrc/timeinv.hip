@@ -736,7 +736,10 @@ __global__ __launch_bounds__(256) void btf_fwd_final_kernel(
   if (seg > 0) {  // entry state: the earlier segments' end states, folded in fp64
     const c64d aL = dpow(widen(a), sh.L);
     c64d e = mkd(0.0, 0.0);
-    for (int64_t s = 0; s < seg; ++s) e = dmad(aL, e, widen(ldc(seg_end, (b * sh.S + s) * sh.F + f)));
+    c32 vbuf[kBtfStream];
+    stream_steps<kBtfStream, true>(
+        0, seg, [&](int j, int64_t s) { vbuf[j] = ldc(seg_end, (b * sh.S + s) * sh.F + f); },
+        [&](int j, int64_t) { e = dmad(aL, e, widen(vbuf[j])); });
     y = narrow(e);
   }
   const int64_t t_beg = seg * sh.L, t_end = min(sh.T, t_beg + sh.L);
@@ -807,11 +810,18 @@ __global__ __launch_bounds__(256) void btf_bwd_final_kernel(
     const c64d pL = dmul(p1, widen(ac));
     const c64d q = mkd(p1.r * (double)sh.L, p1.i * (double)sh.L);
     c64d e = mkd(0.0, 0.0), eh = mkd(0.0, 0.0);
-    for (int64_t s = sh.S - 1; s > seg; --s) {
-      const int64_t i = (b * sh.S + s) * sh.F + f;
-      eh = dmad(pL, eh, dmad(q, e, widen(ldc(seg_h, i))));
-      e = dmad(pL, e, widen(ldc(seg_beg, i)));
-    }
+    c32 vg[kBtfStream], vh[kBtfStream];
+    stream_steps<kBtfStream, false>(
+        seg + 1, sh.S,
+        [&](int j, int64_t s) {
+          const int64_t i = (b * sh.S + s) * sh.F + f;
+          vg[j] = ldc(seg_beg, i);
+          vh[j] = ldc(seg_h, i);
+        },
+        [&](int j, int64_t) {
+          eh = dmad(pL, eh, dmad(q, e, widen(vh[j])));
+          e = dmad(pL, e, widen(vg[j]));
+        });
     gnext = narrow(e);
     hnext = narrow(eh);
   }

@@ -160,15 +160,18 @@ __global__ __launch_bounds__(256) void mosc_carry_kernel(const float* __restrict
   const c32 a = n < sh.N ? ldc(c1, f * sh.N + n) : mk(0.0f, 0.0f);
   // Powers and the fold in fp64: a float32 power is off by ~L ulp, a bias that
   // every hop of a long-memory channel would repeat.
+  // The segments' values are loaded kStream at a time (stream_steps); each
+  // is overwritten only after it has been read.
   c64d e = mkd(0.0, 0.0);
   if (!ADJ) {
     const c64d aL = dpow(widen(a), sh.L);
-    for (int64_t s = 0; s < sh.S; ++s) {
-      const int64_t i = seg_idx(sh, b, s, n, f, NP);
-      const c32 v = ldc(seg, i);
-      stc(seg, i, narrow(e));
-      e = dmad(aL, e, widen(v));
-    }
+    c32 vb[kStream];
+    stream_steps<kStream, true>(
+        0, sh.S, [&](int j, int64_t s) { vb[j] = ldc(seg, seg_idx(sh, b, s, n, f, NP)); },
+        [&](int j, int64_t s) {
+          stc(seg, seg_idx(sh, b, s, n, f, NP), narrow(e));
+          e = dmad(aL, e, widen(vb[j]));
+        });
   } else {
     const c64d ac = dconj(widen(a));
     const int64_t lenLast = sh.T - (sh.S - 1) * sh.L;
@@ -178,18 +181,24 @@ __global__ __launch_bounds__(256) void mosc_carry_kernel(const float* __restrict
     const c64d q = mkd(p1.r * (double)sh.L, p1.i * (double)sh.L);
     const c64d qLast = mkd(p1Last.r * (double)lenLast, p1Last.i * (double)lenLast);
     c64d ef = mkd(0.0, 0.0);
-    for (int64_t s = sh.S - 1; s >= 0; --s) {
-      const bool last = s == sh.S - 1;
-      const int64_t i = seg_idx(sh, b, s, n, f, NP);
-      const c32 v = ldc(seg, i);
-      stc(seg, i, narrow(e));
-      if (TAN) {
-        const c32 vf = ldc(segf, i);
-        stc(segf, i, narrow(ef));
-        ef = dmad(last ? pLast : p, ef, dmad(last ? qLast : q, e, widen(vf)));
-      }
-      e = dmad(last ? pLast : p, e, widen(v));
-    }
+    c32 vb[kStream], vfb[kStream];
+    stream_steps<kStream, false>(
+        0, sh.S,
+        [&](int j, int64_t s) {
+          const int64_t i = seg_idx(sh, b, s, n, f, NP);
+          vb[j] = ldc(seg, i);
+          if (TAN) vfb[j] = ldc(segf, i);
+        },
+        [&](int j, int64_t s) {
+          const bool last = s == sh.S - 1;
+          const int64_t i = seg_idx(sh, b, s, n, f, NP);
+          stc(seg, i, narrow(e));
+          if (TAN) {
+            stc(segf, i, narrow(ef));
+            ef = dmad(last ? pLast : p, ef, dmad(last ? qLast : q, e, widen(vfb[j])));
+          }
+          e = dmad(last ? pLast : p, e, widen(vb[j]));
+        });
   }
 }
 

@@ -680,11 +680,18 @@ struct BtfShape {
   int64_t B, T, F, S, L;
 };
 
-// Steps per streamed chunk of the BTF passes (stream_steps).
-#ifndef RQF_BTF_STREAM
-#define RQF_BTF_STREAM 8
+// Steps per streamed chunk of the BTF passes (stream_steps).  Config 2's
+// workload in (B,T,F) layout: forward 0.322 ms with 8 and 0.312 with 16;
+// backward (one wavefront per SIMD, more state per step) 0.441 with 8 and
+// 0.445 with 16.
+#ifndef RQF_BTF_STREAM_FWD
+#define RQF_BTF_STREAM_FWD 16
 #endif
-constexpr int kBtfStream = RQF_BTF_STREAM;
+#ifndef RQF_BTF_STREAM_BWD
+#define RQF_BTF_STREAM_BWD 8
+#endif
+constexpr int kBtfStreamFwd = RQF_BTF_STREAM_FWD;
+constexpr int kBtfStreamBwd = RQF_BTF_STREAM_BWD;
 // Target task counts (segments x batch x filters).  Each final pass folds all
 // earlier segments' carries per task, so more segments cost the backward,
 // whose final pass holds more state, more than they gain: config 2's workload
@@ -712,8 +719,8 @@ __global__ __launch_bounds__(256) void btf_fwd_local_kernel(
   const float* xb = x + 2 * (b * sh.T * sh.F + f);
   c32 xprev = (k1p && t_beg > 0) ? ldc(xb, (t_beg - 1) * sh.F) : mk(0.0f, 0.0f);
   c32 y = mk(0.0f, 0.0f);
-  c32 xbuf[kBtfStream];
-  stream_steps<kBtfStream, true>(
+  c32 xbuf[kBtfStreamFwd];
+  stream_steps<kBtfStreamFwd, true>(
       t_beg, t_end, [&](int j, int64_t t) { xbuf[j] = ldc(xb, t * sh.F); },
       [&](int j, int64_t) {
         y = cmad(a, y, cmad(k1, xprev, cmul(k0, xbuf[j])));
@@ -736,8 +743,8 @@ __global__ __launch_bounds__(256) void btf_fwd_final_kernel(
   if (seg > 0) {  // entry state: the earlier segments' end states, folded in fp64
     const c64d aL = dpow(widen(a), sh.L);
     c64d e = mkd(0.0, 0.0);
-    c32 vbuf[kBtfStream];
-    stream_steps<kBtfStream, true>(
+    c32 vbuf[kBtfStreamFwd];
+    stream_steps<kBtfStreamFwd, true>(
         0, seg, [&](int j, int64_t s) { vbuf[j] = ldc(seg_end, (b * sh.S + s) * sh.F + f); },
         [&](int j, int64_t) { e = dmad(aL, e, widen(vbuf[j])); });
     y = narrow(e);
@@ -746,8 +753,8 @@ __global__ __launch_bounds__(256) void btf_fwd_final_kernel(
   const float* xb = x + 2 * (b * sh.T * sh.F + f);
   float* ob = out + 2 * (b * sh.T * sh.F + f);
   c32 xprev = (k1p && t_beg > 0) ? ldc(xb, (t_beg - 1) * sh.F) : mk(0.0f, 0.0f);
-  c32 xbuf[kBtfStream];
-  stream_steps<kBtfStream, true>(
+  c32 xbuf[kBtfStreamFwd];
+  stream_steps<kBtfStreamFwd, true>(
       t_beg, t_end, [&](int j, int64_t t) { xbuf[j] = ldc(xb, t * sh.F); },
       [&](int j, int64_t t) {
         y = cmad(a, y, cmad(k1, xprev, cmul(k0, xbuf[j])));
@@ -770,8 +777,8 @@ __global__ __launch_bounds__(256) void btf_bwd_local_kernel(const float* __restr
   const int64_t t_beg = seg * sh.L, t_end = min(sh.T, t_beg + sh.L);
   const float* gb = gout + 2 * (b * sh.T * sh.F + f);
   c32 g = mk(0.0f, 0.0f), h = mk(0.0f, 0.0f);
-  c32 gbuf[kBtfStream];
-  stream_steps<kBtfStream, false>(
+  c32 gbuf[kBtfStreamBwd];
+  stream_steps<kBtfStreamBwd, false>(
       t_beg, t_end, [&](int j, int64_t t) { gbuf[j] = ldc(gb, t * sh.F); },
       [&](int j, int64_t) {
         h = cmad(ac, h, g);
@@ -810,8 +817,8 @@ __global__ __launch_bounds__(256) void btf_bwd_final_kernel(
     const c64d pL = dmul(p1, widen(ac));
     const c64d q = mkd(p1.r * (double)sh.L, p1.i * (double)sh.L);
     c64d e = mkd(0.0, 0.0), eh = mkd(0.0, 0.0);
-    c32 vg[kBtfStream], vh[kBtfStream];
-    stream_steps<kBtfStream, false>(
+    c32 vg[kBtfStreamBwd], vh[kBtfStreamBwd];
+    stream_steps<kBtfStreamBwd, false>(
         seg + 1, sh.S,
         [&](int j, int64_t s) {
           const int64_t i = (b * sh.S + s) * sh.F + f;
@@ -833,8 +840,8 @@ __global__ __launch_bounds__(256) void btf_bwd_final_kernel(
   double s1r = 0, s1i = 0, s0r = 0, s0i = 0, s2r = 0, s2i = 0;
   // x[t] of each step is the x[t-1] the step after it (in time) loaded.
   c32 xt = ldc(xb, (t_end - 1) * sh.F);
-  c32 gbuf[kBtfStream], xpbuf[kBtfStream];
-  stream_steps<kBtfStream, false>(
+  c32 gbuf[kBtfStreamBwd], xpbuf[kBtfStreamBwd];
+  stream_steps<kBtfStreamBwd, false>(
       t_beg, t_end,
       [&](int j, int64_t t) {
         gbuf[j] = ldc(gb, t * sh.F);

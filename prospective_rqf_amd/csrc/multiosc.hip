@@ -48,7 +48,13 @@ using namespace rqf;
 namespace {
 
 constexpr int kMoscMaxOsc = 8;     // oscillators per filter (N <= 8)
-constexpr int kMoscMaxSeg = 256;   // steps per segment, at most
+// Steps per segment, at most.  Config 6 fwd+bwd: 74.2 Gelem/s at 256 (about 4
+// wavefronts per SIMD), 76.7 at 128, 72.3 at 64 (longer carry chains, more
+// segment states).
+#ifndef RQF_MOSC_MAX_SEG
+#define RQF_MOSC_MAX_SEG 128
+#endif
+constexpr int kMoscMaxSeg = RQF_MOSC_MAX_SEG;
 constexpr int kMoscMinSeg = 16;    // steps per segment, at least (when T allows)
 constexpr int64_t kMoscLanes = 65536;  // target number of tasks
 // Steps per streamed chunk (see stream_steps).  Config 6 (B=32 T=16000 F=128,

@@ -195,7 +195,10 @@ typedef struct rqf_selective_inputs {
   const float *write_logits; /* (F,B,T) f32, or NULL */
   const float *bias, *theta, *minimum, *span, *step, *horizon, *theta_minimum,
       *theta_maximum;        /* (F,) f32 */
-  const int64_t *groups;     /* (F,) warp group of each channel, each in [0, G), or NULL */
+  const int64_t *groups;     /* (F,) warp group of each channel, each in [0, G), or NULL.
+                              * Out-of-range entries are clamped into [0, G) on the device
+                              * (no out-of-bounds access; the results are then those of the
+                              * clamped groups): validate on the host. */
   int32_t has_gamma, has_warp, has_write, log_shift;
   float gamma_scale, warp_scale;
   int32_t prospective, gamma_horizon, write_sigmoid;

@@ -30,7 +30,9 @@ def _pick_chunk(filters: int, batch: int) -> int:
     return _CHUNK
 
 
-def _c64(t: torch.Tensor) -> torch.Tensor:
+def _c64(t: torch.Tensor | None) -> torch.Tensor | None:
+    if t is None:
+        return None
     if not t.is_complex():
         t = t.to(torch.cfloat)
     return t.to(torch.complex64).resolve_conj().contiguous()
@@ -42,6 +44,14 @@ def _check_btf(u: torch.Tensor, *coefs: torch.Tensor) -> None:
     for c in coefs:
         if c.shape != (u.shape[2],):
             raise ValueError(f"coefficients must have shape ({u.shape[2]},), got {tuple(c.shape)}")
+
+
+def _check_like(u: torch.Tensor, **tensors) -> None:
+    """Every named (B,T,F) tensor (None allowed) must have the input's shape."""
+    for name, t in tensors.items():
+        if t is not None and t.shape != u.shape:
+            raise ValueError(f"{name} must have the input's shape {tuple(u.shape)}, "
+                             f"got {tuple(t.shape)}")
 
 
 def _ws(B, T, F, device):
@@ -66,9 +76,15 @@ def _chunked_scan_forward_raw(C1, C2, u):
 
 
 def _chunked_scan_backward_raw(C1, C2, u, states, grad_output):
-    """Adjoint of the chunked scan: ``(grad_C1, grad_C2, grad_u)``."""
-    C1, C2, u, states, grad_output = (_c64(t) for t in (C1, C2, u, states, grad_output))
-    _lib.require_device(C1, C2, u, states, grad_output)
+    """Adjoint of the chunked scan: ``(grad_C1, grad_C2, grad_u)``.
+
+    ``states`` (the forward output the reference's kernel reads) is accepted for
+    the reference's signature and may be None: the kernel evaluates
+    ``grad_C1`` from ``u`` with the order of summation exchanged."""
+    C1, C2, u, grad_output = (_c64(t) for t in (C1, C2, u, grad_output))
+    _lib.require_device(C1, C2, u, grad_output)
+    _check_btf(u, C1, C2)
+    _check_like(u, states=states, grad_output=grad_output)
     B, T, F = u.shape
     grad_u = torch.empty_like(u)
     gc1 = torch.empty(F, dtype=torch.complex64, device=u.device)
@@ -76,7 +92,7 @@ def _chunked_scan_backward_raw(C1, C2, u, states, grad_output):
     ws, n = _ws(B, T, F, u.device)
     _lib.check(
         _lib.load().rqf_chunked_scan_bwd(
-            _lib.ptr(C1), _lib.ptr(C2), _lib.ptr(u), _lib.ptr(states), _lib.ptr(grad_output),
+            _lib.ptr(C1), _lib.ptr(C2), _lib.ptr(u), None, _lib.ptr(grad_output),
             _lib.ptr(grad_u), _lib.ptr(gc1), _lib.ptr(gc2), B, T, F, _lib.ptr(ws), n,
             _lib.stream_of(u)),
         "rqf_chunked_scan_bwd",
@@ -91,14 +107,16 @@ class _ChunkedScanFunction(torch.autograd.Function):
     def forward(ctx, C1, C2, u):
         C1, C2, u = _c64(C1), _c64(C2), _c64(u)
         output = _chunked_scan_forward_raw(C1, C2, u)
-        ctx.save_for_backward(C1, C2, u, output)
+        # The reference also saves the output for its backward kernel
+        # (chunked_scan_kernel.py:328); the HIP adjoint does not read it.
+        ctx.save_for_backward(C1, C2, u)
         return output
 
     @staticmethod
     @once_differentiable
     def backward(ctx, grad_output):
-        C1, C2, u, states = ctx.saved_tensors
-        return _chunked_scan_backward_raw(C1, C2, u, states, grad_output)
+        C1, C2, u = ctx.saved_tensors
+        return _chunked_scan_backward_raw(C1, C2, u, None, grad_output)
 
 
 def _triton_chunked_scan(C1, C2, u):
@@ -126,15 +144,17 @@ def _chunked_prospective_forward_raw(C1, tap0, tap1, x):
 
 
 def _chunked_prospective_backward_raw(C1, tap0, tap1, x, states, grad_output):
-    """``(grad_C1, grad_tap0, grad_tap1, grad_x)`` of the two-tap scan, from the
-    forward's output ``states`` (the tensor the reference's autograd context
-    saves).  The reference's ``_ChunkedProspectiveScanFunction.backward``
+    """``(grad_C1, grad_tap0, grad_tap1, grad_x)`` of the two-tap scan.
+    ``states``, the forward output the reference's autograd context saves
+    (chunked_scan_kernel.py:486), is accepted and may be None: the kernel
+    does not read it.  The reference's ``_ChunkedProspectiveScanFunction.backward``
     (chunked_scan_kernel.py:490-504) computes the same with a chunked adjoint
     scan and five pointwise passes; here one three-phase scan
     (``rqf_chunked_prospective_bwd``) produces grad_x and the three sums."""
-    C1, tap0, tap1, x, states, grad_output = (
-        _c64(t) for t in (C1, tap0, tap1, x, states, grad_output))
-    _lib.require_device(C1, tap0, tap1, x, states, grad_output)
+    C1, tap0, tap1, x, grad_output = (_c64(t) for t in (C1, tap0, tap1, x, grad_output))
+    _lib.require_device(C1, tap0, tap1, x, grad_output)
+    _check_btf(x, C1, tap0, tap1)
+    _check_like(x, states=states, grad_output=grad_output)
     B, T, F = x.shape
     grad_x = torch.empty_like(x)
     gc1 = torch.empty(F, dtype=torch.complex64, device=x.device)
@@ -143,7 +163,7 @@ def _chunked_prospective_backward_raw(C1, tap0, tap1, x, states, grad_output):
     ws, n = _ws(B, T, F, x.device)
     _lib.check(
         _lib.load().rqf_chunked_prospective_bwd(
-            _lib.ptr(C1), _lib.ptr(tap0), _lib.ptr(tap1), _lib.ptr(x), _lib.ptr(states),
+            _lib.ptr(C1), _lib.ptr(tap0), _lib.ptr(tap1), _lib.ptr(x), None,
             _lib.ptr(grad_output), _lib.ptr(grad_x), _lib.ptr(gc1), _lib.ptr(gt0),
             _lib.ptr(gt1), B, T, F, _lib.ptr(ws), n, _lib.stream_of(x)),
         "rqf_chunked_prospective_bwd",
@@ -158,14 +178,15 @@ class _ChunkedProspectiveScanFunction(torch.autograd.Function):
     def forward(ctx, C1, tap0, tap1, x):
         C1, tap0, tap1, x = (_c64(t) for t in (C1, tap0, tap1, x))
         output = _chunked_prospective_forward_raw(C1, tap0, tap1, x)
-        ctx.save_for_backward(C1, tap0, tap1, x, output)
+        # The output is not saved: the HIP adjoint does not read it.
+        ctx.save_for_backward(C1, tap0, tap1, x)
         return output
 
     @staticmethod
     @once_differentiable
     def backward(ctx, grad_output):
-        C1, tap0, tap1, x, states = ctx.saved_tensors
-        return _chunked_prospective_backward_raw(C1, tap0, tap1, x, states, grad_output)
+        C1, tap0, tap1, x = ctx.saved_tensors
+        return _chunked_prospective_backward_raw(C1, tap0, tap1, x, None, grad_output)
 
 
 def _triton_chunked_scan_prospective(C1, tap0, tap1, x):

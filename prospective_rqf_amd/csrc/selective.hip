@@ -148,6 +148,17 @@ struct Chan {
   float inv_write_max, inv_gamma_scale;
 };
 
+// Warp group of channel f, a row of warp_logits.  The documented precondition
+// is 0 <= groups[f] < G (the Python layer rejects anything else before a
+// launch); the clamp keeps a C-ABI caller that breaks it inside warp_logits
+// and the team tables.
+__host__ __device__ __forceinline__ int clamp_group(int64_t g, int64_t G) {
+  return (int)(g < 0 ? 0 : (g >= G ? G - 1 : g));
+}
+__device__ __forceinline__ int64_t group_of(const rqf_selective_inputs& p, int64_t f) {
+  return clamp_group(p.groups[f], p.G);
+}
+
 __device__ __forceinline__ Chan load_chan(const rqf_selective_inputs& p, int64_t f) {
   Chan c;
   c.bias = p.bias[f];
@@ -353,7 +364,8 @@ __device__ __forceinline__ RowId row_id(const rqf_selective_inputs& p, int64_t L
   const int64_t c = L / per, rem = L - c * per;
   const int64_t pos = rem / bc;  // channel position in the visiting order
   r.b = c * bc + (rem - pos * bc);
-  r.f = p.order ? (int64_t)p.order[pos] : pos;  // group-contiguous channel order
+  // group-contiguous channel order (clamped like the group indices)
+  r.f = p.order ? (int64_t)min(max(p.order[pos], 0), (int)p.F - 1) : pos;
   r.valid = c < kXcds && r.b < p.B;
   r.row = r.f * p.B + r.b;
   return r;
@@ -525,7 +537,7 @@ __global__ __launch_bounds__(kRowsPerBlock* kWave)
   r.zr = z + 2 * base;
   r.gr = p.has_gamma ? p.gamma_logits + base : nullptr;
   r.wr = p.has_write ? p.write_logits + base : nullptr;
-  r.dr = p.has_warp ? p.warp_logits + (p.groups[id.f] * p.B + id.b) * r.T : nullptr;
+  r.dr = p.has_warp ? p.warp_logits + (group_of(p, id.f) * p.B + id.b) * r.T : nullptr;
   r.rawr = raw ? raw + 2 * base : nullptr;
   r.actr = act ? act + 2 * base : nullptr;
   r.skr = skip ? skip + 2 * base : nullptr;
@@ -606,7 +618,7 @@ __global__ __launch_bounds__(kFwdRbWaves* kWave)
   r.zr = z + 2 * base;
   r.gr = p.has_gamma ? p.gamma_logits + base : nullptr;
   r.wr = p.has_write ? p.write_logits + base : nullptr;
-  r.dr = p.has_warp ? p.warp_logits + (p.groups[id.f] * p.B + id.b) * T : nullptr;
+  r.dr = p.has_warp ? p.warp_logits + (group_of(p, id.f) * p.B + id.b) * T : nullptr;
   r.rawr = raw ? raw + 2 * base : nullptr;
   r.actr = act ? act + 2 * base : nullptr;
   r.skr = skip ? skip + 2 * base : nullptr;
@@ -982,7 +994,7 @@ __global__ __launch_bounds__(kRowsPerBlock* kWave)
   r.zr = z + 2 * base;
   r.gr = p.has_gamma ? p.gamma_logits + base : nullptr;
   r.wr = p.has_write ? p.write_logits + base : nullptr;
-  r.dr = p.has_warp ? p.warp_logits + (p.groups[id.f] * p.B + id.b) * r.T : nullptr;
+  r.dr = p.has_warp ? p.warp_logits + (group_of(p, id.f) * p.B + id.b) * r.T : nullptr;
   r.gyr = gy ? gy + 2 * base : nullptr;
   r.gxr = gx ? gx + 2 * base : nullptr;
   r.ent = entries + 2 * id.row * nc;
@@ -1083,7 +1095,7 @@ __device__ void team_build_global(const int64_t* __restrict__ groups, int F, int
                                   int* first, int* count, int* group, int* gteam, int* nteams,
                                   int* gcount, int* moff) {
   const int tid = threadIdx.x, nt = blockDim.x;
-  auto grp = [&](int f) { return groups ? (int)groups[f] : 0; };
+  auto grp = [&](int f) { return groups ? clamp_group(groups[f], G) : 0; };
   for (int g = tid; g < G; g += nt) {
     int n = 0;
     for (int f = 0; f < F; ++f) n += grp(f) == g;
@@ -1129,7 +1141,7 @@ __global__ __launch_bounds__(256) void team_build_kernel(const int64_t* __restri
   __shared__ int s_count[kBuildGroups], s_moff[kBuildGroups], s_gteam[kBuildGroups + 1];
   const int tid = threadIdx.x, nt = blockDim.x;
   if (F <= kBuildLds && G <= kBuildGroups) {
-    for (int f = tid; f < F; f += nt) sg[f] = groups ? (int)groups[f] : 0;
+    for (int f = tid; f < F; f += nt) sg[f] = groups ? clamp_group(groups[f], G) : 0;
     for (int g = tid; g < G; g += nt) s_count[g] = 0;
     __syncthreads();
     for (int f = tid; f < F; f += nt)
@@ -1424,16 +1436,16 @@ __global__ __launch_bounds__(256) void group_reduce_kernel(const float* __restri
 #pragma unroll
       for (int q = 0; q < 4; ++q) v[q] = in ? ddc[(int64_t)(f + q) * N + i] : 0.0f;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) acc[groups[f + q]][tid] += v[q];
+      for (int q = 0; q < 4; ++q) acc[clamp_group(groups[f + q], G)][tid] += v[q];
     }
-    for (; f < F; ++f) acc[groups[f]][tid] += in ? ddc[(int64_t)f * N + i] : 0.0f;
+    for (; f < F; ++f) acc[clamp_group(groups[f], G)][tid] += in ? ddc[(int64_t)f * N + i] : 0.0f;
     if (in)
       for (int g = 0; g < G; ++g) dd[(int64_t)g * N + i] = acc[g][tid];
   } else if (in) {
     for (int g = 0; g < G; ++g) {
       float s = 0.0f;
       for (int f = 0; f < F; ++f)
-        if (groups[f] == g) s += ddc[(int64_t)f * N + i];
+        if (clamp_group(groups[f], G) == g) s += ddc[(int64_t)f * N + i];
       dd[(int64_t)g * N + i] = s;
     }
   }

@@ -118,12 +118,28 @@ def fbt_recompute_forward_raw(C1, tap0, tap1, x, skip=None):
 
 
 def fbt_recompute_backward_raw(C1, tap0, tap1, x, carry, grad_output):
-    """Kernel-only backward of :func:`fbt_recompute_scan`: ``(gC1, gtap0, gtap1, gx)``."""
+    """Kernel-only backward of :func:`fbt_recompute_scan`: ``(gC1, gtap0, gtap1, gx)``.
+
+    ``carry`` is the forward's ``(F*B, rqf_fbt_carry_chunks(T))`` entry-state
+    tensor; every shape is checked before the launch."""
+    x = _c64(x)
+    if x.dim() != 3:
+        raise ValueError(f"expected (filters, batch, time) input, got shape {tuple(x.shape)}")
     filters, batch, time = x.shape
+    C1, tap0, tap1 = _coefs(C1, tap0, tap1, filters)
     g = _c64(grad_output)
+    if g.shape != x.shape:
+        raise ValueError(f"grad_output must have the input's shape {tuple(x.shape)}, "
+                         f"got {tuple(g.shape)}")
+    lib = _lib.load()
+    want = (filters * batch, max(lib.rqf_fbt_carry_chunks(time), 1))
+    if tuple(carry.shape) != want or carry.dtype != torch.complex64:
+        raise ValueError(f"carry must be complex64 of shape {want}, got {carry.dtype} "
+                         f"{tuple(carry.shape)}")
+    carry = carry.contiguous()
+    _lib.require_device(x, g, carry, C1)
     grad_z = torch.empty_like(x)
     gc1, gt0, gt1 = _bwd_grads(filters, x.device)
-    lib = _lib.load()
     n = lib.rqf_fbt_workspace(filters, batch, time)
     ws = _lib.workspace(n, x.device)
     _lib.check(

@@ -116,6 +116,12 @@ def _backward(C1, C2, u, c_weights, grad_output, num_osc, *, real: bool, compute
     grad_output = _c64(grad_output)
     _lib.require_device(C1, C2, u, cw, grad_output)
     B, T, F = _check(u, C1, C2, num_osc)
+    if cw.shape != (F * num_osc,):
+        raise ValueError(f"c_weights must cover {F * num_osc} oscillators, got "
+                         f"{tuple(c_weights.shape)}")
+    if grad_output.shape != (B, T, F):
+        raise ValueError(f"grad_output must have shape {(B, T, F)}, got "
+                         f"{tuple(grad_output.shape)}")
     dev = u.device
     grad_u = torch.empty_like(u) if compute_grad_u else None
     gc1 = torch.empty(F * num_osc, dtype=torch.complex64, device=dev) if compute_grad_C1 else None

@@ -10,8 +10,11 @@ Flags (read at import, like the reference):
   ORGANICS_DISABLE_TRITON=1                  -> ``_HAS_TRITON`` False
 ``_HAS_TRITON`` keeps the reference's name for "the accelerated kernels are
 usable"; here that means librqf_hip.so is built and not disabled.
-``ORGANICS_RQF_FBT`` is read at call time by the callers (pure.py:144,506),
-see :func:`fbt_enabled`.
+``_HAS_FBT_PROSPECTIVE`` mirrors the cells' import-time flag (pure.py:34-40):
+the fused FBT / selective kernels are importable, which, as in the reference,
+``ORGANICS_DISABLE_TRITON`` does not change.
+``ORGANICS_RQF_FBT`` is read at call time by the callers (pure.py:143-144,
+500-508), see :func:`fbt_enabled` and :func:`selective_use_kernel`.
 
 Only HIP-device inputs on the chunked backend are served.  The reference's
 CPU loop, PyTorch Blelloch scan, legacy sequential kernels and B-matrix
@@ -33,14 +36,26 @@ _SCAN_BACKEND = os.environ.get("ORGANICS_SCAN_BACKEND", "chunked").lower()
 _USE_CHUNKED = _SCAN_BACKEND == "chunked"
 try:
     _lib.load()
-    _HAS_TRITON = not _TRITON_DISABLED
+    _HAS_FBT_PROSPECTIVE = True
 except (OSError, _lib.RQFError):
-    _HAS_TRITON = False
+    _HAS_FBT_PROSPECTIVE = False
+_HAS_TRITON = _HAS_FBT_PROSPECTIVE and not _TRITON_DISABLED
 
 
-def fbt_enabled() -> bool:
-    """Call-time toggle of the fused FBT / selective kernels (pure.py:143-144, 505-506)."""
+def selective_use_kernel() -> bool:
+    """``use_kernel`` of the selective cells, read at call time
+    (``_forward_selective``, pure.py:143-144): the chunked backend is selected
+    and ``ORGANICS_RQF_FBT`` is not ``"0"``."""
     return _SCAN_BACKEND == "chunked" and os.environ.get("ORGANICS_RQF_FBT", "1") != "0"
+
+
+def fbt_enabled(x: torch.Tensor | None = None) -> bool:
+    """Whether the channel-outermost fused path applies (``_fbt_enabled``,
+    pure.py:500-508): the fused kernels are available, ``x`` (when given) is a
+    device tensor, the chunked backend is selected and ``ORGANICS_RQF_FBT`` is
+    not ``"0"`` at call time.  The reference also requires every block to be
+    FBT-eligible; that check belongs to the cell."""
+    return (_HAS_FBT_PROSPECTIVE and (x is None or x.is_cuda) and selective_use_kernel())
 
 
 def _prepare(C1, C2, u):
@@ -61,13 +76,13 @@ def _prepare(C1, C2, u):
 def _require_served(u, B):
     if B is not None:
         raise NotImplementedError("the B-matrix scan is not served by the HIP backend")
-    if not u.is_cuda:
-        raise RuntimeError("sequential_scan/parallel_scan: HIP backend needs a device tensor")
     if not (_HAS_TRITON and _USE_CHUNKED):
         raise RuntimeError(
             "HIP scan backend disabled (ORGANICS_DISABLE_TRITON=1, "
             "ORGANICS_SCAN_BACKEND != chunked, or librqf_hip.so not built)"
         )
+    if not u.is_cuda:
+        raise RuntimeError("sequential_scan/parallel_scan: HIP backend needs a device tensor")
 
 
 def sequential_scan(C1, C2, u, B=None):

@@ -9,6 +9,7 @@ returned tensors and shapes.  The compute runs in ``librqf_hip.so``
 from __future__ import annotations
 
 import ctypes
+import weakref
 
 import torch
 
@@ -24,25 +25,47 @@ def _real_ptr(t: torch.Tensor | None):
     return _lib.ptr(t)
 
 
+# Validated warp-group tensors: id(caller's tensor) -> (weakref to it, its
+# version counter, number of warp rows, device, device int64 copy, order).
+# An entry counts only while the weak reference still resolves to the very
+# tensor looked up and its version is unchanged, so a new tensor that reuses
+# a freed tensor's id or address, or an in-place edit (through any view),
+# is validated afresh.
 _VALID_GROUPS: dict = {}
 
 
-def _check_groups(groups: torch.Tensor, n_groups: int) -> torch.Tensor:
-    """Warp-group indices must address rows of warp_logits (the kernel reads
-    warp_logits[groups[f]]).  Checked once per tensor version; returns the
-    channel visiting order (stable argsort of the groups, int32) that keeps
-    each group's channels adjacent."""
-    key = (groups.data_ptr(), groups._version, groups.numel(), n_groups, groups.device)
-    order = _VALID_GROUPS.get(key)
-    if order is not None:
-        return order
-    if groups.numel() and (int(groups.min()) < 0 or int(groups.max()) >= n_groups):
-        raise ValueError(f"groups must index the {n_groups} warp-logit rows")
+def _check_groups(groups: torch.Tensor, n_groups: int, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """Validate the caller's ``groups`` tensor (F,) against ``n_groups`` warp rows.
+
+    The kernels read ``warp_logits[groups[f]]``, so every entry must lie in
+    ``[0, n_groups)``; otherwise ``ValueError`` is raised before any launch
+    (the reference's controller builds them as ``rank * G // F``,
+    rqf_models/backbones/rqf/selective.py:164-165).  Returns the int64 copy on
+    ``device`` that the kernels read and the channel visiting order (stable
+    argsort of the groups, int32) that keeps each group's channels adjacent.
+    Both are cached per tensor object and version."""
+    key = id(groups)
+    hit = _VALID_GROUPS.get(key)
+    if (hit is not None and hit[0]() is groups and hit[1] == groups._version
+            and hit[2] == n_groups and hit[3] == device):
+        return hit[4], hit[5]
+    dev_groups = groups.to(device=device, dtype=torch.int64).contiguous()
+    if dev_groups.numel():
+        lo, hi = torch.aminmax(dev_groups)
+        if int(lo) < 0 or int(hi) >= n_groups:
+            raise ValueError(f"groups must index the {n_groups} warp-logit rows, "
+                             f"got values in [{int(lo)}, {int(hi)}]")
+    order = torch.argsort(dev_groups, stable=True).to(torch.int32).contiguous()
+    for k in [k for k, v in _VALID_GROUPS.items() if v[0]() is None]:
+        del _VALID_GROUPS[k]
     if len(_VALID_GROUPS) > 64:
         _VALID_GROUPS.clear()
-    order = torch.argsort(groups, stable=True).to(torch.int32).contiguous()
-    _VALID_GROUPS[key] = order
-    return order
+    try:
+        ref = weakref.ref(groups)
+    except TypeError:  # not weak-referenceable: validate on every call
+        return dev_groups, order
+    _VALID_GROUPS[key] = (ref, groups._version, n_groups, device, dev_groups, order)
+    return dev_groups, order
 
 
 def inputs_struct(z: torch.Tensor, inputs) -> tuple[_lib.SelectiveInputsStruct, list]:
@@ -59,19 +82,22 @@ def inputs_struct(z: torch.Tensor, inputs) -> tuple[_lib.SelectiveInputsStruct, 
     wl = vec(inputs.write_logits) if has_write else None
     params = [vec(getattr(inputs, n)) for n in (
         "bias", "theta", "minimum", "span", "step", "horizon", "theta_minimum", "theta_maximum")]
-    groups = inputs.groups.to(device=z.device, dtype=torch.int64).contiguous() if has_warp else None
     for name, v, rows in (("gamma_logits", gl, f), ("write_logits", wl, f)):
         if v is not None and tuple(v.shape) != (rows, b, t):
             raise ValueError(f"{name} must have shape {(rows, b, t)}, got {tuple(v.shape)}")
     g = 0
-    order = None
+    groups = order = None
     if dl is not None:
         if dl.dim() != 3 or tuple(dl.shape[1:]) != (b, t):
             raise ValueError(f"warp_logits must have shape (G, {b}, {t}), got {tuple(dl.shape)}")
         g = dl.shape[0]
-        if groups is None or groups.shape != (f,):
+        if g < 1:
+            raise ValueError("the warp head needs at least one warp-logit row")
+        if not isinstance(inputs.groups, torch.Tensor) or tuple(inputs.groups.shape) != (f,):
             raise ValueError("groups must be a (F,) index tensor when the warp head is on")
-        order = _check_groups(groups, g)
+        if inputs.groups.is_complex() or inputs.groups.is_floating_point():
+            raise ValueError("groups must be an integer index tensor")
+        groups, order = _check_groups(inputs.groups, g, z.device)
     for name, v in zip(("bias", "theta", "minimum", "span", "step", "horizon",
                         "theta_minimum", "theta_maximum"), params):
         if v.shape != (f,):

@@ -107,3 +107,25 @@ def rounded_to_f32(inp):
         r(inp.theta_minimum), r(inp.theta_maximum),
         tuple(float(np.float32(v)) if isinstance(v, float) else v for v in inp.options),
     )
+
+
+def from_torch(inp):
+    """oracle.SelectiveInputs (fp64 numpy) holding exactly the fp32 values of a
+    torch ``SelectiveScanInputs`` (e.g. one built by ``workloads.selective_inputs``)."""
+
+    def npy(v):
+        return v.detach().cpu().to(torch.float64).numpy()
+
+    _, B, T = inp.gamma_logits.shape if inp.options[0] else inp.write_logits.shape
+
+    def logits(v, on):
+        return npy(v) if on and v is not None and v.numel() else np.zeros((0, B, T))
+
+    return oracle.SelectiveInputs(
+        logits(inp.gamma_logits, inp.options[0]), logits(inp.warp_logits, inp.options[1]),
+        logits(inp.write_logits, inp.options[2]), npy(inp.bias), npy(inp.theta),
+        None if inp.groups is None else inp.groups.detach().cpu().numpy().astype(np.int64),
+        npy(inp.minimum), npy(inp.span), npy(inp.step), npy(inp.horizon),
+        npy(inp.theta_minimum), npy(inp.theta_maximum),
+        tuple(float(np.float32(v)) if isinstance(v, float) else v for v in inp.options),
+    )

@@ -47,6 +47,7 @@ from tests.helpers import (
     cotangent_off_relu_kink,
     PARITY_RTOL,
     block_coefficients,
+    chanerr,
     crandn,
     load_checkpoint_params,
     relerr,
@@ -72,6 +73,9 @@ def _dev(a, grad=True):
 
 def _check(pairs, case):
     errs = {name: relerr(got, want) for name, got, want in pairs}
+    # per-channel check of the coefficient gradients
+    errs.update({name + "/channel": chanerr(got, want) for name, got, want in pairs
+                 if name.startswith(("grad_C", "grad_tap"))})
     print("  " + case + ": " + " ".join(f"{k} {v:.1e}" for k, v in errs.items()))
     bad = {k: v for k, v in errs.items() if not v <= PARITY_RTOL}
     assert not bad, (case, errs)

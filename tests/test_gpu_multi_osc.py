@@ -15,7 +15,7 @@ import torch
 from oracle import oracle
 from prospective_rqf_amd import multi_osc_scan as mo
 from prospective_rqf_amd import scan as hip_scan
-from tests.helpers import PARITY_RTOL, crandn, relerr
+from tests.helpers import PARITY_RTOL, chanerr, crandn, relerr
 
 pytestmark = pytest.mark.gpu
 
@@ -75,7 +75,9 @@ def test_multi_osc_forward_backward(shape, N, real):
     gcw_got = CW.grad[:, 0].double() + 1j * CW.grad[:, 1].double()
     errs = {"y": relerr(y, y_ref), "gc1": relerr(C1.grad, gc1_ref),
             "gc2": relerr(C2.grad, gc2_ref), "gcw": relerr(gcw_got.cpu(), gcw_ref),
-            "gu": relerr(U.grad, gu_ref.real if real else gu_ref)}
+            "gu": relerr(U.grad, gu_ref.real if real else gu_ref),
+            "gc1/channel": chanerr(C1.grad, gc1_ref), "gc2/channel": chanerr(C2.grad, gc2_ref),
+            "gcw/channel": chanerr(gcw_got.cpu(), gcw_ref)}
     assert U.grad.dtype == U.dtype
     with torch.no_grad():
         if real:
@@ -167,7 +169,9 @@ def test_long_memory_filters_at_full_length():
     gcw_got = CW.grad[:, 0].double() + 1j * CW.grad[:, 1].double()
     errs = {"y": relerr(y, y_ref), "gc1": relerr(C1.grad, gc1_ref),
             "gc2": relerr(C2.grad, gc2_ref), "gcw": relerr(gcw_got.cpu(), gcw_ref),
-            "gu": relerr(U.grad, gu_ref)}
+            "gu": relerr(U.grad, gu_ref),
+            "gc1/channel": chanerr(C1.grad, gc1_ref), "gc2/channel": chanerr(C2.grad, gc2_ref),
+            "gcw/channel": chanerr(gcw_got.cpu(), gcw_ref)}
     print("  " + " ".join(f"{k} {v:.1e}" for k, v in errs.items()), flush=True)
     bad = {k: v for k, v in errs.items() if not v <= PARITY_RTOL}
     assert not bad, errs

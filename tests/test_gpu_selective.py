@@ -17,7 +17,7 @@ import torch
 from oracle import oracle, torch_ref
 from prospective_rqf_amd.selective_scan import selective_layer_scan
 from prospective_rqf_amd.selective_scan_kernel import selective_backward, selective_forward
-from tests.helpers import PARITY_RTOL, crandn, relerr
+from tests.helpers import PARITY_RTOL, SELECTIVE_CHANNEL_RTOL, chanerr, crandn, relerr
 from tests.selective_cases import CASES, case_id, make_inputs, rounded_to_f32, to_torch
 
 pytestmark = pytest.mark.gpu
@@ -70,17 +70,47 @@ def run_case(F, B, T, case, *, prospective=True, truncated=False, activate=True,
     for j in range(1, nc):
         ent_ref[:, j] = rr[:, j * chunk - 1]
     errs["entries"] = relerr(entries, ent_ref)
+    chan = {}
     for tag, out in outs.items():
         for name, got, want in zip(("dz", "dzw", "dg", "dd", "dw", "dbias", "dtheta"), out, ref):
             if want is None:
                 assert got is None, name
             else:
                 errs[f"{tag}.{name}"] = relerr(got, want)
+                if name in ("dbias", "dtheta"):
+                    chan[f"{tag}.{name}/channel"] = chanerr(got, want)
     bad = {k: v for k, v in errs.items() if not v <= PARITY_RTOL}
+    chan_bar = SELECTIVE_CHANNEL_RTOL
+    if max(chan.values(), default=0.0) > chan_bar:
+        # beyond the fixed bar: compare with the reference formula's own fp32 error
+        ref32 = _fp32_reference_channel_errors(inp, z, gy, gx, truncated, ref)
+        chan_bar = max(chan_bar, 2.0 * max(ref32.values()))
+        print("fp32 reference per-channel errors:", ref32, flush=True)
+    bad.update({k: v for k, v in chan.items() if not v <= chan_bar})
+    errs.update(chan)
     if bad:
         print("errors:", {k: f"{v:.3g}" for k, v in errs.items()}, flush=True)
     assert not bad, bad
     return errs
+
+
+def _fp32_reference_channel_errors(inp, z, gy, gx, truncated, ref):
+    """Per-channel errors of dbias / dtheta from the reference's own formulas
+    evaluated in fp32 (the PyTorch restatement with autograd) against fp64."""
+    ti = to_torch(inp, dtype=torch.float32)
+    leaves = [ti.bias, ti.theta]
+    for v in leaves:
+        v.requires_grad_(True)
+    raw = torch_ref.selective_scan(torch.as_tensor(z.astype(np.complex64)), ti,
+                                   truncated=truncated)
+    loss = 0.0
+    if gy is not None:
+        loss = loss + (torch.as_tensor(gy.astype(np.complex64)).conj() * raw).real.sum()
+    if gx is not None:
+        act = torch_ref.split_relu(raw)
+        loss = loss + (torch.as_tensor(gx.astype(np.complex64)).conj() * act).real.sum()
+    db, dt = torch.autograd.grad(loss, leaves)
+    return {"dbias": chanerr(db, ref[5]), "dtheta": chanerr(dt, ref[6])}
 
 
 @pytest.mark.parametrize("truncated", [False, True])
@@ -284,3 +314,30 @@ def test_layer_scan_autograd_with_drive_gemm(truncated, autocast, shape):
     for name, g, gr in zip(("x", "W", "g", "d", "w", "bias", "theta"), grads, grads_r):
         err = relerr(g, gr)
         assert err <= PARITY_RTOL, (name, err)
+
+
+def test_out_of_range_groups_rejected_before_launch():
+    """A second groups tensor with an out-of-range entry is rejected on the host
+    (ValueError, outputs never allocated) after a valid one was accepted."""
+    rng = np.random.default_rng(31)
+    inp = to_torch(rounded_to_f32(make_inputs(6, 2, 40, CASE_ALL, rng, G=3)), device="cuda")
+    z = torch.zeros(6, 2, 40, dtype=torch.complex64, device="cuda")
+    selective_forward(z, inp, True, True, 32)
+    for bad in ([0, 1, 2, 0, 1, 3], [0, -1, 2, 0, 1, 2]):
+        with pytest.raises(ValueError, match="warp-logit rows"):
+            selective_forward(z, inp._replace(groups=torch.tensor(bad, device="cuda")), True,
+                              True, 32)
+    torch.cuda.synchronize()
+
+
+def test_fbt_toggle_at_call_time(monkeypatch):
+    """ORGANICS_RQF_FBT is read per call (pure.py:143-144, 500-508)."""
+    from prospective_rqf_amd import scan
+
+    x = torch.zeros(2, 3, 4, dtype=torch.complex64, device="cuda")
+    monkeypatch.setenv("ORGANICS_RQF_FBT", "1")
+    assert scan.fbt_enabled(x) and scan.selective_use_kernel()
+    monkeypatch.setenv("ORGANICS_RQF_FBT", "0")
+    assert not scan.fbt_enabled(x) and not scan.selective_use_kernel()
+    monkeypatch.delenv("ORGANICS_RQF_FBT")
+    assert scan.fbt_enabled(x)

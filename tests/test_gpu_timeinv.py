@@ -16,7 +16,7 @@ from prospective_rqf_amd.chunked_scan_kernel import (
     _triton_chunked_scan_prospective,
 )
 from prospective_rqf_amd.fbt_scan_kernel import fbt_prospective_scan, fbt_recompute_scan
-from tests.helpers import PARITY_RTOL, crandn, relerr
+from tests.helpers import PARITY_RTOL, chanerr, crandn, relerr
 
 pytestmark = pytest.mark.gpu
 
@@ -59,6 +59,9 @@ def test_chunked_scan_matches_oracle(shape):
                             ("grad_C1", C1.grad, gc1_ref), ("grad_C2", C2.grad, gc2_ref)):
         err = relerr(got, want)
         assert err <= PARITY_RTOL, (name, err)
+        if name.startswith(("grad_C", "grad_tap")):
+            err = chanerr(got, want)
+            assert err <= PARITY_RTOL, (name + "/channel", err)
 
 
 @pytest.mark.parametrize("shape", [(3, 4096, 32), (2, 300, 5), (1, 2, 7)])
@@ -79,6 +82,9 @@ def test_chunked_prospective_matches_oracle(shape):
                             ("grad_tap1", T1.grad, gt1_ref)):
         err = relerr(got, want)
         assert err <= PARITY_RTOL, (name, err)
+        if name.startswith(("grad_C", "grad_tap")):
+            err = chanerr(got, want)
+            assert err <= PARITY_RTOL, (name + "/channel", err)
 
 
 @pytest.mark.parametrize("variant", ["raw", "act", "recompute"])
@@ -109,6 +115,9 @@ def test_fbt_matches_oracle(variant, shape):
                             ("grad_tap1", T1.grad, gt1_ref)):
         err = relerr(got, want)
         assert err <= PARITY_RTOL, (name, err)
+        if name.startswith(("grad_C", "grad_tap")):
+            err = chanerr(got, want)
+            assert err <= PARITY_RTOL, (name + "/channel", err)
 
 
 @pytest.mark.parametrize("is_complex", [False, True])

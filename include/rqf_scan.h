@@ -20,7 +20,9 @@
  *     argument; a positive hipError_t when a launch fails.
  *   - Results are deterministic: coefficient gradients are reduced from
  *     per-row partial sums in a fixed order (no floating-point atomics).
- *   - Calls are reentrant.  No mutable global state exists.
+ *   - Calls are reentrant.  No mutable global state exists, except for the
+ *     one no-allocation entry point (rqf_fbt_recompute_bwd_noalloc), whose
+ *     static per-GPU scratch calls on one GPU share.
  */
 #ifndef RQF_SCAN_H
 #define RQF_SCAN_H
@@ -38,8 +40,12 @@ enum {
   RQF_OK = 0,
   RQF_ERR_ARG = -1,       /* null pointer, bad shape, or bad chunk */
   RQF_ERR_WORKSPACE = -2, /* workspace missing or too small */
-  RQF_ERR_ALIGN = -3      /* a tensor is not 8-byte aligned */
+  RQF_ERR_ALIGN = -3,     /* a tensor is not 8-byte aligned */
+  RQF_ERR_SCRATCH = -4    /* problem exceeds the static scratch of a no-allocation entry */
 };
+
+/* Bytes of the static device scratch of rqf_fbt_recompute_bwd_noalloc (per GPU). */
+#define RQF_NOALLOC_SCRATCH_BYTES ((size_t)4 << 20)
 
 /* Library version string and the offload target it was built for. */
 const char *rqf_version(void);
@@ -179,6 +185,22 @@ int rqf_fbt_recompute_bwd(const float *c1, const float *tap0, const float *tap1,
                           float *grad_z, float *grad_c1, float *grad_tap0, float *grad_tap1,
                           int64_t F, int64_t B, int64_t T, void *workspace,
                           size_t workspace_bytes, rqf_stream_t stream);
+
+/* rqf_fbt_recompute_bwd without a workspace argument and without allocating.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  The per-row partial sums live in a static device
+ * array of RQF_NOALLOC_SCRATCH_BYTES per GPU (4 MiB: F*B <= 87381 rows), held
+ * until the process ends; larger problems return RQF_ERR_SCRATCH before any
+ * launch.  The first call on a device looks the array's address up (once per
+ * device).  All calls on one GPU share that array: calls that overlap on one
+ * GPU (concurrent streams or threads) race and must be serialised by the
+ * caller.  Results equal rqf_fbt_recompute_bwd's bit for bit. */
+int rqf_fbt_recompute_bwd_noalloc(const float *c1, const float *tap0, const float *tap1,
+                                  const float *z, const float *carry, const float *grad_out,
+                                  float *grad_z, float *grad_c1, float *grad_tap0,
+                                  float *grad_tap1, int64_t F, int64_t B, int64_t T,
+                                  rqf_stream_t stream);
 
 /* ------------------------------------------------------------------------ *
  * Selective fused scan (FBT layout).                                        *

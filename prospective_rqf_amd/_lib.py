@@ -84,6 +84,8 @@ SIGNATURES = {
         ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "rqf_fbt_recompute_bwd": (
         ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
+    "rqf_fbt_recompute_bwd_noalloc": (
+        ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "rqf_selective_fwd": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P]),
     "rqf_selective_skip_fwd": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P, _P]),
     "rqf_selective_bwd_workspace": (_SZ, [_P, _I64]),
@@ -96,6 +98,13 @@ SIGNATURES = {
 
 class RQFError(RuntimeError):
     pass
+
+
+# Return code of a no-allocation entry point whose static scratch is too
+# small for the problem (RQF_ERR_SCRATCH), and that scratch's size
+# (RQF_NOALLOC_SCRATCH_BYTES), as include/rqf_scan.h defines them.
+ERR_SCRATCH = -4
+NOALLOC_SCRATCH_BYTES = 4 << 20
 
 
 def lib_path() -> str:

@@ -25,7 +25,16 @@
 #include "rqf_device.h"
 #include "rqf_scan.h"
 
+#include <atomic>
+#include <mutex>
+
 using namespace rqf;
+
+// Scratch of rqf_fbt_recompute_bwd_noalloc: the per-row fp64 partial sums of
+// the coefficient gradients (6 doubles per (channel, batch) row), in a static
+// device array instead of a caller workspace.  Every GPU the library runs on
+// holds its own copy until the process ends.
+static __device__ __align__(256) unsigned char scratch[RQF_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -1054,6 +1063,38 @@ int fbt_bwd(const float* c1, const float* t0, const float* t1, const float* z, c
   return launch_status();
 }
 
+// Device address of `scratch` on the device that runs `stream`.  The host
+// name of the array is only a stand-in for it, so the address is looked up
+// once per device with hipGetSymbolAddress (that device current) and kept.
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+int scratch_address(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return RQF_ERR_ARG;
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!ptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!ptr) {
+      int cur = -1;
+      if ((e = hipGetDevice(&cur)) != hipSuccess) return (int)e;
+      if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return (int)e;
+      e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      const hipError_t back = cur != dev ? hipSetDevice(cur) : hipSuccess;
+      if (e != hipSuccess) return (int)e;
+      if (back != hipSuccess) return (int)back;
+      if (!ptr) return RQF_ERR_SCRATCH;
+      g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return RQF_OK;
+}
+
 }  // namespace
 
 // ------------------------------- C ABI ------------------------------------
@@ -1144,6 +1185,30 @@ extern "C" int rqf_fbt_recompute_bwd(const float* c1, const float* tap0, const f
                  grad_tap1, F, B, T, ws, ws_bytes, (hipStream_t)stream);
 }
 
+extern "C" int rqf_fbt_recompute_bwd_noalloc(const float* c1, const float* tap0,
+                                             const float* tap1, const float* z,
+                                             const float* carry, const float* grad_out,
+                                             float* grad_z, float* grad_c1, float* grad_tap0,
+                                             float* grad_tap1, int64_t F, int64_t B, int64_t T,
+                                             rqf_stream_t stream) {
+  if (F < 0 || B < 0 || T < 0) return RQF_ERR_ARG;
+  // Size check first, before any pointer is looked at or any HIP call made.
+  constexpr int64_t kMaxRows = (int64_t)(RQF_NOALLOC_SCRATCH_BYTES / (6 * sizeof(double)));
+  if (B > 0 && F > kMaxRows / B) return RQF_ERR_SCRATCH;
+  if (F == 0) return RQF_OK;
+  if (!carry && F * B * T > 0) return RQF_ERR_ARG;
+  const size_t need = fbt_ws(F, B);
+  void* ws = nullptr;
+  if (need) {
+    const int st = scratch_address((hipStream_t)stream, &ws);
+    if (st) return st;
+  }
+  // Every row's partial slot is written before the ordered reduction reads
+  // it (same stream), so nothing is cleared.
+  return fbt_bwd(c1, tap0, tap1, z, nullptr, carry, grad_out, 1, grad_z, grad_c1, grad_tap0,
+                 grad_tap1, F, B, T, ws, RQF_NOALLOC_SCRATCH_BYTES, (hipStream_t)stream);
+}
+
 extern "C" const char* rqf_version(void) { return "rqf_hip 0.1.0 (gfx950)"; }
 
 extern "C" const char* rqf_error_string(int code) {
@@ -1156,6 +1221,8 @@ extern "C" const char* rqf_error_string(int code) {
       return "workspace missing or too small";
     case RQF_ERR_ALIGN:
       return "tensor not 8-byte aligned";
+    case RQF_ERR_SCRATCH:
+      return "problem larger than the static scratch of a no-allocation entry point";
     default:
       return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
   }

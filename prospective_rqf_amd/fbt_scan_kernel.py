@@ -152,6 +152,45 @@ def fbt_recompute_backward_raw(C1, tap0, tap1, x, carry, grad_output):
     return gc1, gt0, gt1, grad_z
 
 
+def fbt_recompute_backward_noalloc(C1, tap0, tap1, x, carry, grad_output, grad_z, grad_C1,
+                                   grad_tap0, grad_tap1):
+    """:func:`fbt_recompute_backward_raw` into caller-owned outputs, allocating
+    nothing: ``rqf_fbt_recompute_bwd_noalloc`` keeps its partial sums in the
+    library's static per-GPU scratch (at most ``F*B = 87381`` rows), so the
+    call is usable where device allocation is not (graph capture, serving
+    loops).  Every tensor must already be complex64, contiguous and on the
+    device, with ``grad_z`` shaped like ``x`` and the three coefficient
+    gradients shaped ``(F,)``; nothing is converted.  Calls that overlap on
+    one GPU share the scratch and must be serialised by the caller."""
+    tensors = dict(C1=C1, tap0=tap0, tap1=tap1, x=x, carry=carry, grad_output=grad_output,
+                   grad_z=grad_z, grad_C1=grad_C1, grad_tap0=grad_tap0, grad_tap1=grad_tap1)
+    for name, t in tensors.items():
+        if t.dtype != torch.complex64 or not t.is_contiguous() or t.is_conj():
+            raise ValueError(f"{name} must be a contiguous complex64 tensor without a "
+                             "pending conjugation (nothing is converted here)")
+    _lib.require_device(*tensors.values())
+    if x.dim() != 3:
+        raise ValueError(f"expected (filters, batch, time) input, got shape {tuple(x.shape)}")
+    filters, batch, time = x.shape
+    for name in ("C1", "tap0", "tap1", "grad_C1", "grad_tap0", "grad_tap1"):
+        if tensors[name].shape != (filters,):
+            raise ValueError(f"{name} must have shape ({filters},)")
+    for name in ("grad_output", "grad_z"):
+        if tensors[name].shape != x.shape:
+            raise ValueError(f"{name} must have the input's shape {tuple(x.shape)}")
+    lib = _lib.load()
+    if tuple(carry.shape) != (filters * batch, max(lib.rqf_fbt_carry_chunks(time), 1)):
+        raise ValueError("carry must be the forward's (F*B, rqf_fbt_carry_chunks(T)) entry states")
+    _lib.check(
+        lib.rqf_fbt_recompute_bwd_noalloc(
+            _lib.ptr(C1), _lib.ptr(tap0), _lib.ptr(tap1), _lib.ptr(x), _lib.ptr(carry),
+            _lib.ptr(grad_output), _lib.ptr(grad_z), _lib.ptr(grad_C1), _lib.ptr(grad_tap0),
+            _lib.ptr(grad_tap1), filters, batch, time, _lib.stream_of(x)),
+        "rqf_fbt_recompute_bwd_noalloc",
+    )
+    return grad_C1, grad_tap0, grad_tap1, grad_z
+
+
 class _FBTRecompute(torch.autograd.Function):
     """Split-ReLU prospective scan that replays the raw state in the backward."""
 

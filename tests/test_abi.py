@@ -52,6 +52,7 @@ def test_library_loads_and_reports_version(built_lib):
     lib = _lib.load()
     assert b"gfx950" in lib.rqf_version()
     assert lib.rqf_error_string(-2) == b"workspace missing or too small"
+    assert b"no-allocation" in lib.rqf_error_string(_lib.ERR_SCRATCH)
     # Pure host-side queries (no device access).
     assert lib.rqf_fbt_carry_chunks(16000) == 63  # one entry state per 256-step tile
     assert lib.rqf_fbt_workspace(128, 32, 16000) >= 6 * 8 * 128 * 32
@@ -107,3 +108,25 @@ def test_product_refuses_cpu_tensors():
     c = torch.zeros(2, dtype=torch.complex64)
     with pytest.raises(_lib.RQFError):
         fbt_prospective_scan(c, c, c, z)
+
+
+def test_header_constants_match_the_binding():
+    text = open(HEADER).read()
+    assert re.search(r"RQF_ERR_SCRATCH = (-\d+)", text).group(1) == str(_lib.ERR_SCRATCH)
+    m = re.search(r"#define RQF_NOALLOC_SCRATCH_BYTES \(\(size_t\)(\d+) << (\d+)\)", text)
+    assert int(m.group(1)) << int(m.group(2)) == _lib.NOALLOC_SCRATCH_BYTES
+
+
+def test_noalloc_rejects_oversized_problems_before_any_device_call(built_lib):
+    """Beyond the static scratch (6 fp64 partials per row) the entry point
+    returns RQF_ERR_SCRATCH before looking at a pointer or calling HIP (here
+    every pointer is NULL and there is no device)."""
+    lib = _lib.load()
+    rows = _lib.NOALLOC_SCRATCH_BYTES // 48
+    args = [None] * 10
+    assert lib.rqf_fbt_recompute_bwd_noalloc(*args, rows + 1, 1, 16, None) == _lib.ERR_SCRATCH
+    assert lib.rqf_fbt_recompute_bwd_noalloc(*args, 1024, rows // 1024 + 1, 16,
+                                             None) == _lib.ERR_SCRATCH
+    assert lib.rqf_fbt_recompute_bwd_noalloc(*args, 2 ** 40, 2 ** 40, 16,
+                                             None) == _lib.ERR_SCRATCH
+    assert lib.rqf_fbt_recompute_bwd_noalloc(*args, -1, 1, 16, None) == -1

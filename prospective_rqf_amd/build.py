@@ -18,7 +18,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_NAME = "librqf_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["selective.hip", "timeinv.hip", "multiosc.hip", "proj.hip"]
+SOURCES = ["selective.hip", "timeinv.hip", "btf.hip", "multiosc.hip", "proj.hip"]
 ARCH = os.environ.get("RQF_OFFLOAD_ARCH", "gfx950")
 
 

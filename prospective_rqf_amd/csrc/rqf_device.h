@@ -395,6 +395,107 @@ __device__ __forceinline__ void stream_steps(int64_t tb, int64_t te, Load&& load
     if (j < rem) step(j, FWD ? t + j : t - j);
 }
 
+// ---------------------------------------------------------------------------
+// Segment scans of the single-pass (batch, time, filters) kernels.  A block
+// pass splits time into consecutive segments of LS steps; a wavefront holds
+// G = 64 / FC of them, FC lanes (filters) each, lane l in segment l / FC.
+// Each lane knows its segment's result from a zero entry; these helpers
+// combine the results of the wavefront's segments in fp64 (Hillis-Steele over
+// the G segments, by cross-lane moves of FC lanes), for time-invariant maps
+// whose multiplier over one segment, m = a^LS (or conj(a)^LS), is the same
+// for every segment of a lane's filter.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ c64d shfl_up_d(c64d v, int d) {
+  return mkd(__shfl_up(v.r, d), __shfl_up(v.i, d));
+}
+__device__ __forceinline__ c64d shfl_down_d(c64d v, int d) {
+  return mkd(__shfl_down(v.r, d), __shfl_down(v.i, d));
+}
+
+// Forward maps y -> m y + s.  Returns the exclusive prefix over the
+// wavefront's segments before this lane's, E_q = sum_{j<q} m^(q-1-j) s_j
+// (zero for q = 0), and sets `incl` to the inclusive one.
+template <int FC>
+__device__ __forceinline__ c64d wave_seg_prefix(c64d s, c64d m, int lane, c64d& incl) {
+  constexpr int G = kWave / FC;
+  incl = s;
+  c64d pw = m;  // m^k
+#pragma unroll
+  for (int k = 1; k < G; k <<= 1) {
+    const c64d prev = shfl_up_d(incl, k * FC);
+    if (lane >= k * FC) incl = dmad(pw, prev, incl);
+    pw = dmul(pw, pw);
+  }
+  const c64d ex = shfl_up_d(incl, FC);
+  return lane >= FC ? ex : mkd(0.0, 0.0);
+}
+
+// Adjoint pair maps over a span of n segments (nL = n*LS steps), applied to the
+// pair (g, h) entering at the span's end:
+//   (g, h) -> (P_n g + G, P_n h + c_n g + H),
+//   P_n = conj(a)^nL,  c_n = nL conj(a)^(nL-1),
+// with (G, H) the span's own pair from a zero entry.  Composing the span of a
+// segment with the span of n segments after it: G' = P_n G_after ... see
+// wave_seg_suffix.
+struct PairMap {
+  c64d P, c;  // P_n, c_n
+};
+__device__ __forceinline__ PairMap pair_map_mul(PairMap x, PairMap y) {
+  // span of x followed (in reverse time: preceded) by span of y
+  PairMap r;
+  r.P = dmul(x.P, y.P);
+  r.c = dmad(x.P, y.c, dmul(x.c, y.P));
+  return r;
+}
+// (g, h) entering at the end of a span with map `mp` and own pair (G, H):
+// the pair at the span's start.
+__device__ __forceinline__ void pair_apply(const PairMap& mp, c64d G, c64d H, c64d& g, c64d& h) {
+  const c64d ng = dmad(mp.P, g, G);
+  h = dmad(mp.P, h, dmad(mp.c, g, H));
+  g = ng;
+}
+
+// Suffix over the wavefront's segments of the adjoint pair maps: returns in
+// (eg, eh) the pair that the segments after this lane's produce from a zero
+// pair at the wavefront's end, and in (ig, ih) the same including this lane's
+// segment.  `one` is the map of one segment.  `span_after` returns the map of
+// the segments after this lane's (q + 1 .. G - 1).
+template <int FC>
+__device__ __forceinline__ void wave_seg_suffix(c64d G0, c64d H0, PairMap one, int lane, c64d& eg,
+                                                c64d& eh, c64d& ig, c64d& ih, PairMap& span_after) {
+  constexpr int G = kWave / FC;
+  const int q = lane / FC;
+  ig = G0;
+  ih = H0;
+  PairMap pw = one;  // map of k segments
+#pragma unroll
+  for (int k = 1; k < G; k <<= 1) {
+    // the composed pair of segments q+k .. (from lanes k*FC above)
+    const c64d ng = shfl_down_d(ig, k * FC), nh = shfl_down_d(ih, k * FC);
+    if (q + k < G) {
+      // this lane's span (k segments) applied after the span that follows it
+      c64d g = ng, h = nh;
+      pair_apply(pw, ig, ih, g, h);
+      ig = g;
+      ih = h;
+    }
+    pw = pair_map_mul(pw, pw);
+  }
+  eg = shfl_down_d(ig, FC);
+  eh = shfl_down_d(ih, FC);
+  if (q + 1 >= G) eg = eh = mkd(0.0, 0.0);
+  // map of G - 1 - q segments, by binary powering of `one`
+  PairMap acc;
+  acc.P = mkd(1.0, 0.0);
+  acc.c = mkd(0.0, 0.0);
+  PairMap base = one;
+  for (int n = G - 1 - q; n > 0; n >>= 1) {
+    if (n & 1) acc = pair_map_mul(acc, base);
+    base = pair_map_mul(base, base);
+  }
+  span_after = acc;
+}
+
 // Sum of a double over the wave (result valid in every lane).
 __device__ __forceinline__ double wave_sum(double v) {
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);

@@ -13,12 +13,8 @@
 // keeps raw[t-1] and g[t+1] in registers, so it needs none of the
 // reference's divisions by c1 (fbt_scan_kernel.py:157-160, 518-521).
 //
-// BTF (the reference's (batch, time, filters) API): lanes map to
-// (batch, time segment, channel) tasks with the channel fastest, so a
-// wavefront reads 64 consecutive complex values per step.  Each task scans
-// its segment serially; segments are stitched by a second pass that folds the
-// end states of the earlier segments with c1^L (three-phase scan; no permute
-// copies, unlike chunked_scan_kernel.py:212-249).
+// The same scans in the reference's (batch, time, filters) layout are in
+// btf.hip.
 //
 // Coefficient gradients are reduced deterministically: per-task partial sums
 // in fp64, then an ordered reduction per channel.
@@ -652,7 +648,7 @@ __global__ __launch_bounds__(kTiWaves* kWave) void fbt_bwd_kernel(
 // grad[f] = sum over m of partial[6*(f*stride_f + m*stride_m) + j] in fp64:
 // one wavefront per channel, lane l sums m = l, l+64, ... in order, then a
 // fixed-shape wave reduction (deterministic).  FBT layout: stride_f = M,
-// stride_m = 1; BTF tasks ((b*S + s)*F + f): stride_f = 1, stride_m = F.
+// stride_m = 1.
 __global__ __launch_bounds__(kWave) void coef_reduce_kernel(const double* __restrict__ partial,
                                                             int64_t F, int64_t M, int64_t stride_f,
                                                             int64_t stride_m,
@@ -681,206 +677,6 @@ __global__ __launch_bounds__(kWave) void coef_reduce_kernel(const double* __rest
   }
 }
 
-// ---------------------------------------------------------------------------
-// BTF three-phase scans.  task = (b*S + seg)*F + f; segment seg covers
-// [seg*L, min(T, seg*L + L)).
-// ---------------------------------------------------------------------------
-struct BtfShape {
-  int64_t B, T, F, S, L;
-};
-
-// Steps per streamed chunk of the BTF passes (stream_steps).  Config 2's
-// workload in (B,T,F) layout: forward 0.322 ms with 8 and 0.312 with 16;
-// backward (one wavefront per SIMD, more state per step) 0.441 with 8 and
-// 0.445 with 16.
-#ifndef RQF_BTF_STREAM_FWD
-#define RQF_BTF_STREAM_FWD 16
-#endif
-#ifndef RQF_BTF_STREAM_BWD
-#define RQF_BTF_STREAM_BWD 8
-#endif
-constexpr int kBtfStreamFwd = RQF_BTF_STREAM_FWD;
-constexpr int kBtfStreamBwd = RQF_BTF_STREAM_BWD;
-// Target task counts (segments x batch x filters).  Each final pass folds all
-// earlier segments' carries per task, so more segments cost the backward,
-// whose final pass holds more state, more than they gain: config 2's workload
-// in (B,T,F) layout measured forward 0.356 ms at 64K tasks and 0.326 at 256K,
-// backward 0.543 at 64K and 0.576 at 256K.
-#ifndef RQF_BTF_LANES_FWD
-#define RQF_BTF_LANES_FWD 262144
-#endif
-#ifndef RQF_BTF_LANES_BWD
-#define RQF_BTF_LANES_BWD 65536
-#endif
-constexpr int64_t kBtfLanesFwd = RQF_BTF_LANES_FWD;
-constexpr int64_t kBtfLanesBwd = RQF_BTF_LANES_BWD;
-
-
-// Phase 1 of the forward: segment end states from a zero entry.
-__global__ __launch_bounds__(256) void btf_fwd_local_kernel(
-    const float* __restrict__ c1, const float* __restrict__ k0p, const float* __restrict__ k1p,
-    const float* __restrict__ x, float* __restrict__ seg_end, BtfShape sh) {
-  const int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (task >= sh.B * sh.S * sh.F) return;
-  const int64_t f = task % sh.F, bs = task / sh.F, seg = bs % sh.S, b = bs / sh.S;
-  const c32 a = ldc(c1, f), k0 = ldc(k0p, f), k1 = k1p ? ldc(k1p, f) : mk(0.0f, 0.0f);
-  const int64_t t_beg = seg * sh.L, t_end = min(sh.T, t_beg + sh.L);
-  const float* xb = x + 2 * (b * sh.T * sh.F + f);
-  c32 xprev = (k1p && t_beg > 0) ? ldc(xb, (t_beg - 1) * sh.F) : mk(0.0f, 0.0f);
-  c32 y = mk(0.0f, 0.0f);
-  c32 xbuf[kBtfStreamFwd];
-  stream_steps<kBtfStreamFwd, true>(
-      t_beg, t_end, [&](int j, int64_t t) { xbuf[j] = ldc(xb, t * sh.F); },
-      [&](int j, int64_t) {
-        y = cmad(a, y, cmad(k1, xprev, cmul(k0, xbuf[j])));
-        xprev = xbuf[j];
-      });
-  stc(seg_end, task, y);
-}
-
-// Phase 2 of the forward: fold earlier segments' end states into the entry
-// state, then rescan the segment writing the output.
-__global__ __launch_bounds__(256) void btf_fwd_final_kernel(
-    const float* __restrict__ c1, const float* __restrict__ k0p, const float* __restrict__ k1p,
-    const float* __restrict__ x, const float* __restrict__ seg_end, float* __restrict__ out,
-    BtfShape sh) {
-  const int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (task >= sh.B * sh.S * sh.F) return;
-  const int64_t f = task % sh.F, bs = task / sh.F, seg = bs % sh.S, b = bs / sh.S;
-  const c32 a = ldc(c1, f), k0 = ldc(k0p, f), k1 = k1p ? ldc(k1p, f) : mk(0.0f, 0.0f);
-  c32 y = mk(0.0f, 0.0f);
-  if (seg > 0) {  // entry state: the earlier segments' end states, folded in fp64
-    const c64d aL = dpow(widen(a), sh.L);
-    c64d e = mkd(0.0, 0.0);
-    c32 vbuf[kBtfStreamFwd];
-    stream_steps<kBtfStreamFwd, true>(
-        0, seg, [&](int j, int64_t s) { vbuf[j] = ldc(seg_end, (b * sh.S + s) * sh.F + f); },
-        [&](int j, int64_t) { e = dmad(aL, e, widen(vbuf[j])); });
-    y = narrow(e);
-  }
-  const int64_t t_beg = seg * sh.L, t_end = min(sh.T, t_beg + sh.L);
-  const float* xb = x + 2 * (b * sh.T * sh.F + f);
-  float* ob = out + 2 * (b * sh.T * sh.F + f);
-  c32 xprev = (k1p && t_beg > 0) ? ldc(xb, (t_beg - 1) * sh.F) : mk(0.0f, 0.0f);
-  c32 xbuf[kBtfStreamFwd];
-  stream_steps<kBtfStreamFwd, true>(
-      t_beg, t_end, [&](int j, int64_t t) { xbuf[j] = ldc(xb, t * sh.F); },
-      [&](int j, int64_t t) {
-        y = cmad(a, y, cmad(k1, xprev, cmul(k0, xbuf[j])));
-        xprev = xbuf[j];
-        stc(ob, t * sh.F, y);
-      });
-}
-
-// Phase 1 of the backward: the adjoint pair (g, h) at each segment's first
-// step from a zero pair after the segment (see btf_bwd_final_kernel).
-__global__ __launch_bounds__(256) void btf_bwd_local_kernel(const float* __restrict__ c1,
-                                                            const float* __restrict__ gout,
-                                                            float* __restrict__ seg_beg,
-                                                            float* __restrict__ seg_h,
-                                                            BtfShape sh) {
-  const int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (task >= sh.B * sh.S * sh.F) return;
-  const int64_t f = task % sh.F, bs = task / sh.F, seg = bs % sh.S, b = bs / sh.S;
-  const c32 ac = conjg(ldc(c1, f));
-  const int64_t t_beg = seg * sh.L, t_end = min(sh.T, t_beg + sh.L);
-  const float* gb = gout + 2 * (b * sh.T * sh.F + f);
-  c32 g = mk(0.0f, 0.0f), h = mk(0.0f, 0.0f);
-  c32 gbuf[kBtfStreamBwd];
-  stream_steps<kBtfStreamBwd, false>(
-      t_beg, t_end, [&](int j, int64_t t) { gbuf[j] = ldc(gb, t * sh.F); },
-      [&](int j, int64_t) {
-        h = cmad(ac, h, g);
-        g = cmad(ac, g, gbuf[j]);
-      });
-  stc(seg_beg, task, g);
-  stc(seg_h, task, h);
-}
-
-// Phase 2 of the backward: carry from the later segments, reverse serial
-// pass, grad_x and per-task coefficient partial sums.  For t descending:
-//   g[t] = conj(C1) g[t+1] + gy[t]              (the adjoint of the drive)
-//   h[t] = conj(C1) h[t+1] + g[t+1]
-//   grad_x[t] = conj(tap0) g[t] + conj(tap1) g[t+1]
-//   sums: conj(d[t]) h[t] (grad_C1), conj(x[t]) g[t] (tap0), conj(x[t-1]) g[t] (tap1)
-// with the drive d[t] = tap0 x[t] + tap1 x[t-1].  The reference's grad_C1 is
-// sum_t g[t] conj(y[t-1]) over the saved states y; exchanging the order of
-// summation (y[t-1] = sum_{r<t} C1^(t-1-r) d[r]) gives sum_r conj(d[r]) h[r],
-// since h[r] = sum_{t>r} conj(C1)^(t-1-r) g[t].  So the pass reads gy and x
-// only, not the saved states.  len steps of zero input take (g, h) to
-// (P g, P h + len P' g), P = conj(C1)^len, P' = conj(C1)^(len-1); only full
-// segments carry (the last one starts from zero).
-__global__ __launch_bounds__(256) void btf_bwd_final_kernel(
-    const float* __restrict__ c1, const float* __restrict__ k0p, const float* __restrict__ k1p,
-    const float* __restrict__ x, const float* __restrict__ gout,
-    const float* __restrict__ seg_beg, const float* __restrict__ seg_h, float* __restrict__ gx,
-    double* __restrict__ partial, BtfShape sh) {
-  const int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (task >= sh.B * sh.S * sh.F) return;
-  const int64_t f = task % sh.F, bs = task / sh.F, seg = bs % sh.S, b = bs / sh.S;
-  const c32 a = ldc(c1, f), k0 = ldc(k0p, f), k1 = k1p ? ldc(k1p, f) : mk(0.0f, 0.0f);
-  const c32 ac = conjg(a);
-  c32 gnext = mk(0.0f, 0.0f), hnext = mk(0.0f, 0.0f);
-  if (seg + 1 < sh.S) {  // the pair entering from the later segments, folded in fp64
-    const c64d p1 = sh.L > 1 ? dconj(dpow(widen(a), sh.L - 1)) : mkd(1.0, 0.0);
-    const c64d pL = dmul(p1, widen(ac));
-    const c64d q = mkd(p1.r * (double)sh.L, p1.i * (double)sh.L);
-    c64d e = mkd(0.0, 0.0), eh = mkd(0.0, 0.0);
-    c32 vg[kBtfStreamBwd], vh[kBtfStreamBwd];
-    stream_steps<kBtfStreamBwd, false>(
-        seg + 1, sh.S,
-        [&](int j, int64_t s) {
-          const int64_t i = (b * sh.S + s) * sh.F + f;
-          vg[j] = ldc(seg_beg, i);
-          vh[j] = ldc(seg_h, i);
-        },
-        [&](int j, int64_t) {
-          eh = dmad(pL, eh, dmad(q, e, widen(vh[j])));
-          e = dmad(pL, e, widen(vg[j]));
-        });
-    gnext = narrow(e);
-    hnext = narrow(eh);
-  }
-  const int64_t t_beg = seg * sh.L, t_end = min(sh.T, t_beg + sh.L);
-  const int64_t base = b * sh.T * sh.F + f;
-  const float* xb = x + 2 * base;
-  const float* gb = gout + 2 * base;
-  float* gxb = gx + 2 * base;
-  double s1r = 0, s1i = 0, s0r = 0, s0i = 0, s2r = 0, s2i = 0;
-  // x[t] of each step is the x[t-1] the step after it (in time) loaded.
-  c32 xt = ldc(xb, (t_end - 1) * sh.F);
-  c32 gbuf[kBtfStreamBwd], xpbuf[kBtfStreamBwd];
-  stream_steps<kBtfStreamBwd, false>(
-      t_beg, t_end,
-      [&](int j, int64_t t) {
-        gbuf[j] = ldc(gb, t * sh.F);
-        xpbuf[j] = t > 0 ? ldc(xb, (t - 1) * sh.F) : mk(0.0f, 0.0f);
-      },
-      [&](int j, int64_t t) {
-        const c32 h = cmad(ac, hnext, gnext);
-        const c32 g = cmad(ac, gnext, gbuf[j]);
-        stc(gxb, t * sh.F, cjmad(k1, gnext, cjmul(k0, g)));
-        const c32 d = cmad(k1, xpbuf[j], cmul(k0, xt));
-        const c32 t1 = cjmul(d, h), t0c = cjmul(xt, g), t2 = cjmul(xpbuf[j], g);
-        s1r += t1.r;
-        s1i += t1.i;
-        s0r += t0c.r;
-        s0i += t0c.i;
-        s2r += t2.r;
-        s2i += t2.i;
-        gnext = g;
-        hnext = h;
-        xt = xpbuf[j];
-      });
-  double* o = partial + 6 * task;
-  o[0] = s1r;
-  o[1] = s1i;
-  o[2] = s0r;
-  o[3] = s0i;
-  o[4] = s2r;
-  o[5] = s2i;
-}
-
 inline bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15) == 0; }
 inline bool aligned8(const void* p) { return p == nullptr || ((uintptr_t)p & 7) == 0; }
 inline size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -888,82 +684,6 @@ inline size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
 int launch_status() {
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? RQF_OK : (int)err;
-}
-
-BtfShape btf_shape(int64_t B, int64_t T, int64_t F, int64_t target) {
-  BtfShape sh;
-  sh.B = B;
-  sh.T = T;
-  sh.F = F;
-  // Enough segments for about `target` tasks, but at least 16 steps per
-  // segment.
-  const int64_t lanes = B * F > 0 ? B * F : 1;
-  int64_t S = (target + lanes - 1) / lanes;
-  const int64_t smax = T / 16 > 1 ? T / 16 : 1;
-  if (S > smax) S = smax;
-  if (S < 1) S = 1;
-  sh.L = T > 0 ? (T + S - 1) / S : 1;
-  sh.S = T > 0 ? (T + sh.L - 1) / sh.L : 1;
-  return sh;
-}
-
-// One workspace serves both directions: the forward's segment end states, or
-// the backward's segment start adjoints and per-task partial sums.
-size_t btf_ws(int64_t B, int64_t T, int64_t F) {
-  const BtfShape fw = btf_shape(B, T, F, kBtfLanesFwd), bw = btf_shape(B, T, F, kBtfLanesBwd);
-  const size_t tf = (size_t)(B * fw.S * F), tb = (size_t)(B * bw.S * F);
-  return std::max(round256(sizeof(float) * 2 * tf),
-                  2 * round256(sizeof(float) * 2 * tb) + round256(sizeof(double) * 6 * tb));
-}
-
-int btf_fwd(const float* c1, const float* k0, const float* k1, const float* x, float* out,
-            int64_t B, int64_t T, int64_t F, void* ws, size_t ws_bytes, hipStream_t s) {
-  if (B < 0 || T < 0 || F < 0) return RQF_ERR_ARG;
-  if (B * T * F == 0) return RQF_OK;
-  if (!c1 || !k0 || !x || !out) return RQF_ERR_ARG;
-  if (!aligned8(x) || !aligned8(out)) return RQF_ERR_ALIGN;
-  const size_t need = btf_ws(B, T, F);
-  if (!ws || ws_bytes < need) return RQF_ERR_WORKSPACE;
-  const BtfShape sh = btf_shape(B, T, F, kBtfLanesFwd);
-  const int64_t tasks = B * sh.S * F;
-  const dim3 grid((unsigned)((tasks + 255) / 256)), block(256);
-  float* seg = (float*)ws;
-  if (sh.S > 1) hipLaunchKernelGGL(btf_fwd_local_kernel, grid, block, 0, s, c1, k0, k1, x, seg, sh);
-  hipLaunchKernelGGL(btf_fwd_final_kernel, grid, block, 0, s, c1, k0, k1, x, seg, out, sh);
-  return launch_status();
-}
-
-int btf_bwd(const float* c1, const float* k0, const float* k1, const float* x,
-            const float* states, const float* gout, float* gx, float* gc1, float* gk0,
-            float* gk1, int64_t B, int64_t T, int64_t F, void* ws, size_t ws_bytes,
-            hipStream_t s) {
-  if (B < 0 || T < 0 || F < 0) return RQF_ERR_ARG;
-  if (F == 0) return RQF_OK;
-  if (!c1 || !k0 || !gc1 || !gk0 || (k1 && !gk1)) return RQF_ERR_ARG;
-  (void)states;  // grad_C1 comes from x (see btf_bwd_final_kernel)
-  if (B * T > 0 && (!x || !gout || !gx)) return RQF_ERR_ARG;
-  if (!aligned8(x) || !aligned8(states) || !aligned8(gout) || !aligned8(gx)) return RQF_ERR_ALIGN;
-  const size_t need = btf_ws(B, T, F);
-  if (need && (!ws || ws_bytes < need)) return RQF_ERR_WORKSPACE;
-  const BtfShape sh = btf_shape(B, T, F, kBtfLanesBwd);
-  const int64_t tasks = B * sh.S * F;
-  const size_t seg_bytes = round256(sizeof(float) * 2 * (size_t)tasks);
-  float* seg = (float*)ws;
-  float* seg_h = (float*)((char*)ws + seg_bytes);
-  double* partial = (double*)((char*)ws + 2 * seg_bytes);
-  if (tasks > 0 && T > 0) {
-    const dim3 grid((unsigned)((tasks + 255) / 256)), block(256);
-    if (sh.S > 1)
-      hipLaunchKernelGGL(btf_bwd_local_kernel, grid, block, 0, s, c1, gout, seg, seg_h, sh);
-    hipLaunchKernelGGL(btf_bwd_final_kernel, grid, block, 0, s, c1, k0, k1, x, gout, seg, seg_h,
-                       gx, partial, sh);
-    hipLaunchKernelGGL(coef_reduce_kernel, dim3((unsigned)F), dim3(kWave), 0, s,
-                       partial, F, B * sh.S, (int64_t)1, F, gc1, gk0, gk1);
-  } else {
-    hipLaunchKernelGGL(coef_reduce_kernel, dim3((unsigned)F), dim3(kWave), 0, s,
-                       partial, F, (int64_t)0, (int64_t)1, F, gc1, gk0, gk1);
-  }
-  return launch_status();
 }
 
 int fbt_fwd(const float* c1, const float* t0, const float* t1, const float* z, const float* skip,
@@ -1098,43 +818,6 @@ int scratch_address(hipStream_t stream, void** out) {
 }  // namespace
 
 // ------------------------------- C ABI ------------------------------------
-
-extern "C" size_t rqf_btf_scan_workspace(int64_t B, int64_t T, int64_t F) {
-  return btf_ws(B, T, F);
-}
-
-extern "C" int rqf_chunked_scan_fwd(const float* c1, const float* c2, const float* u, float* out,
-                                    int64_t B, int64_t T, int64_t F, void* ws, size_t ws_bytes,
-                                    rqf_stream_t stream) {
-  return btf_fwd(c1, c2, nullptr, u, out, B, T, F, ws, ws_bytes, (hipStream_t)stream);
-}
-
-extern "C" int rqf_chunked_scan_bwd(const float* c1, const float* c2, const float* u,
-                                    const float* states, const float* grad_out, float* grad_u,
-                                    float* grad_c1, float* grad_c2, int64_t B, int64_t T,
-                                    int64_t F, void* ws, size_t ws_bytes, rqf_stream_t stream) {
-  return btf_bwd(c1, c2, nullptr, u, states, grad_out, grad_u, grad_c1, grad_c2, nullptr, B, T, F,
-                 ws, ws_bytes, (hipStream_t)stream);
-}
-
-extern "C" int rqf_chunked_prospective_fwd(const float* c1, const float* tap0, const float* tap1,
-                                           const float* x, float* out, int64_t B, int64_t T,
-                                           int64_t F, void* ws, size_t ws_bytes,
-                                           rqf_stream_t stream) {
-  if (!tap1) return RQF_ERR_ARG;
-  return btf_fwd(c1, tap0, tap1, x, out, B, T, F, ws, ws_bytes, (hipStream_t)stream);
-}
-
-extern "C" int rqf_chunked_prospective_bwd(const float* c1, const float* tap0, const float* tap1,
-                                           const float* x, const float* states,
-                                           const float* grad_out, float* grad_x, float* grad_c1,
-                                           float* grad_tap0, float* grad_tap1, int64_t B,
-                                           int64_t T, int64_t F, void* ws, size_t ws_bytes,
-                                           rqf_stream_t stream) {
-  if (!tap1 || !grad_tap1) return RQF_ERR_ARG;
-  return btf_bwd(c1, tap0, tap1, x, states, grad_out, grad_x, grad_c1, grad_tap0, grad_tap1, B, T,
-                 F, ws, ws_bytes, (hipStream_t)stream);
-}
 
 extern "C" int64_t rqf_fbt_carry_chunks(int64_t T) { return T > 0 ? (T + kTiTile - 1) / kTiTile : 0; }
 

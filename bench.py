@@ -494,8 +494,9 @@ def plan_chunked_raw(cfg, args, dev):
     # The backward's contract reads x and gy and writes grad_x; the saved output
     # it is handed is not needed (grad_C1 comes from x, csrc/timeinv.hip).
     nbytes = {"rqf_chunked_prospective_fwd": 16 * N, "rqf_chunked_prospective_bwd": 24 * N}
-    kernels = {"rqf_chunked_prospective_fwd": "btf_fwd_local + btf_fwd_final",
-               "rqf_chunked_prospective_bwd": "btf_bwd_local + btf_bwd_final + coef_reduce_kernel"}
+    kernels = {"rqf_chunked_prospective_fwd": "btf_fwd_kernel<prospective> (single pass)",
+               "rqf_chunked_prospective_bwd": ("btf_bwd_kernel<prospective> (single pass) + "
+                                               "btf_coef_reduce_kernel")}
     config = {"workload": name, "F": F, "B": B, "T": T, "layers": 1,
               "contract": "(B,T,F) two-tap scan; x in, y out; backward reads x and gy, "
                           "writes grad_x; full BPTT"}
@@ -549,8 +550,8 @@ def plan_chunked(cfg, args, dev):
     for li in range(L):
         nbytes[f"rqf_chunked_scan_fwd[L{li}]"] = 16 * N
         nbytes[f"rqf_chunked_scan_bwd[L{li}]"] = 24 * N
-    kernels = {"rqf_chunked_scan_fwd": "btf_fwd_local + btf_fwd_final",
-               "rqf_chunked_scan_bwd": "btf_bwd_local + btf_bwd_final + coef_reduce_kernel"}
+    kernels = {"rqf_chunked_scan_fwd": "btf_fwd_kernel (single pass)",
+               "rqf_chunked_scan_bwd": "btf_bwd_kernel (single pass) + btf_coef_reduce_kernel"}
     config = {"workload": name, "F": F, "B": B, "T": T, "layers": L,
               "contract": "(B,T,F) scan, full BPTT; latency-bound, cache-resident"}
 
@@ -604,9 +605,9 @@ def plan_multi_osc(cfg, args, dev):
         ops = [("rqf_multi_osc_fwd", fwd), ("rqf_multi_osc_bwd", bwd)]
         elems = B * T * F
         nbytes = {"rqf_multi_osc_fwd": 16 * elems, "rqf_multi_osc_bwd": 24 * elems}
-        kernels = {"rqf_multi_osc_fwd": "mosc_fwd_local + mosc_carry + mosc_fwd_final",
-                   "rqf_multi_osc_bwd": ("mosc_bwd_local + mosc_carry + mosc_bwd_final + "
-                                         "mosc_coef_stage1 + mosc_coef_stage2")}
+        kernels = {"rqf_multi_osc_fwd": "mosc_fwd_kernel<4 oscillators> (single pass)",
+                   "rqf_multi_osc_bwd": ("mosc_bwd_kernel<4 oscillators> (single pass) + "
+                                         "mosc_coef_kernel")}
         contract = "complex u in, complex y out; grad_u + grad_C1/C2/c_weights"
     else:
         name = ("fused |y| readout: single-oscillator scan on real input, 128 filters, "
@@ -619,7 +620,7 @@ def plan_multi_osc(cfg, args, dev):
         ops = [("rqf_multi_osc_fwd[abs]", fwd)]
         elems = B * T * F
         nbytes = {"rqf_multi_osc_fwd[abs]": 8 * elems}
-        kernels = {"rqf_multi_osc_fwd": "mosc_fwd_local + mosc_carry + mosc_fwd_final<abs>"}
+        kernels = {"rqf_multi_osc_fwd": "mosc_fwd_kernel<1 oscillator, real, abs> (single pass)"}
         contract = "real u in, |y| real out, no autograd"
     config = {"workload": name, "F": F, "B": B, "T": T, "oscillators": N, "layers": 1,
               "contract": contract}

@@ -100,7 +100,7 @@ int rqf_chunked_prospective_bwd(const float *c1, const float *tap0, const float 
 
 /* ------------------------------------------------------------------------ *
  * Multi-oscillator scans with C-weight reduction, and the |y| readout       *
- * (BTF layout).  N oscillators per filter f (1 <= N <= 8), index f*N + n:   *
+ * (BTF layout).  N >= 1 oscillators per filter f, index f*N + n:          *
  *   x_n[t] = C1_n*x_n[t-1] + C2_n*u[t]                                      *
  *   y[t]   = sum_n cw_n*x_n[t]          (cw NULL: y = x_0, requires N = 1)  *
  * c1, c2, cw: (F*N,) complex (cw is the reference's real (F*N, 2) view).    *
@@ -108,7 +108,7 @@ int rqf_chunked_prospective_bwd(const float *c1, const float *tap0, const float 
  * ------------------------------------------------------------------------ */
 
 /* Workspace bytes of rqf_multi_osc_fwd (backward = 0) or _bwd (backward = 1);
- * 0 for N outside [1, 8]. */
+ * 0 for N < 1.  The forward needs none unless N > 4 with out_abs. */
 size_t rqf_multi_osc_workspace(int64_t B, int64_t T, int64_t F, int64_t N, int32_t backward);
 
 /* Replaces `_sequential_scan_multi_osc_kernel[grid](...)` with EPILOGUE 0 / 1

@@ -68,6 +68,7 @@ __device__ __forceinline__ void stc(float* p, int64_t i, c32 v) {
 struct Lane {
   int fl, sg;     // filter lane and segment of the thread
   int64_t f;      // filter
+  int64_t b;      // batch element
   bool fv;        // f < F
   int64_t base;   // element (b, 0, f)
 };
@@ -77,10 +78,13 @@ __device__ __forceinline__ Lane lane_of(int64_t T, int64_t F) {
   l.fl = (int)threadIdx.x % kFC;
   l.sg = (int)threadIdx.x / kFC;
   const int64_t nfc = (F + kFC - 1) / kFC;
-  const int64_t b = blockIdx.x / nfc;
-  l.f = (blockIdx.x % nfc) * kFC + l.fl;
+  // The filter groups of one batch element share the cache lines of its
+  // (B,T,F) rows: keep them on one XCD.
+  const int64_t blk = xcd_contiguous(blockIdx.x, gridDim.x);
+  l.b = blk / nfc;
+  l.f = (blk % nfc) * kFC + l.fl;
   l.fv = l.f < F;
-  l.base = b * T * F + (l.fv ? l.f : 0);
+  l.base = l.b * T * F + (l.fv ? l.f : 0);
   return l;
 }
 
@@ -305,8 +309,7 @@ __global__ __launch_bounds__(kThreads) void btf_bwd_kernel(
     for (int v = 0; v < kWaves; ++v)
 #pragma unroll
       for (int j = 0; j < 6; ++j) acc[j] += s_red[v][threadIdx.x][j];
-    const int64_t b = blockIdx.x / ((F + kFC - 1) / kFC);
-    double* o = partial + 6 * (b * F + l.f);
+    double* o = partial + 6 * (l.b * F + l.f);
 #pragma unroll
     for (int j = 0; j < 6; ++j) o[j] = acc[j];
   }

@@ -11,33 +11,41 @@
 // readout (scan.py:381-432) compute these with one program per (batch,
 // filter) walking all T steps serially.
 //
-// Here a task is (batch, time segment, filter) with the filter fastest, so a
-// wavefront reads 64 consecutive inputs per step.  A task keeps the filter's
-// NP oscillators (N padded to a power of two; padded oscillators have zero
-// coefficients) in registers over its segment.  Segments are joined by a
-// carry pass per (batch, oscillator, filter) over the segments (three-phase
-// scan).
+// Here, as in btf.hip, a block owns 16 consecutive filters of one batch
+// element and walks the sequence in passes of 32 segments of LS steps; a
+// thread takes one (filter, segment) of each pass with the filter's
+// oscillators (N padded to a power of two NP <= 4, padded ones with zero
+// coefficients) in registers.  It loads its segment's inputs once (the next
+// pass's while the current one computes), scans them from a zero state per
+// oscillator, and gets its entry states from the segments before it: the
+// wavefront's earlier segments by cross-lane moves, the earlier wavefronts'
+// and the block's carry through LDS.  Those folds span at most 10 segment
+// hops and run in fp32 with powers computed once per block in fp64 and
+// rounded; only the carry from pass to pass, a chain of T / pass hops, is
+// kept in fp64.  The thread then replays the segment and writes the output.
+// Filter groups of one batch element run on one XCD (xcd_contiguous): with
+// real input a group reads half of each 128-byte line of a (B,T,F) row.  Inputs are read once, outputs
+// written once, and no carry crosses a block.  More than 4 oscillators run
+// in chunks of 4, each adding its share to the output (or to grad_u).
 //
 // The scanned state is w_n = x_n / C2_n, i.e. w_n[t] = C1_n w_n[t-1] + u[t],
 // with C2_n applied at the output: y = sum_n (cw_n C2_n) w_n.  No division
 // happens; C2 = 0 is fine.
 //
-// Backward.  The adjoint e_n[t] = conj(C1_n) e_n[t+1] + grad_out[t] runs as a
-// reverse three-phase scan (local pass, carry, final pass); grad_u is
-// sum_n conj(cw_n C2_n) e_n.  The reference's coefficient sums pair the
-// adjoint at t with the state at t-1, which a reverse sweep does not have.
-// Exchanging the order of summation pairs them with u instead
-// (mosc_coef_stage2_kernel): against e_n for grad_C2 and grad_cw, and against
-// f_n, the derivative of e_n's recurrence with respect to conj(C1_n), for
-// grad_C1.  f_n is itself a reverse recurrence, f_n[t] = conj(C1_n) f_n[t+1] +
-// e_n[t+1], carried between segments with e_n.  So the final pass reads
-// grad_out and u once and produces grad_u and all three sums, with no forward
-// state, no checkpoints and no per-step state tensor (the reference keeps
-// every state in a (B*F, T, N) scratch tensor).
+// Backward.  The adjoint e_n[t] = conj(C1_n) e_n[t+1] + grad_out[t] runs the
+// same way in reverse time; grad_u is sum_n conj(cw_n C2_n) e_n.  The
+// reference's coefficient sums pair the adjoint at t with the state at t-1,
+// which a reverse sweep does not have.  Exchanging the order of summation
+// pairs them with u instead (mosc_coef_kernel): against e_n for grad_C2 and
+// grad_cw, and against f_n, the derivative of e_n's recurrence with respect to
+// conj(C1_n), for grad_C1.  f_n is itself a reverse recurrence, f_n[t] =
+// conj(C1_n) f_n[t+1] + e_n[t+1], carried between segments with e_n.  So the
+// pass reads grad_out and u once and produces grad_u and all three sums, with
+// no forward state and no per-step state tensor (the reference keeps every
+// state in a (B*F, T, N) scratch tensor).
 //
-// Coefficient gradients are reduced deterministically: per-task fp32 partial
-// sums over at most kMoscMaxSeg steps, then an ordered fp64 reduction per
-// oscillator.
+// Coefficient gradients are reduced deterministically: per-(batch, filter,
+// oscillator) fp64 partial sums, then an ordered reduction over the batch.
 #include "rqf_device.h"
 #include "rqf_scan.h"
 
@@ -47,356 +55,472 @@ using namespace rqf;
 
 namespace {
 
-constexpr int kMoscMaxOsc = 8;     // oscillators per filter (N <= 8)
-// Steps per segment, at most.  Config 6 fwd+bwd: 74.2 Gelem/s at 256 (about 4
-// wavefronts per SIMD), 76.7 at 128, 72.3 at 64 (longer carry chains, more
-// segment states).
-#ifndef RQF_MOSC_MAX_SEG
-#define RQF_MOSC_MAX_SEG 128
-#endif
-constexpr int kMoscMaxSeg = RQF_MOSC_MAX_SEG;
-constexpr int kMoscMinSeg = 16;    // steps per segment, at least (when T allows)
-constexpr int64_t kMoscLanes = 65536;  // target number of tasks
-// Steps per streamed chunk (see stream_steps).  Config 6 (B=32 T=16000 F=128,
-// N=4) fwd+bwd on one MI355X: 70.1 Gelem/s with one load in flight per wave,
-// 71.6 with 8-step chunks, 71.0 with 16, 69.8 with 32 for the local passes
-// (the final passes' 16-step chunks reach 153 VGPRs).
-#ifndef RQF_MOSC_STREAM
-#define RQF_MOSC_STREAM 8
-#endif
-#ifndef RQF_MOSC_STREAM_FINAL
-#define RQF_MOSC_STREAM_FINAL 8
-#endif
-constexpr int kStream = RQF_MOSC_STREAM;
-constexpr int kStreamFinal = RQF_MOSC_STREAM_FINAL;
+constexpr int kMaxChunk = 4;  // oscillators per kernel launch
+constexpr int kFC = 16;       // filters per block
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kNSeg = kThreads / kFC;  // segments per pass
+constexpr int kG = kWave / kFC;        // segments per wavefront
 
-__device__ __forceinline__ c32 ldc(const float* p, int64_t i) { return mk(p[2 * i], p[2 * i + 1]); }
-__device__ __forceinline__ void stc(float* p, int64_t i, c32 v) {
-  p[2 * i] = v.r;
-  p[2 * i + 1] = v.i;
-}
-
-struct MoscShape {
-  int64_t B, T, F, S, L, tasks;
-  int N;
+// Steps per segment, by padded oscillator count (registers: the segment's
+// inputs and the next pass's are held per thread).
+template <int NP>
+struct Seg {
+  static constexpr int fwd = NP <= 2 ? 32 : 16;
+  static constexpr int bwd = NP == 1 ? 16 : 8;
 };
 
-template <bool REAL>
-__device__ __forceinline__ c32 load_u(const float* __restrict__ u, int64_t e) {
-  return REAL ? mk(u[e], 0.0f) : ldc(u, e);
+__device__ __forceinline__ c32 ldc(const float* p, int64_t i) {
+  const float2 v = *reinterpret_cast<const float2*>(p + 2 * i);
+  return mk(v.x, v.y);
+}
+__device__ __forceinline__ void stc(float* p, int64_t i, c32 v) {
+  *reinterpret_cast<float2*>(p + 2 * i) = make_float2(v.r, v.i);
+}
+__device__ __forceinline__ double2 d2(c64d v) { return make_double2(v.r, v.i); }
+__device__ __forceinline__ c64d cd(double2 v) { return mkd(v.x, v.y); }
+
+struct Lane {
+  int fl, sg, lane, w, q;
+  int64_t f, b;
+  bool fv;
+  int64_t base;  // element (b, 0, f)
+};
+
+__device__ __forceinline__ Lane lane_of(int64_t T, int64_t F) {
+  Lane l;
+  l.fl = (int)threadIdx.x % kFC;
+  l.sg = (int)threadIdx.x / kFC;
+  l.lane = lane_id();
+  l.w = wave_id();
+  l.q = l.lane / kFC;
+  const int64_t nfc = (F + kFC - 1) / kFC;
+  // The filter groups of one batch element share the cache lines of its
+  // (B,T,F) rows: keep them on one XCD.
+  const int64_t blk = xcd_contiguous(blockIdx.x, gridDim.x);
+  l.b = blk / nfc;
+  l.f = (blk % nfc) * kFC + l.fl;
+  l.fv = l.f < F;
+  l.base = l.b * T * F + (l.fv ? l.f : 0);
+  return l;
 }
 
-// Coefficients of the filter's oscillators (index f*N + n; zero when n >= N).
+// Inputs of the thread's segment [tb, tb + LS); zero outside [0, T).
+template <int LS, bool REAL>
+__device__ __forceinline__ void load_seg(const float* __restrict__ p, const Lane& l, int64_t tb,
+                                         int64_t T, int64_t F, c32 (&v)[LS]) {
+#pragma unroll
+  for (int j = 0; j < LS; ++j) {
+    const int64_t t = tb + j;
+    const bool in = l.fv && t < T;
+    if (REAL)
+      v[j] = mk(in ? p[l.base + t * F] : 0.0f, 0.0f);
+    else
+      v[j] = in ? ldc(p, l.base + t * F) : mk(0.0f, 0.0f);
+  }
+}
+
+// Coefficients of oscillators n0 .. n0+NP-1 of the lane's filter (index
+// f*N + n; zero past N).
 template <int NP>
-__device__ __forceinline__ void load_osc(const float* __restrict__ p, int64_t f, int N,
+__device__ __forceinline__ void load_osc(const float* __restrict__ p, const Lane& l, int N, int n0,
                                          c32 (&v)[NP]) {
 #pragma unroll
-  for (int n = 0; n < NP; ++n) v[n] = n < N ? ldc(p, f * N + n) : mk(0.0f, 0.0f);
-}
-
-struct Task {
-  int64_t b, s, f, tb, te;
-};
-__device__ __forceinline__ Task task_of(const MoscShape& sh, int64_t task) {
-  Task k;
-  k.f = task % sh.F;
-  const int64_t bs = task / sh.F;
-  k.s = bs % sh.S;
-  k.b = bs / sh.S;
-  k.tb = k.s * sh.L;
-  k.te = min(sh.T, k.tb + sh.L);
-  return k;
-}
-// Segment states: (b, s, n, f) with f fastest.
-__device__ __forceinline__ int64_t seg_idx(const MoscShape& sh, int64_t b, int64_t s, int n,
-                                           int64_t f, int NP) {
-  return ((b * sh.S + s) * NP + n) * sh.F + f;
-}
-
-// One step of the scanned state w_n[t] = C1_n w_n[t-1] + u[t].
-template <bool REAL>
-__device__ __forceinline__ c32 step_w(c32 a, c32 w, c32 ut) {
-  return REAL ? cmadr(a, w, ut.r) : cmad(a, w, ut);
-}
-
-// Phase 1 of the forward: each segment's end states from a zero entry.
-template <int NP, bool REAL>
-__global__ __launch_bounds__(256) void mosc_fwd_local_kernel(const float* __restrict__ c1,
-                                                             const float* __restrict__ u,
-                                                             float* __restrict__ seg,
-                                                             MoscShape sh) {
-  const int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (task >= sh.tasks) return;
-  const Task k = task_of(sh, task);
-  c32 a[NP], w[NP];
-  load_osc<NP>(c1, k.f, sh.N, a);
-#pragma unroll
-  for (int n = 0; n < NP; ++n) w[n] = mk(0.0f, 0.0f);
-  const int64_t base = k.b * sh.T * sh.F + k.f;
-  c32 ub[kStream];
-  stream_steps<kStream, true>(
-      k.tb, k.te, [&](int j, int64_t t) { ub[j] = load_u<REAL>(u, base + t * sh.F); },
-      [&](int j, int64_t) {
-#pragma unroll
-        for (int n = 0; n < NP; ++n) w[n] = step_w<REAL>(a[n], w[n], ub[j]);
-      });
-#pragma unroll
-  for (int n = 0; n < NP; ++n) stc(seg, seg_idx(sh, k.b, k.s, n, k.f, NP), w[n]);
-}
-
-// Phase 2: exclusive fold over the segments, in place, per (b, n, f).
-//   forward: w_in[s+1] = C1^L w_in[s] + w_end[s]                    (w_in[0] = 0)
-//   adjoint: the pair (e, f) entering segment s from its end,
-//            e_out[s-1] = P e_out[s] + e_start[s]
-//            f_out[s-1] = P f_out[s] + len(s) P' e_out[s] + f_start[s]   (TAN)
-//            with P = conj(C1)^len(s), P' = conj(C1)^(len(s)-1), and zero
-//            at s = S-1.
-// len(s) steps of zero input take (e, f) to (P e, P f + len P' e), by
-// induction on the adjoint step (see mosc_bwd_final_kernel).
-template <int NP, bool ADJ, bool TAN>
-__global__ __launch_bounds__(256) void mosc_carry_kernel(const float* __restrict__ c1,
-                                                         float* __restrict__ seg,
-                                                         float* __restrict__ segf,
-                                                         MoscShape sh) {
-  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (id >= sh.B * NP * sh.F) return;
-  const int64_t f = id % sh.F, bn = id / sh.F;
-  const int n = (int)(bn % NP);
-  const int64_t b = bn / NP;
-  const c32 a = n < sh.N ? ldc(c1, f * sh.N + n) : mk(0.0f, 0.0f);
-  // Powers and the fold in fp64: a float32 power is off by ~L ulp, a bias that
-  // every hop of a long-memory channel would repeat.
-  // The segments' values are loaded kStream at a time (stream_steps); each
-  // is overwritten only after it has been read.
-  c64d e = mkd(0.0, 0.0);
-  if (!ADJ) {
-    const c64d aL = dpow(widen(a), sh.L);
-    c32 vb[kStream];
-    stream_steps<kStream, true>(
-        0, sh.S, [&](int j, int64_t s) { vb[j] = ldc(seg, seg_idx(sh, b, s, n, f, NP)); },
-        [&](int j, int64_t s) {
-          stc(seg, seg_idx(sh, b, s, n, f, NP), narrow(e));
-          e = dmad(aL, e, widen(vb[j]));
-        });
-  } else {
-    const c64d ac = dconj(widen(a));
-    const int64_t lenLast = sh.T - (sh.S - 1) * sh.L;
-    const c64d p1 = sh.L > 1 ? dpow(ac, sh.L - 1) : mkd(1.0, 0.0);
-    const c64d p1Last = lenLast > 1 ? dpow(ac, lenLast - 1) : mkd(1.0, 0.0);
-    const c64d p = dmul(p1, ac), pLast = dmul(p1Last, ac);
-    const c64d q = mkd(p1.r * (double)sh.L, p1.i * (double)sh.L);
-    const c64d qLast = mkd(p1Last.r * (double)lenLast, p1Last.i * (double)lenLast);
-    c64d ef = mkd(0.0, 0.0);
-    c32 vb[kStream], vfb[kStream];
-    stream_steps<kStream, false>(
-        0, sh.S,
-        [&](int j, int64_t s) {
-          const int64_t i = seg_idx(sh, b, s, n, f, NP);
-          vb[j] = ldc(seg, i);
-          if (TAN) vfb[j] = ldc(segf, i);
-        },
-        [&](int j, int64_t s) {
-          const bool last = s == sh.S - 1;
-          const int64_t i = seg_idx(sh, b, s, n, f, NP);
-          stc(seg, i, narrow(e));
-          if (TAN) {
-            stc(segf, i, narrow(ef));
-            ef = dmad(last ? pLast : p, ef, dmad(last ? qLast : q, e, widen(vfb[j])));
-          }
-          e = dmad(last ? pLast : p, e, widen(vb[j]));
-        });
-  }
+  for (int n = 0; n < NP; ++n)
+    v[n] = (l.fv && n0 + n < N) ? ldc(p, l.f * N + n0 + n) : mk(0.0f, 0.0f);
 }
 
 // Output weights of the scanned state: y = sum_n (cw_n C2_n) w_n, or C2_0 w_0
 // without C-weights.
 template <int NP, bool CW>
 __device__ __forceinline__ void load_out_weights(const float* __restrict__ c2,
-                                                 const float* __restrict__ cw, int64_t f, int N,
-                                                 c32 (&h)[NP]) {
-  load_osc<NP>(c2, f, N, h);
+                                                 const float* __restrict__ cw, const Lane& l,
+                                                 int N, int n0, c32 (&h)[NP]) {
+  load_osc<NP>(c2, l, N, n0, h);
   if (CW) {
     c32 w[NP];
-    load_osc<NP>(cw, f, N, w);
+    load_osc<NP>(cw, l, N, n0, w);
 #pragma unroll
     for (int n = 0; n < NP; ++n) h[n] = cmul(w[n], h[n]);
   }
 }
 
-// Phase 3 of the forward: rescan each segment from its entry state and write
-// y = sum_n cw_n C2_n w_n (CW) or C2_0 w_0, as complex or as |y| (ABS).
+__device__ __forceinline__ c32 shfl_up_c(c32 v, int d) {
+  return mk(__shfl_up(v.r, d), __shfl_up(v.i, d));
+}
+__device__ __forceinline__ c32 shfl_down_c(c32 v, int d) {
+  return mk(__shfl_down(v.r, d), __shfl_down(v.i, d));
+}
+
+// Powers of one filter's oscillator coefficient a over spans of segments of
+// LS steps, computed once per block in fp64 and rounded: m1 = a^LS (one
+// segment), m2 = m1^2, mG = m1^G (one wavefront's segments), mq[q] = m1^q,
+// and mB = m1^(G*waves) (one pass), kept in fp64 for the carry chain.
+struct FwdMaps {
+  c32 m1, m2, mG, mq[kG];
+  double2 mB;
+};
+template <int LS>
+__device__ __forceinline__ FwdMaps fwd_maps(c32 a) {
+  FwdMaps k;
+  const c64d m1 = dpow(widen(a), LS);
+  k.m1 = narrow(m1);
+  k.m2 = narrow(dmul(m1, m1));
+#pragma unroll
+  for (int q = 0; q < kG; ++q) k.mq[q] = narrow(dpow(m1, q));
+  const c64d mG = dpow(m1, kG);
+  k.mG = narrow(mG);
+  k.mB = d2(dpow(mG, kWaves));
+  return k;
+}
+
+// ---------------------------------------------------------------------------
+// Forward.  yin (optional, complex (B,T,F)) is added to this chunk's y: the
+// earlier chunks' share.  yout receives y (complex) or |y| (ABS).
+// ---------------------------------------------------------------------------
 template <int NP, bool REAL, bool CW, bool ABS>
-__global__ __launch_bounds__(256) void mosc_fwd_final_kernel(
+__global__ __launch_bounds__(kThreads) void mosc_fwd_kernel(
     const float* __restrict__ c1, const float* __restrict__ c2, const float* __restrict__ cw,
-    const float* __restrict__ u, const float* __restrict__ seg, float* __restrict__ out,
-    MoscShape sh) {
-  const int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (task >= sh.tasks) return;
-  const Task k = task_of(sh, task);
-  c32 a[NP], h[NP], w[NP];
-  load_osc<NP>(c1, k.f, sh.N, a);
-  load_out_weights<NP, CW>(c2, cw, k.f, sh.N, h);
+    const float* __restrict__ u, const float* yin, float* yout, int64_t T, int64_t F, int N,
+    int n0) {
+  constexpr int LS = Seg<NP>::fwd;
+  constexpr int kPass = kNSeg * LS;
+  __shared__ c32 s_tot[2][kWaves][NP][kFC];
+  __shared__ double2 s_carry[2][NP][kFC];
+  __shared__ FwdMaps s_k[NP][kFC];
+  const Lane l = lane_of(T, F);
+  c32 a[NP], hw[NP];
+  load_osc<NP>(c1, l, N, n0, a);
+  load_out_weights<NP, CW>(c2, cw, l, N, n0, hw);
+  if (l.sg == 0) {
 #pragma unroll
-  for (int n = 0; n < NP; ++n) w[n] = ldc(seg, seg_idx(sh, k.b, k.s, n, k.f, NP));
-  const int64_t base = k.b * sh.T * sh.F + k.f;
-  c32 ub[kStreamFinal];
-  stream_steps<kStreamFinal, true>(
-      k.tb, k.te, [&](int j, int64_t t) { ub[j] = load_u<REAL>(u, base + t * sh.F); },
-      [&](int j, int64_t t) {
-        c32 y = mk(0.0f, 0.0f);
+    for (int n = 0; n < NP; ++n) {
+      s_carry[0][n][l.fl] = make_double2(0.0, 0.0);
+      s_k[n][l.fl] = fwd_maps<LS>(a[n]);
+    }
+  }
+  __syncthreads();
+  c32 uv[LS], un[LS];
+  load_seg<LS, REAL>(u, l, (int64_t)l.sg * LS, T, F, uv);
+  int p = 0;
+  for (int64_t pt = 0; pt < T; pt += kPass) {
+    const int64_t tb = pt + (int64_t)l.sg * LS;
+    if (pt + kPass < T) load_seg<LS, REAL>(u, l, tb + kPass, T, F, un);
+    // Each oscillator's segment from a zero state.
+    c32 w[NP];
 #pragma unroll
-        for (int n = 0; n < NP; ++n) {
-          w[n] = step_w<REAL>(a[n], w[n], ub[j]);
-          if (CW || n == 0) y = cmad(h[n], w[n], y);
-        }
-        const int64_t e = base + t * sh.F;
+    for (int n = 0; n < NP; ++n) w[n] = mk(0.0f, 0.0f);
+#pragma unroll
+    for (int j = 0; j < LS; ++j)
+#pragma unroll
+      for (int n = 0; n < NP; ++n) w[n] = REAL ? cmadr(a[n], w[n], uv[j].r) : cmad(a[n], w[n], uv[j]);
+    // Entry states: the wavefront's earlier segments (cross-lane), then the
+    // block's carry and the earlier wavefronts (LDS).  Within a pass at most
+    // 10 segment hops are folded, in fp32 with exactly rounded powers; the
+    // carry from pass to pass, a chain of T / pass hops, is kept in fp64.
+#pragma unroll
+    for (int n = 0; n < NP; ++n) {
+      const FwdMaps& k = s_k[n][l.fl];
+      c32 incl = w[n];
+      c32 prev = shfl_up_c(incl, kFC);
+      if (l.q >= 1) incl = cmad(k.m1, prev, incl);
+      prev = shfl_up_c(incl, 2 * kFC);
+      if (l.q >= 2) incl = cmad(k.m2, prev, incl);
+      if (l.q == kG - 1) s_tot[p][l.w][n][l.fl] = incl;
+      const c32 ex = shfl_up_c(incl, kFC);
+      w[n] = l.q >= 1 ? ex : mk(0.0f, 0.0f);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int n = 0; n < NP; ++n) {
+      const FwdMaps& k = s_k[n][l.fl];
+      const c64d carry = cd(s_carry[p][n][l.fl]);
+      c32 cw_ = narrow(carry);
+      for (int v = 0; v < l.w; ++v) cw_ = cmad(k.mG, cw_, s_tot[p][v][n][l.fl]);
+      if (l.w == kWaves - 1 && l.q == kG - 1) {
+        c32 z = mk(0.0f, 0.0f);
+        for (int v = 0; v < kWaves; ++v) z = cmad(k.mG, z, s_tot[p][v][n][l.fl]);
+        s_carry[p ^ 1][n][l.fl] = d2(dmad(cd(k.mB), carry, widen(z)));
+      }
+      w[n] = cmad(k.mq[l.q], cw_, w[n]);
+    }
+    // Replay and write.
+#pragma unroll
+    for (int j = 0; j < LS; ++j) {
+      c32 y = mk(0.0f, 0.0f);
+#pragma unroll
+      for (int n = 0; n < NP; ++n) {
+        w[n] = REAL ? cmadr(a[n], w[n], uv[j].r) : cmad(a[n], w[n], uv[j]);
+        if (CW || n == 0) y = cmad(hw[n], w[n], y);
+      }
+      const int64_t t = tb + j;
+      if (l.fv && t < T) {
+        const int64_t e = l.base + t * F;
+        if (yin) y = cadd(y, ldc(yin, e));
         if (ABS)
-          out[e] = sqrtf(fmaf(y.r, y.r, y.i * y.i));
+          yout[e] = sqrtf(fmaf(y.r, y.r, y.i * y.i));
         else
-          stc(out, e, y);
-      });
-}
-
-// One reverse step of the adjoint pair (see mosc_bwd_final_kernel).
-template <bool TAN>
-__device__ __forceinline__ void step_adj(c32 a, c32& e, c32& f, c32 gt) {
-  if (TAN) f = cjmad(a, f, e);
-  e = cjmad(a, e, gt);
-}
-
-// Phase 1 of the backward: each segment's adjoint pair at its first step from
-// a zero pair after its last step.
-template <int NP, bool TAN>
-__global__ __launch_bounds__(256) void mosc_bwd_local_kernel(const float* __restrict__ c1,
-                                                             const float* __restrict__ gy,
-                                                             float* __restrict__ segb,
-                                                             float* __restrict__ segf,
-                                                             MoscShape sh) {
-  const int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (task >= sh.tasks) return;
-  const Task k = task_of(sh, task);
-  c32 a[NP], d[NP], f[NP];
-  load_osc<NP>(c1, k.f, sh.N, a);
+          stc(yout, e, y);
+      }
+    }
 #pragma unroll
-  for (int n = 0; n < NP; ++n) d[n] = f[n] = mk(0.0f, 0.0f);
-  const int64_t base = k.b * sh.T * sh.F + k.f;
-  c32 gb[kStream];
-  stream_steps<kStream, false>(
-      k.tb, k.te, [&](int j, int64_t t) { gb[j] = ldc(gy, base + t * sh.F); },
-      [&](int j, int64_t) {
-#pragma unroll
-        for (int n = 0; n < NP; ++n) step_adj<TAN>(a[n], d[n], f[n], gb[j]);
-      });
-#pragma unroll
-  for (int n = 0; n < NP; ++n) {
-    const int64_t i = seg_idx(sh, k.b, k.s, n, k.f, NP);
-    stc(segb, i, d[n]);
-    if (TAN) stc(segf, i, f[n]);
+    for (int j = 0; j < LS; ++j) uv[j] = un[j];
+    p ^= 1;
   }
 }
 
-// Phase 3 of the backward, from each segment's exit pair, for t descending:
+// ---------------------------------------------------------------------------
+// Backward, from each segment's exit pair, for t descending:
 //   f_n[t]    = conj(C1_n) f_n[t+1] + e_n[t+1]                  (TAN)
 //   e_n[t]    = conj(C1_n) e_n[t+1] + gy[t]
 //   grad_u[t] = sum_n conj(cw_n C2_n) e_n[t]   (GU; real u: its real part)
 //   Q_n += e_n[t] conj(u[t]),  R_n += f_n[t] conj(u[t])         (TAN)
 // e_n is the reference's adjoint d_n without its conj(cw_n) factor, and
 // f_n[t] = sum_{s>t} conj(C1_n)^(s-1-t) e_n[s], the derivative of e_n's
-// recurrence with respect to conj(C1_n).  Partial sums go to
-// part[(n*4 + j)*tasks + task] (j: Re Q, Im Q, Re R, Im R).
-template <int NP, bool REAL, bool TAN, bool GU>
-__global__ __launch_bounds__(256) void mosc_bwd_final_kernel(
-    const float* __restrict__ c1, const float* __restrict__ c2, const float* __restrict__ cw,
-    const float* __restrict__ u, const float* __restrict__ gy, const float* __restrict__ segb,
-    const float* __restrict__ segf, float* __restrict__ gu, float* __restrict__ part,
-    MoscShape sh) {
-  const int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (task >= sh.tasks) return;
-  const Task k = task_of(sh, task);
-  c32 a[NP], h[NP], d[NP], f[NP], q[NP], r[NP];
-  load_osc<NP>(c1, k.f, sh.N, a);
-  if (GU) load_out_weights<NP, true>(c2, cw, k.f, sh.N, h);
-#pragma unroll
-  for (int n = 0; n < NP; ++n) {
-    const int64_t i = seg_idx(sh, k.b, k.s, n, k.f, NP);
-    d[n] = ldc(segb, i);
-    f[n] = TAN ? ldc(segf, i) : mk(0.0f, 0.0f);
-    q[n] = r[n] = mk(0.0f, 0.0f);
+// recurrence with respect to conj(C1_n).  LS steps of zero input take the
+// pair (e, f) to (P e, P f + LS P' e), P = conj(C1)^LS, P' = conj(C1)^(LS-1)
+// (the PairMap of rqf_device.h).  gin (optional) is added to grad_u: the
+// earlier oscillator chunks' share.  Partial sums go to
+// part[((b*F + f)*N + n)*4 + j] (j: Re Q, Im Q, Re R, Im R).
+// ---------------------------------------------------------------------------
+struct Pair {
+  double2 g, h;
+};
+struct Pair32 {
+  c32 g, h;
+};
+// A pair map in fp32 (see PairMap).
+struct PairMap32 {
+  c32 P, c;
+};
+__device__ __forceinline__ PairMap32 narrow_map(PairMap m) { return {narrow(m.P), narrow(m.c)}; }
+// (g, h) entering a span with map m and own pair (G, H) -> the span's start pair.
+__device__ __forceinline__ void pair_apply32(PairMap32 m, c32 G, c32 H, c32& g, c32& h) {
+  const c32 ng = cmad(m.P, g, G);
+  h = cmad(m.P, h, cmad(m.c, g, H));
+  g = ng;
+}
+
+// Pair map of one segment of LS steps: P = conj(a)^LS, c = LS conj(a)^(LS-1).
+template <int LS>
+__device__ __forceinline__ PairMap one_segment(c32 a) {
+  const c64d p1 = LS > 1 ? dconj(dpow(widen(a), LS - 1)) : mkd(1.0, 0.0);
+  PairMap m;
+  m.P = dmul(p1, dconj(widen(a)));
+  m.c = mkd(p1.r * (double)LS, p1.i * (double)LS);
+  return m;
+}
+
+// One filter's pair maps over spans of segments, computed once per block in
+// fp64 and rounded: one and two segments, one wavefront's G segments, the
+// G-1-q segments after segment q of a wavefront, and one pass (kept in fp64
+// for the carry chain).
+struct BwdMaps {
+  PairMap32 one, two, wave, after[kG];
+  Pair pass;  // (P, c) of the whole pass, fp64
+};
+template <int LS>
+__device__ __forceinline__ BwdMaps bwd_maps(c32 a) {
+  BwdMaps k;
+  const PairMap one = one_segment<LS>(a);
+  const PairMap two = pair_map_mul(one, one);
+  PairMap wave = one;
+  for (int i = 1; i < kG; ++i) wave = pair_map_mul(wave, one);
+  PairMap pass = wave;
+  for (int i = 1; i < kWaves; ++i) pass = pair_map_mul(pass, wave);
+  k.one = narrow_map(one);
+  k.two = narrow_map(two);
+  k.wave = narrow_map(wave);
+  PairMap acc;
+  acc.P = mkd(1.0, 0.0);
+  acc.c = mkd(0.0, 0.0);
+  for (int q = kG - 1; q >= 0; --q) {  // after[q]: the G-1-q segments after q
+    k.after[q] = narrow_map(acc);
+    acc = pair_map_mul(acc, one);
   }
-  const int64_t base = k.b * sh.T * sh.F + k.f;
-  c32 gb[kStreamFinal], ub[kStreamFinal];
-  stream_steps<kStreamFinal, false>(
-      k.tb, k.te,
-      [&](int j, int64_t t) {
-        gb[j] = ldc(gy, base + t * sh.F);
-        if (TAN) ub[j] = load_u<REAL>(u, base + t * sh.F);
-      },
-      [&](int j, int64_t t) {
-        c32 g = mk(0.0f, 0.0f);
-#pragma unroll
-        for (int n = 0; n < NP; ++n) {
-          step_adj<TAN>(a[n], d[n], f[n], gb[j]);
-          if (GU) g = cjmad(h[n], d[n], g);
-          if (TAN) {
-            if (REAL) {
-              q[n] = csmad(ub[j].r, d[n], q[n]);
-              r[n] = csmad(ub[j].r, f[n], r[n]);
-            } else {
-              q[n] = cjmad(ub[j], d[n], q[n]);
-              r[n] = cjmad(ub[j], f[n], r[n]);
-            }
-          }
-        }
-        if (GU) {
-          const int64_t e = base + t * sh.F;
-          if (REAL)
-            gu[e] = g.r;
-          else
-            stc(gu, e, g);
-        }
-      });
-  if (TAN) {
+  k.pass = Pair{d2(pass.P), d2(pass.c)};
+  return k;
+}
+
+template <int NP, bool REAL, bool TAN, bool GU>
+__global__ __launch_bounds__(kThreads) void mosc_bwd_kernel(
+    const float* __restrict__ c1, const float* __restrict__ c2, const float* __restrict__ cw,
+    const float* __restrict__ u, const float* __restrict__ gy, const float* gin, float* gu,
+    double* __restrict__ part, int64_t T, int64_t F, int N, int n0) {
+  constexpr int LS = Seg<NP>::bwd;
+  constexpr int kPass = kNSeg * LS;
+  __shared__ Pair32 s_tot[2][kWaves][NP][kFC];
+  __shared__ Pair s_carry[2][NP][kFC];
+  __shared__ BwdMaps s_k[NP][kFC];
+  __shared__ double s_red[TAN ? kWaves * kFC * 4 * NP : 1];
+  const Lane l = lane_of(T, F);
+  c32 a[NP], hw[NP];
+  load_osc<NP>(c1, l, N, n0, a);
+  if (GU) load_out_weights<NP, true>(c2, cw, l, N, n0, hw);
+  if (l.sg == 0) {
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
-      float* p = part + (int64_t)n * 4 * sh.tasks + task;
-      p[0] = q[n].r;
-      p[sh.tasks] = q[n].i;
-      p[2 * sh.tasks] = r[n].r;
-      p[3 * sh.tasks] = r[n].i;
+      s_carry[0][n][l.fl] = Pair{make_double2(0.0, 0.0), make_double2(0.0, 0.0)};
+      s_k[n][l.fl] = bwd_maps<LS>(a[n]);
+    }
+  }
+  __syncthreads();
+  float qr[NP][4];
+#pragma unroll
+  for (int n = 0; n < NP; ++n) qr[n][0] = qr[n][1] = qr[n][2] = qr[n][3] = 0.0f;
+  const int64_t npass = (T + kPass - 1) / kPass;
+  c32 gv[LS], gn[LS], uv[TAN ? LS : 1], un[TAN ? LS : 1];
+  int64_t pt = (npass - 1) * kPass;
+  load_seg<LS, false>(gy, l, pt + (int64_t)l.sg * LS, T, F, gv);
+  if constexpr (TAN) load_seg<LS, REAL>(u, l, pt + (int64_t)l.sg * LS, T, F, uv);
+  int p = 0;
+  for (; pt >= 0; pt -= kPass) {
+    const int64_t tb = pt + (int64_t)l.sg * LS;
+    if (pt > 0) {
+      load_seg<LS, false>(gy, l, tb - kPass, T, F, gn);
+      if constexpr (TAN) load_seg<LS, REAL>(u, l, tb - kPass, T, F, un);
+    }
+    // Each oscillator's pair at the segment's first step from a zero pair.
+    c32 e[NP], f[NP];
+#pragma unroll
+    for (int n = 0; n < NP; ++n) e[n] = f[n] = mk(0.0f, 0.0f);
+#pragma unroll
+    for (int j = LS - 1; j >= 0; --j)
+#pragma unroll
+      for (int n = 0; n < NP; ++n) {
+        if (TAN) f[n] = cjmad(a[n], f[n], e[n]);
+        e[n] = cjmad(a[n], e[n], gv[j]);
+      }
+    // Entry pairs: the wavefront's later segments (cross-lane), then the
+    // block's carry and the later wavefronts (LDS).  Within a pass at most 10
+    // segment hops are folded, in fp32 with exactly rounded maps; the carry
+    // from pass to pass, a chain of T / pass hops, is kept in fp64.
+#pragma unroll
+    for (int n = 0; n < NP; ++n) {
+      const BwdMaps& k = s_k[n][l.fl];
+      c32 ig = e[n], ih = f[n];
+      c32 ng = shfl_down_c(ig, kFC), nh = shfl_down_c(ih, kFC);
+      if (l.q + 1 < kG) pair_apply32(k.one, ig, ih, ng, nh), ig = ng, ih = nh;
+      ng = shfl_down_c(ig, 2 * kFC);
+      nh = shfl_down_c(ih, 2 * kFC);
+      if (l.q + 2 < kG) pair_apply32(k.two, ig, ih, ng, nh), ig = ng, ih = nh;
+      if (l.q == 0) s_tot[p][l.w][n][l.fl] = Pair32{ig, ih};
+      const c32 xg = shfl_down_c(ig, kFC), xh = shfl_down_c(ih, kFC);
+      e[n] = l.q + 1 < kG ? xg : mk(0.0f, 0.0f);
+      f[n] = l.q + 1 < kG ? xh : mk(0.0f, 0.0f);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int n = 0; n < NP; ++n) {
+      const BwdMaps& k = s_k[n][l.fl];
+      const Pair cr = s_carry[p][n][l.fl];
+      c32 cg = narrow(cd(cr.g)), ch = narrow(cd(cr.h));
+      for (int v = kWaves - 1; v > l.w; --v) {
+        const Pair32 t = s_tot[p][v][n][l.fl];
+        pair_apply32(k.wave, t.g, t.h, cg, ch);
+      }
+      pair_apply32(k.after[l.q], e[n], f[n], cg, ch);
+      if (l.w == 0 && l.q == 0) {
+        c32 zg = mk(0.0f, 0.0f), zh = mk(0.0f, 0.0f);
+        for (int v = kWaves - 1; v >= 0; --v) {
+          const Pair32 t = s_tot[p][v][n][l.fl];
+          pair_apply32(k.wave, t.g, t.h, zg, zh);
+        }
+        PairMap pm;
+        pm.P = cd(k.pass.g);
+        pm.c = cd(k.pass.h);
+        c64d g = cd(cr.g), h = cd(cr.h);
+        pair_apply(pm, widen(zg), widen(zh), g, h);
+        s_carry[p ^ 1][n][l.fl] = Pair{d2(g), d2(h)};
+      }
+      e[n] = cg;
+      f[n] = ch;
+    }
+    // Replay: grad_u and the coefficient sums.
+    float pq[NP][4];
+#pragma unroll
+    for (int n = 0; n < NP; ++n) pq[n][0] = pq[n][1] = pq[n][2] = pq[n][3] = 0.0f;
+    c32 go[GU ? LS : 1];
+#pragma unroll
+    for (int j = LS - 1; j >= 0; --j) {
+      c32 g = mk(0.0f, 0.0f);
+#pragma unroll
+      for (int n = 0; n < NP; ++n) {
+        if (TAN) f[n] = cjmad(a[n], f[n], e[n]);
+        e[n] = cjmad(a[n], e[n], gv[j]);
+        if (GU) g = cjmad(hw[n], e[n], g);
+        if constexpr (TAN) {
+          c32 qv, rv;
+          if (REAL) {
+            qv = cscale(uv[j].r, e[n]);
+            rv = cscale(uv[j].r, f[n]);
+          } else {
+            qv = cjmul(uv[j], e[n]);
+            rv = cjmul(uv[j], f[n]);
+          }
+          pq[n][0] += qv.r;
+          pq[n][1] += qv.i;
+          pq[n][2] += rv.r;
+          pq[n][3] += rv.i;
+        }
+      }
+      if constexpr (GU) go[j] = g;
+    }
+    if constexpr (GU) {
+      // grad_u of the segment, after its steps (no stores inside the chain)
+#pragma unroll
+      for (int j = 0; j < LS; ++j) {
+        const int64_t t = tb + j;
+        if (l.fv && t < T) {
+          const int64_t el = l.base + t * F;
+          if (REAL) {
+            gu[el] = go[j].r + (gin ? gin[el] : 0.0f);
+          } else {
+            stc(gu, el, gin ? cadd(go[j], ldc(gin, el)) : go[j]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < NP; ++n)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) qr[n][k] += pq[n][k];
+#pragma unroll
+    for (int j = 0; j < LS; ++j) {
+      gv[j] = gn[j];
+      if constexpr (TAN) uv[j] = un[j];
+    }
+    p ^= 1;
+  }
+  if (!TAN) return;
+  // Per (filter, oscillator) sums over the block's segments, in a fixed order:
+  // the wavefront's segments by shuffles, then the wavefronts in LDS.
+#pragma unroll
+  for (int n = 0; n < NP; ++n)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      double v = (double)qr[n][k];
+      for (int off = kWave / 2; off >= kFC; off >>= 1) v += __shfl_down(v, off);
+      if (l.lane < kFC) s_red[((l.w * kFC) + l.lane) * 4 * NP + 4 * n + k] = v;
+    }
+  __syncthreads();
+  if (threadIdx.x < kFC && l.fv) {
+#pragma unroll
+    for (int n = 0; n < NP; ++n) {
+      if (n0 + n >= N) break;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        double acc = 0.0;
+        for (int v = 0; v < kWaves; ++v) acc += s_red[((v * kFC) + threadIdx.x) * 4 * NP + 4 * n + k];
+        part[((l.b * F + l.f) * N + n0 + n) * 4 + k] = acc;
+      }
     }
   }
 }
 
-// Coefficient-gradient reduction, stage 1: partial sums over a run of task
-// rows m in [m0, m1) (m = b*S + s), in fp64, in m order.  Thread i covers
-// (nj, f) = (i / F, i % F) of the 4*NP*F sums, so a wavefront reads
-// consecutive f of one row; the loads of 16 rows issue together.
-__global__ __launch_bounds__(256) void mosc_coef_stage1_kernel(const float* __restrict__ part,
-                                                               MoscShape sh, int NP, int64_t run,
-                                                               double* __restrict__ s1) {
-  const int64_t n_sums = (int64_t)4 * NP * sh.F;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n_sums) return;
-  const int64_t c = blockIdx.y;
-  const int64_t nj = i / sh.F, f = i - nj * sh.F;
-  const int64_t M = sh.B * sh.S;
-  const int64_t m0 = c * run, m1 = min(M, m0 + run);
-  const float* p = part + nj * sh.tasks + f;
-  double acc = 0.0;
-  for (int64_t m = m0; m < m1; m += 16) {
-    float v[16];
-#pragma unroll
-    for (int k = 0; k < 16; ++k) v[k] = m + k < m1 ? p[(m + k) * sh.F] : 0.0f;
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int k = 0; k < 16; ++k) acc += v[k];
-  }
-  s1[c * n_sums + i] = acc;
-}
-
-// Stage 2: grad_C1, grad_C2, grad_cw of oscillator n of filter f (one
-// wavefront per f*N + n) from the stage-1 sums of Q and R (lane l adds chunks
-// l, l+64, ..., then a fixed-shape wave sum), then
+// grad_C1, grad_C2, grad_cw of oscillator n of filter f (one wavefront per
+// f*N + n) from the partial sums of Q and R (lane l adds b = l, l + 64, ...,
+// then a fixed-shape wave sum), then
 //   grad_C1 = conj(cw C2) R,   grad_C2 = conj(cw) Q,   grad_cw = conj(C2) Q.
 // These are the reference's sums, with x_n = C2_n w_n and d_n = conj(cw_n) e_n
 // and the order of summation exchanged (u[r] enters w_n[t] with C1^(t-r)):
@@ -405,22 +529,23 @@ __global__ __launch_bounds__(256) void mosc_coef_stage1_kernel(const float* __re
 //                               = conj(C2_n) sum_r e_n[r] conj(u[r])
 //   sum_t d_n[t] conj(x_n[t-1]) = conj(cw_n C2_n) sum_r conj(u[r]) sum_{t>r} conj(C1)^(t-1-r) e_n[t]
 //                               = conj(cw_n C2_n) sum_r f_n[r] conj(u[r]).
-__global__ __launch_bounds__(kWave) void mosc_coef_stage2_kernel(
-    const double* __restrict__ s1, int64_t chunks, const float* __restrict__ c2,
-    const float* __restrict__ cw, MoscShape sh, int NP, float* __restrict__ gc1,
-    float* __restrict__ gc2, float* __restrict__ gcw) {
-  const int64_t fn = blockIdx.x;  // f*N + n: one wavefront each
-  const int64_t f = fn / sh.N;
-  const int n = (int)(fn - f * sh.N);
+__global__ __launch_bounds__(kWave) void mosc_coef_kernel(const double* __restrict__ part,
+                                                          int64_t B, int64_t F, int N,
+                                                          const float* __restrict__ c2,
+                                                          const float* __restrict__ cw,
+                                                          float* __restrict__ gc1,
+                                                          float* __restrict__ gc2,
+                                                          float* __restrict__ gcw) {
+  const int64_t fn = blockIdx.x;  // f*N + n
   const int lane = threadIdx.x;
-  const int64_t n_sums = (int64_t)4 * NP * sh.F;
   double s[4] = {0, 0, 0, 0};
-  for (int64_t c = lane; c < chunks; c += kWave) {
+  for (int64_t b = lane; b < B; b += kWave) {
+    const double* p = part + (b * F * N + fn) * 4;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) s[j] += s1[c * n_sums + ((int64_t)n * 4 + j) * sh.F + f];
+    for (int k = 0; k < 4; ++k) s[k] += p[k];
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) s[j] = wave_sum(s[j]);
+  for (int k = 0; k < 4; ++k) s[k] = wave_sum(s[k]);
   if (lane == 0) {
     const c64d q = mkd(s[0], s[1]), r = mkd(s[2], s[3]);
     const c64d g2 = dconj(widen(ldc(c2, fn))), gw = dconj(widen(ldc(cw, fn)));
@@ -441,86 +566,59 @@ int launch_status() {
 
 int pad_osc(int N) {
   int np = 1;
-  while (np < N) np <<= 1;
+  while (np < N && np < kMaxChunk) np <<= 1;
   return np;
 }
 
-MoscShape mosc_shape(int64_t B, int64_t T, int64_t F, int N) {
-  MoscShape sh;
-  sh.B = B;
-  sh.T = T;
-  sh.F = F;
-  sh.N = N;
-  const int64_t lanes = std::max<int64_t>(B * F, 1);
-  int64_t S = (kMoscLanes + lanes - 1) / lanes;
-  S = std::min<int64_t>(S, std::max<int64_t>(T / kMoscMinSeg, 1));
-  S = std::max<int64_t>(S, (T + kMoscMaxSeg - 1) / kMoscMaxSeg);
-  S = std::max<int64_t>(S, 1);
-  sh.L = T > 0 ? (T + S - 1) / S : 1;
-  sh.S = T > 0 ? (T + sh.L - 1) / sh.L : 1;
-  sh.tasks = B * sh.S * F;
-  return sh;
+dim3 mosc_grid(int64_t B, int64_t F) { return dim3((unsigned)(B * ((F + kFC - 1) / kFC))); }
+
+bool bad_shape(int64_t B, int64_t T, int64_t F, int64_t N) {
+  return B < 0 || T < 0 || F < 0 || N < 1 || N > (int64_t)1 << 20;
 }
 
-// Segment states of one kind: (b, s, n, f) complex.
-size_t mosc_states(const MoscShape& sh) {
-  return round256((size_t)(sh.B * sh.S * pad_osc(sh.N) * sh.F) * 8);
-}
-
-// Workspace: forward, the w entries; backward, the adjoint pair's entries and
-// the per-task partial sums.
-struct MoscWs {
-  size_t seg, segf, part, s1, total;
-};
-// Rows of task partials per stage-1 chunk of the coefficient reduction, and
-// the number of chunks.
-constexpr int64_t kCoefRun = 16;
-int64_t coef_run(const MoscShape&) { return kCoefRun; }
-int64_t coef_chunks(const MoscShape& sh) {
-  return std::max<int64_t>((sh.B * sh.S + coef_run(sh) - 1) / coef_run(sh), 1);
-}
-MoscWs mosc_ws(const MoscShape& sh, bool backward) {
-  const size_t states = mosc_states(sh);
-  MoscWs w;
-  w.seg = 0;
-  if (!backward) {
-    w.segf = w.part = w.s1 = w.total = states;
-    return w;
-  }
-  w.segf = states;
-  w.part = 2 * states;
-  w.s1 = w.part + round256((size_t)sh.tasks * pad_osc(sh.N) * 4 * 4);
-  w.total = w.s1 + round256((size_t)coef_chunks(sh) * 4 * pad_osc(sh.N) * sh.F * 8);
-  return w;
+// Workspace: forward, a complex (B,T,F) partial when a |y| output needs more
+// than one chunk of oscillators; backward, the per-(batch, filter, oscillator)
+// partial sums.
+size_t mosc_ws(int64_t B, int64_t T, int64_t F, int64_t N, bool backward) {
+  if (backward) return round256(sizeof(double) * 4 * (size_t)std::max<int64_t>(B * F * N, 1));
+  return N > kMaxChunk ? round256(sizeof(float) * 2 * (size_t)(B * T * F)) : 0;
 }
 
 template <class Fn>
-int with_np(int N, Fn&& fn) {
-  switch (pad_osc(N)) {
-    case 1: fn(std::integral_constant<int, 1>{}); return RQF_OK;
-    case 2: fn(std::integral_constant<int, 2>{}); return RQF_OK;
-    case 4: fn(std::integral_constant<int, 4>{}); return RQF_OK;
-    case 8: fn(std::integral_constant<int, 8>{}); return RQF_OK;
-    default: return RQF_ERR_ARG;
+void with_np(int np, Fn&& fn) {
+  switch (np) {
+    case 1: fn(std::integral_constant<int, 1>{}); return;
+    case 2: fn(std::integral_constant<int, 2>{}); return;
+    default: fn(std::integral_constant<int, 4>{}); return;
   }
 }
 
-bool bad_shape(int64_t B, int64_t T, int64_t F, int64_t N) {
-  return B < 0 || T < 0 || F < 0 || N < 1 || N > kMoscMaxOsc;
+template <int NP, bool REAL>
+void launch_fwd(const float* c1, const float* c2, const float* cw, const float* u,
+                const float* yin, float* yout, bool abs_out, int64_t B, int64_t T, int64_t F,
+                int N, int n0, hipStream_t s) {
+  const dim3 grid = mosc_grid(B, F), block(kThreads);
+  if (cw && abs_out)
+    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, true, true>), grid, block, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
+  else if (cw)
+    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, true, false>), grid, block, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
+  else if (abs_out)
+    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, false, true>), grid, block, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
+  else
+    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, false, false>), grid, block, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
 }
 
-// Phases 1-3 of the backward, for the gradients requested (tan: the
-// coefficient sums; gu: grad_u).
-template <int NP, bool REAL, bool TAN, bool GU>
+template <int NP, bool REAL>
 void launch_bwd(const float* c1, const float* c2, const float* cw, const float* u,
-                const float* gy, float* segb, float* segf, float* gu, float* part,
-                const MoscShape& sh, hipStream_t s) {
-  const dim3 block(256), grid((unsigned)((sh.tasks + 255) / 256));
-  const dim3 cgrid((unsigned)((sh.B * NP * sh.F + 255) / 256));
-  hipLaunchKernelGGL((mosc_bwd_local_kernel<NP, TAN>), grid, block, 0, s, c1, gy, segb, segf, sh);
-  hipLaunchKernelGGL((mosc_carry_kernel<NP, true, TAN>), cgrid, block, 0, s, c1, segb, segf, sh);
-  hipLaunchKernelGGL((mosc_bwd_final_kernel<NP, REAL, TAN, GU>), grid, block, 0, s, c1, c2, cw,
-                     u, gy, segb, segf, gu, part, sh);
+                const float* gy, const float* gin, float* gu, double* part, bool tan, bool gu_on,
+                int64_t B, int64_t T, int64_t F, int N, int n0, hipStream_t s) {
+  const dim3 grid = mosc_grid(B, F), block(kThreads);
+  if (tan && gu_on)
+    hipLaunchKernelGGL((mosc_bwd_kernel<NP, REAL, true, true>), grid, block, 0, s, c1, c2, cw, u, gy, gin, gu, part, T, F, N, n0);
+  else if (tan)
+    hipLaunchKernelGGL((mosc_bwd_kernel<NP, REAL, true, false>), grid, block, 0, s, c1, c2, cw, u, gy, gin, gu, part, T, F, N, n0);
+  else
+    hipLaunchKernelGGL((mosc_bwd_kernel<NP, REAL, false, true>), grid, block, 0, s, c1, c2, cw, u, gy, gin, gu, part, T, F, N, n0);
 }
 
 }  // namespace
@@ -530,7 +628,7 @@ void launch_bwd(const float* c1, const float* c2, const float* cw, const float* 
 extern "C" size_t rqf_multi_osc_workspace(int64_t B, int64_t T, int64_t F, int64_t N,
                                           int32_t backward) {
   if (bad_shape(B, T, F, N)) return 0;
-  return mosc_ws(mosc_shape(B, T, F, (int)N), backward != 0).total;
+  return mosc_ws(B, T, F, N, backward != 0);
 }
 
 extern "C" int rqf_multi_osc_fwd(const float* c1, const float* c2, const float* cw,
@@ -543,44 +641,29 @@ extern "C" int rqf_multi_osc_fwd(const float* c1, const float* c2, const float* 
   if (!aligned8(c1) || !aligned8(c2) || !aligned8(cw) || !(u_real ? aligned4(u) : aligned8(u)) ||
       !(out_abs ? aligned4(out) : aligned8(out)))
     return RQF_ERR_ALIGN;
-  const MoscShape sh = mosc_shape(B, T, F, (int)N);
-  const MoscWs w = mosc_ws(sh, false);
-  if (!workspace || workspace_bytes < w.total) return RQF_ERR_WORKSPACE;
-  float* seg = (float*)((char*)workspace + w.seg);
+  const size_t need = mosc_ws(B, T, F, N, false);
+  if (need && (!workspace || workspace_bytes < need)) return RQF_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 block(256), grid((unsigned)((sh.tasks + 255) / 256));
-  const int64_t carriers = B * pad_osc((int)N) * F;
-  const dim3 cgrid((unsigned)((carriers + 255) / 256));
-  const int rc = with_np((int)N, [&](auto npc) {
-    constexpr int NP = decltype(npc)::value;
-    if (u_real)
-      hipLaunchKernelGGL((mosc_fwd_local_kernel<NP, true>), grid, block, 0, s, c1, u, seg, sh);
-    else
-      hipLaunchKernelGGL((mosc_fwd_local_kernel<NP, false>), grid, block, 0, s, c1, u, seg, sh);
-    hipLaunchKernelGGL((mosc_carry_kernel<NP, false, false>), cgrid, block, 0, s, c1, seg,
-                       nullptr, sh);
-    const bool has_cw = cw != nullptr;
-    if (u_real) {
-      if (has_cw && out_abs)
-        hipLaunchKernelGGL((mosc_fwd_final_kernel<NP, true, true, true>), grid, block, 0, s, c1, c2, cw, u, seg, out, sh);
-      else if (has_cw)
-        hipLaunchKernelGGL((mosc_fwd_final_kernel<NP, true, true, false>), grid, block, 0, s, c1, c2, cw, u, seg, out, sh);
-      else if (out_abs)
-        hipLaunchKernelGGL((mosc_fwd_final_kernel<NP, true, false, true>), grid, block, 0, s, c1, c2, cw, u, seg, out, sh);
+  const int chunks = (int)((N + kMaxChunk - 1) / kMaxChunk);
+  // Complex partial of y between chunks: the output itself, or the workspace
+  // when the output is |y|.
+  float* ypart = out_abs ? (float*)workspace : out;
+  for (int c = 0; c < chunks; ++c) {
+    const int n0 = c * kMaxChunk;
+    const int np = pad_osc((int)std::min<int64_t>(N - n0, kMaxChunk));
+    const bool last = c + 1 == chunks;
+    const float* yin = c > 0 ? ypart : nullptr;
+    float* yout = last ? out : ypart;
+    const bool abs_here = last && out_abs;
+    with_np(np, [&](auto npc) {
+      constexpr int NP = decltype(npc)::value;
+      if (u_real)
+        launch_fwd<NP, true>(c1, c2, cw, u, yin, yout, abs_here, B, T, F, (int)N, n0, s);
       else
-        hipLaunchKernelGGL((mosc_fwd_final_kernel<NP, true, false, false>), grid, block, 0, s, c1, c2, cw, u, seg, out, sh);
-    } else {
-      if (has_cw && out_abs)
-        hipLaunchKernelGGL((mosc_fwd_final_kernel<NP, false, true, true>), grid, block, 0, s, c1, c2, cw, u, seg, out, sh);
-      else if (has_cw)
-        hipLaunchKernelGGL((mosc_fwd_final_kernel<NP, false, true, false>), grid, block, 0, s, c1, c2, cw, u, seg, out, sh);
-      else if (out_abs)
-        hipLaunchKernelGGL((mosc_fwd_final_kernel<NP, false, false, true>), grid, block, 0, s, c1, c2, cw, u, seg, out, sh);
-      else
-        hipLaunchKernelGGL((mosc_fwd_final_kernel<NP, false, false, false>), grid, block, 0, s, c1, c2, cw, u, seg, out, sh);
-    }
-  });
-  return rc ? rc : launch_status();
+        launch_fwd<NP, false>(c1, c2, cw, u, yin, yout, abs_here, B, T, F, (int)N, n0, s);
+    });
+  }
+  return launch_status();
 }
 
 extern "C" int rqf_multi_osc_bwd(const float* c1, const float* c2, const float* cw,
@@ -596,49 +679,30 @@ extern "C" int rqf_multi_osc_bwd(const float* c1, const float* c2, const float* 
       !(u_real ? aligned4(u) && aligned4(grad_u) : aligned8(u) && aligned8(grad_u)) ||
       !aligned8(grad_c1) || !aligned8(grad_c2) || !aligned8(grad_cw))
     return RQF_ERR_ALIGN;
-  const MoscShape sh = mosc_shape(B, T, F, (int)N);
-  const MoscWs w = mosc_ws(sh, true);
-  if (w.total && (!workspace || workspace_bytes < w.total)) return RQF_ERR_WORKSPACE;
-  char* ws = (char*)workspace;
-  float* segb = (float*)(ws + w.seg);
-  float* segf = (float*)(ws + w.segf);
-  float* part = (float*)(ws + w.part);
+  const size_t need = mosc_ws(B, T, F, N, true);
+  if (!workspace || workspace_bytes < need) return RQF_ERR_WORKSPACE;
+  double* part = (double*)workspace;
   const bool coefs = grad_c1 || grad_c2 || grad_cw;
   hipStream_t s = (hipStream_t)stream;
-  const int rc = with_np((int)N, [&](auto npc) {
-    constexpr int NP = decltype(npc)::value;
-    if (B * T == 0 || (!coefs && !grad_u)) return;
-    if (u_real) {
-      if (coefs && grad_u)
-        launch_bwd<NP, true, true, true>(c1, c2, cw, u, grad_out, segb, segf, grad_u, part, sh, s);
-      else if (coefs)
-        launch_bwd<NP, true, true, false>(c1, c2, cw, u, grad_out, segb, segf, grad_u, part, sh, s);
-      else
-        launch_bwd<NP, true, false, true>(c1, c2, cw, u, grad_out, segb, segf, grad_u, part, sh, s);
-    } else {
-      if (coefs && grad_u)
-        launch_bwd<NP, false, true, true>(c1, c2, cw, u, grad_out, segb, segf, grad_u, part, sh, s);
-      else if (coefs)
-        launch_bwd<NP, false, true, false>(c1, c2, cw, u, grad_out, segb, segf, grad_u, part, sh, s);
-      else
-        launch_bwd<NP, false, false, true>(c1, c2, cw, u, grad_out, segb, segf, grad_u, part, sh, s);
+  if (B * T > 0 && (coefs || grad_u)) {
+    const int chunks = (int)((N + kMaxChunk - 1) / kMaxChunk);
+    for (int c = 0; c < chunks; ++c) {
+      const int n0 = c * kMaxChunk;
+      const int np = pad_osc((int)std::min<int64_t>(N - n0, kMaxChunk));
+      const float* gin = c > 0 ? grad_u : nullptr;
+      with_np(np, [&](auto npc) {
+        constexpr int NP = decltype(npc)::value;
+        if (u_real)
+          launch_bwd<NP, true>(c1, c2, cw, u, grad_out, gin, grad_u, part, coefs, grad_u != nullptr,
+                               B, T, F, (int)N, n0, s);
+        else
+          launch_bwd<NP, false>(c1, c2, cw, u, grad_out, gin, grad_u, part, coefs,
+                                grad_u != nullptr, B, T, F, (int)N, n0, s);
+      });
     }
-  });
-  if (rc) return rc;
-  if (coefs) {
-    MoscShape rs = sh;
-    if (B * T == 0) {
-      rs.B = 0;  // no partial rows: the reduction writes zeros
-      rs.S = 0;
-    }
-    const int NP = pad_osc((int)N);
-    const int64_t chunks = coef_chunks(sh), n_sums = (int64_t)4 * NP * F;
-    double* s1 = (double*)(ws + w.s1);
-    hipLaunchKernelGGL(mosc_coef_stage1_kernel,
-                       dim3((unsigned)((n_sums + 255) / 256), (unsigned)chunks), dim3(256), 0, s,
-                       part, rs, NP, coef_run(sh), s1);
-    hipLaunchKernelGGL(mosc_coef_stage2_kernel, dim3((unsigned)(F * N)), dim3(kWave), 0, s, s1,
-                       chunks, c2, cw, rs, NP, grad_c1, grad_c2, grad_cw);
   }
+  if (coefs)
+    hipLaunchKernelGGL(mosc_coef_kernel, dim3((unsigned)(F * N)), dim3(kWave), 0, s, part,
+                       B * T > 0 ? B : (int64_t)0, F, (int)N, c2, cw, grad_c1, grad_c2, grad_cw);
   return launch_status();
 }

@@ -54,17 +54,14 @@ constexpr int kTM = RQF_PROJ_TM, kTN = RQF_PROJ_TN;
 #ifndef RQF_PROJ_WAVES
 #define RQF_PROJ_WAVES 3
 #endif
-constexpr int kPM = 64 * kTM, kPN = 64 * kTN, kPK = 16, kPThreads = 256, kPXcds = 8;
+constexpr int kPM = 64 * kTM, kPN = 64 * kTN, kPK = 16, kPThreads = 256;
 // The host pads the weights' M to a multiple of 128 whatever the tile.
 constexpr int kPMPad = 128;
 static_assert(kPM % kPMPad == 0 || kPMPad % kPM == 0, "M tiles cover the padded weights");
 
 // Blocks are dealt round-robin over the XCDs; give each XCD a contiguous range
 // of tile ids.
-__device__ __forceinline__ int64_t proj_xcd_order(int64_t P, int64_t n) {
-  const int64_t x = P % kPXcds, j = P / kPXcds, q = n / kPXcds, r = n % kPXcds;
-  return x * q + (x < r ? x : r) + j;
-}
+__device__ __forceinline__ int64_t proj_xcd_order(int64_t P, int64_t n) { return xcd_contiguous(P, n); }
 
 // Real B row j (0-based after the complex rows), or null past the last row.
 __device__ __forceinline__ const float* real_row(const rqf_proj_gemm_args& g, int64_t j) {

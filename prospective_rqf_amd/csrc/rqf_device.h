@@ -113,6 +113,17 @@ __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
 }
 
+// MI355X deals the blocks of a launch round-robin over its 8 XCDs (block P
+// runs on XCD P % 8), and each XCD has its own L2.  Map P to a logical block
+// id so that every XCD runs one contiguous range of the n logical blocks:
+// neighbouring logical blocks, which usually share cache lines, then share an
+// L2.  A bijection on [0, n) for any n.
+constexpr int kXcdCount = 8;
+__device__ __forceinline__ int64_t xcd_contiguous(int64_t P, int64_t n) {
+  const int64_t x = P % kXcdCount, j = P / kXcdCount, q = n / kXcdCount, r = n % kXcdCount;
+  return x * q + (x < r ? x : r) + j;
+}
+
 // ---------------------------------------------------------------------------
 // Cross-lane primitives
 // ---------------------------------------------------------------------------

@@ -82,14 +82,10 @@ namespace {
 constexpr int kFwdK = RQF_SEL_FWD_K;  // steps per lane per tile, forward
 constexpr int kBwdK = RQF_SEL_BWD_K;  // steps per lane per tile, backward
 constexpr int kRowsPerBlock = 4;      // wavefronts (rows) per block
-constexpr int kXcds = 8;              // MI355X: 8 XCDs, blocks dealt round-robin
+constexpr int kXcds = kXcdCount;      // MI355X: 8 XCDs, blocks dealt round-robin
 
-// Blocks are dispatched round-robin over the XCDs; remap so that XCD x runs a
-// contiguous range of logical blocks.
-__device__ __forceinline__ int64_t xcd_remap(int64_t P, int64_t n) {
-  const int64_t x = P % kXcds, j = P / kXcds, q = n / kXcds, r = n % kXcds;
-  return x * q + (x < r ? x : r) + j;
-}
+// XCD x runs a contiguous range of logical blocks.
+__device__ __forceinline__ int64_t xcd_remap(int64_t P, int64_t n) { return xcd_contiguous(P, n); }
 
 // Option specialisation.  Like the reference's constexpr kernel flags
 // (selective_scan_kernel.py:35-46), the structural options can be compile-time

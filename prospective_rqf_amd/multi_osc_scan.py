@@ -22,8 +22,9 @@ Per filter f with N oscillators (coefficient index ``f*N + n``)::
     x_n[t] = C1_n x_n[t-1] + C2_n u[t]
     y[t]   = sum_n cw_n x_n[t]          cw = c_weights[:, 0] + 1j*c_weights[:, 1]
 
-The kernels are ``rqf_multi_osc_fwd`` / ``rqf_multi_osc_bwd`` of librqf_hip.so
-(N <= 8).  Gradients follow the reference's kernels: ``grad_C1 = sum d
+The kernels are ``rqf_multi_osc_fwd`` / ``rqf_multi_osc_bwd`` of librqf_hip.so;
+any N >= 1 (the reference pads N to a power of two, triton_scan_kernel.py:1855-1900;
+the kernels run the oscillators in chunks of up to four).  Gradients follow the reference's kernels: ``grad_C1 = sum d
 conj(x[t-1])``, ``grad_C2 = sum d conj(u)``, ``grad_u = sum_n conj(C2_n) d_n``
 (its real part for real ``u``) and ``grad_c_weights = (Re, Im) of
 sum grad_y conj(x_n)``, with ``d_n[t] = conj(C1_n) d_n[t+1] + conj(cw_n)
@@ -41,7 +42,7 @@ from torch.autograd.function import once_differentiable
 
 from prospective_rqf_amd import _lib
 
-MAX_OSC = 8
+MAX_OSC = 1 << 20  # a bound on the C ABI's argument, not on the kernels
 
 
 def _c64(t: torch.Tensor) -> torch.Tensor:
@@ -76,7 +77,7 @@ def _check(u: torch.Tensor, C1: torch.Tensor, C2: torch.Tensor, num_osc: int) ->
     if u.dim() != 3:
         raise ValueError(f"expected (batch, time, filters) input, got shape {tuple(u.shape)}")
     if not 1 <= num_osc <= MAX_OSC:
-        raise ValueError(f"num_osc must be in [1, {MAX_OSC}] for the HIP kernels, got {num_osc}")
+        raise ValueError(f"num_osc must be in [1, {MAX_OSC}], got {num_osc}")
     B, T, F = u.shape
     if C1.shape != (F * num_osc,) or C2.shape != (F * num_osc,):
         raise ValueError(f"C1/C2 must have shape ({F * num_osc},) for {F} filters x {num_osc} "

@@ -1,9 +1,11 @@
 """GPU parity of the multi-oscillator scans and the fused |y| readout.
 
 Compares ``rqf_multi_osc_fwd`` / ``rqf_multi_osc_bwd`` (through the reference's
-Python names) with the fp64 oracle, for complex and real inputs, one to eight
-oscillators, segment edges (T below, at and above the 256-step segment bound)
-and the autograd boundaries, including the ``needs_input_grad`` gating the
+Python names) with the fp64 oracle, for complex and real inputs, 1 to 17
+oscillators (more than 4 run in chunks of 4), sequence lengths below, at and
+across the kernels' pass lengths (a block walks T in passes of 256 to 1024
+steps; T = 3000 takes three or more), filter counts that leave a partial
+16-filter group, and the autograd boundaries, including the ``needs_input_grad`` gating the
 reference's kernels implement (triton_scan_kernel.py:2280-2410).  Bar:
 normwise max relative error <= 1e-4 per output and gradient tensor.
 """
@@ -57,7 +59,7 @@ SHAPES = [(2, 1, 5), (2, 37, 3), (3, 256, 4), (2, 257, 3), (1, 1000, 2), (4, 300
 
 
 @pytest.mark.parametrize("real", [False, True])
-@pytest.mark.parametrize("N", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("N", [1, 2, 3, 4, 5, 8, 12, 17])
 @pytest.mark.parametrize("shape", SHAPES)
 def test_multi_osc_forward_backward(shape, N, real):
     B, T, F = shape
@@ -213,12 +215,14 @@ def test_sequential_scan_abs(real, in_f):
     assert got_g.requires_grad and relerr(got_g, want) <= PARITY_RTOL
 
 
-def test_rejects_unsupported_oscillator_counts_and_host_tensors():
+def test_rejects_bad_oscillator_shapes_and_host_tensors():
     u = torch.zeros(1, 4, 2, dtype=torch.complex64, device="cuda")
     c = torch.zeros(2 * 9, dtype=torch.complex64, device="cuda")
     cw = torch.zeros(2 * 9, 2, device="cuda")
     with pytest.raises(ValueError):
-        mo._triton_sequential_scan_multi_osc(c, c, u, cw, 9)
+        mo._triton_sequential_scan_multi_osc(c, c, u, cw, 0)
+    with pytest.raises(ValueError):  # coefficients for 9 oscillators, 8 claimed
+        mo._triton_sequential_scan_multi_osc(c, c, u, cw, 8)
     with pytest.raises(RuntimeError):
         mo._triton_sequential_scan_multi_osc(c.cpu()[:4], c.cpu()[:4], u.cpu(), cw.cpu()[:4], 2)
 

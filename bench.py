@@ -306,7 +306,7 @@ def plan_selective(cfg, args, dev):
     kernels = {
         "rqf_selective_fwd": "selective_fwd_rb_kernel",
         "rqf_selective_bwd": ("team_build_kernel + selective_bwd_team_kernel + "
-                              "team_reduce_kernel + partial_reduce_kernel"),
+                              "bwd_finish_kernel"),
     }
     if stack != "none":
         contract += f"; encoder residual add (raw + h, act + h) {stack}"

@@ -1133,35 +1133,54 @@ __global__ __launch_bounds__(256) void team_build_kernel(const int64_t* __restri
                                                          int* gteam, int* nteams, int* gcount,
                                                          int* moff, int* sfirst, int* sn,
                                                          int* gsplit, int* nsplits) {
-  __shared__ int sg[kBuildLds];
+  __shared__ int4 sg4[kBuildLds / 4];
   __shared__ int s_count[kBuildGroups], s_moff[kBuildGroups], s_gteam[kBuildGroups + 1];
+  __shared__ int s_gsplit[kBuildGroups + 1];
+  int* sg = reinterpret_cast<int*>(sg4);
   const int tid = threadIdx.x, nt = blockDim.x;
   if (F <= kBuildLds && G <= kBuildGroups) {
-    for (int f = tid; f < F; f += nt) sg[f] = groups ? clamp_group(groups[f], G) : 0;
+    // Everything after the one read of `groups` stays in LDS; the global
+    // tables are written once and never read back here.
+    const int F4 = (F + 3) & ~3;
+    for (int f = tid; f < F4; f += nt) sg[f] = f < F ? (groups ? clamp_group(groups[f], G) : 0) : -1;
     for (int g = tid; g < G; g += nt) s_count[g] = 0;
     __syncthreads();
-    for (int f = tid; f < F; f += nt)
-      if ((unsigned)sg[f] < (unsigned)G) atomicAdd(&s_count[sg[f]], 1);
+    for (int f = tid; f < F; f += nt) atomicAdd(&s_count[sg[f]], 1);
     __syncthreads();
     if (tid == 0) {
-      int off = 0, toff = 0;
+      int off = 0, toff = 0, soff = 0;
       for (int g = 0; g < G; ++g) {
+        const int ntm = (s_count[g] + kTeam - 1) / kTeam;
         s_moff[g] = off;
         s_gteam[g] = toff;
+        s_gsplit[g] = soff;
         off += s_count[g];
-        toff += (s_count[g] + kTeam - 1) / kTeam;
+        toff += ntm;
+        soff += (ntm + Q - 1) / Q;  // splits: runs of up to Q consecutive teams
       }
       s_gteam[G] = toff;
+      s_gsplit[G] = soff;
       *nteams = toff;
+      *nsplits = soff;
     }
     __syncthreads();
+    // Stable rank of channel f within its group: earlier channels of the same
+    // group, counted four at a time from LDS.
     for (int f = tid; f < F; f += nt) {
       const int g = sg[f];
       int rank = 0;
-      for (int q = 0; q < f; ++q) rank += sg[q] == g;
+      const int q4 = f >> 2;
+      for (int j = 0; j < q4; ++j) {
+        const int4 v = sg4[j];
+        rank += (v.x == g) + (v.y == g) + (v.z == g) + (v.w == g);
+      }
+      for (int q = q4 << 2; q < f; ++q) rank += sg[q] == g;
       order[s_moff[g] + rank] = f;
     }
-    for (int g = tid; g <= G; g += nt) gteam[g] = s_gteam[g];
+    for (int g = tid; g <= G; g += nt) {
+      gteam[g] = s_gteam[g];
+      gsplit[g] = s_gsplit[g];
+    }
     for (int g = tid; g < G; g += nt) {
       const int n = s_count[g], ntm = (n + kTeam - 1) / kTeam;
       gcount[g] = n;
@@ -1172,10 +1191,14 @@ __global__ __launch_bounds__(256) void team_build_kernel(const int64_t* __restri
         count[id] = min(kTeam, n - t * kTeam);
         group[id] = g;
       }
+      for (int j = 0; j * Q < ntm; ++j) {
+        sfirst[s_gsplit[g] + j] = s_gteam[g] + j * Q;
+        sn[s_gsplit[g] + j] = min(Q, ntm - j * Q);
+      }
     }
-  } else {
-    team_build_global(groups, F, G, order, first, count, group, gteam, nteams, gcount, moff);
+    return;
   }
+  team_build_global(groups, F, G, order, first, count, group, gteam, nteams, gcount, moff);
   // Splits: runs of up to Q consecutive teams of one group.
   __syncthreads();
   if (tid == 0) {
@@ -1381,13 +1404,11 @@ __global__ __launch_bounds__(kTeam* kWave)
 
 // dd[g, b, t] = sum over the splits of group g (fixed order) of dd_part[split, b, t],
 // for groups not served by exactly one split (those wrote dd directly).
-// VEC: N % 4 == 0 and 16-byte aligned dd; each thread sums one float4.
+// VEC: N % 4 == 0 and 16-byte aligned dd; thread i sums one float4.
 template <bool VEC>
-__global__ __launch_bounds__(256) void team_reduce_kernel(const float* __restrict__ dd_part,
-                                                          const int* __restrict__ gsplit,
-                                                          float* __restrict__ dd, int64_t G,
-                                                          int64_t N) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void team_reduce_at(int64_t i, const float* __restrict__ dd_part,
+                                               const int* __restrict__ gsplit,
+                                               float* __restrict__ dd, int64_t G, int64_t N) {
   if (VEC) {
     const int64_t n4 = N / 4;
     if (i >= G * n4) return;
@@ -1451,12 +1472,11 @@ __global__ __launch_bounds__(256) void group_reduce_kernel(const float* __restri
 // dbias[f] = sum_b partial[f*B + b] in fp64, same for dtheta: one wavefront
 // per channel, lane l sums b = l, l+64, ... in order, then a fixed-shape wave
 // reduction (deterministic).
-__global__ __launch_bounds__(kWave) void partial_reduce_kernel(const double* __restrict__ partial,
-                                                               float* __restrict__ dbias,
-                                                               float* __restrict__ dtheta,
-                                                               int64_t F, int64_t B) {
-  const int64_t f = blockIdx.x;
-  const int lane = threadIdx.x;
+__device__ __forceinline__ void partial_reduce_at(int64_t f, int lane,
+                                                  const double* __restrict__ partial,
+                                                  float* __restrict__ dbias,
+                                                  float* __restrict__ dtheta, int64_t F,
+                                                  int64_t B) {
   double sb = 0.0, st = 0.0;
   for (int64_t b = lane; b < B; b += kWave) {
     sb += partial[f * B + b];
@@ -1468,6 +1488,42 @@ __global__ __launch_bounds__(kWave) void partial_reduce_kernel(const double* __r
     dbias[f] = (float)sb;
     dtheta[f] = (float)st;
   }
+}
+
+// The backward's closing pass, one launch: blocks [0, dd_blocks) sum the
+// split partial rows of the warp-logit gradient (dd_part may be null, then
+// dd_blocks is 0), the blocks after them reduce dbias and dtheta, one
+// wavefront per channel.
+constexpr int kFinishThreads = 256;
+template <bool VEC>
+__global__ __launch_bounds__(kFinishThreads) void bwd_finish_kernel(
+    const float* __restrict__ dd_part, const int* __restrict__ gsplit, float* __restrict__ dd,
+    int64_t G, int64_t N, int64_t dd_blocks, const double* __restrict__ partial,
+    float* __restrict__ dbias, float* __restrict__ dtheta, int64_t F, int64_t B) {
+  if ((int64_t)blockIdx.x < dd_blocks) {
+    team_reduce_at<VEC>((int64_t)blockIdx.x * kFinishThreads + threadIdx.x, dd_part, gsplit, dd,
+                        G, N);
+    return;
+  }
+  const int64_t f = ((int64_t)blockIdx.x - dd_blocks) * (kFinishThreads / kWave) + wave_id();
+  if (f < F) partial_reduce_at(f, lane_id(), partial, dbias, dtheta, F, B);
+}
+
+void launch_finish(const float* dd_part, const int* gsplit, float* dd, int64_t G, int64_t N,
+                   const double* partial, float* dbias, float* dtheta, int64_t F, int64_t B,
+                   hipStream_t s) {
+  const bool vec = dd_part && N % 4 == 0 && ((uintptr_t)dd & 15) == 0;
+  const int64_t items = dd_part ? (vec ? G * (N / 4) : G * N) : 0;
+  const int64_t dd_blocks = (items + kFinishThreads - 1) / kFinishThreads;
+  const int64_t pr_blocks = (F + kFinishThreads / kWave - 1) / (kFinishThreads / kWave);
+  const dim3 grid((unsigned)(dd_blocks + pr_blocks)), block(kFinishThreads);
+  if (dd_blocks + pr_blocks == 0) return;
+  if (vec)
+    hipLaunchKernelGGL(bwd_finish_kernel<true>, grid, block, 0, s, dd_part, gsplit, dd, G, N,
+                       dd_blocks, partial, dbias, dtheta, F, B);
+  else
+    hipLaunchKernelGGL(bwd_finish_kernel<false>, grid, block, 0, s, dd_part, gsplit, dd, G, N,
+                       dd_blocks, partial, dbias, dtheta, F, B);
 }
 
 // Zero-fill of n 32-bit words (graph-capture safe, unlike a memset node).
@@ -1760,15 +1816,8 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
         hipLaunchKernelGGL((selective_bwd_team_kernel<O, false>), grid, block, 0, s, *in, z, ent,
                            ent_chunk, nc, gy, gx, (int)truncated, tm, o);
     });
-    if (in->has_warp) {
-      const int64_t N = in->B * T;
-      if (N % 4 == 0 && aligned16(dd))
-        hipLaunchKernelGGL(team_reduce_kernel<true>, dim3((unsigned)((in->G * N / 4 + 255) / 256)),
-                           dim3(256), 0, s, o.dd_part, gsplit, dd, in->G, N);
-      else
-        hipLaunchKernelGGL(team_reduce_kernel<false>, dim3((unsigned)((in->G * N + 255) / 256)),
-                           dim3(256), 0, s, o.dd_part, gsplit, dd, in->G, N);
-    }
+    launch_finish(o.dd_part, gsplit, dd, in->G, in->B * T, partial, dbias, dtheta, in->F, in->B,
+                  s);
 #else
     o.ddc = in->has_warp ? (float*)(ws + w.dd) : nullptr;
     const dim3 grid = row_grid(in), block(kRowsPerBlock * kWave);
@@ -1783,14 +1832,13 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
       hipLaunchKernelGGL(group_reduce_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, s,
                          o.ddc, in->groups, dd, (int)in->F, (int)in->G, N);
     }
+    launch_finish(nullptr, nullptr, nullptr, 0, 0, partial, dbias, dtheta, in->F, in->B, s);
 #endif
   } else {
     zero_words(partial, 4 * R, s);
     if (in->has_warp && dd) zero_words(dd, in->G * in->B * T, s);
+    launch_finish(nullptr, nullptr, nullptr, 0, 0, partial, dbias, dtheta, in->F, in->B, s);
   }
-  if (in->F > 0)
-    hipLaunchKernelGGL(partial_reduce_kernel, dim3((unsigned)in->F), dim3(kWave), 0, s, partial,
-                       dbias, dtheta, in->F, in->B);
   return launch_status();
 }
 

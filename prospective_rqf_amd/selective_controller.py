@@ -1,0 +1,310 @@
+"""Selector heads -> ``SelectiveScanInputs``: the producer side of the selective scan.
+
+Restates the reference's selective controller as plain tensor code, so that
+what reaches the selective kernels can be built (and checked) without the
+reference's model classes:
+
+* ``SelectiveRQFConfig``: the controller settings and their validation
+  (rqf_models/backbones/rqf/selective.py:17-79).
+* ``FilterState``: the log-space leaves and bound buffers of one RQF filter
+  module that the controller reads and projects
+  (rqf_models/backbones/rqf/filter.py:216-262, 365-434): ``tau``, ``gamma``,
+  ``theta``, the frequency band (``_theta_bounds``) and ``clamp_parameters``.
+  The selective Pure RQF block accepts log-space parameters only
+  (pure.py:115-121), so only that parametrisation is restated.
+* ``SelectiveController``: the construction-time checks, the parameter
+  projection and the warp-group ranks (selective.py:100-165), and ``forward``,
+  which projects a complex ``(I, B, T)`` selector source through the gamma,
+  warp and write heads and assembles the scan inputs (selective.py:201-278).
+
+``forward`` is ``assemble(*project(source))``: ``project`` is the head GEMM,
+``assemble`` everything after it (bias logit under the interior or
+straight-through clamp, horizon broadcast, theta band, options tuple).
+Benchmarks and tests call ``assemble`` with seeded logits.
+
+The reference's ``_SplitProjection`` (selective.py:82-97) exists to skip
+zero-gradient blocks and autocast in backward; its forward is the one GEMM
+``cat(weights) @ v`` split by head, which is what ``project`` computes.
+"""
+
+from __future__ import annotations
+
+import math
+from collections.abc import Mapping
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+from torch import Tensor
+
+from prospective_rqf_amd.selective_scan import SelectiveScanInputs
+
+
+@dataclass(frozen=True)
+class SelectiveRQFConfig:
+    """Controller settings, same fields, defaults and checks as selective.py:17-66."""
+
+    gamma_control: bool = True
+    gamma_link: str = "sigmoid"
+    gamma_features: str = "real_imag"
+    gamma_max_log_scale: float = math.log(1.25)
+    gamma_edge: str = "interior_clamp"
+    gamma_edge_margin: float = 1e-3
+    write_control: bool = False
+    write_link: str = "sigmoid"
+    write_max: float = 2.0
+    frequency_warp: str = "none"
+    warp_bound: str = "band"
+    num_groups: int = 4
+    max_log_scale: float = math.log(1.25)
+    input_source: str = "layer_output"
+
+    def __post_init__(self) -> None:
+        for name, choices in (
+            ("gamma_link", {"sigmoid", "log_shift"}),
+            ("gamma_features", {"real_imag", "modulus"}),
+            ("gamma_edge", {"interior_clamp", "st_clamp"}),
+            ("write_link", {"affine", "sigmoid"}),
+            ("frequency_warp", {"none", "global", "grouped"}),
+            ("warp_bound", {"band", "none"}),
+            ("input_source", {"layer_input", "layer_output"}),
+        ):
+            if getattr(self, name) not in choices:
+                raise ValueError(f"selective.{name} must be one of {sorted(choices)}")
+        if type(self.gamma_control) is not bool or type(self.write_control) is not bool:
+            raise ValueError("selective controller switches must be booleans")
+        if type(self.num_groups) is not int or self.num_groups < 1:
+            raise ValueError("selective.num_groups must be a positive integer")
+        if not math.isfinite(self.write_max) or self.write_max <= 1:
+            raise ValueError("selective.write_max must be finite and greater than one")
+        if not math.isfinite(self.gamma_edge_margin) or not 0 < self.gamma_edge_margin < 0.5:
+            raise ValueError("selective.gamma_edge_margin must be finite and in (0, 0.5)")
+        for name in ("gamma_max_log_scale", "max_log_scale"):
+            value = getattr(self, name)
+            if not math.isfinite(value) or value <= 0:
+                raise ValueError(f"selective.{name} must be finite and positive")
+        if not self.gamma_control:
+            if self.gamma_link != "sigmoid" or self.gamma_features != "real_imag":
+                raise ValueError("non-default gamma links/features require gamma_control")
+            if not self.write_control and self.frequency_warp == "none":
+                raise ValueError("selective requires a controller; use None for static RQFs")
+
+    @classmethod
+    def resolve(cls, value: SelectiveRQFConfig | Mapping[str, Any] | None
+                ) -> SelectiveRQFConfig | None:
+        """None, a config, or a mapping of its fields (selective.py:68-79)."""
+        if value is None or isinstance(value, cls):
+            return value
+        if isinstance(value, Mapping):
+            return cls(**value)
+        raise TypeError("selective must be a SelectiveRQFConfig, mapping, or None")
+
+    @property
+    def warp_groups(self) -> int:
+        """Rows of the warp head: 1 (global), num_groups (grouped) or 0 (selective.py:106-112)."""
+        if self.frequency_warp == "global":
+            return 1
+        return self.num_groups if self.frequency_warp == "grouped" else 0
+
+
+@dataclass
+class FilterState:
+    """Log-space leaves and bound buffers of one RQF filter module.
+
+    Field names follow the module's state (filter.py:216-262, 350-361):
+    ``log_tau``, ``log_gamma``, ``log_theta`` (leaves) and the per-filter
+    bounds ``min_gamma``/``max_gamma`` and ``min_freq``/``max_freq`` (the
+    ``_min_*``/``_max_*`` buffers).  ``dt`` is the sample period.  The three
+    settings the controller writes at construction start at the module's
+    defaults (filter.py:231-233).  Leaves keep their own dtype; the controller
+    computes in float64 only for float64 leaves (selective.py:214).
+    """
+
+    log_tau: Tensor
+    log_gamma: Tensor
+    log_theta: Tensor
+    min_gamma: Tensor
+    max_gamma: Tensor
+    min_freq: Tensor
+    max_freq: Tensor
+    dt: float
+    clamp_gamma: bool = False
+    gamma_log_headroom: float = 0.0
+    gamma_edge_margin: float = 0.0
+    theta_nyquist_bound: bool = False
+
+    @property
+    def num_filters(self) -> int:
+        return int(self.log_theta.shape[0])
+
+    @property
+    def tau(self) -> Tensor:
+        return torch.exp(self.log_tau)
+
+    @property
+    def gamma(self) -> Tensor:
+        return torch.exp(self.log_gamma)
+
+    @property
+    def theta(self) -> Tensor:
+        return torch.exp(self.log_theta)
+
+    def theta_bounds(self) -> tuple[Tensor, Tensor]:
+        """``[2 pi f_min tau, 2 pi f_max tau]``, capped at ``pi tau / dt`` under the
+        Nyquist bound (filter.py:371-378)."""
+        tau = self.tau
+        lower = 2 * math.pi * self.min_freq * tau
+        upper = 2 * math.pi * self.max_freq * tau
+        if self.theta_nyquist_bound:
+            upper = torch.minimum(upper, math.pi * tau / self.dt)
+        return lower, upper
+
+    @torch.no_grad()
+    def clamp_parameters(self) -> None:
+        """Project ``log_theta`` into the band and ``log_gamma`` into
+        ``[min + margin, max - margin]`` less the log headroom, then (with
+        ``clamp_gamma``) into the stability band (filter.py:380-412).  In place,
+        as the module's post-step projection."""
+        lower, upper = self.theta_bounds()
+        self.log_theta.clamp_(min=torch.log(lower), max=torch.log(upper))
+        margin = self.gamma_edge_margin * (self.max_gamma - self.min_gamma)
+        self.log_gamma.clamp_(min=torch.log(self.min_gamma + margin),
+                              max=torch.log(self.max_gamma - margin) - self.gamma_log_headroom)
+        if self.clamp_gamma:
+            omega_tau = self.log_theta.exp()
+            gamma_min = 1 - 1 / torch.sqrt(1 + omega_tau**2)
+            gamma_crit = omega_tau / (1 + omega_tau)
+            eps = 1e-6
+            self.log_gamma.copy_(torch.minimum(
+                torch.maximum(self.log_gamma, gamma_min.clamp_min(1e-12).log() + eps),
+                gamma_crit.log() - eps))
+
+
+class SelectiveController:
+    """The selector heads of one selective RQF layer (selective.py:100-278).
+
+    Construction validates the filter's bounds against the settings, writes
+    the settings the filter's projection uses (log headroom, interior margin,
+    Nyquist bound), projects the filter's parameters once, and ranks the
+    channels by ``log_theta`` into warp groups.  Heads are zero-initialised
+    like the reference's; assign ``W_gamma``/``W_write``/``W_delta`` to use
+    trained or random heads.
+    """
+
+    def __init__(self, n_in: int, rqf: FilterState, config: SelectiveRQFConfig) -> None:
+        self.config = config
+        self.n_in = n_in
+        n_out = rqf.num_filters
+        groups = config.warp_groups
+        if groups > n_out:
+            raise ValueError("selective.num_groups cannot exceed any layer's width")
+        lo, hi = rqf.min_gamma, rqf.max_gamma
+        if not bool(((lo > 0) & (hi > lo) & (hi <= 1)).all()):
+            raise ValueError("selective gamma bounds require 0 < min_gamma < max_gamma <= 1")
+        if config.gamma_link == "log_shift":
+            if not bool((lo.log() < hi.log() - config.gamma_max_log_scale).all()):
+                raise ValueError("gamma_max_log_scale leaves no resting gamma range")
+            rqf.gamma_log_headroom = config.gamma_max_log_scale
+        interior_gamma = (config.gamma_control and config.gamma_link == "sigmoid"
+                          and config.gamma_edge == "interior_clamp")
+        if interior_gamma:
+            rqf.gamma_edge_margin = config.gamma_edge_margin
+            span = hi - lo
+            if not bool(((lo + span * config.gamma_edge_margin > lo)
+                         & (hi - span * config.gamma_edge_margin < hi)).all()):
+                raise ValueError("gamma_edge_margin is too small for the parameter precision")
+        if groups and config.warp_bound == "band":
+            rqf.theta_nyquist_bound = True
+            lower, upper = rqf.theta_bounds()
+            if not bool((torch.isfinite(lower) & torch.isfinite(upper)
+                         & (lower > 0) & (upper >= lower)).all()):
+                raise ValueError("selective frequency band has no positive Nyquist-safe range")
+        if config.gamma_link == "log_shift" or interior_gamma or rqf.theta_nyquist_bound:
+            rqf.clamp_parameters()
+        dev, f32 = rqf.log_theta.device, torch.float32
+        modulus = config.gamma_features == "modulus"
+        self.W_gamma = (torch.zeros(n_out, n_in if modulus else 2 * n_in, dtype=f32, device=dev)
+                        if config.gamma_control else None)
+        self.W_write = (torch.zeros(n_out, 2 * n_in, dtype=f32, device=dev)
+                        if config.write_control else None)
+        self.W_delta = torch.zeros(groups, 2 * n_in, dtype=f32, device=dev) if groups else None
+        # Stable ranks of log_theta, cut into `groups` equal rank ranges.
+        ranks = rqf.log_theta.detach().argsort(stable=True).argsort()
+        self.warp_groups = ranks * groups // n_out if groups else None
+
+    @staticmethod
+    def compute_dtype(rqf: FilterState) -> torch.dtype:
+        return torch.float64 if rqf.log_gamma.dtype == torch.float64 else torch.float32
+
+    def project(self, source: Tensor, rqf: FilterState) -> tuple[Tensor, Tensor, Tensor]:
+        """Gamma, warp and write logits ``(rows, B, T)`` of a complex ``(I, B, T)``
+        source: one GEMM over ``[Re; Im]`` (or the gamma head over the per-input
+        modulus), in float32 or float64, never autocast (selective.py:212-229)."""
+        _, batch, time = source.shape
+        dtype = self.compute_dtype(rqf)
+        with torch.autocast(source.device.type, enabled=False):
+            v = torch.cat((source.real, source.imag), dim=0).reshape(2 * self.n_in, -1).to(dtype)
+            modulus = self.config.gamma_features == "modulus"
+            heads = (None if modulus else self.W_gamma, self.W_delta, self.W_write)
+            weights = [h.to(dtype) for h in heads if h is not None]
+            if weights:
+                sizes = [0 if h is None else h.shape[0] for h in heads]
+                g, d, w = (torch.cat(weights) @ v).split(sizes)
+            else:
+                g = d = w = v.new_empty((0, batch * time))
+            if modulus:
+                features = torch.linalg.vector_norm(v.reshape(2, self.n_in, -1), dim=0)
+                g = self.W_gamma.to(dtype) @ features
+        return (g.reshape(g.shape[0], batch, time), d.reshape(d.shape[0], batch, time),
+                w.reshape(w.shape[0], batch, time))
+
+    def assemble(self, gamma_logits: Tensor, warp_logits: Tensor, write_logits: Tensor,
+                 rqf: FilterState, *, prospective: bool, mode: str,
+                 prospective_tau: float | list[float] | Tensor | None) -> SelectiveScanInputs:
+        """Everything after the head GEMM (selective.py:230-278)."""
+        dtype = self.compute_dtype(rqf)
+        cfg = self.config
+        lo = rqf.min_gamma.to(dtype)
+        span = rqf.max_gamma.to(dtype) - lo
+        log_shift = cfg.gamma_link == "log_shift"
+        bias = rqf.log_gamma if log_shift else rqf.gamma
+        if self.W_gamma is not None and not log_shift:
+            resting = (bias - lo) / span
+            if cfg.gamma_edge == "st_clamp":
+                # Forward value clamped into (eps, 1 - eps), identity derivative.
+                eps = torch.finfo(dtype).eps
+                interior = resting.clamp(eps, 1 - eps)
+                resting = resting + (interior - resting).detach()
+            bias = torch.logit(resting)
+        tau = rqf.tau.to(dtype)
+        horizon = (torch.ones_like(tau) if prospective_tau is None
+                   else torch.as_tensor(prospective_tau, device=tau.device, dtype=dtype) / tau)
+        horizon = torch.broadcast_to(horizon, tau.shape).contiguous()
+        options = (
+            self.W_gamma is not None,
+            self.W_delta is not None,
+            self.W_write is not None,
+            log_shift,
+            cfg.gamma_max_log_scale,
+            cfg.max_log_scale,
+            prospective,
+            mode == "gamma" and prospective_tau is None,
+            self.W_write is not None and cfg.write_link == "sigmoid",
+            float(cfg.write_max),
+            -math.log(cfg.write_max - 1),
+            self.W_delta is not None and cfg.warp_bound == "band",
+        )
+        theta_minimum, theta_maximum = rqf.theta_bounds()
+        return SelectiveScanInputs(
+            gamma_logits, warp_logits, write_logits, bias.to(dtype), rqf.theta.to(dtype),
+            self.warp_groups, lo, span, rqf.dt / tau, horizon, theta_minimum.to(dtype),
+            theta_maximum.to(dtype), options)
+
+    def forward(self, source: Tensor, rqf: FilterState, *, prospective: bool, mode: str,
+                prospective_tau: float | list[float] | Tensor | None) -> SelectiveScanInputs:
+        """Scan inputs of a complex ``(I, B, T)`` selector source (selective.py:201-278)."""
+        g, d, w = self.project(source, rqf)
+        return self.assemble(g, d, w, rqf, prospective=prospective, mode=mode,
+                             prospective_tau=prospective_tau)
+
+    __call__ = forward

@@ -12,6 +12,9 @@ Per-channel parameters follow the reference's resonant "paper recipe"
 * warp groups = rank(theta) * G // F (selective.py:164-165)
 * sigmoid gamma link: bias = logit((gamma - lo)/span) (selective.py:227-236)
 
+The selective scan inputs are assembled by the restated selective controller
+(``selective_controller``) from that filter state.
+
 ZOH two-tap coefficients for the static (non-selective) scans follow
 ``RQF.compute_two_tap_coefficients`` (filter.py:630-646).
 """
@@ -22,6 +25,11 @@ import math
 
 import torch
 
+from prospective_rqf_amd.selective_controller import (
+    FilterState,
+    SelectiveController,
+    SelectiveRQFConfig,
+)
 from prospective_rqf_amd.selective_scan import SelectiveScanInputs
 
 LN_1_25 = math.log(1.25)
@@ -60,40 +68,54 @@ def zoh_two_tap(gamma, theta, eta, ratio):
     return C1, gamma * eta * phi + extra, -extra
 
 
+def recipe_filter(F: int, *, samp: float, tau: float, seq_duration: float,
+                  max_freq_factor: float = 1.0, generator: torch.Generator | None = None,
+                  dtype=torch.float32) -> FilterState:
+    """Log-space filter state of the resonant recipe (filter.py:250-262, 330-361):
+    log_theta log-uniform as in :func:`recipe_params`, critical-damping gamma
+    clamped into [1e-6, 1 - 1e-6], f_min = 1/seq_duration, f_max = 1/tau."""
+    p = recipe_params(F, samp=samp, tau=tau, seq_duration=seq_duration, margin=0.0,
+                      max_freq_factor=max_freq_factor, generator=generator)
+    full = lambda v: torch.full((F,), v, dtype=dtype)  # noqa: E731
+    return FilterState(
+        log_tau=torch.log(full(tau)), log_gamma=torch.log(p["gamma"].to(dtype)),
+        log_theta=torch.log(p["theta"]).to(dtype), min_gamma=full(1e-6),
+        max_gamma=full(1.0 - 1e-6), min_freq=full(1.0 / seq_duration),
+        max_freq=1.0 / full(tau), dt=1.0 / samp)
+
+
 def selective_inputs(F, B, T, *, G=8, gamma=True, write=True, warp="grouped", log_shift=False,
                      prospective=True, gamma_horizon=False, write_sigmoid=True, write_max=2.0,
                      gamma_scale=LN_1_25, warp_scale=LN_1_25, bound_warp=True, samp=16000.0,
                      tau=5.0 / 16000.0, seq_duration=1.0, logit_std=1.0, device="cpu", seed=0):
-    """SelectiveScanInputs with N(0, logit_std^2) logits and recipe parameters."""
+    """SelectiveScanInputs of a recipe filter with N(0, logit_std^2) head logits.
+
+    Every field but the logits comes from the selective controller
+    (``selective_controller.SelectiveController``, the restatement of
+    selective.py:100-278 pinned against the reference's own): the filter
+    projection at construction, the bias logit, warp-group ranks, theta band,
+    horizon and options.  The logits stand in for the head GEMM's output."""
     g = torch.Generator().manual_seed(seed)
-    p = recipe_params(F, samp=samp, tau=tau, seq_duration=seq_duration, generator=g)
-    n_warp = 0 if warp == "none" else (1 if warp == "global" else G)
-    if log_shift:
-        bias = torch.log(p["gamma"]) - gamma_scale  # resting log gamma below the ceiling
-    elif gamma:
-        bias = torch.logit((p["gamma"] - p["lo"]) / p["span"])
-    else:
-        bias = p["gamma"]
-    ranks = p["theta"].argsort(stable=True).argsort()
-    groups = ranks * n_warp // F if n_warp else None
+    rqf = recipe_filter(F, samp=samp, tau=tau, seq_duration=seq_duration, generator=g)
+    config = SelectiveRQFConfig(
+        gamma_control=bool(gamma), gamma_link="log_shift" if log_shift else "sigmoid",
+        gamma_max_log_scale=float(gamma_scale), write_control=bool(write),
+        write_link="sigmoid" if write_sigmoid else "affine", write_max=float(write_max),
+        frequency_warp=warp, warp_bound="band" if bound_warp else "none",
+        num_groups=G if warp == "grouped" else 4, max_log_scale=float(warp_scale))
+    ctl = SelectiveController(1, rqf, config)
+    n_warp = config.warp_groups
 
     def logits(rows):
         return (logit_std * torch.randn(rows, B, T, generator=g)).float()
 
-    options = (
-        bool(gamma), n_warp > 0, bool(write), bool(log_shift), float(gamma_scale),
-        float(warp_scale), bool(prospective), bool(gamma_horizon), bool(write and write_sigmoid),
-        float(write_max), -math.log(write_max - 1), bool(n_warp > 0 and bound_warp),
-    )
-    f32 = lambda v: v.float().to(device)  # noqa: E731
-    return SelectiveScanInputs(
-        logits(F).to(device) if gamma else torch.empty(0, B, T, device=device),
-        logits(n_warp).to(device) if n_warp else torch.empty(0, B, T, device=device),
-        logits(F).to(device) if write else torch.empty(0, B, T, device=device),
-        f32(bias), f32(p["theta"]), None if groups is None else groups.to(device),
-        f32(p["lo"]), f32(p["span"]), f32(p["eta"]), f32(torch.ones(F, dtype=torch.float64)),
-        f32(p["theta_lo"]), f32(p["theta_hi"]), options,
-    )
+    inp = ctl.assemble(logits(F) if gamma else torch.empty(0, B, T),
+                       logits(n_warp) if n_warp else torch.empty(0, B, T),
+                       logits(F) if write else torch.empty(0, B, T), rqf,
+                       prospective=bool(prospective), mode="gamma" if gamma_horizon else "tau",
+                       prospective_tau=None)
+    move = lambda v: None if v is None else v.to(device)  # noqa: E731
+    return SelectiveScanInputs(*(move(v) for v in inp[:-1]), inp.options)
 
 
 def randn_c64(*shape, generator=None, device="cpu"):

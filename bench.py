@@ -82,6 +82,12 @@ def _args():
                     help="config 2: 'btf' runs the same workload on (batch, time, filters) "
                          "tensors through the chunked prospective scan (the layout RQF-S4 "
                          "and the non-FBT Pure RQF cells use, block.py:690-733)")
+    ap.add_argument("--layer0", action="store_true",
+                    help="config 2: time the whole real-input layer 0 through "
+                         "fbt_layer0_real_scan (fbt_scan_kernel.py:899-1032): the stacked "
+                         "[Wr; Wi] projection of the waveform on the MFMA projection GEMM, the "
+                         "recompute scan, and in the backward grad_h and grad_[Wr; Wi] besides "
+                         "the coefficient gradients")
     ap.add_argument("--act-only", action="store_true",
                     help="config 3 with the act-only contract (no raw output, no gy)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -318,7 +324,7 @@ def plan_selective(cfg, args, dev):
         name += f" [whole layer, {layer} weight gradients]"
     config = {"workload": name, "F": F, "B": B, "T": T, "G": G, "layers": len(layers),
               "chunk": chunk, "contract": contract}
-    cpu_steps = args.cpu_steps or (200 if cfg == 3 else 100)
+    cpu_steps = args.cpu_steps or (500 if cfg == 3 else 100)
 
     def cpu():
         return cpu_baseline_selective(F, min(B, 64), G, cpu_steps, log_scale, samp, tau, seq,
@@ -326,6 +332,45 @@ def plan_selective(cfg, args, dev):
 
     return Plan(name, config, F * B * T * len(layers), (state, ops), nbytes, kernels, cpu,
                 contract)
+
+
+def _plan_layer0(F, B, T, coefs, u, w, state, name, gy):
+    """Config 2 as layer 0 of the raw-waveform encoder: one real input row (the
+    waveform), the complex drive weight w as the stacked real [Re w; Im w]."""
+    import torch
+
+    from prospective_rqf_amd.fbt_scan_kernel import fbt_layer0_real_scan
+
+    state.clear()
+    state["gy"] = gy
+    coefs = [c.detach().clone().requires_grad_(True) for c in coefs]
+    w_stacked = torch.cat((w.real, w.imag))[:, None].contiguous().requires_grad_(True)
+    h = u.reshape(1, B * T).contiguous().requires_grad_(True)
+
+    def fwd(st):
+        st["act"] = fbt_layer0_real_scan(w_stacked, h, *coefs, B)
+
+    def bwd(st):
+        st.pop("act").backward(st["gy"])
+        st["grads"] = (w_stacked.grad, h.grad, *(c.grad for c in coefs))
+        for t in (w_stacked, h, *coefs):
+            t.grad = None
+
+    ops = [("fbt_layer0_real_scan_fwd", fwd), ("fbt_layer0_real_scan_bwd", bwd)]
+    elems = F * B * T
+    # Bytes the layer must move: the waveform in and the activation out, then
+    # the cotangent in and grad_h out; the drive z between the projection and
+    # the scan is this implementation's choice, not counted.
+    nbytes = {"fbt_layer0_real_scan_fwd": 8 * elems + 4 * B * T,
+              "fbt_layer0_real_scan_bwd": 8 * elems + 8 * B * T}
+    kernels = {"fbt_layer0_real_scan_fwd": "proj_gemm_kernel (z = [Wr; Wi] h) + fbt_fwd_rb_kernel",
+               "fbt_layer0_real_scan_bwd": ("fbt_bwd_rb_kernel / fbt_bwd_kernel + coef_reduce_kernel "
+                                            "+ proj_gemm_kernel (grad_h) + split-K grad_w")}
+    contract = ("layer 0 on the raw waveform: stacked real projection + split-ReLU recompute "
+                "scan; gy cotangent; grads of [Wr; Wi], the waveform and the coefficients")
+    config = {"workload": name + " [whole layer 0: fbt_layer0_real_scan]", "F": F, "B": B, "T": T,
+              "layers": 1, "contract": contract}
+    return Plan(config["workload"], config, elems, (state, ops), nbytes, kernels, None, contract)
 
 
 def plan_fbt(cfg, args, dev):
@@ -371,6 +416,8 @@ def plan_fbt(cfg, args, dev):
     for li in range(L):
         state[f"gy{li}"] = _cn(g, dev, F, B, T)
 
+    if cfg == 2 and args.layer0:
+        return _plan_layer0(F, B, T, coefs[0], u, w, state, name, gy=state["gy0"])
     ops = []
     stack = args.stack if cfg == 5 else "none"
     if stack != "none":
@@ -704,9 +751,12 @@ def cpu_baseline_selective(F, B, G, steps, log_scale, samp, tau, seq, layers):
         "kind": "port",
         "sample": (f"fp32 PyTorch restatement of reference_layer_scan after the drive GEMM "
                    f"(oracle/torch_ref.py), fwd + autograd bwd, {len(layers)} layer(s), F={F} "
-                   f"B={B} T={steps} (T reduced from the GPU shape), median of 3 after 1 "
-                   f"warm-up; torch threads={threads}, os.cpu_count()={os.cpu_count()}, "
-                   f"cpu={_cpu_model()}"),
+                   f"B={B} T={steps} (T reduced from the GPU shape: like the reference's loop, "
+                   f"whose backward of each A[..., t] select materialises a full (F,B,T) "
+                   f"gradient, the cost per element grows with T, about 8x from T=200 to "
+                   f"T=1000, so T=2000 would take minutes per run), median of 3 after 1 "
+                   f"warm-up; torch threads={threads} (the GPU box's CPU share is 16 "
+                   f"threads), os.cpu_count()={os.cpu_count()}, cpu={_cpu_model()}"),
     }
 
 
@@ -928,7 +978,7 @@ def main():
     if proj_ms:
         result["detail"]["outside_scan_ms"] = {k: round(v, 4) for k, v in proj_ms.items()}
         result["detail"]["scan_only_ms"] = round(scan_ms - sum(proj_ms.values()), 4)
-    if args.cpu:
+    if args.cpu and plan.cpu is not None:
         result["cpu_baseline"] = plan.cpu()
     print(json.dumps(result), flush=True)
 

@@ -216,3 +216,94 @@ def fbt_recompute_scan(C1, tap0, tap1, x_fbt, skip=None):
     With ``skip`` (the layer input, same shape) the result is
     ``split-ReLU(scan) + skip``, the residual add fused into the kernel."""
     return _FBTRecompute.apply(C1, tap0, tap1, x_fbt, skip)
+
+
+# ---------------------------------------------------------------------------
+# Layer 0 on a real input: stacked real projection + recompute scan
+# ---------------------------------------------------------------------------
+
+
+def _pack_layer0(w_stacked):
+    """Weights of ``z = A h`` for the MFMA projection GEMM: rows 2f and 2f+1 are
+    ``Wr_f`` and ``Wi_f``, so the kernel writes complex row f of ``z``
+    interleaved, as the recompute scan reads it."""
+    from prospective_rqf_amd import projection
+
+    f = w_stacked.shape[0] // 2
+    a = torch.empty(2 * f, w_stacked.shape[1], dtype=torch.float32, device=w_stacked.device)
+    a[0::2], a[1::2] = w_stacked[:f], w_stacked[f:]
+    return projection._padded(a)
+
+
+def _pack_layer0_dh(w_stacked):
+    """Weights of ``grad_h = A [Re gz_0, Im gz_0, Re gz_1, ...]``: row k is
+    ``(Wr[0,k], Wi[0,k], Wr[1,k], ...)``, i.e. ``grad_h = Re(W^H gz)``."""
+    from prospective_rqf_amd import projection
+
+    f = w_stacked.shape[0] // 2
+    a = torch.empty(w_stacked.shape[1], 2 * f, dtype=torch.float32, device=w_stacked.device)
+    a[:, 0::2], a[:, 1::2] = w_stacked[:f].T, w_stacked[f:].T
+    return projection._padded(a)
+
+
+class _Layer0RealScan(torch.autograd.Function):
+    """Real-input layer-0 projection feeding the split-ReLU recompute scan
+    (rqf_models/ops/fbt_scan_kernel.py:899-1002).
+
+    The reference writes the stacked real GEMM ``[Wr; Wi] @ h`` to planar
+    ``(zr, zi)`` buffers and runs planar twins of the recompute kernels.  Here
+    the MFMA projection GEMM (``rqf_proj_gemm``) writes ``z`` interleaved, so
+    the ordinary recompute kernels consume it; the backward reads ``grad_z``
+    where the scan leaves it for ``grad_h = [Wr; Wi]^T [Re gz; Im gz]``, and
+    forms ``grad_w_stacked = [Re gz; Im gz] h^T`` as one split-K complex GEMM
+    against the (narrow) input."""
+
+    @staticmethod
+    def forward(ctx, w_stacked, h_real, C1, tap0, tap1, batch):
+        from prospective_rqf_amd import projection
+
+        if w_stacked.dim() != 2 or w_stacked.shape[0] % 2 or w_stacked.is_complex():
+            raise ValueError("w_stacked must be a real (2*num_filters, d_model) matrix, got "
+                             f"{tuple(w_stacked.shape)} {w_stacked.dtype}")
+        if h_real.dim() != 2 or h_real.is_complex() or h_real.shape[0] != w_stacked.shape[1]:
+            raise ValueError(f"h_real must be a real ({w_stacked.shape[1]}, batch*time) matrix, "
+                             f"got {tuple(h_real.shape)} {h_real.dtype}")
+        batch = int(batch)
+        if batch < 1 or h_real.shape[1] % batch:
+            raise ValueError(f"batch {batch} does not divide the {h_real.shape[1]} columns")
+        _lib.require_device(w_stacked, h_real)
+        w = w_stacked.detach().to(torch.float32).contiguous()
+        h = h_real.detach().to(torch.float32).contiguous()
+        filters, cols = w.shape[0] // 2, h.shape[1]
+        z, _ = projection._proj_gemm(_pack_layer0(w), None, h, cols, filters, 0, h.device)
+        z = z.view(filters, batch, cols // batch)
+        act, carry, (C1, tap0, tap1, z) = fbt_recompute_forward_raw(C1, tap0, tap1, z)
+        ctx.save_for_backward(w, h, z, carry, C1, tap0, tap1)
+        return act
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad_act):
+        from prospective_rqf_amd import projection
+
+        w, h, z, carry, C1, tap0, tap1 = ctx.saved_tensors
+        gc1, gt0, gt1, gz = fbt_recompute_backward_raw(C1, tap0, tap1, z, carry, grad_act)
+        filters, cols = w.shape[0] // 2, h.shape[1]
+        gz = gz.view(filters, cols)
+        grad_w = grad_h = None
+        if ctx.needs_input_grad[0]:
+            g = projection.weight_grad(gz, h.to(torch.complex64))  # gz @ h^T, complex (F, D)
+            grad_w = torch.cat((g.real, g.imag))
+        if ctx.needs_input_grad[1]:
+            _, grad_h = projection._proj_gemm(_pack_layer0_dh(w), gz, None, cols, 0, h.shape[0],
+                                              h.device)
+        return grad_w, grad_h, gc1, gt0, gt1, None
+
+
+def fbt_layer0_real_scan(w_stacked, h_real, C1, tap0, tap1, batch):
+    """Real-input layer-0 projection + split-ReLU prospective scan
+    (rqf_models/ops/fbt_scan_kernel.py:1005-1032): ``(2F, D)`` real
+    ``[Wr; Wi]``, ``(D, batch*time)`` real ``h``, complex ``(F,)`` coefficients;
+    returns the complex ``(F, batch, time)`` activated output, equal up to fp32
+    summation order to ``fbt_recompute_scan(C1, tap0, tap1, (Wr + i Wi) @ h)``."""
+    return _Layer0RealScan.apply(w_stacked, h_real, C1, tap0, tap1, batch)

@@ -1,0 +1,123 @@
+"""Layer 0 on a real input: ``fbt_layer0_real_scan`` (fbt_scan_kernel.py:899-1032).
+
+GPU parity against an fp64 composition: ``z = (Wr + i Wi) h`` in float64,
+the oracle's FBT two-tap scan with the split-ReLU mask and its adjoint
+(``oracle.twotap_fwd`` / ``twotap_bwd``, pinned elsewhere against closed
+forms and brute force), then the projection's own chain rule in float64:
+``grad_h = Re(W^H gz)`` and ``grad_[Wr; Wi] = [Re gz; Im gz] h^T`` with
+``gz`` the oracle's drive gradient.  Input widths 1 (raw waveform), 20
+(MFCC features) and 64, rows on and off the 256-step tile, and the
+``needs_input_grad`` gating.  Bar: normwise relative error <= 1e-4 per
+tensor, and per channel (floor 1e-2) for the coefficient gradients.  The
+cotangent is zeroed where the fp64 state lies within 1e-4 of its maximum of a
+split-ReLU kink: there the mask is decided by rounding, and with long-memory
+poles one flipped element moves ``grad_h`` by ~1e-3.
+
+Host-side argument checks run on the CPU (no launch).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from prospective_rqf_amd.fbt_scan_kernel import fbt_layer0_real_scan, fbt_recompute_scan
+from tests.helpers import PARITY_RTOL, chanerr, cotangent_off_relu_kink, crandn, relerr
+
+
+def _coeffs(rng, F):
+    c1 = rng.uniform(0.8, 0.995, F) * np.exp(1j * rng.uniform(0, 2 * np.pi, F))
+    c = [np.asarray(v, np.complex64).astype(np.complex128)
+         for v in (c1, 0.1 * crandn(rng, F), 0.5 * crandn(rng, F))]
+    return c
+
+
+def _f32(a):
+    return np.asarray(a, np.float32).astype(np.float64)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("F,D,B,T", [(16, 1, 2, 1000), (8, 20, 3, 4096), (5, 64, 2, 1023),
+                                     (3, 2, 1, 1), (32, 1, 4, 16000)])
+def test_layer0_matches_fp64_composition(F, D, B, T):
+    from oracle import oracle
+
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    print(f"case: layer0 F={F} D={D} B={B} T={T}", flush=True)
+    rng = np.random.default_rng(F * 31 + D * 7 + T)
+    c1, t0, t1 = _coeffs(rng, F)
+    w = _f32(rng.standard_normal((2 * F, D)) / np.sqrt(D))
+    h = _f32(rng.standard_normal((D, B * T)))
+    gy = np.asarray(crandn(rng, F, B, T), np.complex64).astype(np.complex128)
+    z = ((w[:F] + 1j * w[F:]) @ h).reshape(F, B, T)
+    y_ref, act_ref = oracle.twotap_fwd(c1, t0, t1, z, layout=oracle.FBT, act=True)
+    # Where the state is within rounding of a split-ReLU kink the fp32 replay
+    # and the oracle may take different branches; keep the cotangent off them.
+    gy, _ = cotangent_off_relu_kink(y_ref, gy)
+    gy = gy.astype(np.complex64).astype(np.complex128)
+    gz_ref, gc1_ref, gt0_ref, gt1_ref = oracle.twotap_bwd(c1, t0, t1, z, y_ref, gy,
+                                                          layout=oracle.FBT, mask_act=True)
+    gz2 = gz_ref.reshape(F, B * T)
+    gw_ref = np.concatenate([gz2.real @ h.T, gz2.imag @ h.T])
+    gh_ref = w[:F].T @ gz2.real + w[F:].T @ gz2.imag
+
+    dev = lambda a, dt: torch.as_tensor(a.astype(dt), device="cuda").requires_grad_(True)  # noqa
+    W, H = dev(w, np.float32), dev(h, np.float32)
+    C1, T0, T1 = (dev(v, np.complex64) for v in (c1, t0, t1))
+    act = fbt_layer0_real_scan(W, H, C1, T0, T1, B)
+    assert act.shape == (F, B, T) and act.dtype == torch.complex64
+    act.backward(torch.as_tensor(gy.astype(np.complex64), device="cuda"))
+    for name, got, want in (("act", act, act_ref), ("grad_w_stacked", W.grad, gw_ref),
+                            ("grad_h", H.grad, gh_ref), ("grad_C1", C1.grad, gc1_ref),
+                            ("grad_tap0", T0.grad, gt0_ref), ("grad_tap1", T1.grad, gt1_ref)):
+        err = relerr(got, want)
+        assert err <= PARITY_RTOL, (name, err)
+        if name.startswith(("grad_C", "grad_tap")):
+            assert chanerr(got, want) <= PARITY_RTOL, (name + "/channel", chanerr(got, want))
+
+
+@pytest.mark.gpu
+def test_layer0_equals_complex_path_and_gates_gradients():
+    """Same result as the complex projection into the recompute scan (the
+    reference's stated equivalence), and grads only where asked."""
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    print("case: layer0 vs complex path", flush=True)
+    g = torch.Generator().manual_seed(5)
+    F, D, B, T = 12, 4, 2, 777
+    w = torch.randn(2 * F, D, generator=g).cuda()
+    h = torch.randn(D, B * T, generator=g).cuda()
+    c1 = (0.95 * torch.exp(1j * torch.rand(F, generator=g, dtype=torch.float64) * 6.28)).to(
+        torch.complex64).cuda()
+    t0 = torch.randn(F, generator=g, dtype=torch.complex64).cuda()
+    t1 = torch.randn(F, generator=g, dtype=torch.complex64).cuda()
+    act = fbt_layer0_real_scan(w, h, c1, t0, t1, B)
+    z = (torch.complex(w[:F], w[F:]) @ h.to(torch.complex64)).reshape(F, B, T)
+    ref = fbt_recompute_scan(c1, t0, t1, z)
+    assert relerr(act, ref) <= 1e-5
+    # Only h asks for a gradient.
+    hh = h.clone().requires_grad_(True)
+    out = fbt_layer0_real_scan(w, hh, c1, t0, t1, B)
+    out.real.sum().backward()
+    assert hh.grad is not None and hh.grad.shape == h.shape and torch.isfinite(hh.grad).all()
+
+
+@pytest.mark.parametrize("bad", ["odd_rows", "complex_w", "width", "batch"])
+def test_layer0_rejects_bad_shapes_before_launch(bad):
+    F, D, B, T = 4, 3, 2, 10
+    w = torch.zeros(2 * F, D)
+    h = torch.zeros(D, B * T)
+    c = torch.zeros(F, dtype=torch.complex64)
+    batch = B
+    if bad == "odd_rows":
+        w = torch.zeros(2 * F + 1, D)
+    elif bad == "complex_w":
+        w = torch.zeros(2 * F, D, dtype=torch.complex64)
+    elif bad == "width":
+        h = torch.zeros(D + 1, B * T)
+    else:
+        batch = 3
+    with pytest.raises(ValueError):
+        fbt_layer0_real_scan(w, h, c, c, c, batch)

@@ -12,21 +12,28 @@
 // filter) walking all T steps serially.
 //
 // Here, as in btf.hip, a block owns 16 consecutive filters of one batch
-// element and walks the sequence in passes of 32 segments of LS steps; a
-// thread takes one (filter, segment) of each pass with the filter's
-// oscillators (N padded to a power of two NP <= 4, padded ones with zero
-// coefficients) in registers.  It loads its segment's inputs once (the next
-// pass's while the current one computes), scans them from a zero state per
-// oscillator, and gets its entry states from the segments before it: the
-// wavefront's earlier segments by cross-lane moves, the earlier wavefronts'
-// and the block's carry through LDS.  Those folds span at most 10 segment
-// hops and run in fp32 with powers computed once per block in fp64 and
-// rounded; only the carry from pass to pass, a chain of T / pass hops, is
-// kept in fp64.  The thread then replays the segment and writes the output.
+// element and walks the sequence in passes of 4 segments of LS steps per
+// wavefront; a thread takes one (filter, segment) of each pass with the
+// filter's oscillators (N padded to a power of two NP <= 4, padded ones with
+// zero coefficients) in registers.  It loads its segment's inputs once (the
+// next pass's while the current one computes), scans them from a zero state
+// per oscillator, and gets its entry states from the segments before it: the
+// wavefront's earlier segments by cross-lane moves (fp32, at most 3 hops,
+// exactly rounded maps), the earlier wavefronts' and the block's carry
+// through LDS.  The thread then replays the segment and writes the output.
+//   * Forward: each thread folds the earlier wavefronts' totals itself (fp32);
+//     one thread per (filter, oscillator) extends the carry in fp64.  Blocks
+//     of 16 wavefronts where the registers allow (real input), else 8.
+//   * Backward: after the barrier one wavefront, one lane per (oscillator,
+//     filter), walks the block's wavefronts from the carry in fp64, records
+//     the pair entering each in LDS and extends the carry; after a second
+//     barrier each thread applies one map to its entry.  That keeps the
+//     serial part of the fold off every other wavefront.
 // Filter groups of one batch element run on one XCD (xcd_contiguous): with
-// real input a group reads half of each 128-byte line of a (B,T,F) row.  Inputs are read once, outputs
-// written once, and no carry crosses a block.  More than 4 oscillators run
-// in chunks of 4, each adding its share to the output (or to grad_u).
+// real input a group reads half of each 128-byte line of a (B,T,F) row.
+// Inputs are read once, outputs written once, and no carry crosses a block.
+// More than 4 oscillators run in chunks of 4, each adding its share to the
+// output (or to grad_u).
 //
 // The scanned state is w_n = x_n / C2_n, i.e. w_n[t] = C1_n w_n[t-1] + u[t],
 // with C2_n applied at the output: y = sum_n (cw_n C2_n) w_n.  No division
@@ -155,12 +162,13 @@ __device__ __forceinline__ c32 shfl_down_c(c32 v, int d) {
 // Powers of one filter's oscillator coefficient a over spans of segments of
 // LS steps, computed once per block in fp64 and rounded: m1 = a^LS (one
 // segment), m2 = m1^2, mG = m1^G (one wavefront's segments), mq[q] = m1^q,
-// and mB = m1^(G*waves) (one pass), kept in fp64 for the carry chain.
+// and mB = m1^(G*W) (one pass of W wavefronts), kept in fp64 for the carry
+// chain.
 struct FwdMaps {
   c32 m1, m2, mG, mq[kG];
   double2 mB;
 };
-template <int LS>
+template <int LS, int W>
 __device__ __forceinline__ FwdMaps fwd_maps(c32 a) {
   FwdMaps k;
   const c64d m1 = dpow(widen(a), LS);
@@ -170,22 +178,24 @@ __device__ __forceinline__ FwdMaps fwd_maps(c32 a) {
   for (int q = 0; q < kG; ++q) k.mq[q] = narrow(dpow(m1, q));
   const c64d mG = dpow(m1, kG);
   k.mG = narrow(mG);
-  k.mB = d2(dpow(mG, kWaves));
+  k.mB = d2(dpow(mG, W));
   return k;
 }
 
 // ---------------------------------------------------------------------------
 // Forward.  yin (optional, complex (B,T,F)) is added to this chunk's y: the
-// earlier chunks' share.  yout receives y (complex) or |y| (ABS).
+// earlier chunks' share.  yout receives y (complex) or |y| (ABS).  A block
+// has W wavefronts: 16 (4 per SIMD) where the registers allow it, to hide
+// more memory latency per CU, else 8.
 // ---------------------------------------------------------------------------
-template <int NP, bool REAL, bool CW, bool ABS>
-__global__ __launch_bounds__(kThreads) void mosc_fwd_kernel(
+template <int NP, bool REAL, bool CW, bool ABS, int W>
+__global__ __launch_bounds__(W* kWave) void mosc_fwd_kernel(
     const float* __restrict__ c1, const float* __restrict__ c2, const float* __restrict__ cw,
     const float* __restrict__ u, const float* yin, float* yout, int64_t T, int64_t F, int N,
     int n0) {
   constexpr int LS = Seg<NP>::fwd;
-  constexpr int kPass = kNSeg * LS;
-  __shared__ c32 s_tot[2][kWaves][NP][kFC];
+  constexpr int kPass = W * kG * LS;
+  __shared__ c32 s_tot[2][W][NP][kFC];
   __shared__ double2 s_carry[2][NP][kFC];
   __shared__ FwdMaps s_k[NP][kFC];
   const Lane l = lane_of(T, F);
@@ -196,7 +206,7 @@ __global__ __launch_bounds__(kThreads) void mosc_fwd_kernel(
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
       s_carry[0][n][l.fl] = make_double2(0.0, 0.0);
-      s_k[n][l.fl] = fwd_maps<LS>(a[n]);
+      s_k[n][l.fl] = fwd_maps<LS, W>(a[n]);
     }
   }
   __syncthreads();
@@ -237,9 +247,9 @@ __global__ __launch_bounds__(kThreads) void mosc_fwd_kernel(
       const c64d carry = cd(s_carry[p][n][l.fl]);
       c32 cw_ = narrow(carry);
       for (int v = 0; v < l.w; ++v) cw_ = cmad(k.mG, cw_, s_tot[p][v][n][l.fl]);
-      if (l.w == kWaves - 1 && l.q == kG - 1) {
+      if (l.w == W - 1 && l.q == kG - 1) {
         c32 z = mk(0.0f, 0.0f);
-        for (int v = 0; v < kWaves; ++v) z = cmad(k.mG, z, s_tot[p][v][n][l.fl]);
+        for (int v = 0; v < W; ++v) z = cmad(k.mG, z, s_tot[p][v][n][l.fl]);
         s_carry[p ^ 1][n][l.fl] = d2(dmad(cd(k.mB), carry, widen(z)));
       }
       w[n] = cmad(k.mq[l.q], cw_, w[n]);
@@ -312,12 +322,12 @@ __device__ __forceinline__ PairMap one_segment(c32 a) {
 }
 
 // One filter's pair maps over spans of segments, computed once per block in
-// fp64 and rounded: one and two segments, one wavefront's G segments, the
-// G-1-q segments after segment q of a wavefront, and one pass (kept in fp64
-// for the carry chain).
+// fp64 and rounded: one and two segments, the G-1-q segments after segment q
+// of a wavefront, and one wavefront's G segments (also kept in fp64 for the
+// carry chain).
 struct BwdMaps {
-  PairMap32 one, two, wave, after[kG];
-  Pair pass;  // (P, c) of the whole pass, fp64
+  PairMap32 one, two, after[kG];
+  Pair wave;  // (P, c) of one wavefront's segments, fp64
 };
 template <int LS>
 __device__ __forceinline__ BwdMaps bwd_maps(c32 a) {
@@ -326,11 +336,9 @@ __device__ __forceinline__ BwdMaps bwd_maps(c32 a) {
   const PairMap two = pair_map_mul(one, one);
   PairMap wave = one;
   for (int i = 1; i < kG; ++i) wave = pair_map_mul(wave, one);
-  PairMap pass = wave;
-  for (int i = 1; i < kWaves; ++i) pass = pair_map_mul(pass, wave);
   k.one = narrow_map(one);
   k.two = narrow_map(two);
-  k.wave = narrow_map(wave);
+  k.wave = Pair{d2(wave.P), d2(wave.c)};
   PairMap acc;
   acc.P = mkd(1.0, 0.0);
   acc.c = mkd(0.0, 0.0);
@@ -338,7 +346,6 @@ __device__ __forceinline__ BwdMaps bwd_maps(c32 a) {
     k.after[q] = narrow_map(acc);
     acc = pair_map_mul(acc, one);
   }
-  k.pass = Pair{d2(pass.P), d2(pass.c)};
   return k;
 }
 
@@ -349,8 +356,11 @@ __global__ __launch_bounds__(kThreads) void mosc_bwd_kernel(
     double* __restrict__ part, int64_t T, int64_t F, int N, int n0) {
   constexpr int LS = Seg<NP>::bwd;
   constexpr int kPass = kNSeg * LS;
-  __shared__ Pair32 s_tot[2][kWaves][NP][kFC];
-  __shared__ Pair s_carry[2][NP][kFC];
+  // Per pass: each wavefront's pair from a zero entry (s_tot), the pair
+  // entering each wavefront (s_ent) and the block's carry (fp64).
+  __shared__ Pair32 s_tot[kWaves][NP][kFC];
+  __shared__ Pair32 s_ent[kWaves][NP][kFC];
+  __shared__ Pair s_carry[NP][kFC];
   __shared__ BwdMaps s_k[NP][kFC];
   __shared__ double s_red[TAN ? kWaves * kFC * 4 * NP : 1];
   const Lane l = lane_of(T, F);
@@ -360,7 +370,7 @@ __global__ __launch_bounds__(kThreads) void mosc_bwd_kernel(
   if (l.sg == 0) {
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
-      s_carry[0][n][l.fl] = Pair{make_double2(0.0, 0.0), make_double2(0.0, 0.0)};
+      s_carry[n][l.fl] = Pair{make_double2(0.0, 0.0), make_double2(0.0, 0.0)};
       s_k[n][l.fl] = bwd_maps<LS>(a[n]);
     }
   }
@@ -373,7 +383,6 @@ __global__ __launch_bounds__(kThreads) void mosc_bwd_kernel(
   int64_t pt = (npass - 1) * kPass;
   load_seg<LS, false>(gy, l, pt + (int64_t)l.sg * LS, T, F, gv);
   if constexpr (TAN) load_seg<LS, REAL>(u, l, pt + (int64_t)l.sg * LS, T, F, uv);
-  int p = 0;
   for (; pt >= 0; pt -= kPass) {
     const int64_t tb = pt + (int64_t)l.sg * LS;
     if (pt > 0) {
@@ -391,10 +400,11 @@ __global__ __launch_bounds__(kThreads) void mosc_bwd_kernel(
         if (TAN) f[n] = cjmad(a[n], f[n], e[n]);
         e[n] = cjmad(a[n], e[n], gv[j]);
       }
-    // Entry pairs: the wavefront's later segments (cross-lane), then the
-    // block's carry and the later wavefronts (LDS).  Within a pass at most 10
-    // segment hops are folded, in fp32 with exactly rounded maps; the carry
-    // from pass to pass, a chain of T / pass hops, is kept in fp64.
+    // Entry pairs.  The wavefront's later segments come by cross-lane moves
+    // (at most 3 hops, fp32 with exactly rounded maps).  Then one wavefront
+    // walks the block's wavefronts from the carry, latest first, one lane per
+    // (oscillator, filter): it records the pair entering each wavefront and
+    // carries the chain on, in fp64, to the next (earlier) pass.
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
       const BwdMaps& k = s_k[n][l.fl];
@@ -404,35 +414,34 @@ __global__ __launch_bounds__(kThreads) void mosc_bwd_kernel(
       ng = shfl_down_c(ig, 2 * kFC);
       nh = shfl_down_c(ih, 2 * kFC);
       if (l.q + 2 < kG) pair_apply32(k.two, ig, ih, ng, nh), ig = ng, ih = nh;
-      if (l.q == 0) s_tot[p][l.w][n][l.fl] = Pair32{ig, ih};
+      if (l.q == 0) s_tot[l.w][n][l.fl] = Pair32{ig, ih};
       const c32 xg = shfl_down_c(ig, kFC), xh = shfl_down_c(ih, kFC);
       e[n] = l.q + 1 < kG ? xg : mk(0.0f, 0.0f);
       f[n] = l.q + 1 < kG ? xh : mk(0.0f, 0.0f);
     }
     __syncthreads();
+    if (l.w == 0 && l.lane < NP * kFC) {
+      const int n = l.lane / kFC, fl = l.lane % kFC;
+      const Pair wm = s_k[n][fl].wave;
+      PairMap pm;
+      pm.P = cd(wm.g);
+      pm.c = cd(wm.h);
+      const Pair cr = s_carry[n][fl];
+      c64d g = cd(cr.g), h = cd(cr.h);
+#pragma unroll 1
+      for (int v = kWaves - 1; v >= 0; --v) {
+        s_ent[v][n][fl] = Pair32{narrow(g), narrow(h)};
+        const Pair32 t = s_tot[v][n][fl];
+        pair_apply(pm, widen(t.g), widen(t.h), g, h);
+      }
+      s_carry[n][fl] = Pair{d2(g), d2(h)};
+    }
+    __syncthreads();
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
-      const BwdMaps& k = s_k[n][l.fl];
-      const Pair cr = s_carry[p][n][l.fl];
-      c32 cg = narrow(cd(cr.g)), ch = narrow(cd(cr.h));
-      for (int v = kWaves - 1; v > l.w; --v) {
-        const Pair32 t = s_tot[p][v][n][l.fl];
-        pair_apply32(k.wave, t.g, t.h, cg, ch);
-      }
-      pair_apply32(k.after[l.q], e[n], f[n], cg, ch);
-      if (l.w == 0 && l.q == 0) {
-        c32 zg = mk(0.0f, 0.0f), zh = mk(0.0f, 0.0f);
-        for (int v = kWaves - 1; v >= 0; --v) {
-          const Pair32 t = s_tot[p][v][n][l.fl];
-          pair_apply32(k.wave, t.g, t.h, zg, zh);
-        }
-        PairMap pm;
-        pm.P = cd(k.pass.g);
-        pm.c = cd(k.pass.h);
-        c64d g = cd(cr.g), h = cd(cr.h);
-        pair_apply(pm, widen(zg), widen(zh), g, h);
-        s_carry[p ^ 1][n][l.fl] = Pair{d2(g), d2(h)};
-      }
+      const Pair32 en = s_ent[l.w][n][l.fl];
+      c32 cg = en.g, ch = en.h;
+      pair_apply32(s_k[n][l.fl].after[l.q], e[n], f[n], cg, ch);
       e[n] = cg;
       f[n] = ch;
     }
@@ -450,18 +459,18 @@ __global__ __launch_bounds__(kThreads) void mosc_bwd_kernel(
         e[n] = cjmad(a[n], e[n], gv[j]);
         if (GU) g = cjmad(hw[n], e[n], g);
         if constexpr (TAN) {
-          c32 qv, rv;
-          if (REAL) {
-            qv = cscale(uv[j].r, e[n]);
-            rv = cscale(uv[j].r, f[n]);
-          } else {
-            qv = cjmul(uv[j], e[n]);
-            rv = cjmul(uv[j], f[n]);
+          // Q += e conj(u), R += f conj(u), as fused multiply-adds.
+          const c32 uj = uv[j];
+          pq[n][0] = fmaf(uj.r, e[n].r, pq[n][0]);
+          pq[n][1] = fmaf(uj.r, e[n].i, pq[n][1]);
+          pq[n][2] = fmaf(uj.r, f[n].r, pq[n][2]);
+          pq[n][3] = fmaf(uj.r, f[n].i, pq[n][3]);
+          if (!REAL) {
+            pq[n][0] = fmaf(uj.i, e[n].i, pq[n][0]);
+            pq[n][1] = fmaf(-uj.i, e[n].r, pq[n][1]);
+            pq[n][2] = fmaf(uj.i, f[n].i, pq[n][2]);
+            pq[n][3] = fmaf(-uj.i, f[n].r, pq[n][3]);
           }
-          pq[n][0] += qv.r;
-          pq[n][1] += qv.i;
-          pq[n][2] += rv.r;
-          pq[n][3] += rv.i;
         }
       }
       if constexpr (GU) go[j] = g;
@@ -490,7 +499,6 @@ __global__ __launch_bounds__(kThreads) void mosc_bwd_kernel(
       gv[j] = gn[j];
       if constexpr (TAN) uv[j] = un[j];
     }
-    p ^= 1;
   }
   if (!TAN) return;
   // Per (filter, oscillator) sums over the block's segments, in a fixed order:
@@ -597,15 +605,18 @@ template <int NP, bool REAL>
 void launch_fwd(const float* c1, const float* c2, const float* cw, const float* u,
                 const float* yin, float* yout, bool abs_out, int64_t B, int64_t T, int64_t F,
                 int N, int n0, hipStream_t s) {
-  const dim3 grid = mosc_grid(B, F), block(kThreads);
+  // 16 wavefronts per block where the kernel fits in 128 VGPRs (real input;
+  // without C-weights, which only one oscillator has, at most two), else 8.
+  constexpr int W = REAL ? 16 : 8, W1 = REAL && NP <= 2 ? 16 : 8;
+  const dim3 grid = mosc_grid(B, F), block(W * kWave), block1(W1 * kWave);
   if (cw && abs_out)
-    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, true, true>), grid, block, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
+    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, true, true, W>), grid, block, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
   else if (cw)
-    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, true, false>), grid, block, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
+    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, true, false, W>), grid, block, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
   else if (abs_out)
-    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, false, true>), grid, block, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
+    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, false, true, W1>), grid, block1, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
   else
-    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, false, false>), grid, block, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
+    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, false, false, W1>), grid, block1, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
 }
 
 template <int NP, bool REAL>

@@ -311,6 +311,24 @@ typedef struct rqf_proj_gemm_args {
 int rqf_proj_gemm(const rqf_proj_gemm_args *args, rqf_stream_t stream);
 
 /* ------------------------------------------------------------------------ *
+ * Gradients of the real-input layer 0's projection z = (Wr + i Wi) h, for  *
+ * a narrow input, from grad_z (complex64, F x n) in one pass:              *
+ *   grad_h (D x n)          = Re(W^H grad_z) = Wr^T Re(gz) + Wi^T Im(gz)    *
+ *   grad_w_stacked (2F x D) = [Re gz; Im gz] h^T                            *
+ * with w_stacked the real (2F x D) [Wr; Wi] and h the real (D x n) input.   *
+ * Replaces the backward GEMMs of _Layer0RealScan                            *
+ * (rqf_models/ops/fbt_scan_kernel.py:993-996).  Either output may be NULL.  *
+ * grad_h needs 1 <= D <= 16, grad_w_stacked 1 <= D <= 2 and a workspace of  *
+ * rqf_layer0_grads_workspace(F, D, n) bytes (its per-wavefront partials,    *
+ * reduced in a fixed order in fp64); wider inputs get RQF_ERR_ARG (use     *
+ * rqf_proj_gemm and a library GEMM).  Deterministic.                        *
+ * ------------------------------------------------------------------------ */
+size_t rqf_layer0_grads_workspace(int64_t F, int64_t D, int64_t n);
+int rqf_layer0_grads(const float *w_stacked, const float *grad_z, const float *h, float *grad_h,
+                     float *grad_w_stacked, int64_t F, int64_t D, int64_t n, void *workspace,
+                     size_t workspace_bytes, rqf_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
  * Self-test of the wave-level scan primitives (no reference counterpart):   *
  * in: 64 lanes x 4 complex (P, s) affine maps; out: inclusive prefix (fwd)  *
  * and suffix (rev) compositions.                                            *

@@ -57,6 +57,8 @@ class ProjGemmArgs(ctypes.Structure):
 
 SIGNATURES = {
     "rqf_proj_gemm": (ctypes.c_int, [_P, _P]),
+    "rqf_layer0_grads_workspace": (_SZ, [_I64, _I64, _I64]),
+    "rqf_layer0_grads": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
     "rqf_version": (ctypes.c_char_p, []),
     "rqf_error_string": (ctypes.c_char_p, [ctypes.c_int]),
     "rqf_btf_scan_workspace": (_SZ, [_I64, _I64, _I64]),

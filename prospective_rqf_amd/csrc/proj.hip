@@ -330,3 +330,206 @@ extern "C" int rqf_proj_gemm(const rqf_proj_gemm_args* args, rqf_stream_t stream
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? RQF_OK : (int)err;
 }
+
+// ---------------------------------------------------------------------------
+// Gradients of the real-input layer 0's projection z = (Wr + i Wi) h for a
+// narrow input (rqf_models/ops/fbt_scan_kernel.py:993-996):
+//   grad_h (D, n)        = Re(W^H gz) = Wr^T Re(gz) + Wi^T Im(gz)
+//   grad_w_stacked (2F, D) = [Re gz; Im gz] h^T.
+// With D output rows the MFMA GEMM above would spend most of its 128-row
+// tiles on padding, and the weight gradient is a reduction over all n
+// columns; this pass reads gz once.  A thread owns kL0Cols adjacent columns
+// and walks the F filters, with the weights read as wave-uniform scalars:
+// it accumulates grad_h for its columns, and (D <= kL0MaxDW) its share of
+// each filter's weight gradient, which a wavefront sum per filter turns
+// into one partial per (wavefront, filter); layer0_wpart_reduce_kernel adds
+// the partials in a fixed order in fp64.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int kL0Threads = 256;
+constexpr int kL0Cols = 4;    // columns per thread (two float4 loads of gz per filter)
+constexpr int kL0MaxD = 16;   // widest input for grad_h
+constexpr int kL0MaxDW = 2;   // widest input whose grad_w rides the same pass
+
+__device__ __forceinline__ float wave_sum_f(float v) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// VEC: n % 4 == 0 and gz 16-byte aligned, so a thread's columns all exist.
+template <int DM, bool GH, bool GW, bool VEC>
+__global__ __launch_bounds__(kL0Threads) void layer0_grads_kernel(
+    const float* __restrict__ w, const float* __restrict__ gz, const float* __restrict__ h,
+    float* __restrict__ gh, float* __restrict__ wpart, int64_t F, int D, int64_t n) {
+  const int64_t j0 = ((int64_t)blockIdx.x * kL0Threads + threadIdx.x) * kL0Cols;
+  const float* __restrict__ wr = w;          // (F, D): Re W
+  const float* __restrict__ wi = w + F * D;  // (F, D): Im W
+  float acc[kL0Cols][DM];
+  float hv[GW ? kL0Cols : 1][DM];
+#pragma unroll
+  for (int c = 0; c < kL0Cols; ++c)
+#pragma unroll
+    for (int d = 0; d < DM; ++d) {
+      acc[c][d] = 0.0f;
+      if (GW) hv[c][d] = (d < D && j0 + c < n) ? h[d * n + j0 + c] : 0.0f;
+    }
+  const int wv = (int)(threadIdx.x / kWave);
+  float* __restrict__ wp = GW ? wpart + ((int64_t)blockIdx.x * (kL0Threads / kWave) + wv) * F * D * 2
+                              : nullptr;
+  for (int64_t f = 0; f < F; ++f) {
+    const float* row = gz + 2 * (f * n + j0);
+    float g[2 * kL0Cols];
+    if (VEC) {
+#pragma unroll
+      for (int q = 0; q < kL0Cols / 2; ++q) {
+        const float4 v = *reinterpret_cast<const float4*>(row + 4 * q);
+        g[4 * q] = v.x, g[4 * q + 1] = v.y, g[4 * q + 2] = v.z, g[4 * q + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < kL0Cols; ++c) {
+        const bool in = j0 + c < n;
+        g[2 * c] = in ? row[2 * c] : 0.0f;
+        g[2 * c + 1] = in ? row[2 * c + 1] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < DM; ++d) {
+      if (d >= D) continue;
+      if (GH) {
+        const float r = wr[f * D + d], i = wi[f * D + d];
+#pragma unroll
+        for (int c = 0; c < kL0Cols; ++c)
+          acc[c][d] = fmaf(r, g[2 * c], fmaf(i, g[2 * c + 1], acc[c][d]));
+      }
+      if (GW) {
+        float sr = 0.0f, si = 0.0f;
+#pragma unroll
+        for (int c = 0; c < kL0Cols; ++c) {
+          sr = fmaf(g[2 * c], hv[c][d], sr);
+          si = fmaf(g[2 * c + 1], hv[c][d], si);
+        }
+        sr = wave_sum_f(sr);
+        si = wave_sum_f(si);
+        if (lane_id() == 0) {
+          wp[(f * D + d) * 2] = sr;
+          wp[(f * D + d) * 2 + 1] = si;
+        }
+      }
+    }
+  }
+  if (GH) {
+#pragma unroll
+    for (int d = 0; d < DM; ++d)
+      if (d < D)
+#pragma unroll
+        for (int c = 0; c < kL0Cols; ++c)
+          if (j0 + c < n) gh[d * n + j0 + c] = acc[c][d];
+  }
+}
+
+// grad_w_stacked[f][d] = sum over the P partials (fixed order, fp64) of the
+// real parts, grad_w_stacked[F + f][d] of the imaginary parts; one wavefront
+// per (f, d), lane l adding partials l, l + 64, ...
+__global__ __launch_bounds__(kWave) void layer0_wpart_reduce_kernel(const float* __restrict__ wpart,
+                                                                    int64_t P, int64_t F, int D,
+                                                                    float* __restrict__ gw) {
+  const int64_t fd = blockIdx.x;  // f * D + d
+  const int lane = threadIdx.x;
+  double sr = 0.0, si = 0.0;
+  for (int64_t p = lane; p < P; p += kWave) {
+    sr += wpart[(p * F * D + fd) * 2];
+    si += wpart[(p * F * D + fd) * 2 + 1];
+  }
+  sr = wave_sum(sr);
+  si = wave_sum(si);
+  if (lane == 0) {
+    const int64_t f = fd / D, d = fd % D;
+    gw[f * D + d] = (float)sr;
+    gw[(F + f) * D + d] = (float)si;
+  }
+}
+
+int64_t layer0_blocks(int64_t n) {
+  return (n + (int64_t)kL0Threads * kL0Cols - 1) / ((int64_t)kL0Threads * kL0Cols);
+}
+
+template <int DM, bool GH, bool GW>
+void launch_layer0(const float* w, const float* gz, const float* h, float* gh, float* wpart,
+                   int64_t F, int D, int64_t n, bool vec, hipStream_t s) {
+  const dim3 grid((unsigned)layer0_blocks(n)), block(kL0Threads);
+  if (vec)
+    hipLaunchKernelGGL((layer0_grads_kernel<DM, GH, GW, true>), grid, block, 0, s, w, gz, h, gh,
+                       wpart, F, D, n);
+  else
+    hipLaunchKernelGGL((layer0_grads_kernel<DM, GH, GW, false>), grid, block, 0, s, w, gz, h,
+                       gh, wpart, F, D, n);
+}
+
+template <int DM>
+void launch_layer0_d(const float* w, const float* gz, const float* h, float* gh, float* wpart,
+                     int64_t F, int D, int64_t n, bool vec, hipStream_t s) {
+  if (gh && wpart) {
+    if constexpr (DM <= kL0MaxDW) launch_layer0<DM, true, true>(w, gz, h, gh, wpart, F, D, n, vec, s);
+  } else if (gh) {
+    launch_layer0<DM, true, false>(w, gz, h, gh, wpart, F, D, n, vec, s);
+  } else if constexpr (DM <= kL0MaxDW) {
+    launch_layer0<DM, false, true>(w, gz, h, gh, wpart, F, D, n, vec, s);
+  }
+}
+}  // namespace
+
+extern "C" size_t rqf_layer0_grads_workspace(int64_t F, int64_t D, int64_t n) {
+  if (F < 0 || D < 1 || D > kL0MaxDW || n < 0) return 0;
+  const size_t bytes = sizeof(float) * 2 * (size_t)layer0_blocks(n) * (kL0Threads / kWave) *
+                       (size_t)F * (size_t)D;
+  return (bytes + 255) & ~(size_t)255;
+}
+
+extern "C" int rqf_layer0_grads(const float* w_stacked, const float* grad_z, const float* h,
+                                float* grad_h, float* grad_w_stacked, int64_t F, int64_t D,
+                                int64_t n, void* workspace, size_t workspace_bytes,
+                                rqf_stream_t stream) {
+  if (F < 0 || D < 1 || n < 0) return RQF_ERR_ARG;
+  if ((grad_h && D > kL0MaxD) || (grad_w_stacked && D > kL0MaxDW)) return RQF_ERR_ARG;
+  if (!grad_h && !grad_w_stacked) return RQF_OK;
+  hipStream_t s = (hipStream_t)stream;
+  // Empty sizes need no special case: with F = 0 the filter loop is empty and
+  // grad_h is written as zeros; with n = 0 there are no partials and the
+  // reduction writes zeros.
+  if ((F > 0 && n > 0 && !grad_z) || (F > 0 && grad_h && !w_stacked) ||
+      (n > 0 && grad_w_stacked && !h))
+    return RQF_ERR_ARG;
+  if (!aligned(w_stacked, 4) || !aligned(grad_z, 8) || !aligned(h, 4) || !aligned(grad_h, 4) ||
+      !aligned(grad_w_stacked, 4))
+    return RQF_ERR_ALIGN;
+  if (layer0_blocks(n) > 0x7fffffff || F * D > 0x7fffffff) return RQF_ERR_ARG;
+  float* wpart = nullptr;
+  if (grad_w_stacked) {
+    const size_t need = rqf_layer0_grads_workspace(F, D, n);
+    if (need && (!workspace || workspace_bytes < need)) return RQF_ERR_WORKSPACE;
+    wpart = (float*)workspace;
+  }
+  const bool vec = n % kL0Cols == 0 && aligned(grad_z, 16);
+  const int d = (int)D;
+  if (n == 0)
+    ;  // no columns: only the weight-gradient reduction (zeros) runs
+  else if (d <= 1)
+    launch_layer0_d<1>(w_stacked, grad_z, h, grad_h, wpart, F, d, n, vec, s);
+  else if (d <= 2)
+    launch_layer0_d<2>(w_stacked, grad_z, h, grad_h, wpart, F, d, n, vec, s);
+  else if (d <= 4)
+    launch_layer0_d<4>(w_stacked, grad_z, h, grad_h, wpart, F, d, n, vec, s);
+  else if (d <= 8)
+    launch_layer0_d<8>(w_stacked, grad_z, h, grad_h, wpart, F, d, n, vec, s);
+  else
+    launch_layer0_d<16>(w_stacked, grad_z, h, grad_h, wpart, F, d, n, vec, s);
+  if (grad_w_stacked && F > 0) {
+    const int64_t P = layer0_blocks(n) * (kL0Threads / kWave);
+    hipLaunchKernelGGL(layer0_wpart_reduce_kernel, dim3((unsigned)(F * D)), dim3(kWave), 0, s,
+                       wpart, P, F, d, grad_w_stacked);
+  }
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? RQF_OK : (int)err;
+}

@@ -246,6 +246,47 @@ def _pack_layer0_dh(w_stacked):
     return projection._padded(a)
 
 
+# Widest real inputs whose input gradient, and whose weight gradient, the
+# one-pass kernel (rqf_layer0_grads) serves.
+_LAYER0_NARROW_H = 16
+_LAYER0_NARROW_W = 2
+
+
+def _layer0_grads(w, gz, h, need_w, need_h):
+    """``(grad_w_stacked, grad_h)`` of ``z = (Wr + i Wi) h`` from ``gz`` (F, n):
+    ``[Re gz; Im gz] h^T`` and ``Re(W^H gz)``.  One pass over ``gz`` where the
+    input is narrow enough; otherwise the MFMA projection GEMM for ``grad_h``
+    and a real split-K GEMM on ``gz``'s interleaved storage for the weights."""
+    from prospective_rqf_amd import projection
+
+    filters, cols = gz.shape
+    width = h.shape[0]
+    fused_h = need_h and width <= _LAYER0_NARROW_H
+    fused_w = need_w and width <= _LAYER0_NARROW_W
+    grad_w = grad_h = None
+    if fused_h or fused_w:
+        lib = _lib.load()
+        if fused_h:
+            grad_h = torch.empty(width, cols, dtype=torch.float32, device=gz.device)
+        if fused_w:
+            grad_w = torch.empty(2 * filters, width, dtype=torch.float32, device=gz.device)
+        n = lib.rqf_layer0_grads_workspace(filters, width, cols) if fused_w else 0
+        ws = _lib.workspace(n, gz.device)
+        _lib.check(lib.rqf_layer0_grads(_lib.ptr(w), _lib.ptr(gz), _lib.ptr(h), _lib.ptr(grad_h),
+                                        _lib.ptr(grad_w), filters, width, cols, _lib.ptr(ws), n,
+                                        _lib.stream_of(gz)), "rqf_layer0_grads")
+    if need_h and grad_h is None:
+        grad_h = projection._proj_gemm(_pack_layer0_dh(w), gz, None, cols, 0, width,
+                                       gz.device)[1]
+    if need_w and grad_w is None:
+        hx = torch.zeros(2 * width, 2 * cols, dtype=torch.float32, device=h.device)
+        hx[:width, 0::2] = h
+        hx[width:, 1::2] = h
+        g = projection.weight_grad(torch.view_as_real(gz).reshape(filters, 2 * cols), hx)
+        grad_w = torch.cat((g[:, :width], g[:, width:]))
+    return grad_w, grad_h
+
+
 class _Layer0RealScan(torch.autograd.Function):
     """Real-input layer-0 projection feeding the split-ReLU recompute scan
     (rqf_models/ops/fbt_scan_kernel.py:899-1002).
@@ -254,9 +295,10 @@ class _Layer0RealScan(torch.autograd.Function):
     ``(zr, zi)`` buffers and runs planar twins of the recompute kernels.  Here
     the MFMA projection GEMM (``rqf_proj_gemm``) writes ``z`` interleaved, so
     the ordinary recompute kernels consume it; the backward reads ``grad_z``
-    where the scan leaves it for ``grad_h = [Wr; Wi]^T [Re gz; Im gz]``, and
-    forms ``grad_w_stacked = [Re gz; Im gz] h^T`` as one split-K complex GEMM
-    against the (narrow) input."""
+    where the scan leaves it: ``grad_h = [Wr; Wi]^T [Re gz; Im gz]`` and
+    ``grad_w_stacked = [Re gz; Im gz] h^T`` in one pass for narrow inputs
+    (``rqf_layer0_grads``: up to 16 wide for grad_h, 2 for the weights, which
+    covers the raw waveform), else a GEMM each."""
 
     @staticmethod
     def forward(ctx, w_stacked, h_real, C1, tap0, tap1, batch):
@@ -290,13 +332,8 @@ class _Layer0RealScan(torch.autograd.Function):
         gc1, gt0, gt1, gz = fbt_recompute_backward_raw(C1, tap0, tap1, z, carry, grad_act)
         filters, cols = w.shape[0] // 2, h.shape[1]
         gz = gz.view(filters, cols)
-        grad_w = grad_h = None
-        if ctx.needs_input_grad[0]:
-            g = projection.weight_grad(gz, h.to(torch.complex64))  # gz @ h^T, complex (F, D)
-            grad_w = torch.cat((g.real, g.imag))
-        if ctx.needs_input_grad[1]:
-            _, grad_h = projection._proj_gemm(_pack_layer0_dh(w), gz, None, cols, 0, h.shape[0],
-                                              h.device)
+        grad_w, grad_h = _layer0_grads(w, gz, h, ctx.needs_input_grad[0],
+                                       ctx.needs_input_grad[1])
         return grad_w, grad_h, gc1, gt0, gt1, None
 
 

@@ -5,8 +5,9 @@ the oracle's FBT two-tap scan with the split-ReLU mask and its adjoint
 (``oracle.twotap_fwd`` / ``twotap_bwd``, pinned elsewhere against closed
 forms and brute force), then the projection's own chain rule in float64:
 ``grad_h = Re(W^H gz)`` and ``grad_[Wr; Wi] = [Re gz; Im gz] h^T`` with
-``gz`` the oracle's drive gradient.  Input widths 1 (raw waveform), 20
-(MFCC features) and 64, rows on and off the 256-step tile, and the
+``gz`` the oracle's drive gradient.  Input widths 1 (raw waveform), 2, 3
+and 16 (the one-pass input-gradient kernel, odd and even batch*time), 20
+(MFCC features) and 64 (the MFMA GEMM), rows on and off the 256-step tile, and the
 ``needs_input_grad`` gating.  Bar: normwise relative error <= 1e-4 per
 tensor, and per channel (floor 1e-2) for the coefficient gradients.  The
 cotangent is zeroed where the fp64 state lies within 1e-4 of its maximum of a
@@ -39,7 +40,8 @@ def _f32(a):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("F,D,B,T", [(16, 1, 2, 1000), (8, 20, 3, 4096), (5, 64, 2, 1023),
-                                     (3, 2, 1, 1), (32, 1, 4, 16000)])
+                                     (3, 2, 1, 1), (32, 1, 4, 16000), (6, 16, 2, 777),
+                                     (4, 3, 3, 501)])
 def test_layer0_matches_fp64_composition(F, D, B, T):
     from oracle import oracle
 

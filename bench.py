@@ -359,13 +359,14 @@ def _plan_layer0(F, B, T, coefs, u, w, state, name, gy):
     ops = [("fbt_layer0_real_scan_fwd", fwd), ("fbt_layer0_real_scan_bwd", bwd)]
     elems = F * B * T
     # Bytes the layer must move: the waveform in and the activation out, then
-    # the cotangent in and grad_h out; the drive z between the projection and
-    # the scan is this implementation's choice, not counted.
+    # the cotangent in and grad_h out.  grad_z, which the backward writes and
+    # reads once more for the projection's gradients, is not counted.
     nbytes = {"fbt_layer0_real_scan_fwd": 8 * elems + 4 * B * T,
               "fbt_layer0_real_scan_bwd": 8 * elems + 8 * B * T}
-    kernels = {"fbt_layer0_real_scan_fwd": "proj_gemm_kernel (z = [Wr; Wi] h) + fbt_fwd_rb_kernel",
-               "fbt_layer0_real_scan_bwd": ("fbt_bwd_rb_kernel / fbt_bwd_kernel + coef_reduce_kernel "
-                                            "+ proj_gemm_kernel (grad_h) + split-K grad_w")}
+    kernels = {"fbt_layer0_real_scan_fwd": "fbt_fwd_rb_kernel<layer-0 drive z = wz x>",
+               "fbt_layer0_real_scan_bwd": ("fbt_bwd_rb_kernel / fbt_bwd_kernel <layer-0 drive> "
+                                            "+ coef_reduce_kernel + layer0_grads_kernel + "
+                                            "layer0_wpart_reduce_kernel")}
     contract = ("layer 0 on the raw waveform: stacked real projection + split-ReLU recompute "
                 "scan; gy cotangent; grads of [Wr; Wi], the waveform and the coefficients")
     config = {"workload": name + " [whole layer 0: fbt_layer0_real_scan]", "F": F, "B": B, "T": T,

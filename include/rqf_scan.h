@@ -178,6 +178,27 @@ int rqf_fbt_recompute_skip_fwd(const float *c1, const float *tap0, const float *
                                const float *z, const float *skip, float *act, float *carry,
                                int64_t F, int64_t B, int64_t T, rqf_stream_t stream);
 
+/* Layer 0 on a real input of one feature per step (the raw waveform): the
+ * recompute scan with its drive formed on the fly, z[f,b,t] = wz[f] x[b,t],
+ * from x real (B, T) and wz complex (F,), instead of read from a
+ * materialised (F,B,T) drive.  Replaces the stacked real GEMM plus
+ * `_fbt_recompute_planar_forward_kernel` of `_Layer0RealScan.forward`
+ * (rqf_models/ops/fbt_scan_kernel.py:692-761, 939-972) for D = 1.  Same
+ * outputs as rqf_fbt_recompute_fwd on z = wz x. */
+int rqf_fbt_layer0_fwd(const float *c1, const float *tap0, const float *tap1, const float *wz,
+                       const float *x, float *act, float *carry, int64_t F, int64_t B, int64_t T,
+                       rqf_stream_t stream);
+
+/* The backward of rqf_fbt_layer0_fwd: replays the scan from the carries with
+ * the drive formed from x, and writes grad_z (F,B,T) complex and the
+ * coefficient gradients, as rqf_fbt_recompute_bwd on z = wz x.  Replaces
+ * `_fbt_recompute_planar_backward_kernel` (fbt_scan_kernel.py:764-896);
+ * grad_z feeds rqf_layer0_grads.  Workspace: rqf_fbt_workspace(F, B, T). */
+int rqf_fbt_layer0_bwd(const float *c1, const float *tap0, const float *tap1, const float *wz,
+                       const float *x, const float *carry, const float *grad_out, float *grad_z,
+                       float *grad_c1, float *grad_tap0, float *grad_tap1, int64_t F, int64_t B,
+                       int64_t T, void *workspace, size_t workspace_bytes, rqf_stream_t stream);
+
 /* Replaces `_fbt_recompute_backward_kernel[grid](...)`
  * (rqf_models/ops/fbt_scan_kernel.py:653-669). */
 int rqf_fbt_recompute_bwd(const float *c1, const float *tap0, const float *tap1,

@@ -86,6 +86,10 @@ SIGNATURES = {
         ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "rqf_fbt_recompute_bwd": (
         ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
+    "rqf_fbt_layer0_fwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
+    "rqf_fbt_layer0_bwd": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
     "rqf_fbt_recompute_bwd_noalloc": (
         ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "rqf_selective_fwd": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P]),

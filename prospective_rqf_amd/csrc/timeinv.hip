@@ -95,6 +95,78 @@ __device__ __forceinline__ void store8(float* __restrict__ row, int64_t tb, int6
 }
 
 // ---------------------------------------------------------------------------
+// The drive z of a row: read from a complex (F*B, T) array, or (L0: layer 0
+// on a real input of one feature) formed on the fly as z[f,b,t] = wz[f]
+// x[b,t] from the real (B, T) input and the filter's complex weight.  In the
+// L0 form every row of one batch element reads the same x row, which stays
+// in L2, so the drive costs no HBM traffic of its own.
+// ---------------------------------------------------------------------------
+struct Drive {
+  const float* z;   // complex (F*B, T) (not L0)
+  const float* x;   // real (B, T): set for L0, null otherwise
+  const float* wz;  // complex (F,) (L0)
+};
+
+struct RowDrive {
+  const float* zr;  // the row's z
+  const float* xr;  // the row's x (L0)
+  c32 wz;           // the row's weight (L0)
+};
+
+template <bool L0>
+__device__ __forceinline__ RowDrive row_drive(const float* z, const float* x, const float* wz,
+                                              int64_t row, int64_t f, int64_t B, int64_t T) {
+  RowDrive r;
+  r.zr = L0 ? nullptr : z + 2 * row * T;
+  r.xr = L0 ? x + (row % B) * T : nullptr;
+  r.wz = L0 ? ldc(wz, f) : mk(0.0f, 0.0f);
+  return r;
+}
+
+// z at step t (0 outside [0, T)).
+template <bool L0>
+__device__ __forceinline__ c32 drive_at(const RowDrive& r, int64_t t, int64_t T) {
+  if (t < 0 || t >= T) return mk(0.0f, 0.0f);
+  return L0 ? cscale(r.xr[t], r.wz) : ldc(r.zr, t);
+}
+
+// z at the lane's K steps [tb, tb + K).  FULL: the whole tile is in range and
+// rows are 16-byte aligned (L0: T % 4 == 0 and x aligned; otherwise the
+// complex row is aligned and, with LDS, moved through the wavefront's slice).
+template <int K, bool L0, bool LDS>
+__device__ __forceinline__ void drive_tile(const RowDrive& r, int64_t t0, int64_t tb, int64_t T,
+                                           int lane, bool full, float4* io, c32 (&v)[K]) {
+  if (L0) {
+    if (full) {
+      static_assert(K % 4 == 0, "whole float4s of x per lane");
+#pragma unroll
+      for (int j = 0; j < K / 4; ++j) {
+        const float4 q = *reinterpret_cast<const float4*>(r.xr + tb + 4 * j);
+        v[4 * j] = cscale(q.x, r.wz);
+        v[4 * j + 1] = cscale(q.y, r.wz);
+        v[4 * j + 2] = cscale(q.z, r.wz);
+        v[4 * j + 3] = cscale(q.w, r.wz);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < K; ++k) v[k] = tb + k < T ? cscale(r.xr[tb + k], r.wz) : mk(0.0f, 0.0f);
+    }
+  } else if (full && LDS) {
+    load_c_lds<K>(r.zr, (int)t0, lane, io, v);
+  } else if (full) {
+#pragma unroll
+    for (int j = 0; j < K / 2; ++j) {
+      const float4 q = *reinterpret_cast<const float4*>(r.zr + 2 * tb + 4 * j);
+      v[2 * j] = mk(q.x, q.y);
+      v[2 * j + 1] = mk(q.z, q.w);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < K; ++k) v[k] = (tb + k < T) ? ldc(r.zr, tb + k) : mk(0.0f, 0.0f);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // FBT forward: raw (optional), split-ReLU act (optional), entry carry per tile
 // (optional).
 // ---------------------------------------------------------------------------
@@ -181,10 +253,11 @@ static_assert(kTfTile % kTiTile == 0, "forward tiles hold whole carry tiles");
 
 // skip (nullable, FBT like z): added to the act output (a residual connection
 // around the layer); raw and the carries stay the scan's own states.
-template <bool VEC>
+template <bool VEC, bool L0 = false>
 __global__ __launch_bounds__(kTfWaves* kWave) void fbt_fwd_rb_kernel(
     const float* __restrict__ c1, const float* __restrict__ tap0, const float* __restrict__ tap1,
-    const float* __restrict__ z, const float* __restrict__ skip, float* __restrict__ raw,
+    const float* __restrict__ z, const float* __restrict__ x, const float* __restrict__ wz,
+    const float* __restrict__ skip, float* __restrict__ raw,
     float* __restrict__ act, float* __restrict__ carry, int64_t F, int64_t B, int64_t T,
     int64_t nc) {
   constexpr int K = kTfK, W = kTfWaves;
@@ -200,7 +273,7 @@ __global__ __launch_bounds__(kTfWaves* kWave) void fbt_fwd_rb_kernel(
   const ScanPow pw = scan_pow_fwd(A, lane);
   const c32 pex = narrow(dpow(A, lane));          // power of the lanes before this one
   const c32 ptile = uniform(narrow(dpow(A, kWave)));  // a tile's map
-  const float* zr = z + 2 * row * T;
+  const RowDrive rd = row_drive<L0>(z, x, wz, row, f, B, T);
   float* rawr = raw ? raw + 2 * row * T : nullptr;
   float* actr = act ? act + 2 * row * T : nullptr;
   const float* skr = skip ? skip + 2 * row * T : nullptr;
@@ -215,13 +288,8 @@ __global__ __launch_bounds__(kTfWaves* kWave) void fbt_fwd_rb_kernel(
     c32 s = mk(0.0f, 0.0f);
     if (has) {
       c32 zv[K];
-      if (full) {
-        load_c_lds<K>(zr, (int)t0, lane, io, zv);
-      } else {
-#pragma unroll
-        for (int k = 0; k < K; ++k) zv[k] = (tb + k < T) ? ldc(zr, tb + k) : mk(0.0f, 0.0f);
-      }
-      const c32 zlast = t0 > 0 ? ldc(zr, t0 - 1) : mk(0.0f, 0.0f);
+      drive_tile<K, L0, true>(rd, t0, tb, T, lane, full, io, zv);
+      const c32 zlast = drive_at<L0>(rd, t0 - 1, T);
       const c32 zp0 = shift_up(zv[K - 1], zlast, lane);
 #pragma unroll
       for (int k = 0; k < K; ++k) u[k] = cmad(k1, k ? zv[k - 1] : zp0, cmul(k0, zv[k]));
@@ -369,10 +437,11 @@ __device__ __forceinline__ void st_tile(float* __restrict__ row, int64_t t0, int
 }
 
 // Super-tiles are walked from the end; wavefront w takes tile w of each.
-template <bool VEC, bool REPLAY>
+template <bool VEC, bool REPLAY, bool L0 = false>
 __global__ __launch_bounds__(kRbWaves* kWave) void fbt_bwd_rb_kernel(
     const float* __restrict__ c1, const float* __restrict__ tap0, const float* __restrict__ tap1,
-    const float* __restrict__ z, const float* __restrict__ raw, const float* __restrict__ carry,
+    const float* __restrict__ z, const float* __restrict__ x, const float* __restrict__ wz,
+    const float* __restrict__ raw, const float* __restrict__ carry,
     const float* __restrict__ gout, int mask, float* __restrict__ gz,
     double* __restrict__ partial, int64_t F, int64_t B, int64_t T, int64_t nc) {
   constexpr int K = kTbK, TILE = kTbTile, W = kRbWaves;
@@ -397,7 +466,7 @@ __global__ __launch_bounds__(kRbWaves* kWave) void fbt_bwd_rb_kernel(
   const RevPow pr = scan_pow_rev(A, lane);
   const c32 psfx = narrow(dpow(Ac, kWave - lane));     // this lane and the ones after it
   const c32 ptile = uniform(narrow(dpow(Ac, kWave)));  // a whole tile
-  const float* zr = z + 2 * row * T;
+  const RowDrive rd = row_drive<L0>(z, x, wz, row, f, B, T);
   const float* rr = REPLAY ? nullptr : raw + 2 * row * T;
   const float* gr = gout + 2 * row * T;
   float* gzr = gz + 2 * row * T;
@@ -417,9 +486,9 @@ __global__ __launch_bounds__(kRbWaves* kWave) void fbt_bwd_rb_kernel(
     c32 zp0 = mk(0.0f, 0.0f), yp0 = mk(0.0f, 0.0f);
     c32 r = mk(0.0f, 0.0f);
     if (has) {
-      ld_tile<K>(zr, t0, tb, T, lane, full, io, zv);
+      drive_tile<K, L0, RQF_TI_BWD_LDS_IO>(rd, t0, tb, T, lane, full, io, zv);
       ld_tile<K>(gr, t0, tb, T, lane, full, io, ev);
-      const c32 zprev_tile = t0 > 0 ? ldc(zr, t0 - 1) : mk(0.0f, 0.0f);
+      const c32 zprev_tile = drive_at<L0>(rd, t0 - 1, T);
       zp0 = shift_up(zv[K - 1], zprev_tile, lane);
       if (REPLAY) {
         c32 u[K];
@@ -516,10 +585,11 @@ __global__ __launch_bounds__(kRbWaves* kWave) void fbt_bwd_rb_kernel(
 // is read.  MASK: cotangent is on the split-ReLU output.
 // partial: per row, 6 doubles (gc1.re, gc1.im, gk0.re, gk0.im, gk1.re, gk1.im).
 // ---------------------------------------------------------------------------
-template <bool VEC, bool REPLAY>
+template <bool VEC, bool REPLAY, bool L0 = false>
 __global__ __launch_bounds__(kTiWaves* kWave) void fbt_bwd_kernel(
     const float* __restrict__ c1, const float* __restrict__ tap0, const float* __restrict__ tap1,
-    const float* __restrict__ z, const float* __restrict__ raw, const float* __restrict__ carry,
+    const float* __restrict__ z, const float* __restrict__ x, const float* __restrict__ wz,
+    const float* __restrict__ raw, const float* __restrict__ carry,
     const float* __restrict__ gout, int mask, float* __restrict__ gz,
     double* __restrict__ partial, int64_t F, int64_t B, int64_t T, int64_t nc) {
   const int lane = lane_id();
@@ -531,18 +601,22 @@ __global__ __launch_bounds__(kTiWaves* kWave) void fbt_bwd_kernel(
   const c64d A = dpow(widen(a), kTiK);
   const ScanPow pf = scan_pow_fwd(A, lane);  // the replay's forward scan; in-row adjoint powers
   const RevPow pr = scan_pow_rev(A, lane);
-  const float* zr = z + 2 * row * T;
+  const RowDrive rd = row_drive<L0>(z, x, wz, row, f, B, T);
   const float* rr = REPLAY ? nullptr : raw + 2 * row * T;
   const float* gr = gout + 2 * row * T;
   float* gzr = gz + 2 * row * T;
   c32 gcarry = mk(0.0f, 0.0f);
   double s1r = 0, s1i = 0, s0r = 0, s0i = 0, s2r = 0, s2i = 0;
   const int64_t ntiles = (T + kTiTile - 1) / kTiTile;
+  // The lane's kTiK drive values from step tb (per-lane range check, as load8).
+  auto load_z = [&](int64_t tb, c32(&v)[kTiK]) {
+    drive_tile<kTiK, L0, false>(rd, 0, tb, T, lane, VEC && tb + kTiK <= T, nullptr, v);
+  };
 #if RQF_TI_PREFETCH
   // The previous tile's (in walk order: next) drive and cotangent are loaded
   // before this tile's scans (software pipeline).
   c32 znext[kTiK], enext[kTiK];
-  load8<VEC>(zr, (ntiles - 1) * kTiTile + lane * kTiK, T, znext);
+  load_z((ntiles - 1) * kTiTile + lane * kTiK, znext);
   load8<VEC>(gr, (ntiles - 1) * kTiTile + lane * kTiK, T, enext);
 #endif
   for (int64_t tile = ntiles - 1; tile >= 0; --tile) {
@@ -557,14 +631,14 @@ __global__ __launch_bounds__(kTiWaves* kWave) void fbt_bwd_kernel(
       ev[k] = enext[k];
     }
     if (tile > 0) {
-      load8<VEC>(zr, tb - kTiTile, T, znext);
+      load_z(tb - kTiTile, znext);
       load8<VEC>(gr, tb - kTiTile, T, enext);
     }
 #else
-    load8<VEC>(zr, tb, T, zv);
+    load_z(tb, zv);
     load8<VEC>(gr, tb, T, ev);
 #endif
-    const c32 zprev_tile = t0 > 0 ? ldc(zr, t0 - 1) : mk(0.0f, 0.0f);
+    const c32 zprev_tile = drive_at<L0>(rd, t0 - 1, T);
     const c32 zp0 = shift_up(zv[kTiK - 1], zprev_tile, lane);
     c32 yp0;
     if (REPLAY) {
@@ -679,6 +753,7 @@ __global__ __launch_bounds__(kWave) void coef_reduce_kernel(const double* __rest
 
 inline bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15) == 0; }
 inline bool aligned8(const void* p) { return p == nullptr || ((uintptr_t)p & 7) == 0; }
+inline bool aligned4(const void* p) { return p == nullptr || ((uintptr_t)p & 3) == 0; }
 inline size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 int launch_status() {
@@ -686,94 +761,112 @@ int launch_status() {
   return err == hipSuccess ? RQF_OK : (int)err;
 }
 
-int fbt_fwd(const float* c1, const float* t0, const float* t1, const float* z, const float* skip,
+// z may also come as the layer-0 drive (drv.x set: z = wz[f] x[b, t]).
+int fbt_fwd(const float* c1, const float* t0, const float* t1, Drive drv, const float* skip,
             float* raw, float* act, float* carry, int64_t F, int64_t B, int64_t T,
             hipStream_t s) {
   if (F < 0 || B < 0 || T < 0) return RQF_ERR_ARG;
   const int64_t R = F * B;
   if (R == 0 || T == 0) return RQF_OK;
-  if (!c1 || !t0 || !t1 || !z || (!raw && !act)) return RQF_ERR_ARG;
-  if (!aligned8(z) || !aligned8(skip) || !aligned8(raw) || !aligned8(act) || !aligned8(carry))
+  const bool l0 = drv.x != nullptr;
+  if (!c1 || !t0 || !t1 || (l0 ? !drv.wz : !drv.z) || (!raw && !act))
+    return RQF_ERR_ARG;
+  if (!aligned8(drv.z) || !aligned8(drv.wz) || !aligned4(drv.x) || !aligned8(skip) ||
+      !aligned8(raw) || !aligned8(act) || !aligned8(carry))
     return RQF_ERR_ALIGN;
   if (skip && !act) return RQF_ERR_ARG;
   const int64_t nc = (T + kTiTile - 1) / kTiTile;
-  const bool vec =
-      T % 2 == 0 && aligned16(z) && aligned16(skip) && aligned16(raw) && aligned16(act);
-  if (!RQF_TI_FWD_RB && skip) return RQF_ERR_ARG;  // the per-row forward has no skip input
+  const bool vec = T % 2 == 0 && (l0 ? T % 4 == 0 && aligned16(drv.x) : aligned16(drv.z)) &&
+                   aligned16(skip) && aligned16(raw) && aligned16(act);
+  // the per-row forward has no skip input and no layer-0 drive
+  if (!RQF_TI_FWD_RB && (skip || l0)) return RQF_ERR_ARG;
   if (RQF_TI_FWD_RB) {
     const dim3 grid((unsigned)R), block(kTfWaves * kWave);
-    if (vec)
-      hipLaunchKernelGGL(fbt_fwd_rb_kernel<true>, grid, block, 0, s, c1, t0, t1, z, skip, raw, act, carry,
-                         F, B, T, nc);
+    if (l0 && vec)
+      hipLaunchKernelGGL((fbt_fwd_rb_kernel<true, true>), grid, block, 0, s, c1, t0, t1, drv.z, drv.x, drv.wz,
+                         skip, raw, act, carry, F, B, T, nc);
+    else if (l0)
+      hipLaunchKernelGGL((fbt_fwd_rb_kernel<false, true>), grid, block, 0, s, c1, t0, t1, drv.z, drv.x, drv.wz,
+                         skip, raw, act, carry, F, B, T, nc);
+    else if (vec)
+      hipLaunchKernelGGL((fbt_fwd_rb_kernel<true, false>), grid, block, 0, s, c1, t0, t1, drv.z, drv.x, drv.wz,
+                         skip, raw, act, carry, F, B, T, nc);
     else
-      hipLaunchKernelGGL(fbt_fwd_rb_kernel<false>, grid, block, 0, s, c1, t0, t1, z, skip, raw, act,
-                         carry, F, B, T, nc);
+      hipLaunchKernelGGL((fbt_fwd_rb_kernel<false, false>), grid, block, 0, s, c1, t0, t1, drv.z, drv.x, drv.wz,
+                         skip, raw, act, carry, F, B, T, nc);
     return launch_status();
   }
   const dim3 grid((unsigned)((R + kTiWaves - 1) / kTiWaves)), block(kTiWaves * kWave);
   if (vec)
-    hipLaunchKernelGGL(fbt_fwd_kernel<true>, grid, block, 0, s, c1, t0, t1, z, raw, act, carry, F,
-                       B, T, nc);
+    hipLaunchKernelGGL(fbt_fwd_kernel<true>, grid, block, 0, s, c1, t0, t1, drv.z, raw, act,
+                       carry, F, B, T, nc);
   else
-    hipLaunchKernelGGL(fbt_fwd_kernel<false>, grid, block, 0, s, c1, t0, t1, z, raw, act, carry,
-                       F, B, T, nc);
+    hipLaunchKernelGGL(fbt_fwd_kernel<false>, grid, block, 0, s, c1, t0, t1, drv.z, raw, act,
+                       carry, F, B, T, nc);
   return launch_status();
 }
 
 size_t fbt_ws(int64_t F, int64_t B) { return round256(sizeof(double) * 6 * (size_t)(F * B)); }
 
-int fbt_bwd(const float* c1, const float* t0, const float* t1, const float* z, const float* raw,
+template <bool L0>
+void launch_fbt_bwd_kernels(bool rowblock, bool vec, const float* c1, const float* t0,
+                            const float* t1, Drive drv, const float* raw, const float* carry,
+                            const float* gout, int mask, float* gz, double* partial, int64_t F,
+                            int64_t B, int64_t T, int64_t nc, hipStream_t s) {
+  const int64_t R = F * B;
+  const dim3 grid = rowblock ? dim3((unsigned)R) : dim3((unsigned)((R + kTiWaves - 1) / kTiWaves));
+  const dim3 block = rowblock ? dim3(kRbWaves * kWave) : dim3(kTiWaves * kWave);
+#define RQF_FBT_BWD(KERNEL, V, REPLAY)                                                         \
+  hipLaunchKernelGGL((KERNEL<V, REPLAY, L0>), grid, block, 0, s, c1, t0, t1, drv.z, drv.x,      \
+                     drv.wz, raw, carry, gout, mask, gz, partial, F, B, T, nc)
+  if (rowblock) {
+    if (carry) {
+      if (vec) RQF_FBT_BWD(fbt_bwd_rb_kernel, true, true);
+      else RQF_FBT_BWD(fbt_bwd_rb_kernel, false, true);
+    } else {
+      if (vec) RQF_FBT_BWD(fbt_bwd_rb_kernel, true, false);
+      else RQF_FBT_BWD(fbt_bwd_rb_kernel, false, false);
+    }
+  } else if (carry) {
+    if (vec) RQF_FBT_BWD(fbt_bwd_kernel, true, true);
+    else RQF_FBT_BWD(fbt_bwd_kernel, false, true);
+  } else {
+    if (vec) RQF_FBT_BWD(fbt_bwd_kernel, true, false);
+    else RQF_FBT_BWD(fbt_bwd_kernel, false, false);
+  }
+#undef RQF_FBT_BWD
+}
+
+// z may also come as the layer-0 drive (drv.x set: z = wz[f] x[b, t]).
+int fbt_bwd(const float* c1, const float* t0, const float* t1, Drive drv, const float* raw,
             const float* carry, const float* gout, int mask, float* gz, float* gc1, float* gt0,
             float* gt1, int64_t F, int64_t B, int64_t T, void* ws, size_t ws_bytes,
             hipStream_t s) {
   if (F < 0 || B < 0 || T < 0) return RQF_ERR_ARG;
   if (F == 0) return RQF_OK;
   if (!gc1 || !gt0 || !gt1) return RQF_ERR_ARG;
-  if (B * T > 0 && (!c1 || !t0 || !t1 || !z || !gout || !gz || (!raw && !carry)))
+  const bool l0 = drv.x != nullptr;
+  if (B * T > 0 && (!c1 || !t0 || !t1 || (l0 ? !drv.wz : !drv.z) || !gout || !gz ||
+                    (!raw && !carry)))
     return RQF_ERR_ARG;
-  if (!aligned8(z) || !aligned8(raw) || !aligned8(gout) || !aligned8(gz)) return RQF_ERR_ALIGN;
+  if (!aligned8(drv.z) || !aligned8(drv.wz) || !aligned4(drv.x) || !aligned8(raw) ||
+      !aligned8(gout) || !aligned8(gz))
+    return RQF_ERR_ALIGN;
   const size_t need = fbt_ws(F, B);
   if (need && (!ws || ws_bytes < need)) return RQF_ERR_WORKSPACE;
   double* partial = (double*)ws;
   const int64_t R = F * B;
   if (R > 0 && T > 0) {
     const int64_t nc = (T + kTiTile - 1) / kTiTile;
-    const bool vec = T % 2 == 0 && aligned16(z) && aligned16(raw) && aligned16(gout) && aligned16(gz);
+    const bool vec = T % 2 == 0 && (l0 ? T % 4 == 0 && aligned16(drv.x) : aligned16(drv.z)) &&
+                     aligned16(raw) && aligned16(gout) && aligned16(gz);
     const bool rowblock = RQF_TI_ROWBLOCK == 2 || (RQF_TI_ROWBLOCK == 1 && T % kTiTile == 0);
-    const dim3 grid = rowblock ? dim3((unsigned)R)
-                               : dim3((unsigned)((R + kTiWaves - 1) / kTiWaves));
-    const dim3 block = rowblock ? dim3(kRbWaves * kWave) : dim3(kTiWaves * kWave);
-    if (rowblock) {
-      if (carry) {
-        if (vec)
-          hipLaunchKernelGGL((fbt_bwd_rb_kernel<true, true>), grid, block, 0, s, c1, t0, t1, z,
-                             raw, carry, gout, mask, gz, partial, F, B, T, nc);
-        else
-          hipLaunchKernelGGL((fbt_bwd_rb_kernel<false, true>), grid, block, 0, s, c1, t0, t1, z,
-                             raw, carry, gout, mask, gz, partial, F, B, T, nc);
-      } else {
-        if (vec)
-          hipLaunchKernelGGL((fbt_bwd_rb_kernel<true, false>), grid, block, 0, s, c1, t0, t1, z,
-                             raw, carry, gout, mask, gz, partial, F, B, T, nc);
-        else
-          hipLaunchKernelGGL((fbt_bwd_rb_kernel<false, false>), grid, block, 0, s, c1, t0, t1, z,
-                             raw, carry, gout, mask, gz, partial, F, B, T, nc);
-      }
-    } else if (carry) {
-      if (vec)
-        hipLaunchKernelGGL((fbt_bwd_kernel<true, true>), grid, block, 0, s, c1, t0, t1, z, raw,
-                           carry, gout, mask, gz, partial, F, B, T, nc);
-      else
-        hipLaunchKernelGGL((fbt_bwd_kernel<false, true>), grid, block, 0, s, c1, t0, t1, z, raw,
-                           carry, gout, mask, gz, partial, F, B, T, nc);
-    } else {
-      if (vec)
-        hipLaunchKernelGGL((fbt_bwd_kernel<true, false>), grid, block, 0, s, c1, t0, t1, z, raw,
-                           carry, gout, mask, gz, partial, F, B, T, nc);
-      else
-        hipLaunchKernelGGL((fbt_bwd_kernel<false, false>), grid, block, 0, s, c1, t0, t1, z, raw,
-                           carry, gout, mask, gz, partial, F, B, T, nc);
-    }
+    if (l0)
+      launch_fbt_bwd_kernels<true>(rowblock, vec, c1, t0, t1, drv, raw, carry, gout, mask, gz,
+                                   partial, F, B, T, nc, s);
+    else
+      launch_fbt_bwd_kernels<false>(rowblock, vec, c1, t0, t1, drv, raw, carry, gout, mask, gz,
+                                    partial, F, B, T, nc, s);
     hipLaunchKernelGGL(coef_reduce_kernel, dim3((unsigned)F), dim3(kWave), 0, s,
                        partial, F, B, B, (int64_t)1, gc1, gt0, gt1);
   } else {
@@ -830,7 +923,7 @@ extern "C" int rqf_fbt_prospective_fwd(const float* c1, const float* tap0, const
                                        const float* z, float* raw, float* act, int64_t F,
                                        int64_t B, int64_t T, rqf_stream_t stream) {
   if (!raw && F * B * T > 0) return RQF_ERR_ARG;
-  return fbt_fwd(c1, tap0, tap1, z, nullptr, raw, act, nullptr, F, B, T, (hipStream_t)stream);
+  return fbt_fwd(c1, tap0, tap1, Drive{z, nullptr, nullptr}, nullptr, raw, act, nullptr, F, B, T, (hipStream_t)stream);
 }
 
 extern "C" int rqf_fbt_prospective_bwd(const float* c1, const float* tap0, const float* tap1,
@@ -839,7 +932,7 @@ extern "C" int rqf_fbt_prospective_bwd(const float* c1, const float* tap0, const
                                        float* grad_tap0, float* grad_tap1, int64_t F, int64_t B,
                                        int64_t T, void* ws, size_t ws_bytes, rqf_stream_t stream) {
   if (!raw && F * B * T > 0) return RQF_ERR_ARG;
-  return fbt_bwd(c1, tap0, tap1, z, raw, nullptr, grad_out, fuse_act, grad_z, grad_c1, grad_tap0,
+  return fbt_bwd(c1, tap0, tap1, Drive{z, nullptr, nullptr}, raw, nullptr, grad_out, fuse_act, grad_z, grad_c1, grad_tap0,
                  grad_tap1, F, B, T, ws, ws_bytes, (hipStream_t)stream);
 }
 
@@ -847,7 +940,7 @@ extern "C" int rqf_fbt_recompute_fwd(const float* c1, const float* tap0, const f
                                      const float* z, float* act, float* carry, int64_t F,
                                      int64_t B, int64_t T, rqf_stream_t stream) {
   if ((!act || !carry) && F * B * T > 0) return RQF_ERR_ARG;
-  return fbt_fwd(c1, tap0, tap1, z, nullptr, nullptr, act, carry, F, B, T, (hipStream_t)stream);
+  return fbt_fwd(c1, tap0, tap1, Drive{z, nullptr, nullptr}, nullptr, nullptr, act, carry, F, B, T, (hipStream_t)stream);
 }
 
 extern "C" int rqf_fbt_recompute_skip_fwd(const float* c1, const float* tap0, const float* tap1,
@@ -855,7 +948,7 @@ extern "C" int rqf_fbt_recompute_skip_fwd(const float* c1, const float* tap0, co
                                           float* carry, int64_t F, int64_t B, int64_t T,
                                           rqf_stream_t stream) {
   if ((!act || !carry || !skip) && F * B * T > 0) return RQF_ERR_ARG;
-  return fbt_fwd(c1, tap0, tap1, z, skip, nullptr, act, carry, F, B, T, (hipStream_t)stream);
+  return fbt_fwd(c1, tap0, tap1, Drive{z, nullptr, nullptr}, skip, nullptr, act, carry, F, B, T, (hipStream_t)stream);
 }
 
 extern "C" int rqf_fbt_recompute_bwd(const float* c1, const float* tap0, const float* tap1,
@@ -864,7 +957,7 @@ extern "C" int rqf_fbt_recompute_bwd(const float* c1, const float* tap0, const f
                                      float* grad_tap1, int64_t F, int64_t B, int64_t T, void* ws,
                                      size_t ws_bytes, rqf_stream_t stream) {
   if (!carry && F * B * T > 0) return RQF_ERR_ARG;
-  return fbt_bwd(c1, tap0, tap1, z, nullptr, carry, grad_out, 1, grad_z, grad_c1, grad_tap0,
+  return fbt_bwd(c1, tap0, tap1, Drive{z, nullptr, nullptr}, nullptr, carry, grad_out, 1, grad_z, grad_c1, grad_tap0,
                  grad_tap1, F, B, T, ws, ws_bytes, (hipStream_t)stream);
 }
 
@@ -888,7 +981,7 @@ extern "C" int rqf_fbt_recompute_bwd_noalloc(const float* c1, const float* tap0,
   }
   // Every row's partial slot is written before the ordered reduction reads
   // it (same stream), so nothing is cleared.
-  return fbt_bwd(c1, tap0, tap1, z, nullptr, carry, grad_out, 1, grad_z, grad_c1, grad_tap0,
+  return fbt_bwd(c1, tap0, tap1, Drive{z, nullptr, nullptr}, nullptr, carry, grad_out, 1, grad_z, grad_c1, grad_tap0,
                  grad_tap1, F, B, T, ws, RQF_NOALLOC_SCRATCH_BYTES, (hipStream_t)stream);
 }
 
@@ -909,4 +1002,24 @@ extern "C" const char* rqf_error_string(int code) {
     default:
       return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
   }
+}
+
+extern "C" int rqf_fbt_layer0_fwd(const float* c1, const float* tap0, const float* tap1,
+                                  const float* wz, const float* x, float* act, float* carry,
+                                  int64_t F, int64_t B, int64_t T, rqf_stream_t stream) {
+  if (!x && F * B * T > 0) return RQF_ERR_ARG;
+  return fbt_fwd(c1, tap0, tap1, Drive{nullptr, x, wz}, nullptr, nullptr, act, carry, F, B, T,
+                 (hipStream_t)stream);
+}
+
+extern "C" int rqf_fbt_layer0_bwd(const float* c1, const float* tap0, const float* tap1,
+                                  const float* wz, const float* x, const float* carry,
+                                  const float* grad_out, float* grad_z, float* grad_c1,
+                                  float* grad_tap0, float* grad_tap1, int64_t F, int64_t B,
+                                  int64_t T, void* workspace, size_t workspace_bytes,
+                                  rqf_stream_t stream) {
+  if (!x && F * B * T > 0) return RQF_ERR_ARG;
+  return fbt_bwd(c1, tap0, tap1, Drive{nullptr, x, wz}, nullptr, carry, grad_out, 1, grad_z,
+                 grad_c1, grad_tap0, grad_tap1, F, B, T, workspace, workspace_bytes,
+                 (hipStream_t)stream);
 }

@@ -292,9 +292,12 @@ class _Layer0RealScan(torch.autograd.Function):
     (rqf_models/ops/fbt_scan_kernel.py:899-1002).
 
     The reference writes the stacked real GEMM ``[Wr; Wi] @ h`` to planar
-    ``(zr, zi)`` buffers and runs planar twins of the recompute kernels.  Here
-    the MFMA projection GEMM (``rqf_proj_gemm``) writes ``z`` interleaved, so
-    the ordinary recompute kernels consume it; the backward reads ``grad_z``
+    ``(zr, zi)`` buffers and runs planar twins of the recompute kernels.  Here,
+    with one input feature (the raw waveform), the scan kernels form the drive
+    ``z = (Wr + i Wi) x`` themselves (``rqf_fbt_layer0_fwd`` / ``_bwd``): no
+    GEMM and no drive tensor.  Wider inputs go through the MFMA projection
+    GEMM (``rqf_proj_gemm``), which writes ``z`` interleaved, so the ordinary
+    recompute kernels consume it.  The backward reads ``grad_z``
     where the scan leaves it: ``grad_h = [Wr; Wi]^T [Re gz; Im gz]`` and
     ``grad_w_stacked = [Re gz; Im gz] h^T`` in one pass for narrow inputs
     (``rqf_layer0_grads``: up to 16 wide for grad_h, 2 for the weights, which
@@ -317,10 +320,28 @@ class _Layer0RealScan(torch.autograd.Function):
         w = w_stacked.detach().to(torch.float32).contiguous()
         h = h_real.detach().to(torch.float32).contiguous()
         filters, cols = w.shape[0] // 2, h.shape[1]
+        time = cols // batch
+        if w.shape[1] == 1:
+            # One input feature: the scan forms z = (Wr + i Wi) x itself.
+            C1, tap0, tap1 = _coefs(C1, tap0, tap1, filters)
+            _lib.require_device(C1)
+            wz = torch.complex(w[:filters, 0], w[filters:, 0]).contiguous()
+            lib = _lib.load()
+            act = torch.empty(filters, batch, time, dtype=torch.complex64, device=h.device)
+            carry = torch.empty((filters * batch, max(lib.rqf_fbt_carry_chunks(time), 1)),
+                                dtype=torch.complex64, device=h.device)
+            _lib.check(lib.rqf_fbt_layer0_fwd(
+                _lib.ptr(C1), _lib.ptr(tap0), _lib.ptr(tap1), _lib.ptr(wz), _lib.ptr(h),
+                _lib.ptr(act), _lib.ptr(carry), filters, batch, time, _lib.stream_of(h)),
+                "rqf_fbt_layer0_fwd")
+            ctx.save_for_backward(w, h, wz, carry, C1, tap0, tap1)
+            ctx.fused = True
+            return act
         z, _ = projection._proj_gemm(_pack_layer0(w), None, h, cols, filters, 0, h.device)
-        z = z.view(filters, batch, cols // batch)
+        z = z.view(filters, batch, time)
         act, carry, (C1, tap0, tap1, z) = fbt_recompute_forward_raw(C1, tap0, tap1, z)
         ctx.save_for_backward(w, h, z, carry, C1, tap0, tap1)
+        ctx.fused = False
         return act
 
     @staticmethod
@@ -329,8 +350,24 @@ class _Layer0RealScan(torch.autograd.Function):
         from prospective_rqf_amd import projection
 
         w, h, z, carry, C1, tap0, tap1 = ctx.saved_tensors
-        gc1, gt0, gt1, gz = fbt_recompute_backward_raw(C1, tap0, tap1, z, carry, grad_act)
         filters, cols = w.shape[0] // 2, h.shape[1]
+        if ctx.fused:  # z holds the drive weight wz; the scan forms the drive from h
+            g = _c64(grad_act)
+            batch = carry.shape[0] // filters
+            if g.shape != (filters, batch, cols // batch):
+                raise ValueError(f"grad_output must have shape {(filters, batch, cols // batch)}")
+            lib = _lib.load()
+            gz = torch.empty(filters, cols, dtype=torch.complex64, device=h.device)
+            gc1, gt0, gt1 = _bwd_grads(filters, h.device)
+            n = lib.rqf_fbt_workspace(filters, batch, cols // batch)
+            ws = _lib.workspace(n, h.device)
+            _lib.check(lib.rqf_fbt_layer0_bwd(
+                _lib.ptr(C1), _lib.ptr(tap0), _lib.ptr(tap1), _lib.ptr(z), _lib.ptr(h),
+                _lib.ptr(carry), _lib.ptr(g), _lib.ptr(gz), _lib.ptr(gc1), _lib.ptr(gt0),
+                _lib.ptr(gt1), filters, batch, cols // batch, _lib.ptr(ws), n,
+                _lib.stream_of(h)), "rqf_fbt_layer0_bwd")
+        else:
+            gc1, gt0, gt1, gz = fbt_recompute_backward_raw(C1, tap0, tap1, z, carry, grad_act)
         gz = gz.view(filters, cols)
         grad_w, grad_h = _layer0_grads(w, gz, h, ctx.needs_input_grad[0],
                                        ctx.needs_input_grad[1])

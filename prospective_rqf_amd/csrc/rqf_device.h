@@ -144,9 +144,11 @@ __device__ __forceinline__ float dpp0(float src) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(src), CTRL, 0xf, 0xf, true));
 }
 
-// GFX9 DPP controls.
+// GFX9 DPP controls.  wave_shl:1 / wave_shr:1 move a value one lane across
+// the whole 64-lane wavefront (GFX9 only).
 constexpr int kRowShl1 = 0x101, kRowShl2 = 0x102, kRowShl4 = 0x104, kRowShl8 = 0x108;
 constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
+constexpr int kWaveShl1 = 0x130, kWaveShr1 = 0x138;
 constexpr int kRowBcast15 = 0x142, kRowBcast31 = 0x143;
 
 __device__ __forceinline__ float bperm(float v, int src_lane) {
@@ -160,22 +162,20 @@ __device__ __forceinline__ c32 readlane(c32 v, int lane) {
 }
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
-// Value of `v` held by lane-1 (lane 0 receives `fill`).
+// Value of `v` held by lane-1 (lane 0 receives `fill`): one DPP wave shift
+// per float, the lane without a source keeping `fill`.  (`lane` is unused.)
+__device__ __forceinline__ float shift_up(float v, float fill, int) {
+  return dpp<kWaveShr1>(v, fill);
+}
 __device__ __forceinline__ c32 shift_up(c32 v, c32 fill, int lane) {
-  const int src = lane == 0 ? 0 : lane - 1;
-  c32 o = mk(bperm(v.r, src), bperm(v.i, src));
-  return lane == 0 ? fill : o;
+  return mk(shift_up(v.r, fill.r, lane), shift_up(v.i, fill.i, lane));
 }
 // Value of `v` held by lane+1 (lane 63 receives `fill`).
-__device__ __forceinline__ c32 shift_down(c32 v, c32 fill, int lane) {
-  const int src = lane == kWave - 1 ? lane : lane + 1;
-  c32 o = mk(bperm(v.r, src), bperm(v.i, src));
-  return lane == kWave - 1 ? fill : o;
+__device__ __forceinline__ float shift_down(float v, float fill, int) {
+  return dpp<kWaveShl1>(v, fill);
 }
-
-__device__ __forceinline__ float shift_down(float v, float fill, int lane) {
-  const float o = bperm(v, lane == kWave - 1 ? lane : lane + 1);
-  return lane == kWave - 1 ? fill : o;
+__device__ __forceinline__ c32 shift_down(c32 v, c32 fill, int lane) {
+  return mk(shift_down(v.r, fill.r, lane), shift_down(v.i, fill.i, lane));
 }
 
 // One Hillis-Steele step of the prefix scan of affine maps x -> P x + s.

@@ -36,6 +36,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <cstring>
 #include <initializer_list>
 #include <type_traits>
 
@@ -734,37 +735,52 @@ __device__ __forceinline__ void lds_warp(const BwdRow& r, int lane, float (&wt)[
   }
 }
 
+// Per-step values of one backward tile, kept from its replay phase for its
+// gradient phase.
+template <int K>
+struct BwdTile {
+  c32 A[K], phi[K];       // decay and ZOH phi of every step (A = 0 past the end)
+  c32 yprev[K], ecot[K];  // forward state before the step; cotangent on raw
+  // ivd = 1/|a|^2, aim = Im a, dsq = |a|^2 of the ZOH exponent a, reused by the VJP
+  float gam[K], thu[K], gate[K], wtk[K], ivd[K], aim[K], dsq[K];
+  c32 zp0;   // z of the step before the lane's first
+  float c0;  // lag-tap weight gate*ratio*gamma of the lane's first step
+};
+
+// Replay phase of a backward tile: the coefficients of every step, the
+// forward replay from the tile's entry state and the cotangent e on raw.
 // SHARED: tanh(warp logit) and exp(warp_scale * tanh) of the tile come from
 // the team's LDS stage (r.swt, r.sws) instead of per-lane loads and math.
 // zv: the tile's drive; zprev_tile: z[t0 - 1] (0 at t0 = 0).
 template <int K, bool VEC, bool TAIL, bool SHARED>
-__device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Chan& c, BwdRow& r,
-                                         int t0, int lane, const c32 (&zv)[K], c32 zprev_tile) {
+__device__ __forceinline__ void bwd_tile_replay(const rqf_selective_inputs& p, const Chan& c,
+                                                const BwdRow& r, int t0, int lane,
+                                                const c32 (&zv)[K], c32 zprev_tile,
+                                                BwdTile<K>& s) {
   const int T = r.T;
   const int tb = t0 + lane * K;
   float gv[K], wv[K], dv[K];
   if (r.gr) load_f<K, VEC, TAIL>(r.gr, tb, T, gv); else zero(gv);
   if (r.wr) load_f<K, VEC, TAIL>(r.wr, tb, T, wv); else zero(wv);
   if (!SHARED && r.dr) load_f<K, VEC, TAIL>(r.dr, tb, T, dv); else zero(dv);
-  const c32 zp0 = shift_up(zv[K - 1], zprev_tile, lane);
+  s.zp0 = shift_up(zv[K - 1], zprev_tile, lane);
 
   // Coefficients; kept per step: A, phi, gamma, gate and (unless SHARED)
   // theta_u and tanh(warp logit).
-  c32 A[K], phi[K], u[K];
-  // ivd = 1/|a|^2, aim = Im a, dsq = |a|^2 of the ZOH exponent a, reused by the VJP
-  float gam[K], thu[K], gate[K], wtk[K], ivd[K], aim[K], dsq[K];
+  c32 u[K];
   float swt[K], sws[K];
   if (SHARED) lds_warp<K>(r, lane, swt, sws);
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const Ctl q = SHARED ? controller_w(p, c, gv[k], swt[k], sws[k], wv[k])
                          : controller(p, c, gv[k], dv[k], wv[k]);
-    step_coef(p, c, q, zv[k], k ? zv[k - 1] : zp0, A[k], phi[k], u[k], ivd[k], aim[k], dsq[k]);
-    gam[k] = q.gamma;
-    gate[k] = q.gate;
+    step_coef(p, c, q, zv[k], k ? zv[k - 1] : s.zp0, s.A[k], s.phi[k], u[k], s.ivd[k],
+              s.aim[k], s.dsq[k]);
+    s.gam[k] = q.gamma;
+    s.gate[k] = q.gate;
     if (!SHARED) {
-      thu[k] = q.theta_u;
-      wtk[k] = q.wt;
+      s.thu[k] = q.theta_u;
+      s.wtk[k] = q.wt;
     }
     if (TAIL && tb + k >= T) u[k] = mk(0.0f, 0.0f);
     RQF_STEP_FENCE();
@@ -775,7 +791,6 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
 #endif
   // Forward states y[t-1] of every step, and the cotangent e[t] on raw: the
   // raw output plus the split-ReLU cotangent where raw > 0.
-  c32 yprev[K], ecot[K];
   c32 ey[K], ex[K];
   if (r.gyr) {
     load_c<K, VEC, TAIL>(r.gyr, tb, T, ey);
@@ -794,21 +809,22 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
     const c32 y0 = mk(r.ent[2 * (t0 / r.chunk)], r.ent[2 * (t0 / r.chunk) + 1]);
     c32 Am[K];
 #pragma unroll
-    for (int k = 0; k < K; ++k) Am[k] = (TAIL && tb + k >= T) ? mk(1.0f, 0.0f) : A[k];
-    c32 P = Am[0], s = u[0];
+    for (int k = 0; k < K; ++k) Am[k] = (TAIL && tb + k >= T) ? mk(1.0f, 0.0f) : s.A[k];
+    c32 P = Am[0], sy = u[0];
 #pragma unroll
     for (int k = 1; k < K; ++k) {
-      s = cmad(Am[k], s, u[k]);
+      sy = cmad(Am[k], sy, u[k]);
       P = cmul(Am[k], P);
     }
-    if (lane == 0) s = cmad(P, y0, s);
-    wave_scan_fwd(P, s);
-    c32 yk = shift_up(s, y0, lane);
+    if (lane == 0) sy = cmad(P, y0, sy);
+    wave_scan_fwd(P, sy);
+    c32 yk = shift_up(sy, y0, lane);
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-      yprev[k] = yk;
+      s.yprev[k] = yk;
       yk = cmad(Am[k], yk, u[k]);
-      ecot[k] = mk(ey[k].r + (yk.r > 0.0f ? ex[k].r : 0.0f), ey[k].i + (yk.i > 0.0f ? ex[k].i : 0.0f));
+      s.ecot[k] = mk(ey[k].r + (yk.r > 0.0f ? ex[k].r : 0.0f),
+                     ey[k].i + (yk.i > 0.0f ? ex[k].i : 0.0f));
     }
   }
   if (TAIL) {
@@ -816,38 +832,41 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
 #pragma unroll
     for (int k = 0; k < K; ++k)
       if (tb + k >= T) {
-        A[k] = mk(0.0f, 0.0f);
-        gate[k] = 0.0f;
+        s.A[k] = mk(0.0f, 0.0f);
+        s.gate[k] = 0.0f;
       }
   }
   // Lag-tap weight cn = gate*ratio*gamma (gated n = -cn*A) of the lane's first step.
-  const float c0 = p.prospective ? gate[0] * ratio_gamma(p, c, gam[0]) : 0.0f;
-  const c32 A_lane_next = shift_down(A[0], r.Afirst, lane);
-  const float cn_lane_next = shift_down(c0, r.cfirst, lane);
-  r.Afirst = readlane(A[0], 0);
-  r.cfirst = readlane(c0, 0);
+  s.c0 = p.prospective ? s.gate[0] * ratio_gamma(p, c, s.gam[0]) : 0.0f;
+}
 
-  RQF_PHASE_FENCE();
-  // Adjoint d[t] = e[t] + conj(A[t+1]) d[t+1]  (truncated: d = e).
-  c32 dnext;
-  if (r.truncated) {
-    dnext = shift_down(ecot[0], r.dcarry, lane);
-    r.dcarry = readlane(ecot[0], 0);
-  } else {
-    c32 Q = mk(1.0f, 0.0f), rr = mk(0.0f, 0.0f);
+// The lane's adjoint map d_first = rr + Q d_next over its K steps, where
+// d_next is the adjoint at the step after the lane's last and A_lane_next
+// the decay of that step: the suffix composition of d[t] = e[t] + conj(A[t+1]) d[t+1].
+template <int K>
+__device__ __forceinline__ void bwd_lane_adjoint(const BwdTile<K>& s, c32 A_lane_next, c32& Q,
+                                                 c32& rr) {
+  Q = mk(1.0f, 0.0f);
+  rr = mk(0.0f, 0.0f);
 #pragma unroll
-    for (int k = K - 1; k >= 0; --k) {
-      const c32 An = k + 1 < K ? A[k + 1] : A_lane_next;
-      rr = cjmad(An, rr, ecot[k]);
-      Q = cjmul(An, Q);
-    }
-    if (lane == kWave - 1) rr = cmad(Q, r.dcarry, rr);
-    wave_scan_rev(Q, rr, lane);
-    dnext = shift_down(rr, r.dcarry, lane);
-    r.dcarry = readlane(rr, 0);
+  for (int k = K - 1; k >= 0; --k) {
+    const c32 An = k + 1 < K ? s.A[k + 1] : A_lane_next;
+    rr = cjmad(An, rr, s.ecot[k]);
+    Q = cjmul(An, Q);
   }
+}
 
-  RQF_PHASE_FENCE();
+// Gradient phase of a backward tile, given the adjoint dnext at the step
+// after the lane's last (the cotangent there when truncated), the decay
+// A_lane_next and the lag-tap weight cn_lane_next of that step.
+template <int K, bool VEC, bool TAIL, bool SHARED>
+__device__ __forceinline__ void bwd_tile_grads(const rqf_selective_inputs& p, const Chan& c,
+                                               BwdRow& r, int t0, int lane, const c32 (&zv)[K],
+                                               const BwdTile<K>& s, c32 dnext, c32 A_lane_next,
+                                               float cn_lane_next) {
+  const int T = r.T;
+  const int tb = t0 + lane * K;
+  float swt[K], sws[K];
   if (SHARED) {
     // Re-read the staged warp values here rather than keep them live across
     // the scans (the compiler barrier stops it from reusing the first read).
@@ -859,36 +878,36 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
   float tile_bias = 0.0f, tile_theta = 0.0f;
 #pragma unroll
   for (int k = K - 1; k >= 0; --k) {
-    const c32 An = k + 1 < K ? A[k + 1] : A_lane_next;
+    const c32 An = k + 1 < K ? s.A[k + 1] : A_lane_next;
     float cn;
     if (k + 1 < K)
-      cn = p.prospective ? gate[k + 1] * ratio_gamma(p, c, gam[k + 1]) : 0.0f;
+      cn = p.prospective ? s.gate[k + 1] * ratio_gamma(p, c, s.gam[k + 1]) : 0.0f;
     else
       cn = cn_lane_next;
-    const c32 d = r.truncated ? ecot[k] : cjmad(An, dnext, ecot[k]);
-    const float gamma = gam[k], gt = gate[k];
+    const c32 d = r.truncated ? s.ecot[k] : cjmad(An, dnext, s.ecot[k]);
+    const float gamma = s.gam[k], gt = s.gate[k];
     const float rg = p.prospective ? ratio_gamma(p, c, gamma) : 0.0f;
     const float gh = gamma * c.eta;
     // Step map: y = A y_prev + gt*(gh*phi*z + rg*A*(z - zp)); the un-gated taps
     // are bp = gh*phi + rg*A on z and bn = -rg*A on zp.
     // x-path input gradient conj(gt*bp) d, and the W-path one adds the next
-    // step's lag tap conj(n[t+1]) d[t+1] with n[t+1] = -cn*A[t+1].
-    const c32 gphi = cscale(gt * gh, phi[k]);
-    const c32 gbp = p.prospective ? csmad(gt * rg, A[k], gphi) : gphi;
+    // step's lag tap conj(n[t+1]) d[t+1] with n[t+1] = -cn*s.A[t+1].
+    const c32 gphi = cscale(gt * gh, s.phi[k]);
+    const c32 gbp = p.prospective ? csmad(gt * rg, s.A[k], gphi) : gphi;
     const c32 cur = cjmul(gbp, d);
     gz[k] = cur;
     gzw[k] = p.prospective ? cjmad(cscale(-cn, An), dnext, cur) : cur;
     dnext = d;
     // cz = conj(z) d; for the prospective tap cw = conj(z - zp) d.
     const c32 cz = cjmul(zv[k], d);
-    const float pz = cdot(phi[k], cz);  // Re(conj(phi z) d)
+    const float pz = cdot(s.phi[k], cz);  // Re(conj(phi z) d)
     float dgate = gh * pz;              // dL/dgate = Re(conj(drive) d)
     float dgamma = gt * c.eta * pz;     // through gh = gamma*eta
-    c32 dA = cjmul(yprev[k], d);        // dL/dA = conj(y_prev + gt*rg*(z - zp)) d
+    c32 dA = cjmul(s.yprev[k], d);        // dL/dA = conj(y_prev + gt*rg*(z - zp)) d
     if (p.prospective) {
-      const c32 zp = k ? zv[k - 1] : zp0;
+      const c32 zp = k ? zv[k - 1] : s.zp0;
       const c32 cw = cjmul(csub(zv[k], zp), d);
-      const float aw = cdot(A[k], cw);  // Re(conj(A (z - zp)) d)
+      const float aw = cdot(s.A[k], cw);  // Re(conj(A (z - zp)) d)
       dgate = fmaf(rg, aw, dgate);
       if (!p.gamma_horizon) dgamma = fmaf(gt * c.horizon, aw, dgamma);  // through rg
       dA = csmad(gt * rg, cw, dA);
@@ -897,22 +916,22 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
     // selective_scan_kernel.py:119-148), here to degree 4 for |a| < 1/32
     // (truncation < 1e-10 relative) and (A - phi)/a above, where the
     // cancellation in A - phi costs at most ~1e-5 relative.
-    const float th_u = SHARED ? (p.has_warp ? c.theta * sws[k] : c.theta) : thu[k];
+    const float th_u = SHARED ? (p.has_warp ? c.theta * sws[k] : c.theta) : s.thu[k];
     const float theta = clamp_theta(p, c, th_u);
-    const c32 a = mk(-gh, aim[k]);
+    const c32 a = mk(-gh, s.aim[k]);
     c32 fp;
-    if (dsq[k] < 9.765625e-4f) {
+    if (s.dsq[k] < 9.765625e-4f) {
       c32 sr = cmadrr(a, 1.0f / 144.0f, 1.0f / 30.0f);
       sr = cmadr(a, sr, 1.0f / 8.0f);
       sr = cmadr(a, sr, 1.0f / 3.0f);
       fp = cmadr(a, sr, 0.5f);
     } else {
       // 1/|a|^2 as the ZOH formed it
-      fp = cscale(ivd[k], cmul(csub(A[k], phi[k]), conjg(a)));
+      fp = cscale(s.ivd[k], cmul(csub(s.A[k], s.phi[k]), conjg(a)));
     }
     // da = conj(A) dA + conj(phi') dphi with dphi = gt*gh*cz; then through
     // a = (-gamma*eta, (1 - gamma)*theta*eta).
-    const c32 da = cjmad(fp, cscale(gt * gh, cz), cjmul(A[k], dA));
+    const c32 da = cjmad(fp, cscale(gt * gh, cz), cjmul(s.A[k], dA));
     dgamma -= c.eta * fmaf(theta, da.i, da.r);
     float dth = c.eta * (1.0f - gamma) * da.i;
     // controller chain rules (selective_scan_kernel.py:441-460)
@@ -935,8 +954,8 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
     }
     if (p.has_warp) {
       // exp(scale*w) = d theta_u / d theta
-      const float ws = SHARED ? sws[k] : thu[k] * c.inv_theta;
-      const float wt = SHARED ? swt[k] : wtk[k];
+      const float ws = SHARED ? sws[k] : s.thu[k] * c.inv_theta;
+      const float wt = SHARED ? swt[k] : s.wtk[k];
       // torch.clamp passes the gradient at both exact edges
       if (p.bound_warp && !(th_u >= c.thlo && th_u <= c.thhi)) dth = 0.0f;
       gd[k] = dth * theta * p.warp_scale * (1.0f - wt * wt);
@@ -967,6 +986,39 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
       r.sdd[lane * (K / 4) + j] =
           make_float4(gd[4 * j], gd[4 * j + 1], gd[4 * j + 2], gd[4 * j + 3]);
   }
+}
+
+// One backward tile of a row walked by one wavefront: the tile's exit adjoint
+// state (r.dcarry) and the next tile's first decay and lag-tap weight
+// (r.Afirst, r.cfirst) come in through r and go out for the tile before it.
+template <int K, bool VEC, bool TAIL, bool SHARED>
+__device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Chan& c, BwdRow& r,
+                                         int t0, int lane, const c32 (&zv)[K], c32 zprev_tile) {
+  BwdTile<K> s;
+  bwd_tile_replay<K, VEC, TAIL, SHARED>(p, c, r, t0, lane, zv, zprev_tile, s);
+  const c32 A_lane_next = shift_down(s.A[0], r.Afirst, lane);
+  const float cn_lane_next = shift_down(s.c0, r.cfirst, lane);
+  r.Afirst = readlane(s.A[0], 0);
+  r.cfirst = readlane(s.c0, 0);
+
+  RQF_PHASE_FENCE();
+  // Adjoint d[t] = e[t] + conj(A[t+1]) d[t+1]  (truncated: d = e).
+  c32 dnext;
+  if (r.truncated) {
+    dnext = shift_down(s.ecot[0], r.dcarry, lane);
+    r.dcarry = readlane(s.ecot[0], 0);
+  } else {
+    c32 Q, rr;
+    bwd_lane_adjoint<K>(s, A_lane_next, Q, rr);
+    if (lane == kWave - 1) rr = cmad(Q, r.dcarry, rr);
+    wave_scan_rev(Q, rr, lane);
+    dnext = shift_down(rr, r.dcarry, lane);
+    r.dcarry = readlane(rr, 0);
+  }
+
+  RQF_PHASE_FENCE();
+  bwd_tile_grads<K, VEC, TAIL, SHARED>(p, c, r, t0, lane, zv, s, dnext, A_lane_next,
+                                       cn_lane_next);
 }
 
 template <int O, bool VEC>
@@ -1077,19 +1129,21 @@ struct Teams {
   const int* sn;      // (S,) teams in each split
   const int* gsplit;  // (G+1,) first split of each group
   const int* nsplits; // (1,) number of splits in use
+  const int* gteam;   // (G+1,) first team of each group
   int slots;          // S: upper bound on the number of teams (and splits)
 };
 
 // Group-sorted channel order and team table, built on the device from the
-// group indices (int64, as the reference's warp_groups buffer).  Groups,
+// group indices (int64, as the reference's warp_groups buffer); a team is up
+// to `tsize` consecutive channels of one group.  Groups,
 // per-group counts and offsets are staged in LDS (F <= kBuildLds and
 // G <= kBuildGroups, else a slower pass over global memory).
 constexpr int kBuildLds = 4096;
 constexpr int kBuildGroups = 1024;
 // The team table without LDS staging (F > kBuildLds or G > kBuildGroups).
-__device__ void team_build_global(const int64_t* __restrict__ groups, int F, int G, int* order,
-                                  int* first, int* count, int* group, int* gteam, int* nteams,
-                                  int* gcount, int* moff) {
+__device__ void team_build_global(const int64_t* __restrict__ groups, int F, int G, int tsize,
+                                  int* order, int* first, int* count, int* group, int* gteam,
+                                  int* nteams, int* gcount, int* moff) {
   const int tid = threadIdx.x, nt = blockDim.x;
   auto grp = [&](int f) { return groups ? clamp_group(groups[f], G) : 0; };
   for (int g = tid; g < G; g += nt) {
@@ -1104,7 +1158,7 @@ __device__ void team_build_global(const int64_t* __restrict__ groups, int F, int
       moff[g] = off;
       gteam[g] = toff;
       off += gcount[g];
-      toff += (gcount[g] + kTeam - 1) / kTeam;
+      toff += (gcount[g] + tsize - 1) / tsize;
     }
     gteam[G] = toff;
     *nteams = toff;
@@ -1117,18 +1171,18 @@ __device__ void team_build_global(const int64_t* __restrict__ groups, int F, int
     order[moff[g] + rank] = f;
   }
   for (int g = tid; g < G; g += nt) {
-    const int n = gcount[g], ntm = (n + kTeam - 1) / kTeam;
+    const int n = gcount[g], ntm = (n + tsize - 1) / tsize;
     for (int t = 0; t < ntm; ++t) {
       const int id = gteam[g] + t;
-      first[id] = moff[g] + t * kTeam;
-      count[id] = min(kTeam, n - t * kTeam);
+      first[id] = moff[g] + t * tsize;
+      count[id] = min(tsize, n - t * tsize);
       group[id] = g;
     }
   }
 }
 
 __global__ __launch_bounds__(256) void team_build_kernel(const int64_t* __restrict__ groups,
-                                                         int F, int G, int Q, int* order,
+                                                         int F, int G, int Q, int tsize, int* order,
                                                          int* first, int* count, int* group,
                                                          int* gteam, int* nteams, int* gcount,
                                                          int* moff, int* sfirst, int* sn,
@@ -1150,7 +1204,7 @@ __global__ __launch_bounds__(256) void team_build_kernel(const int64_t* __restri
     if (tid == 0) {
       int off = 0, toff = 0, soff = 0;
       for (int g = 0; g < G; ++g) {
-        const int ntm = (s_count[g] + kTeam - 1) / kTeam;
+        const int ntm = (s_count[g] + tsize - 1) / tsize;
         s_moff[g] = off;
         s_gteam[g] = toff;
         s_gsplit[g] = soff;
@@ -1182,13 +1236,13 @@ __global__ __launch_bounds__(256) void team_build_kernel(const int64_t* __restri
       gsplit[g] = s_gsplit[g];
     }
     for (int g = tid; g < G; g += nt) {
-      const int n = s_count[g], ntm = (n + kTeam - 1) / kTeam;
+      const int n = s_count[g], ntm = (n + tsize - 1) / tsize;
       gcount[g] = n;
       moff[g] = s_moff[g];
       for (int t = 0; t < ntm; ++t) {
         const int id = s_gteam[g] + t;
-        first[id] = s_moff[g] + t * kTeam;
-        count[id] = min(kTeam, n - t * kTeam);
+        first[id] = s_moff[g] + t * tsize;
+        count[id] = min(tsize, n - t * tsize);
         group[id] = g;
       }
       for (int j = 0; j * Q < ntm; ++j) {
@@ -1198,7 +1252,8 @@ __global__ __launch_bounds__(256) void team_build_kernel(const int64_t* __restri
     }
     return;
   }
-  team_build_global(groups, F, G, order, first, count, group, gteam, nteams, gcount, moff);
+  team_build_global(groups, F, G, tsize, order, first, count, group, gteam, nteams, gcount,
+                    moff);
   // Splits: runs of up to Q consecutive teams of one group.
   __syncthreads();
   if (tid == 0) {
@@ -1398,6 +1453,264 @@ __global__ __launch_bounds__(kTeam* kWave)
     if (lane == 0) {
       o.partial[row] = sb;
       o.partial[p.F * p.B + row] = st;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward, group form: one block per (warp group, batch element) runs every
+// team of the group, so the group's warp-logit gradient is complete inside
+// the block: no split partial rows and no closing pass over them.  The block
+// is TC x kGrpTW wavefronts, TC channel slots (one team) times kGrpTW
+// time slots, and walks the rows backwards in super-tiles of kGrpTW
+// consecutive tiles, time slot w taking tile w of each, so that concurrent
+// wavefronts stream adjacent stretches of every row.  A wavefront replays its
+// tile's forward from the stored entry state (entries are kept per tile),
+// scans the tile's adjoint from a zero state and publishes the tile's map
+//     D = R + Q conj(A') D'
+// with D the adjoint at the tile's first step and A', D' the decay and the
+// adjoint at the first step of the tile after it.  After one barrier every
+// wavefront composes the maps of the tiles after its own onto the channel's
+// carry, forms its gradients and stages its warp-logit gradient in LDS; after
+// a second barrier the block sums the team's channels into the segment's
+// group sum.  Warp values are staged per segment of kGrpSegSt super-tiles for
+// all teams, and each channel's carry and fp64 sums are parked in LDS between
+// segments, as in the split form above.
+// ---------------------------------------------------------------------------
+#ifndef RQF_GRP_TIME_SLOTS
+#define RQF_GRP_TIME_SLOTS 3
+#endif
+constexpr int kGrpTW = RQF_GRP_TIME_SLOTS;  // time slots: tiles per super-tile
+#ifndef RQF_GRP_SEG_SUPER_TILES
+#define RQF_GRP_SEG_SUPER_TILES 4
+#endif
+constexpr int kGrpSegSt = RQF_GRP_SEG_SUPER_TILES;  // super-tiles per staged segment
+constexpr int kGrpMaxChans = 256;  // channels of one group whose state LDS parks
+
+// TC: channel slots (the team size) of a block of TC * kGrpTW wavefronts.
+template <int O, bool VEC, int TC>
+__global__ __launch_bounds__(TC* kGrpTW* kWave)
+    __attribute__((amdgpu_waves_per_eu(RQF_BWD_WAVES_PER_EU))) void selective_bwd_grp_kernel(
+        const rqf_selective_inputs pin, const float* __restrict__ z,
+        const float* __restrict__ entries, int chunk, int nc, const float* __restrict__ gy,
+        const float* __restrict__ gx, int truncated, Teams tm, BwdOut o) {
+  const rqf_selective_inputs p = with_options<O>(pin);
+  constexpr int K = kBwdK, TILE = kWave * K, NT = TC * kGrpTW * kWave, ST = kGrpTW * TILE;
+  constexpr int SEG = kGrpSegSt * ST;
+  constexpr int kChans = kGrpMaxChans;
+  __shared__ float4 s_dd[kGrpTW][TC][TILE / 4];   // the super-tile's warp gradients
+  __shared__ float4 s_wt[SEG / 4], s_ws[SEG / 4];  // staged tanh(warp), exp(scale*tanh)
+  __shared__ float s_seg[SEG];                     // the segment's group gradient so far
+  __shared__ float4 s_map[kGrpTW][TC][2];          // (R, Q), (A at the first step, cn, -)
+  __shared__ float4 s_park[kChans];                // (D, A) carry of each channel
+  __shared__ float s_pcf[kChans];                  // lag-tap weight of the carry
+  __shared__ double s_sum[kChans][kGrpTW][2];      // dbias, dtheta sums per time slot
+  const int lane = lane_id();
+  const int w = wave_id();
+  const int cs = w % TC, tw = w / TC;
+  const int64_t L = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t g = L / p.B, b = L - g * p.B;
+  if (g >= p.G) return;  // block-uniform
+  const int team0 = tm.gteam[g], nteam = tm.gteam[g + 1] - team0;
+  const int T = (int)p.T;
+  float* ddrow = o.dd + (g * p.B + b) * T;
+  if (nteam == 0) {
+    // a group without channels has a zero warp-logit gradient
+    for (int t = (int)threadIdx.x; t < T; t += NT) ddrow[t] = 0.0f;
+    return;
+  }
+  const float* dwr = p.warp_logits + (g * p.B + b) * T;
+  const int ntiles = (T + TILE - 1) / TILE;
+  const int full = VEC ? T / TILE : 0;
+  const int nst = (ntiles + kGrpTW - 1) / kGrpTW;
+  const int nseg = (nst + kGrpSegSt - 1) / kGrpSegSt;
+  float* swt = reinterpret_cast<float*>(&s_wt[0]);
+  float* sws = reinterpret_cast<float*>(&s_ws[0]);
+  const float* sdd = reinterpret_cast<const float*>(&s_dd[0][0][0]);
+
+  BwdRow r;
+  r.T = T;
+  r.chunk = chunk;
+  r.truncated = truncated;
+  r.dr = nullptr;
+  r.ddr = nullptr;
+  r.sdd = &s_dd[tw][cs][0];
+  r.swt = swt;
+  r.sws = sws;
+  r.dcarry = mk(0.0f, 0.0f);
+  r.Afirst = mk(0.0f, 0.0f);
+  r.cfirst = 0.0f;
+  Chan c;
+  // The channel's carry: adjoint, decay and lag-tap weight at the first step
+  // after the super-tile being walked.
+  c32 Dc = mk(0.0f, 0.0f), Ac = mk(0.0f, 0.0f);
+  float cc = 0.0f;
+  for (int sg = nseg - 1; sg >= 0; --sg) {
+    const int st_lo = sg * kGrpSegSt, st_hi = min(nst, st_lo + kGrpSegSt);
+    const int s0 = st_lo * ST;
+    {
+      // Stage the segment's warp values for all teams.  The previous
+      // segment's last barrier ordered its reads before these writes.
+      const int n = (st_hi - st_lo) * ST;
+      for (int i = (int)threadIdx.x; i < n; i += NT) {
+        const int t = s0 + i;
+        const float wt = warp_tanh(p, t < T ? dwr[t] : 0.0f);
+        swt[i] = wt;
+        sws[i] = warp_factor(p, wt);
+      }
+      __syncthreads();
+    }
+    for (int qi = 0; qi < nteam; ++qi) {
+      const int ch = qi * TC + cs;
+      const int team = team0 + qi;
+      const int members = tm.count[team];
+      const bool active = cs < members;
+      const int64_t f = tm.order[tm.first[team] + (active ? cs : 0)];
+      const int64_t row = f * p.B + b;
+      c = load_chan(p, f);
+      const int64_t base = row * T;
+      r.zr = z + 2 * base;
+      r.gr = p.has_gamma ? p.gamma_logits + base : nullptr;
+      r.wr = p.has_write ? p.write_logits + base : nullptr;
+      r.gyr = gy ? gy + 2 * base : nullptr;
+      r.gxr = gx ? gx + 2 * base : nullptr;
+      r.ent = entries + 2 * row * nc;
+      r.dzr = o.dz + 2 * base;
+      r.dzwr = o.dzw + 2 * base;
+      r.dgr = o.dg ? o.dg + base : nullptr;
+      r.dwr = o.dw ? o.dw + base : nullptr;
+      r.sum_bias = 0.0;
+      r.sum_theta = 0.0;
+      if (sg == nseg - 1) {
+        Dc = mk(0.0f, 0.0f);
+        Ac = mk(0.0f, 0.0f);
+        cc = 0.0f;
+      } else {
+        const float4 v = s_park[ch];
+        Dc = mk(v.x, v.y);
+        Ac = mk(v.z, v.w);
+        cc = s_pcf[ch];
+      }
+      for (int st = st_hi - 1; st >= st_lo; --st) {
+        const int tile = st * kGrpTW + tw;
+        const int t0 = tile * TILE;
+        const bool valid = active && tile < ntiles;
+        r.swt = swt + (t0 - s0);
+        r.sws = sws + (t0 - s0);
+        BwdTile<K> s;
+        c32 zv[K];
+        c32 Q = mk(1.0f, 0.0f), rr = mk(0.0f, 0.0f);
+        if (valid) {
+          const c32 zprev_tile =
+              t0 > 0 ? mk(r.zr[2 * (t0 - 1)], r.zr[2 * (t0 - 1) + 1]) : mk(0.0f, 0.0f);
+          if (tile >= full) {
+            load_c<K, VEC, true>(r.zr, t0 + lane * K, T, zv);
+            bwd_tile_replay<K, VEC, true, true>(p, c, r, t0, lane, zv, zprev_tile, s);
+          } else {
+            load_c<K, VEC, false>(r.zr, t0 + lane * K, T, zv);
+            bwd_tile_replay<K, VEC, false, true>(p, c, r, t0, lane, zv, zprev_tile, s);
+          }
+          if (!truncated) {
+            // Lane 63's step after its last is the next tile's first: its
+            // decay stays out of the tile's own map (1 here) and comes in with D'.
+            bwd_lane_adjoint<K>(s, shift_down(s.A[0], mk(1.0f, 0.0f), lane), Q, rr);
+            wave_scan_rev(Q, rr, lane);
+          }
+          if (lane == 0) {
+            s_map[tw][cs][0] = truncated ? make_float4(s.ecot[0].r, s.ecot[0].i, 0.0f, 0.0f)
+                                         : make_float4(rr.r, rr.i, Q.r, Q.i);
+            s_map[tw][cs][1] = make_float4(s.A[0].r, s.A[0].i, s.c0, 0.0f);
+          }
+        } else if (active && lane == 0) {
+          // a tile past the row's end: zero adjoint, decay and lag tap
+          s_map[tw][cs][0] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          s_map[tw][cs][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        __syncthreads();
+        // Compose the maps of the super-tile's tiles, latest first, onto the
+        // carry: (Dn, An, cn) at the first step after tile tw, and the carry
+        // for the super-tile before this one.
+        c32 Dn = Dc, An = Ac, D1 = Dc, A1 = Ac;
+        float cn = cc, c1 = cc;
+#pragma unroll
+        for (int j = kGrpTW - 1; j >= 0; --j) {
+          if (j == tw) {
+            D1 = Dn;
+            A1 = An;
+            c1 = cn;
+          }
+          const float4 m0 = s_map[j][cs][0], m1 = s_map[j][cs][1];
+          Dn = truncated ? mk(m0.x, m0.y) : cmad(mk(m0.z, m0.w), cjmul(An, Dn), mk(m0.x, m0.y));
+          An = mk(m1.x, m1.y);
+          cn = m1.z;
+        }
+        Dc = Dn;
+        Ac = An;
+        cc = cn;
+        if (valid) {
+          const c32 A_lane_next = shift_down(s.A[0], A1, lane);
+          const float cn_lane_next = shift_down(s.c0, c1, lane);
+          c32 dnext;
+          if (truncated) {
+            dnext = shift_down(s.ecot[0], D1, lane);
+          } else {
+            // the lane's adjoint at its first step, then the next lane's
+            const c32 dfirst = cmad(Q, cjmul(A1, D1), rr);
+            dnext = shift_down(dfirst, D1, lane);
+          }
+          if (tile >= full)
+            bwd_tile_grads<K, VEC, true, true>(p, c, r, t0, lane, zv, s, dnext, A_lane_next,
+                                               cn_lane_next);
+          else
+            bwd_tile_grads<K, VEC, false, true>(p, c, r, t0, lane, zv, s, dnext, A_lane_next,
+                                                cn_lane_next);
+        }
+        __syncthreads();
+        // Step i of the super-tile: the team's sum (fixed channel order) joins
+        // the segment's group sum (fixed team order); each thread owns the same
+        // steps for every team, so s_seg needs no barrier of its own.
+        for (int i = (int)threadIdx.x; i < ST; i += NT) {
+          const int slot = i / TILE, k = i - slot * TILE;
+          float acc = 0.0f;
+          for (int m = 0; m < members; ++m) acc += sdd[(slot * TC + m) * TILE + k];
+          const int t = st * ST + i, j = t - s0;
+          if (qi > 0) acc = s_seg[j] + acc;
+          if (qi + 1 < nteam)
+            s_seg[j] = acc;
+          else if (t < T)
+            ddrow[t] = acc;
+        }
+      }
+      if (active) {
+        // Park the channel's carry (every time slot holds the same one) and
+        // add this wavefront's sums to its slot.
+        if (sg > 0 && tw == 0 && lane == 0) {
+          s_park[ch] = make_float4(Dc.r, Dc.i, Ac.r, Ac.i);
+          s_pcf[ch] = cc;
+        }
+        const double sb = wave_sum(r.sum_bias);
+        const double sth = wave_sum(r.sum_theta);
+        if (lane == 0) {
+          s_sum[ch][tw][0] = (sg == nseg - 1 ? 0.0 : s_sum[ch][tw][0]) + sb;
+          s_sum[ch][tw][1] = (sg == nseg - 1 ? 0.0 : s_sum[ch][tw][1]) + sth;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // Per-row fp64 partials of dbias and dtheta: the time slots in fixed order.
+  for (int i = (int)threadIdx.x; i < nteam * TC; i += NT) {
+    const int team = team0 + i / TC, m = i % TC;
+    if (m < tm.count[team]) {
+      const int64_t row = (int64_t)tm.order[tm.first[team] + m] * p.B + b;
+      double sb = 0.0, sth = 0.0;
+#pragma unroll
+      for (int j = 0; j < kGrpTW; ++j) {
+        sb += s_sum[i][j][0];
+        sth += s_sum[i][j][1];
+      }
+      o.partial[row] = sb;
+      o.partial[p.F * p.B + row] = sth;
     }
   }
 }
@@ -1693,16 +2006,42 @@ int split_teams(const rqf_selective_inputs* in) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(kMaxSplitTeams, q));
 }
 
+// The group form of the backward needs the warp head and no group with more
+// channels than its LDS parks (F <= kGrpMaxChans).  It runs only when the
+// environment variable RQF_BWD_FORM=group asks for it: measured at configs 3
+// and 4 it is slower than the split form (2.84 against 2.78 ms and 0.79 / 0.77
+// against 0.75 / 0.65 ms with 4 channel slots).  One block per CU moves its
+// 12 wavefronts in lockstep between the barriers, so their memory waits no
+// longer overlap other blocks' arithmetic; with 2 channel slots the 6-wavefront
+// blocks sit unevenly on the SIMDs and a second block does not fit at
+// 3 waves per SIMD (4.03 ms).
+bool use_group_form(const rqf_selective_inputs* in) {
+  if (!RQF_BWD_TEAMS || !in->has_warp || in->F > kGrpMaxChans) return false;
+  if (std::getenv("RQF_BWD_SPLIT_TEAMS")) return false;
+  const char* e = std::getenv("RQF_BWD_FORM");
+  return e && !std::strcmp(e, "group");
+}
+
+// Channel slots of a group-form block: 4 (12 wavefronts), or 2 (6 wavefronts)
+// with RQF_GRP_CHANNEL_SLOTS=2.
+int group_channel_slots(const rqf_selective_inputs*) {
+  const char* e = std::getenv("RQF_GRP_CHANNEL_SLOTS");
+  return e && !std::strcmp(e, "2") ? 2 : 4;
+}
+
 struct SelWs {
   size_t partial, tile_entries, teams, dd, total;
-  int slots, split_slots, Q, G;
+  int slots, split_slots, Q, G, tsize;
+  bool group_form;
 };
 SelWs sel_ws_layout(const rqf_selective_inputs* in, int64_t chunk) {
   SelWs w;
   const int64_t R = in->F * in->B;
   w.G = in->has_warp ? (int)in->G : 1;
-  const int teams = (int)((in->F + kTeam - 1) / kTeam);
-  w.slots = w.G + teams;  // teams of all groups <= ceil(F/kTeam) + G
+  w.group_form = use_group_form(in);
+  w.tsize = w.group_form ? group_channel_slots(in) : kTeam;
+  const int teams = (int)((in->F + w.tsize - 1) / w.tsize);
+  w.slots = w.G + teams;  // teams of all groups <= ceil(F/tsize) + G
   w.Q = split_teams(in);
   w.split_slots = std::min(w.slots, (teams + w.G) / w.Q + w.G);
   w.partial = 0;
@@ -1714,7 +2053,8 @@ SelWs sel_ws_layout(const rqf_selective_inputs* in, int64_t chunk) {
   off += round256(sizeof(int) * (size_t)(in->F + 5 * w.slots + 4 * w.G + 4));
   w.dd = off;
 #if RQF_BWD_TEAMS
-  if (in->has_warp) off += round256(sizeof(float) * (size_t)w.split_slots * in->B * in->T);
+  if (in->has_warp && !w.group_form)
+    off += round256(sizeof(float) * (size_t)w.split_slots * in->B * in->T);
 #else
   if (in->has_warp) off += round256(sizeof(float) * (size_t)R * (size_t)in->T);
 #endif
@@ -1790,7 +2130,7 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
     int* nsplits = gsplit + (w.G + 1);
     hipLaunchKernelGGL(team_build_kernel, dim3(1), dim3(256), 0, s,
                        in->has_warp ? in->groups : (const int64_t*)nullptr, (int)in->F, w.G, w.Q,
-                       order, first, count, group, gteam, nteams, gcount, moff, sfirst, sn,
+                       w.tsize, order, first, count, group, gteam, nteams, gcount, moff, sfirst, sn,
                        gsplit, nsplits);
     Teams tm;
     tm.order = order;
@@ -1802,9 +2142,32 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
     tm.sn = sn;
     tm.gsplit = gsplit;
     tm.nsplits = nsplits;
+    tm.gteam = gteam;
     tm.slots = w.split_slots;
-    o.dd_part = in->has_warp ? (float*)(ws + w.dd) : nullptr;
     o.dd = in->has_warp ? dd : nullptr;
+    if (w.group_form) {
+      const dim3 grid((unsigned)(in->G * in->B)), block(w.tsize * kGrpTW * kWave);
+      with_option_set(options_of(in), [&](auto oc) {
+        constexpr int O = decltype(oc)::value;
+        if constexpr (O != kOptRuntime && !(O & kOptWarp)) {
+          return;  // not reached: the group form needs the warp head
+        } else {
+          auto launch = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, grid, block, 0, s, *in, z, ent, ent_chunk, nc, gy, gx,
+                               (int)truncated, tm, o);
+          };
+          if (w.tsize == 2)
+            vec ? launch(selective_bwd_grp_kernel<O, true, 2>)
+                : launch(selective_bwd_grp_kernel<O, false, 2>);
+          else
+            vec ? launch(selective_bwd_grp_kernel<O, true, 4>)
+                : launch(selective_bwd_grp_kernel<O, false, 4>);
+        }
+      });
+      launch_finish(nullptr, nullptr, nullptr, 0, 0, partial, dbias, dtheta, in->F, in->B, s);
+      return launch_status();
+    }
+    o.dd_part = in->has_warp ? (float*)(ws + w.dd) : nullptr;
     const int64_t bc = (in->B + kXcds - 1) / kXcds;
     const dim3 grid((unsigned)(kXcds * w.split_slots * bc)), block(kTeam * kWave);
     with_option_set(options_of(in), [&](auto oc) {

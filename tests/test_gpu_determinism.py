@@ -51,13 +51,19 @@ def _same(a, b, what):
             assert torch.equal(x, y), (what, i)
 
 
+@pytest.mark.parametrize("form", ["group", "split"])
 @pytest.mark.parametrize("truncated", [False, True])
-def test_selective_repeat_bitwise(monkeypatch, truncated):
-    """16 channels per warp group = 4 teams; two teams per split = two split
-    rows per group summed by the split reduction."""
+def test_selective_repeat_bitwise(monkeypatch, truncated, form):
+    """16 channels per warp group = 4 teams: all four in one block (group
+    form), or two teams per split = two split rows per group summed by the
+    split reduction."""
     F, B, T, G, chunk = 64, 8, 4096, 4, 256
-    print(f"case: selective repeat F={F} B={B} T={T} G={G} truncated={truncated}", flush=True)
-    monkeypatch.setenv("RQF_BWD_SPLIT_TEAMS", "2")
+    print(f"case: selective repeat F={F} B={B} T={T} G={G} truncated={truncated} "
+          f"form={form}", flush=True)
+    if form == "group":
+        monkeypatch.setenv("RQF_BWD_FORM", "group")
+    else:
+        monkeypatch.setenv("RQF_BWD_SPLIT_TEAMS", "2")
     g = torch.Generator(device="cuda").manual_seed(5)
     inp = workloads.selective_inputs(F, B, T, G=G, device="cuda", seed=3)
     z, gy, gx = _cn(g, F, B, T), _cn(g, F, B, T), _cn(g, F, B, T)

@@ -258,6 +258,61 @@ def test_split_teams_carry_state_across_segments(monkeypatch, F, B, T, warp, G, 
     run_case(F, B, T, case, chunk=256, G=G, truncated=truncated, seed=F + T)
 
 
+def _empty_groups(inp, z):
+    """Channels only in groups 0, 2 and 4 of 5: groups 1 and 3 have none."""
+    inp.groups[:] = 2 * (np.arange(inp.groups.shape[0]) % 3)
+
+
+@pytest.mark.parametrize("F,B,T,warp,G,chunk,truncated,edit", [
+    # one partial super-tile (3 time slots, 1-2 of them past the row's end)
+    (5, 2, 1, "grouped", 3, 32, False, None),
+    (5, 2, 33, "grouped", 3, 32, True, None),
+    (5, 2, 256, "grouped", 3, 256, False, None),
+    (5, 2, 257, "grouped", 3, 256, True, None),
+    # super-tile and segment edges (a super-tile is 768 steps, a segment 3072);
+    # odd T runs the unvectorised loads
+    (6, 2, 767, "grouped", 2, 256, False, None),
+    (6, 2, 768, "grouped", 2, 256, True, None),
+    (6, 2, 1000, "global", 1, 256, False, None),
+    (6, 2, 3072, "grouped", 2, 256, False, None),
+    (6, 2, 3073, "grouped", 2, 256, True, None),
+    (6, 2, 6999, "grouped", 2, 256, False, None),
+    # entry states every 4 steps, and per-tile entries rebuilt from 1024-step chunks
+    (6, 2, 2000, "grouped", 2, 4, False, None),
+    (6, 2, 3000, "grouped", 2, 1024, True, None),
+    # 10 channels per group (teams of 4, 4 and 2) over two segments; global warp
+    # with 5 teams; two groups without channels
+    (20, 2, 4500, "grouped", 2, 256, False, None),
+    (20, 3, 4500, "global", 1, 256, True, None),
+    (9, 2, 2300, "grouped", 5, 256, False, _empty_groups),
+])
+@pytest.mark.parametrize("slots", ["2", "4"])
+def test_group_form(monkeypatch, F, B, T, warp, G, chunk, truncated, edit, slots):
+    """The group form of the backward (one block per warp group and batch
+    element; adjoint maps composed across the time slots of a super-tile), in
+    blocks of 2 and 4 channel slots, forced at shapes whose grid would pick
+    the split form."""
+    print(f"case: group form F={F} B={B} T={T} warp={warp} G={G} chunk={chunk} "
+          f"truncated={truncated} edit={edit is not None} slots={slots}", flush=True)
+    monkeypatch.setenv("RQF_BWD_FORM", "group")
+    monkeypatch.setenv("RQF_GRP_CHANNEL_SLOTS", slots)
+    run_case(F, B, T, dict(CASE_ALL, warp=warp), chunk=chunk, G=G, truncated=truncated,
+             edit=edit, seed=F + T + chunk)
+
+
+@pytest.mark.parametrize("truncated", [False, True])
+@pytest.mark.parametrize("prospective", [False, True])
+@pytest.mark.parametrize("case", [c for c in CASES if c["warp"] != "none"], ids=case_id)
+def test_group_form_controller_cases(monkeypatch, case, prospective, truncated):
+    """Every controller case with a warp head, through the group form."""
+    print(f"case: group form {case_id(case)} prospective={prospective} "
+          f"truncated={truncated}", flush=True)
+    monkeypatch.setenv("RQF_BWD_FORM", "group")
+    run_case(5, 2, 1100, case, prospective=prospective, truncated=truncated,
+             gamma_horizon=prospective and case["gamma"] and not case["log_shift"],
+             chunk=256, seed=len(case_id(case)) + 7)
+
+
 def test_long_rows_subset_of_north_star_shape():
     """T = 16000 rows with the config-3 option set (grouped warp, sigmoid write)."""
     print("case: long rows T=16000", flush=True)

@@ -713,8 +713,8 @@ struct BwdRow {
   float* dwr;
   float* ddr;     // per-channel warp-logit gradient (global), or
   float4* sdd;    // this wavefront's slot of the team's LDS warp-gradient tile
-  const float* swt;  // team LDS stage of the tile: tanh(warp logit) per step
-  const float* sws;  // and exp(warp_scale * tanh)
+  const float* swg;  // team LDS stage of the tile: warp_scale*(1 - tanh(warp logit)^2)
+  const float* sws;  // and exp(warp_scale * tanh(warp logit)) per step
   int T, chunk, truncated;
   c32 dcarry;  // adjoint (truncated: cotangent) at the next tile's first step
   c32 Afirst;  // A at the next tile's first step (0 past the end)
@@ -722,25 +722,42 @@ struct BwdRow {
   double sum_bias, sum_theta;
 };
 
-// Warp values of the lane's K steps from the team's LDS stage (SHARED).
+// Staged warp values of the lane's K steps (SHARED): the frequency factor
+// exp(warp_scale * tanh) and the tanh derivative factor warp_scale*(1 - tanh^2).
 template <int K>
-__device__ __forceinline__ void lds_warp(const BwdRow& r, int lane, float (&wt)[K], float (&ws)[K]) {
+__device__ __forceinline__ void lds_warp_factor(const BwdRow& r, int lane, float (&ws)[K]) {
   static_assert(K % 4 == 0, "whole float4s of staged warp values per lane");
 #pragma unroll
   for (int j = 0; j < K / 4; ++j) {
-    const float4 a = reinterpret_cast<const float4*>(r.swt)[lane * (K / 4) + j];
     const float4 b = reinterpret_cast<const float4*>(r.sws)[lane * (K / 4) + j];
-    wt[4 * j] = a.x, wt[4 * j + 1] = a.y, wt[4 * j + 2] = a.z, wt[4 * j + 3] = a.w;
     ws[4 * j] = b.x, ws[4 * j + 1] = b.y, ws[4 * j + 2] = b.z, ws[4 * j + 3] = b.w;
   }
+}
+template <int K>
+__device__ __forceinline__ void lds_warp(const BwdRow& r, int lane, float (&wg)[K], float (&ws)[K]) {
+  lds_warp_factor<K>(r, lane, ws);
+#pragma unroll
+  for (int j = 0; j < K / 4; ++j) {
+    const float4 a = reinterpret_cast<const float4*>(r.swg)[lane * (K / 4) + j];
+    wg[4 * j] = a.x, wg[4 * j + 1] = a.y, wg[4 * j + 2] = a.z, wg[4 * j + 3] = a.w;
+  }
+}
+// The staged values of one step: exp(warp_scale * wt), warp_scale*(1 - wt^2).
+__device__ __forceinline__ void warp_stage(const rqf_selective_inputs& p, float dv, float& ws,
+                                           float& wg) {
+  const float wt = warp_tanh(p, dv);
+  ws = warp_factor(p, wt);
+  wg = p.warp_scale * fmaf(-wt, wt, 1.0f);
 }
 
 // Per-step values of one backward tile, kept from its replay phase for its
 // gradient phase.
 template <int K>
 struct BwdTile {
-  c32 A[K], phi[K];       // decay and ZOH phi of every step (A = 0 past the end)
+  static_assert(K >= 2, "a lane holds its first step and the product M of the rest");
+  c32 A[K], phi[K];  // decay and ZOH phi of every step (A = 0 past the end)
   c32 yprev[K], ecot[K];  // forward state before the step; cotangent on raw
+  c32 M;  // product of A over the lane's steps after its first (full tiles)
   // ivd = 1/|a|^2, aim = Im a, dsq = |a|^2 of the ZOH exponent a, reused by the VJP
   float gam[K], thu[K], gate[K], wtk[K], ivd[K], aim[K], dsq[K];
   c32 zp0;   // z of the step before the lane's first
@@ -749,8 +766,8 @@ struct BwdTile {
 
 // Replay phase of a backward tile: the coefficients of every step, the
 // forward replay from the tile's entry state and the cotangent e on raw.
-// SHARED: tanh(warp logit) and exp(warp_scale * tanh) of the tile come from
-// the team's LDS stage (r.swt, r.sws) instead of per-lane loads and math.
+// SHARED: the warp values of the tile come from the team's LDS stage (r.swg,
+// r.sws) instead of per-lane loads and math.
 // zv: the tile's drive; zprev_tile: z[t0 - 1] (0 at t0 = 0).
 template <int K, bool VEC, bool TAIL, bool SHARED>
 __device__ __forceinline__ void bwd_tile_replay(const rqf_selective_inputs& p, const Chan& c,
@@ -768,11 +785,12 @@ __device__ __forceinline__ void bwd_tile_replay(const rqf_selective_inputs& p, c
   // Coefficients; kept per step: A, phi, gamma, gate and (unless SHARED)
   // theta_u and tanh(warp logit).
   c32 u[K];
-  float swt[K], sws[K];
-  if (SHARED) lds_warp<K>(r, lane, swt, sws);
+  float sws[K];
+  if (SHARED) lds_warp_factor<K>(r, lane, sws);
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    const Ctl q = SHARED ? controller_w(p, c, gv[k], swt[k], sws[k], wv[k])
+    // (only the non-SHARED form keeps the Ctl's tanh)
+    const Ctl q = SHARED ? controller_w(p, c, gv[k], 0.0f, sws[k], wv[k])
                          : controller(p, c, gv[k], dv[k], wv[k]);
     step_coef(p, c, q, zv[k], k ? zv[k - 1] : s.zp0, s.A[k], s.phi[k], u[k], s.ivd[k],
               s.aim[k], s.dsq[k]);
@@ -805,17 +823,21 @@ __device__ __forceinline__ void bwd_tile_replay(const rqf_selective_inputs& p, c
     for (int k = 0; k < K; ++k) ex[k] = mk(0.0f, 0.0f);
   }
   {
-    // Replay the forward from the tile's entry state.
+    // Replay the forward from the tile's entry state.  The lane's map is
+    // P = A[0] * M with M the product over its later steps, which the adjoint's
+    // map reuses.
     const c32 y0 = mk(r.ent[2 * (t0 / r.chunk)], r.ent[2 * (t0 / r.chunk) + 1]);
     c32 Am[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) Am[k] = (TAIL && tb + k >= T) ? mk(1.0f, 0.0f) : s.A[k];
-    c32 P = Am[0], sy = u[0];
+    c32 sy = u[0];
+    s.M = Am[1];
 #pragma unroll
     for (int k = 1; k < K; ++k) {
       sy = cmad(Am[k], sy, u[k]);
-      P = cmul(Am[k], P);
+      if (k > 1) s.M = cmul(Am[k], s.M);
     }
+    c32 P = cmul(s.M, Am[0]);
     if (lane == 0) sy = cmad(P, y0, sy);
     wave_scan_fwd(P, sy);
     c32 yk = shift_up(sy, y0, lane);
@@ -843,7 +865,9 @@ __device__ __forceinline__ void bwd_tile_replay(const rqf_selective_inputs& p, c
 // The lane's adjoint map d_first = rr + Q d_next over its K steps, where
 // d_next is the adjoint at the step after the lane's last and A_lane_next
 // the decay of that step: the suffix composition of d[t] = e[t] + conj(A[t+1]) d[t+1].
-template <int K>
+// On full tiles Q = conj(M A_lane_next) from the replay's product M; on the
+// last (TAIL) tile the replay's A past the row's end differs (1, not 0).
+template <int K, bool TAIL>
 __device__ __forceinline__ void bwd_lane_adjoint(const BwdTile<K>& s, c32 A_lane_next, c32& Q,
                                                  c32& rr) {
   Q = mk(1.0f, 0.0f);
@@ -852,8 +876,9 @@ __device__ __forceinline__ void bwd_lane_adjoint(const BwdTile<K>& s, c32 A_lane
   for (int k = K - 1; k >= 0; --k) {
     const c32 An = k + 1 < K ? s.A[k + 1] : A_lane_next;
     rr = cjmad(An, rr, s.ecot[k]);
-    Q = cjmul(An, Q);
+    if (TAIL) Q = cjmul(An, Q);
   }
+  if (!TAIL) Q = conjg(cmul(s.M, A_lane_next));
 }
 
 // Gradient phase of a backward tile, given the adjoint dnext at the step
@@ -866,12 +891,12 @@ __device__ __forceinline__ void bwd_tile_grads(const rqf_selective_inputs& p, co
                                                float cn_lane_next) {
   const int T = r.T;
   const int tb = t0 + lane * K;
-  float swt[K], sws[K];
+  float swg[K], sws[K];
   if (SHARED) {
     // Re-read the staged warp values here rather than keep them live across
     // the scans (the compiler barrier stops it from reusing the first read).
     __asm__ volatile("" ::: "memory");
-    lds_warp<K>(r, lane, swt, sws);
+    lds_warp<K>(r, lane, swg, sws);
   }
   c32 gz[K], gzw[K];
   float gg[K], gw[K], gd[K];
@@ -903,7 +928,7 @@ __device__ __forceinline__ void bwd_tile_grads(const rqf_selective_inputs& p, co
     const float pz = cdot(s.phi[k], cz);  // Re(conj(phi z) d)
     float dgate = gh * pz;              // dL/dgate = Re(conj(drive) d)
     float dgamma = gt * c.eta * pz;     // through gh = gamma*eta
-    c32 dA = cjmul(s.yprev[k], d);        // dL/dA = conj(y_prev + gt*rg*(z - zp)) d
+    c32 dA = cjmul(s.yprev[k], d);      // dL/dA = conj(y_prev + gt*rg*(z - zp)) d
     if (p.prospective) {
       const c32 zp = k ? zv[k - 1] : s.zp0;
       const c32 cw = cjmul(csub(zv[k], zp), d);
@@ -930,7 +955,9 @@ __device__ __forceinline__ void bwd_tile_grads(const rqf_selective_inputs& p, co
       fp = cscale(s.ivd[k], cmul(csub(s.A[k], s.phi[k]), conjg(a)));
     }
     // da = conj(A) dA + conj(phi') dphi with dphi = gt*gh*cz; then through
-    // a = (-gamma*eta, (1 - gamma)*theta*eta).
+    // a = (-gamma*eta, (1 - gamma)*theta*eta).  (Folding the two terms through
+    // the step map into conj(y + gt*gh*(phi' - phi)*z) d saves four operations
+    // but cancels when A -> 0: y and gt*gh*phi*z are then nearly equal.)
     const c32 da = cjmad(fp, cscale(gt * gh, cz), cjmul(s.A[k], dA));
     dgamma -= c.eta * fmaf(theta, da.i, da.r);
     float dth = c.eta * (1.0f - gamma) * da.i;
@@ -955,10 +982,11 @@ __device__ __forceinline__ void bwd_tile_grads(const rqf_selective_inputs& p, co
     if (p.has_warp) {
       // exp(scale*w) = d theta_u / d theta
       const float ws = SHARED ? sws[k] : s.thu[k] * c.inv_theta;
-      const float wt = SHARED ? swt[k] : s.wtk[k];
+      // d exp(scale*tanh(w))/dw = exp(scale*tanh(w)) * scale*(1 - tanh(w)^2)
+      const float wg = SHARED ? swg[k] : p.warp_scale * fmaf(-s.wtk[k], s.wtk[k], 1.0f);
       // torch.clamp passes the gradient at both exact edges
       if (p.bound_warp && !(th_u >= c.thlo && th_u <= c.thhi)) dth = 0.0f;
-      gd[k] = dth * theta * p.warp_scale * (1.0f - wt * wt);
+      gd[k] = dth * theta * wg;
       dth *= ws;
     } else {
       gd[k] = 0.0f;
@@ -1009,7 +1037,7 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
     r.dcarry = readlane(s.ecot[0], 0);
   } else {
     c32 Q, rr;
-    bwd_lane_adjoint<K>(s, A_lane_next, Q, rr);
+    bwd_lane_adjoint<K, TAIL>(s, A_lane_next, Q, rr);
     if (lane == kWave - 1) rr = cmad(Q, r.dcarry, rr);
     wave_scan_rev(Q, rr, lane);
     dnext = shift_down(rr, r.dcarry, lane);
@@ -1052,7 +1080,7 @@ __global__ __launch_bounds__(kRowsPerBlock* kWave)
   r.dwr = o.dw ? o.dw + base : nullptr;
   r.ddr = o.ddc ? o.ddc + base : nullptr;
   r.sdd = nullptr;
-  r.swt = nullptr;
+  r.swg = nullptr;
   r.sws = nullptr;
   r.dcarry = mk(0.0f, 0.0f);
   r.Afirst = mk(0.0f, 0.0f);
@@ -1287,7 +1315,7 @@ __global__ __launch_bounds__(kTeam* kWave)
   constexpr int PER = TILE >= NT ? TILE / NT : 1;  // tile elements per thread (reduction)
   constexpr int kChans = kMaxSplitTeams * kTeam;
   __shared__ float4 s_dd[2][kTeam][TILE / 4];
-  __shared__ float4 s_wt[SEG / 4], s_ws[SEG / 4];  // staged tanh(warp), exp(scale*tanh)
+  __shared__ float4 s_wg[SEG / 4], s_ws[SEG / 4];  // staged scale*(1 - tanh^2), exp(scale*tanh)
   __shared__ float s_seg[SEG];                     // the segment's group gradient so far
   __shared__ float4 s_carry[kChans];               // (dcarry, Afirst) of each channel
   __shared__ float s_cfirst[kChans];
@@ -1321,7 +1349,7 @@ __global__ __launch_bounds__(kTeam* kWave)
   const int full = VEC ? T / TILE : 0;
   const int seg_tiles = warp ? kSegTiles : ntiles;  // no warp: one segment
   const int nseg = (ntiles + seg_tiles - 1) / seg_tiles;
-  float* swt = reinterpret_cast<float*>(&s_wt[0]);
+  float* swg = reinterpret_cast<float*>(&s_wg[0]);
   float* sws = reinterpret_cast<float*>(&s_ws[0]);
 
   BwdRow r;
@@ -1331,7 +1359,7 @@ __global__ __launch_bounds__(kTeam* kWave)
   r.dr = nullptr;
   r.ddr = nullptr;
   r.sdd = nullptr;
-  r.swt = swt;
+  r.swg = swg;
   r.sws = sws;
   Chan c;
   int64_t row = 0;
@@ -1347,9 +1375,7 @@ __global__ __launch_bounds__(kTeam* kWave)
       const int n = (tile_hi - tile_lo) * TILE;
       for (int i = (int)threadIdx.x; i < n; i += NT) {
         const int t = s0 + i;
-        const float wt = warp_tanh(p, t < T ? dwr[t] : 0.0f);
-        swt[i] = wt;
-        sws[i] = warp_factor(p, wt);
+        warp_stage(p, t < T ? dwr[t] : 0.0f, sws[i], swg[i]);
       }
       __syncthreads();
     }
@@ -1390,7 +1416,7 @@ __global__ __launch_bounds__(kTeam* kWave)
       for (int tile = tile_hi - 1; tile >= tile_lo; --tile) {
         const int t0 = tile * TILE;
         if (warp) {
-          r.swt = swt + (t0 - s0);
+          r.swg = swg + (t0 - s0);
           r.sws = sws + (t0 - s0);
           r.sdd = &s_dd[parity][w][0];
         }
@@ -1499,7 +1525,7 @@ __global__ __launch_bounds__(TC* kGrpTW* kWave)
   constexpr int SEG = kGrpSegSt * ST;
   constexpr int kChans = kGrpMaxChans;
   __shared__ float4 s_dd[kGrpTW][TC][TILE / 4];   // the super-tile's warp gradients
-  __shared__ float4 s_wt[SEG / 4], s_ws[SEG / 4];  // staged tanh(warp), exp(scale*tanh)
+  __shared__ float4 s_wg[SEG / 4], s_ws[SEG / 4];  // staged scale*(1 - tanh^2), exp(scale*tanh)
   __shared__ float s_seg[SEG];                     // the segment's group gradient so far
   __shared__ float4 s_map[kGrpTW][TC][2];          // (R, Q), (A at the first step, cn, -)
   __shared__ float4 s_park[kChans];                // (D, A) carry of each channel
@@ -1524,7 +1550,7 @@ __global__ __launch_bounds__(TC* kGrpTW* kWave)
   const int full = VEC ? T / TILE : 0;
   const int nst = (ntiles + kGrpTW - 1) / kGrpTW;
   const int nseg = (nst + kGrpSegSt - 1) / kGrpSegSt;
-  float* swt = reinterpret_cast<float*>(&s_wt[0]);
+  float* swg = reinterpret_cast<float*>(&s_wg[0]);
   float* sws = reinterpret_cast<float*>(&s_ws[0]);
   const float* sdd = reinterpret_cast<const float*>(&s_dd[0][0][0]);
 
@@ -1535,7 +1561,7 @@ __global__ __launch_bounds__(TC* kGrpTW* kWave)
   r.dr = nullptr;
   r.ddr = nullptr;
   r.sdd = &s_dd[tw][cs][0];
-  r.swt = swt;
+  r.swg = swg;
   r.sws = sws;
   r.dcarry = mk(0.0f, 0.0f);
   r.Afirst = mk(0.0f, 0.0f);
@@ -1554,9 +1580,7 @@ __global__ __launch_bounds__(TC* kGrpTW* kWave)
       const int n = (st_hi - st_lo) * ST;
       for (int i = (int)threadIdx.x; i < n; i += NT) {
         const int t = s0 + i;
-        const float wt = warp_tanh(p, t < T ? dwr[t] : 0.0f);
-        swt[i] = wt;
-        sws[i] = warp_factor(p, wt);
+        warp_stage(p, t < T ? dwr[t] : 0.0f, sws[i], swg[i]);
       }
       __syncthreads();
     }
@@ -1595,7 +1619,7 @@ __global__ __launch_bounds__(TC* kGrpTW* kWave)
         const int tile = st * kGrpTW + tw;
         const int t0 = tile * TILE;
         const bool valid = active && tile < ntiles;
-        r.swt = swt + (t0 - s0);
+        r.swg = swg + (t0 - s0);
         r.sws = sws + (t0 - s0);
         BwdTile<K> s;
         c32 zv[K];
@@ -1613,7 +1637,11 @@ __global__ __launch_bounds__(TC* kGrpTW* kWave)
           if (!truncated) {
             // Lane 63's step after its last is the next tile's first: its
             // decay stays out of the tile's own map (1 here) and comes in with D'.
-            bwd_lane_adjoint<K>(s, shift_down(s.A[0], mk(1.0f, 0.0f), lane), Q, rr);
+            const c32 A_ln = shift_down(s.A[0], mk(1.0f, 0.0f), lane);
+            if (tile >= full)
+              bwd_lane_adjoint<K, true>(s, A_ln, Q, rr);
+            else
+              bwd_lane_adjoint<K, false>(s, A_ln, Q, rr);
             wave_scan_rev(Q, rr, lane);
           }
           if (lane == 0) {

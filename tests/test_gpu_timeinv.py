@@ -41,8 +41,11 @@ def _dev(a):
     return torch.as_tensor(np.asarray(a, dtype=np.complex64), device="cuda").requires_grad_(True)
 
 
+# T at and past 1024- and 2048-step edges (2048, 2049, 1025, 4352) and F past
+# filter groups (130, 200).
 @pytest.mark.parametrize("shape", [(4, 16000, 32), (2, 1023, 8), (2, 777, 16), (4, 161, 64),
-                                   (1, 1, 3), (3, 17, 1), (2, 64, 130)])
+                                   (1, 1, 3), (3, 17, 1), (2, 64, 130), (3, 2048, 64),
+                                   (3, 2049, 64), (2, 1025, 200), (2, 4352, 128)])
 def test_chunked_scan_matches_oracle(shape):
     B, T, F = shape
     print(f"case: chunked_scan {shape}", flush=True)
@@ -64,7 +67,7 @@ def test_chunked_scan_matches_oracle(shape):
             assert err <= PARITY_RTOL, (name + "/channel", err)
 
 
-@pytest.mark.parametrize("shape", [(3, 4096, 32), (2, 300, 5), (1, 2, 7)])
+@pytest.mark.parametrize("shape", [(3, 4096, 32), (2, 300, 5), (1, 2, 7), (2, 2304, 96)])
 def test_chunked_prospective_matches_oracle(shape):
     B, T, F = shape
     print(f"case: chunked_prospective {shape}", flush=True)

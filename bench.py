@@ -53,6 +53,11 @@ def _args():
                          "7: fused |y| readout scan")
     ap.add_argument("--cpu-baseline", dest="cpu", action="store_true", default=True)
     ap.add_argument("--no-cpu-baseline", dest="cpu", action="store_false")
+    ap.add_argument("--cpu-reps", type=int, default=3,
+                    help="timed runs of the CPU baseline sample (median reported, after one "
+                         "warm-up run)")
+    ap.add_argument("--cpu-batch", type=int, default=0,
+                    help="batch of the CPU baseline sample (0: the config's, capped at 64)")
     ap.add_argument("--cpu-steps", type=int, default=0,
                     help="time steps of the CPU baseline sample (0: the config's default)")
     ap.add_argument("--batch", type=int, default=0,
@@ -327,8 +332,8 @@ def plan_selective(cfg, args, dev):
     cpu_steps = args.cpu_steps or (500 if cfg == 3 else 100)
 
     def cpu():
-        return cpu_baseline_selective(F, min(B, 64), G, cpu_steps, log_scale, samp, tau, seq,
-                                      layers)
+        return cpu_baseline_selective(F, args.cpu_batch or min(B, 64), G, cpu_steps, log_scale,
+                                      samp, tau, seq, layers)
 
     return Plan(name, config, F * B * T * len(layers), (state, ops), nbytes, kernels, cpu,
                 contract)
@@ -693,13 +698,23 @@ def _cpu_threads():
     return threads
 
 
-def _median_time(run, reps=3):
-    run()  # warm-up
+CPU_REPS = 3
+
+
+def _median_time(run, reps=None):
+    """Median wall time of ``reps`` runs after one warm-up run; each run's time
+    goes to stderr as it ends (long samples would otherwise print nothing for
+    minutes)."""
+    reps = CPU_REPS if reps is None else reps
     times = []
-    for _ in range(reps):
+    for i in range(reps + 1):
         t0 = time.perf_counter()
         run()
-        times.append(time.perf_counter() - t0)
+        dt = time.perf_counter() - t0
+        print(f"cpu baseline: {'warm-up' if i == 0 else f'run {i} of {reps}'} {dt:.1f} s",
+              file=sys.stderr, flush=True)
+        if i:
+            times.append(dt)
     times.sort()
     return times[len(times) // 2]
 
@@ -755,7 +770,7 @@ def cpu_baseline_selective(F, B, G, steps, log_scale, samp, tau, seq, layers):
                    f"B={B} T={steps} (T reduced from the GPU shape: like the reference's loop, "
                    f"whose backward of each A[..., t] select materialises a full (F,B,T) "
                    f"gradient, the cost per element grows with T, about 8x from T=200 to "
-                   f"T=1000, so T=2000 would take minutes per run), median of 3 after 1 "
+                   f"T=1000, so T=2000 takes minutes per run), median of {CPU_REPS} after 1 "
                    f"warm-up; torch threads={threads} (the GPU box's CPU share is 16 "
                    f"threads), os.cpu_count()={os.cpu_count()}, cpu={_cpu_model()}"),
     }
@@ -800,7 +815,7 @@ def cpu_baseline_timeinv(F, B, steps, L, *, prospective, coef, btf=None):
         "cores": threads,
         "kind": "port",
         "sample": (f"fp32 PyTorch restatement of {what} (oracle/torch_ref.py), (B,T,F) layout, "
-                   f"fwd + autograd bwd, {L} layer(s), F={F} B={B} T={steps}, median of 3 after "
+                   f"fwd + autograd bwd, {L} layer(s), F={F} B={B} T={steps}, median of {CPU_REPS} after "
                    f"1 warm-up; torch threads={threads}, os.cpu_count()={os.cpu_count()}, "
                    f"cpu={_cpu_model()}"),
     }
@@ -841,7 +856,7 @@ def cpu_baseline_multi_osc(F, N, B, steps, c1, c2, cw, *, absolute):
         "cores": threads,
         "kind": "port",
         "sample": (f"fp32 PyTorch restatement of {what} (oracle/torch_ref.py), (B,T,F) layout, "
-                   f"N={N} oscillators, F={F} B={B} T={steps} (T reduced), median of 3 after 1 "
+                   f"N={N} oscillators, F={F} B={B} T={steps} (T reduced), median of {CPU_REPS} after 1 "
                    f"warm-up; torch threads={threads}, os.cpu_count()={os.cpu_count()}, "
                    f"cpu={_cpu_model()}"),
     }
@@ -874,7 +889,9 @@ def traffic_from_table(workload_key, entry):
 
 
 def main():
+    global CPU_REPS
     args = _args()
+    CPU_REPS = max(1, args.cpu_reps)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (single-GPU scan kernels; "
               "no collectives). Run with --gpus 1.", file=sys.stderr)

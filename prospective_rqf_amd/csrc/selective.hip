@@ -883,12 +883,13 @@ __device__ __forceinline__ void bwd_lane_adjoint(const BwdTile<K>& s, c32 A_lane
 
 // Gradient phase of a backward tile, given the adjoint dnext at the step
 // after the lane's last (the cotangent there when truncated), the decay
-// A_lane_next and the lag-tap weight cn_lane_next of that step.
+// A_lane_next and the lag-tap weight cn_lane_next of that step.  gd_out
+// (optional) receives the lane's warp-logit gradients.
 template <int K, bool VEC, bool TAIL, bool SHARED>
 __device__ __forceinline__ void bwd_tile_grads(const rqf_selective_inputs& p, const Chan& c,
                                                BwdRow& r, int t0, int lane, const c32 (&zv)[K],
                                                const BwdTile<K>& s, c32 dnext, c32 A_lane_next,
-                                               float cn_lane_next) {
+                                               float cn_lane_next, float* gd_out = nullptr) {
   const int T = r.T;
   const int tb = t0 + lane * K;
   float swg[K], sws[K];
@@ -1013,6 +1014,10 @@ __device__ __forceinline__ void bwd_tile_grads(const rqf_selective_inputs& p, co
     for (int j = 0; j < K / 4; ++j)
       r.sdd[lane * (K / 4) + j] =
           make_float4(gd[4 * j], gd[4 * j + 1], gd[4 * j + 2], gd[4 * j + 3]);
+  }
+  if (gd_out) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) gd_out[k] = gd[k];
   }
 }
 
@@ -1487,7 +1492,7 @@ __global__ __launch_bounds__(kTeam* kWave)
 // Backward, group form: one block per (warp group, batch element) runs every
 // team of the group, so the group's warp-logit gradient is complete inside
 // the block: no split partial rows and no closing pass over them.  The block
-// is TC x kGrpTW wavefronts, TC channel slots (one team) times kGrpTW
+// is kGrpTC x kGrpTW wavefronts, kGrpTC channel slots (one team) times kGrpTW
 // time slots, and walks the rows backwards in super-tiles of kGrpTW
 // consecutive tiles, time slot w taking tile w of each, so that concurrent
 // wavefronts stream adjacent stretches of every row.  A wavefront replays its
@@ -1495,45 +1500,84 @@ __global__ __launch_bounds__(kTeam* kWave)
 // scans the tile's adjoint from a zero state and publishes the tile's map
 //     D = R + Q conj(A') D'
 // with D the adjoint at the tile's first step and A', D' the decay and the
-// adjoint at the first step of the tile after it.  After one barrier every
-// wavefront composes the maps of the tiles after its own onto the channel's
-// carry, forms its gradients and stages its warp-logit gradient in LDS; after
-// a second barrier the block sums the team's channels into the segment's
-// group sum.  Warp values are staged per segment of kGrpSegSt super-tiles for
-// all teams, and each channel's carry and fp64 sums are parked in LDS between
-// segments, as in the split form above.
+// adjoint at the first step of the tile after it.  The channel's wavefronts
+// then meet (a barrier of the channel's kGrpTW wavefronts only, on an LDS
+// counter) and each composes the maps of the tiles after its own onto the
+// channel's carry and forms its gradients.  The group's warp-logit gradient is
+// summed in a fixed order, team after team and channel after channel: a
+// wavefront waits on an LDS counter until the channel before it has added its
+// tile, then adds its own straight from registers.  There is no block-wide
+// barrier per super-tile, so the channels drift apart and their memory waits
+// overlap each other's arithmetic, as independent blocks would.  (With two
+// block barriers per super-tile the 12 wavefronts moved in lockstep: 2.84
+// against 2.78 ms for the split form at config 3.)  Warp values are staged
+// per segment of kGrpSegSt super-tiles for all teams, behind block barriers;
+// each channel's carry and fp64 sums are parked in LDS between segments.
+//
+// Every wait is bounded: one that runs out sets a flag that ends every other
+// wait of the block at once, and the block then writes NaN for its channels'
+// dbias and dtheta partials, so a broken dependency shows as NaN gradients
+// instead of hanging the GPU.  The waits only point to earlier channels of the
+// same super-tile or to the channel's own wavefronts at the same super-tile,
+// so none of them is circular.
 // ---------------------------------------------------------------------------
 #ifndef RQF_GRP_TIME_SLOTS
 #define RQF_GRP_TIME_SLOTS 3
 #endif
+constexpr int kGrpTC = kTeam;               // channel slots: one team
 constexpr int kGrpTW = RQF_GRP_TIME_SLOTS;  // time slots: tiles per super-tile
+constexpr int kGrpWaves = kGrpTC * kGrpTW;
 #ifndef RQF_GRP_SEG_SUPER_TILES
 #define RQF_GRP_SEG_SUPER_TILES 4
 #endif
 constexpr int kGrpSegSt = RQF_GRP_SEG_SUPER_TILES;  // super-tiles per staged segment
 constexpr int kGrpMaxChans = 256;  // channels of one group whose state LDS parks
+constexpr int kGrpSpins = 1 << 20;  // bound on one wait (tens of ms)
 
-// TC: channel slots (the team size) of a block of TC * kGrpTW wavefronts.
-template <int O, bool VEC, int TC>
-__global__ __launch_bounds__(TC* kGrpTW* kWave)
+// Wait until the LDS counter reaches `target`; false if the wait ran out or
+// another wait of the block did.
+__device__ __forceinline__ bool lds_await(int* counter, int target, int* abort) {
+  for (int n = 0; n < kGrpSpins; ++n) {
+    if (__hip_atomic_load(counter, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target)
+      return true;
+    if (__hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  __hip_atomic_store(abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  return false;
+}
+// Count one more arrival after the wavefront's earlier LDS writes (all lanes
+// take part in the fence; lane 0 counts).
+__device__ __forceinline__ void lds_release_add(int* counter, int lane) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  if (lane == 0) __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+template <int O, bool VEC>
+__global__ __launch_bounds__(kGrpWaves* kWave)
     __attribute__((amdgpu_waves_per_eu(RQF_BWD_WAVES_PER_EU))) void selective_bwd_grp_kernel(
         const rqf_selective_inputs pin, const float* __restrict__ z,
         const float* __restrict__ entries, int chunk, int nc, const float* __restrict__ gy,
         const float* __restrict__ gx, int truncated, Teams tm, BwdOut o) {
   const rqf_selective_inputs p = with_options<O>(pin);
-  constexpr int K = kBwdK, TILE = kWave * K, NT = TC * kGrpTW * kWave, ST = kGrpTW * TILE;
+  constexpr int K = kBwdK, TILE = kWave * K, NT = kGrpWaves * kWave, ST = kGrpTW * TILE;
   constexpr int SEG = kGrpSegSt * ST;
   constexpr int kChans = kGrpMaxChans;
-  __shared__ float4 s_dd[kGrpTW][TC][TILE / 4];   // the super-tile's warp gradients
+  static_assert(K % 4 == 0, "whole float4s of warp gradient per lane");
   __shared__ float4 s_wg[SEG / 4], s_ws[SEG / 4];  // staged scale*(1 - tanh^2), exp(scale*tanh)
-  __shared__ float s_seg[SEG];                     // the segment's group gradient so far
-  __shared__ float4 s_map[kGrpTW][TC][2];          // (R, Q), (A at the first step, cn, -)
+  __shared__ float4 s_seg[SEG / 4];                // the segment's group gradient so far
+  __shared__ float4 s_map[2][kGrpTC][kGrpTW][2];   // (R, Q), (A at the first step, cn, -)
+  __shared__ int s_arrive[kGrpTC];                 // channel barrier arrivals
+  __shared__ int s_added[kGrpSegSt][kGrpTW];       // group-sum contributions so far
+  __shared__ int s_abort;
   __shared__ float4 s_park[kChans];                // (D, A) carry of each channel
   __shared__ float s_pcf[kChans];                  // lag-tap weight of the carry
   __shared__ double s_sum[kChans][kGrpTW][2];      // dbias, dtheta sums per time slot
   const int lane = lane_id();
   const int w = wave_id();
-  const int cs = w % TC, tw = w / TC;
+  // A channel's time slots are consecutive wavefronts, which the SIMDs take
+  // round-robin: each SIMD holds wavefronts of different channels.
+  const int cs = w / kGrpTW, tw = w % kGrpTW;
   const int64_t L = xcd_remap(blockIdx.x, gridDim.x);
   const int64_t g = L / p.B, b = L - g * p.B;
   if (g >= p.G) return;  // block-uniform
@@ -1552,7 +1596,9 @@ __global__ __launch_bounds__(TC* kGrpTW* kWave)
   const int nseg = (nst + kGrpSegSt - 1) / kGrpSegSt;
   float* swg = reinterpret_cast<float*>(&s_wg[0]);
   float* sws = reinterpret_cast<float*>(&s_ws[0]);
-  const float* sdd = reinterpret_cast<const float*>(&s_dd[0][0][0]);
+  float* sseg = reinterpret_cast<float*>(&s_seg[0]);
+  if (threadIdx.x < kGrpTC) s_arrive[threadIdx.x] = 0;
+  if (threadIdx.x == 0) s_abort = 0;
 
   BwdRow r;
   r.T = T;
@@ -1560,13 +1606,14 @@ __global__ __launch_bounds__(TC* kGrpTW* kWave)
   r.truncated = truncated;
   r.dr = nullptr;
   r.ddr = nullptr;
-  r.sdd = &s_dd[tw][cs][0];
+  r.sdd = nullptr;
   r.swg = swg;
   r.sws = sws;
   r.dcarry = mk(0.0f, 0.0f);
   r.Afirst = mk(0.0f, 0.0f);
   r.cfirst = 0.0f;
   Chan c;
+  int gen = 0;  // channel barriers passed (the same count in every slot of a channel)
   // The channel's carry: adjoint, decay and lag-tap weight at the first step
   // after the super-tile being walked.
   c32 Dc = mk(0.0f, 0.0f), Ac = mk(0.0f, 0.0f);
@@ -1575,21 +1622,23 @@ __global__ __launch_bounds__(TC* kGrpTW* kWave)
     const int st_lo = sg * kGrpSegSt, st_hi = min(nst, st_lo + kGrpSegSt);
     const int s0 = st_lo * ST;
     {
-      // Stage the segment's warp values for all teams.  The previous
-      // segment's last barrier ordered its reads before these writes.
+      // Stage the segment's warp values for all teams.  Every wavefront has
+      // left the previous segment (the barrier) before they are replaced.
+      __syncthreads();
       const int n = (st_hi - st_lo) * ST;
       for (int i = (int)threadIdx.x; i < n; i += NT) {
         const int t = s0 + i;
         warp_stage(p, t < T ? dwr[t] : 0.0f, sws[i], swg[i]);
       }
+      if (threadIdx.x < kGrpSegSt * kGrpTW) (&s_added[0][0])[threadIdx.x] = 0;
       __syncthreads();
     }
     for (int qi = 0; qi < nteam; ++qi) {
-      const int ch = qi * TC + cs;
+      const int ch = qi * kGrpTC + cs;
       const int team = team0 + qi;
       const int members = tm.count[team];
-      const bool active = cs < members;
-      const int64_t f = tm.order[tm.first[team] + (active ? cs : 0)];
+      if (cs >= members) continue;  // the whole channel slot sits this team out
+      const int64_t f = tm.order[tm.first[team] + cs];
       const int64_t row = f * p.B + b;
       c = load_chan(p, f);
       const int64_t base = row * T;
@@ -1615,10 +1664,14 @@ __global__ __launch_bounds__(TC* kGrpTW* kWave)
         Ac = mk(v.z, v.w);
         cc = s_pcf[ch];
       }
+      // this channel's place in the group sum's order, and the last place
+      const int place = qi * kGrpTC + cs;
+      const int last = (nteam - 1) * kGrpTC + tm.count[team0 + nteam - 1] - 1;
       for (int st = st_hi - 1; st >= st_lo; --st) {
         const int tile = st * kGrpTW + tw;
         const int t0 = tile * TILE;
-        const bool valid = active && tile < ntiles;
+        const bool valid = tile < ntiles;
+        const int buf = gen & 1;
         r.swg = swg + (t0 - s0);
         r.sws = sws + (t0 - s0);
         BwdTile<K> s;
@@ -1645,16 +1698,19 @@ __global__ __launch_bounds__(TC* kGrpTW* kWave)
             wave_scan_rev(Q, rr, lane);
           }
           if (lane == 0) {
-            s_map[tw][cs][0] = truncated ? make_float4(s.ecot[0].r, s.ecot[0].i, 0.0f, 0.0f)
-                                         : make_float4(rr.r, rr.i, Q.r, Q.i);
-            s_map[tw][cs][1] = make_float4(s.A[0].r, s.A[0].i, s.c0, 0.0f);
+            s_map[buf][cs][tw][0] = truncated ? make_float4(s.ecot[0].r, s.ecot[0].i, 0.0f, 0.0f)
+                                              : make_float4(rr.r, rr.i, Q.r, Q.i);
+            s_map[buf][cs][tw][1] = make_float4(s.A[0].r, s.A[0].i, s.c0, 0.0f);
           }
-        } else if (active && lane == 0) {
+        } else if (lane == 0) {
           // a tile past the row's end: zero adjoint, decay and lag tap
-          s_map[tw][cs][0] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-          s_map[tw][cs][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          s_map[buf][cs][tw][0] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          s_map[buf][cs][tw][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
-        __syncthreads();
+        // Channel barrier: the channel's maps of this super-tile are in.
+        ++gen;
+        lds_release_add(&s_arrive[cs], lane);
+        lds_await(&s_arrive[cs], kGrpTW * gen, &s_abort);
         // Compose the maps of the super-tile's tiles, latest first, onto the
         // carry: (Dn, An, cn) at the first step after tile tw, and the carry
         // for the super-tile before this one.
@@ -1667,7 +1723,7 @@ __global__ __launch_bounds__(TC* kGrpTW* kWave)
             A1 = An;
             c1 = cn;
           }
-          const float4 m0 = s_map[j][cs][0], m1 = s_map[j][cs][1];
+          const float4 m0 = s_map[buf][cs][j][0], m1 = s_map[buf][cs][j][1];
           Dn = truncated ? mk(m0.x, m0.y) : cmad(mk(m0.z, m0.w), cjmul(An, Dn), mk(m0.x, m0.y));
           An = mk(m1.x, m1.y);
           cn = m1.z;
@@ -1675,6 +1731,9 @@ __global__ __launch_bounds__(TC* kGrpTW* kWave)
         Dc = Dn;
         Ac = An;
         cc = cn;
+        float gd[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) gd[k] = 0.0f;
         if (valid) {
           const c32 A_lane_next = shift_down(s.A[0], A1, lane);
           const float cn_lane_next = shift_down(s.c0, c1, lane);
@@ -1688,47 +1747,51 @@ __global__ __launch_bounds__(TC* kGrpTW* kWave)
           }
           if (tile >= full)
             bwd_tile_grads<K, VEC, true, true>(p, c, r, t0, lane, zv, s, dnext, A_lane_next,
-                                               cn_lane_next);
+                                               cn_lane_next, gd);
           else
             bwd_tile_grads<K, VEC, false, true>(p, c, r, t0, lane, zv, s, dnext, A_lane_next,
-                                                cn_lane_next);
+                                                cn_lane_next, gd);
         }
-        __syncthreads();
-        // Step i of the super-tile: the team's sum (fixed channel order) joins
-        // the segment's group sum (fixed team order); each thread owns the same
-        // steps for every team, so s_seg needs no barrier of its own.
-        for (int i = (int)threadIdx.x; i < ST; i += NT) {
-          const int slot = i / TILE, k = i - slot * TILE;
-          float acc = 0.0f;
-          for (int m = 0; m < members; ++m) acc += sdd[(slot * TC + m) * TILE + k];
-          const int t = st * ST + i, j = t - s0;
-          if (qi > 0) acc = s_seg[j] + acc;
-          if (qi + 1 < nteam)
-            s_seg[j] = acc;
-          else if (t < T)
-            ddrow[t] = acc;
+        // The group sum of this tile's steps, in the fixed (team, channel)
+        // order: wait for the channel before, add, pass on.
+        int* added = &s_added[st - st_lo][tw];
+        lds_await(added, place, &s_abort);
+        const int j0 = t0 - s0 + lane * K, tb = t0 + lane * K;
+        float4 acc = make_float4(gd[0], gd[1], gd[2], gd[3]);
+        if (place > 0) {
+          const float4 prev = reinterpret_cast<const float4*>(sseg + j0)[0];
+          acc = make_float4(prev.x + acc.x, prev.y + acc.y, prev.z + acc.z, prev.w + acc.w);
         }
+        if (place < last) {
+          reinterpret_cast<float4*>(sseg + j0)[0] = acc;
+        } else if (VEC && tb + K <= T) {
+          *reinterpret_cast<float4*>(ddrow + tb) = acc;
+        } else {
+          const float a4[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            if (tb + k < T) ddrow[tb + k] = a4[k];
+        }
+        lds_release_add(added, lane);
       }
-      if (active) {
-        // Park the channel's carry (every time slot holds the same one) and
-        // add this wavefront's sums to its slot.
-        if (sg > 0 && tw == 0 && lane == 0) {
-          s_park[ch] = make_float4(Dc.r, Dc.i, Ac.r, Ac.i);
-          s_pcf[ch] = cc;
-        }
-        const double sb = wave_sum(r.sum_bias);
-        const double sth = wave_sum(r.sum_theta);
-        if (lane == 0) {
-          s_sum[ch][tw][0] = (sg == nseg - 1 ? 0.0 : s_sum[ch][tw][0]) + sb;
-          s_sum[ch][tw][1] = (sg == nseg - 1 ? 0.0 : s_sum[ch][tw][1]) + sth;
-        }
+      // Park the channel's carry (every time slot holds the same one) and add
+      // this wavefront's sums to its slot.
+      if (sg > 0 && tw == 0 && lane == 0) {
+        s_park[ch] = make_float4(Dc.r, Dc.i, Ac.r, Ac.i);
+        s_pcf[ch] = cc;
+      }
+      const double sb = wave_sum(r.sum_bias);
+      const double sth = wave_sum(r.sum_theta);
+      if (lane == 0) {
+        s_sum[ch][tw][0] = (sg == nseg - 1 ? 0.0 : s_sum[ch][tw][0]) + sb;
+        s_sum[ch][tw][1] = (sg == nseg - 1 ? 0.0 : s_sum[ch][tw][1]) + sth;
       }
     }
   }
   __syncthreads();
   // Per-row fp64 partials of dbias and dtheta: the time slots in fixed order.
-  for (int i = (int)threadIdx.x; i < nteam * TC; i += NT) {
-    const int team = team0 + i / TC, m = i % TC;
+  for (int i = (int)threadIdx.x; i < nteam * kGrpTC; i += NT) {
+    const int team = team0 + i / kGrpTC, m = i % kGrpTC;
     if (m < tm.count[team]) {
       const int64_t row = (int64_t)tm.order[tm.first[team] + m] * p.B + b;
       double sb = 0.0, sth = 0.0;
@@ -1737,6 +1800,7 @@ __global__ __launch_bounds__(TC* kGrpTW* kWave)
         sb += s_sum[i][j][0];
         sth += s_sum[i][j][1];
       }
+      if (s_abort) sb = sth = __builtin_nan("");  // a wait ran out: flag the results
       o.partial[row] = sb;
       o.partial[p.F * p.B + row] = sth;
     }
@@ -2035,26 +2099,24 @@ int split_teams(const rqf_selective_inputs* in) {
 }
 
 // The group form of the backward needs the warp head and no group with more
-// channels than its LDS parks (F <= kGrpMaxChans).  It runs only when the
-// environment variable RQF_BWD_FORM=group asks for it: measured at configs 3
-// and 4 it is slower than the split form (2.84 against 2.78 ms and 0.79 / 0.77
-// against 0.75 / 0.65 ms with 4 channel slots).  One block per CU moves its
-// 12 wavefronts in lockstep between the barriers, so their memory waits no
-// longer overlap other blocks' arithmetic; with 2 channel slots the 6-wavefront
-// blocks sit unevenly on the SIMDs and a second block does not fit at
-// 3 waves per SIMD (4.03 ms).
+// channels than its LDS parks (F <= kGrpMaxChans).  It runs by default when
+// the (group, batch element) blocks give every CU one and the rows' last
+// super-tile is nearly full (at most 1/32 of the time slots idle): at config 3
+// (T = 16000, 63 tiles in 21 super-tiles) it measured 2.70 against 2.75 ms for
+// the split form, at config 4 (T = 4096, 16 tiles in 6 super-tiles, an eighth
+// of the slots idle) 0.73 / 0.69 against 0.74 / 0.64 ms.  The environment
+// variable RQF_BWD_FORM=group|split picks a form for tests and tuning; setting
+// RQF_BWD_SPLIT_TEAMS picks the split form.
 bool use_group_form(const rqf_selective_inputs* in) {
   if (!RQF_BWD_TEAMS || !in->has_warp || in->F > kGrpMaxChans) return false;
   if (std::getenv("RQF_BWD_SPLIT_TEAMS")) return false;
-  const char* e = std::getenv("RQF_BWD_FORM");
-  return e && !std::strcmp(e, "group");
-}
-
-// Channel slots of a group-form block: 4 (12 wavefronts), or 2 (6 wavefronts)
-// with RQF_GRP_CHANNEL_SLOTS=2.
-int group_channel_slots(const rqf_selective_inputs*) {
-  const char* e = std::getenv("RQF_GRP_CHANNEL_SLOTS");
-  return e && !std::strcmp(e, "2") ? 2 : 4;
+  if (const char* e = std::getenv("RQF_BWD_FORM")) {
+    if (!std::strcmp(e, "group")) return true;
+    if (!std::strcmp(e, "split")) return false;
+  }
+  const int64_t ntiles = (in->T + kBwdTile - 1) / kBwdTile;
+  const int64_t nst = (ntiles + kGrpTW - 1) / kGrpTW;
+  return in->G * in->B >= kCus && (nst * kGrpTW - ntiles) * 32 <= ntiles;
 }
 
 struct SelWs {
@@ -2067,7 +2129,7 @@ SelWs sel_ws_layout(const rqf_selective_inputs* in, int64_t chunk) {
   const int64_t R = in->F * in->B;
   w.G = in->has_warp ? (int)in->G : 1;
   w.group_form = use_group_form(in);
-  w.tsize = w.group_form ? group_channel_slots(in) : kTeam;
+  w.tsize = kTeam;
   const int teams = (int)((in->F + w.tsize - 1) / w.tsize);
   w.slots = w.G + teams;  // teams of all groups <= ceil(F/tsize) + G
   w.Q = split_teams(in);
@@ -2123,7 +2185,7 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
   char* ws = (char*)workspace;
   double* partial = (double*)(ws + w.partial);
   if (nonempty) {
-    const bool vec = vec_ok(in, {z, gy, gx, dz, dzw, dg, dw});
+    const bool vec = vec_ok(in, {z, gy, gx, dz, dzw, dg, dw, dd});
     const float* ent = entries;
     int ent_chunk = chunk_int(chunk), nc = (int)((T + chunk - 1) / chunk);
     if (chunk > kBwdTile) {
@@ -2174,22 +2236,17 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
     tm.slots = w.split_slots;
     o.dd = in->has_warp ? dd : nullptr;
     if (w.group_form) {
-      const dim3 grid((unsigned)(in->G * in->B)), block(w.tsize * kGrpTW * kWave);
+      const dim3 grid((unsigned)(in->G * in->B)), block(kGrpWaves * kWave);
       with_option_set(options_of(in), [&](auto oc) {
         constexpr int O = decltype(oc)::value;
         if constexpr (O != kOptRuntime && !(O & kOptWarp)) {
           return;  // not reached: the group form needs the warp head
+        } else if (vec) {
+          hipLaunchKernelGGL((selective_bwd_grp_kernel<O, true>), grid, block, 0, s, *in, z, ent,
+                             ent_chunk, nc, gy, gx, (int)truncated, tm, o);
         } else {
-          auto launch = [&](auto kernel) {
-            hipLaunchKernelGGL(kernel, grid, block, 0, s, *in, z, ent, ent_chunk, nc, gy, gx,
-                               (int)truncated, tm, o);
-          };
-          if (w.tsize == 2)
-            vec ? launch(selective_bwd_grp_kernel<O, true, 2>)
-                : launch(selective_bwd_grp_kernel<O, false, 2>);
-          else
-            vec ? launch(selective_bwd_grp_kernel<O, true, 4>)
-                : launch(selective_bwd_grp_kernel<O, false, 4>);
+          hipLaunchKernelGGL((selective_bwd_grp_kernel<O, false>), grid, block, 0, s, *in, z,
+                             ent, ent_chunk, nc, gy, gx, (int)truncated, tm, o);
         }
       });
       launch_finish(nullptr, nullptr, nullptr, 0, 0, partial, dbias, dtheta, in->F, in->B, s);

@@ -262,7 +262,7 @@ def _config3_inputs(B, T=16000, seed=0):
     return workloads.selective_inputs(256, B, T, G=8, device="cuda", seed=seed)
 
 
-@pytest.mark.parametrize("form", ["group2", "group4", "split"])
+@pytest.mark.parametrize("form", ["group", "split"])
 def test_config3_team_layout(monkeypatch, form):
     """F = 256 in 8 warp groups of 32 channels (8 teams of 4 per group), in
     both forms of the backward: one block running all 8 teams of a group (the
@@ -270,9 +270,8 @@ def test_config3_team_layout(monkeypatch, form):
     split rows per group summed by the split reduction."""
     F, B, T, chunk = 256, 2, 16000, 256
     print(f"case: config 3 team layout F={F} B={B} T={T} form={form}", flush=True)
-    if form.startswith("group"):
+    if form == "group":
         monkeypatch.setenv("RQF_BWD_FORM", "group")
-        monkeypatch.setenv("RQF_GRP_CHANNEL_SLOTS", form[-1])
     else:
         monkeypatch.setenv("RQF_BWD_SPLIT_TEAMS", "2")
     rng = np.random.default_rng(3000)
@@ -296,20 +295,17 @@ def test_config3_team_layout(monkeypatch, form):
                 SELECTIVE_CHANNEL_RTOL)
 
 
-@pytest.mark.parametrize("form", ["group2", "group4", "split"])
+@pytest.mark.parametrize("form", ["group", "split"])
 def test_config3_full_shape_properties(monkeypatch, form):
     """The full config-3 shape (B = 64) against small-batch calls on the same
     rows, both in the same form of the backward: per-row outputs bit for bit,
-    warp-logit gradients to rounding (bit for bit in the group form with the
-    same channel slots; in the split form the grid's split layout changes the
-    order of the channel sum), and dbias / dtheta as the fp64 sum over the
-    small batches."""
+    warp-logit gradients to rounding (bit for bit in the group form; in the
+    split form the grid's split layout changes the order of the channel sum),
+    and dbias / dtheta as the fp64 sum over the small batches."""
     F, B, T, chunk, SB = 256, 64, 16000, 256, 4
     print(f"case: config 3 full shape B={B} vs {B // SB} calls of B={SB} form={form}",
           flush=True)
-    monkeypatch.setenv("RQF_BWD_FORM", form[:5])
-    if form.startswith("group"):
-        monkeypatch.setenv("RQF_GRP_CHANNEL_SLOTS", form[-1])
+    monkeypatch.setenv("RQF_BWD_FORM", form)
     g = torch.Generator(device="cuda").manual_seed(33)
 
     def cn(*shape):
@@ -347,5 +343,5 @@ def test_config3_full_shape_properties(monkeypatch, form):
             "dbias/channel": chanerr(full[5], dbias_sum),
             "dtheta/channel": chanerr(full[6], dtheta_sum)}
     print("  " + " ".join(f"{k} {v:.1e}" for k, v in errs.items()), flush=True)
-    assert worst_dd <= (0.0 if form.startswith("group") else 1e-6)
+    assert worst_dd <= (0.0 if form == "group" else 1e-6)
     assert max(errs.values()) <= 1e-5, errs

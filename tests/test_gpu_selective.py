@@ -286,16 +286,14 @@ def _empty_groups(inp, z):
     (20, 3, 4500, "global", 1, 256, True, None),
     (9, 2, 2300, "grouped", 5, 256, False, _empty_groups),
 ])
-@pytest.mark.parametrize("slots", ["2", "4"])
-def test_group_form(monkeypatch, F, B, T, warp, G, chunk, truncated, edit, slots):
+def test_group_form(monkeypatch, F, B, T, warp, G, chunk, truncated, edit):
     """The group form of the backward (one block per warp group and batch
-    element; adjoint maps composed across the time slots of a super-tile), in
-    blocks of 2 and 4 channel slots, forced at shapes whose grid would pick
-    the split form."""
+    element; adjoint maps composed across the time slots of a super-tile, the
+    group sum added channel after channel), forced at shapes whose grid would
+    pick the split form."""
     print(f"case: group form F={F} B={B} T={T} warp={warp} G={G} chunk={chunk} "
-          f"truncated={truncated} edit={edit is not None} slots={slots}", flush=True)
+          f"truncated={truncated} edit={edit is not None}", flush=True)
     monkeypatch.setenv("RQF_BWD_FORM", "group")
-    monkeypatch.setenv("RQF_GRP_CHANNEL_SLOTS", slots)
     run_case(F, B, T, dict(CASE_ALL, warp=warp), chunk=chunk, G=G, truncated=truncated,
              edit=edit, seed=F + T + chunk)
 

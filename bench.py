@@ -316,7 +316,9 @@ def plan_selective(cfg, args, dev):
         nbytes[f"rqf_selective_bwd[L{li}]"] = bb
     kernels = {
         "rqf_selective_fwd": "selective_fwd_rb_kernel",
-        "rqf_selective_bwd": ("team_build_kernel + selective_bwd_team_kernel + "
+        "rqf_selective_bwd": ("team_build_kernel + selective_bwd_grp_kernel (group form: "
+                              "G*B >= 256 and full super-tiles, e.g. config 3) or "
+                              "selective_bwd_team_kernel (split form, e.g. config 4) + "
                               "bwd_finish_kernel"),
     }
     if stack != "none":

@@ -317,9 +317,9 @@ def plan_selective(cfg, args, dev):
     kernels = {
         "rqf_selective_fwd": "selective_fwd_rb_kernel",
         "rqf_selective_bwd": ("team_build_kernel + selective_bwd_grp_kernel (group form: "
-                              "G*B >= 256 and full super-tiles, e.g. config 3) or "
-                              "selective_bwd_team_kernel (split form, e.g. config 4) + "
-                              "bwd_finish_kernel"),
+                              "G*B >= 256, nearly full super-tiles and a gx cotangent, e.g. "
+                              "config 3 and config 4's layer 0) or selective_bwd_team_kernel "
+                              "(split form, e.g. config 4's layer 1) + bwd_finish_kernel"),
     }
     if stack != "none":
         contract += f"; encoder residual add (raw + h, act + h) {stack}"

@@ -1492,16 +1492,18 @@ __global__ __launch_bounds__(kTeam* kWave)
 // Backward, group form: one block per (warp group, batch element) runs every
 // team of the group, so the group's warp-logit gradient is complete inside
 // the block: no split partial rows and no closing pass over them.  The block
-// is kGrpTC x kGrpTW wavefronts, kGrpTC channel slots (one team) times kGrpTW
-// time slots, and walks the rows backwards in super-tiles of kGrpTW
-// consecutive tiles, time slot w taking tile w of each, so that concurrent
+// lists its group's channels itself from `groups` (no team table, no launch
+// before it).  The block
+// is TC x TW = 12 wavefronts, TC channel slots (one team of TC channels) times
+// TW time slots, and walks the rows backwards in super-tiles of TW consecutive
+// tiles, time slot w taking tile w of each, so that concurrent
 // wavefronts stream adjacent stretches of every row.  A wavefront replays its
 // tile's forward from the stored entry state (entries are kept per tile),
 // scans the tile's adjoint from a zero state and publishes the tile's map
 //     D = R + Q conj(A') D'
 // with D the adjoint at the tile's first step and A', D' the decay and the
 // adjoint at the first step of the tile after it.  The channel's wavefronts
-// then meet (a barrier of the channel's kGrpTW wavefronts only, on an LDS
+// then meet (a barrier of the channel's TW wavefronts only, on an LDS
 // counter) and each composes the maps of the tiles after its own onto the
 // channel's carry and forms its gradients.  The group's warp-logit gradient is
 // summed in a fixed order, team after team and channel after channel: a
@@ -1511,8 +1513,11 @@ __global__ __launch_bounds__(kTeam* kWave)
 // overlap each other's arithmetic, as independent blocks would.  (With two
 // block barriers per super-tile the 12 wavefronts moved in lockstep: 2.84
 // against 2.78 ms for the split form at config 3.)  Warp values are staged
-// per segment of kGrpSegSt super-tiles for all teams, behind block barriers;
-// each channel's carry and fp64 sums are parked in LDS between segments.
+// per segment of 12 tiles for all teams, behind block barriers; each
+// channel's carry and fp64 sums are parked in LDS between segments.  Two
+// shapes: 4 x 3 (teams of 4) and 3 x 4 (teams of 3), whichever leaves fewer
+// slots idle at the row length and group size (T = 4096: 16 tiles fill four
+// super-tiles of 4 but leave 2 of 18 slots idle in super-tiles of 3).
 //
 // Every wait is bounded: one that runs out sets a flag that ends every other
 // wait of the block at once, and the block then writes NaN for its channels'
@@ -1521,16 +1526,8 @@ __global__ __launch_bounds__(kTeam* kWave)
 // same super-tile or to the channel's own wavefronts at the same super-tile,
 // so none of them is circular.
 // ---------------------------------------------------------------------------
-#ifndef RQF_GRP_TIME_SLOTS
-#define RQF_GRP_TIME_SLOTS 3
-#endif
-constexpr int kGrpTC = kTeam;               // channel slots: one team
-constexpr int kGrpTW = RQF_GRP_TIME_SLOTS;  // time slots: tiles per super-tile
-constexpr int kGrpWaves = kGrpTC * kGrpTW;
-#ifndef RQF_GRP_SEG_SUPER_TILES
-#define RQF_GRP_SEG_SUPER_TILES 4
-#endif
-constexpr int kGrpSegSt = RQF_GRP_SEG_SUPER_TILES;  // super-tiles per staged segment
+constexpr int kGrpWaves = 12;      // channel slots x time slots
+constexpr int kGrpSegTiles = 12;   // tiles per staged segment
 constexpr int kGrpMaxChans = 256;  // channels of one group whose state LDS parks
 constexpr int kGrpSpins = 1 << 20;  // bound on one wait (tens of ms)
 
@@ -1553,16 +1550,20 @@ __device__ __forceinline__ void lds_release_add(int* counter, int lane) {
   if (lane == 0) __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-template <int O, bool VEC>
+template <int O, bool VEC, int TC>
 __global__ __launch_bounds__(kGrpWaves* kWave)
     __attribute__((amdgpu_waves_per_eu(RQF_BWD_WAVES_PER_EU))) void selective_bwd_grp_kernel(
         const rqf_selective_inputs pin, const float* __restrict__ z,
         const float* __restrict__ entries, int chunk, int nc, const float* __restrict__ gy,
-        const float* __restrict__ gx, int truncated, Teams tm, BwdOut o) {
+        const float* __restrict__ gx, int truncated, BwdOut o) {
   const rqf_selective_inputs p = with_options<O>(pin);
+  constexpr int kGrpTC = TC, kGrpTW = kGrpWaves / TC, kGrpSegSt = kGrpSegTiles / kGrpTW;
+  static_assert(kGrpTC * kGrpTW == kGrpWaves && kGrpSegSt * kGrpTW == kGrpSegTiles,
+                "slot shape");
   constexpr int K = kBwdK, TILE = kWave * K, NT = kGrpWaves * kWave, ST = kGrpTW * TILE;
   constexpr int SEG = kGrpSegSt * ST;
-  constexpr int kChans = kGrpMaxChans;
+  // channel places: whole teams of TC covering up to kGrpMaxChans channels
+  constexpr int kChans = (kGrpMaxChans + TC - 1) / TC * TC;
   static_assert(K % 4 == 0, "whole float4s of warp gradient per lane");
   __shared__ float4 s_wg[SEG / 4], s_ws[SEG / 4];  // staged scale*(1 - tanh^2), exp(scale*tanh)
   __shared__ float4 s_seg[SEG / 4];                // the segment's group gradient so far
@@ -1573,6 +1574,8 @@ __global__ __launch_bounds__(kGrpWaves* kWave)
   __shared__ float4 s_park[kChans];                // (D, A) carry of each channel
   __shared__ float s_pcf[kChans];                  // lag-tap weight of the carry
   __shared__ double s_sum[kChans][kGrpTW][2];      // dbias, dtheta sums per time slot
+  __shared__ int s_order[kChans];                  // the group's channels, ascending
+  __shared__ int s_wcnt[kGrpWaves];
   const int lane = lane_id();
   const int w = wave_id();
   // A channel's time slots are consecutive wavefronts, which the SIMDs take
@@ -1581,7 +1584,26 @@ __global__ __launch_bounds__(kGrpWaves* kWave)
   const int64_t L = xcd_remap(blockIdx.x, gridDim.x);
   const int64_t g = L / p.B, b = L - g * p.B;
   if (g >= p.G) return;  // block-uniform
-  const int team0 = tm.gteam[g], nteam = tm.gteam[g + 1] - team0;
+  // The group's channels in ascending order, straight from `groups` (one
+  // channel per thread: F <= kGrpMaxChans < NT): a ballot per wavefront
+  // places each after the earlier wavefronts' members.  Teams are runs of TC
+  // consecutive members, the last one partial.
+  int ng = 0;
+  {
+    const int f = (int)threadIdx.x;
+    const bool mine = f < p.F && group_of(p, f) == g;
+    const unsigned long long m = __ballot(mine);
+    if (lane == 0) s_wcnt[w] = __popcll(m);
+    __syncthreads();
+    int off = 0;
+    for (int v = 0; v < kGrpWaves; ++v) {
+      off += v < w ? s_wcnt[v] : 0;
+      ng += s_wcnt[v];
+    }
+    if (mine) s_order[off + __popcll(m & ((1ull << lane) - 1ull))] = f;
+    __syncthreads();
+  }
+  const int nteam = (ng + TC - 1) / TC;
   const int T = (int)p.T;
   float* ddrow = o.dd + (g * p.B + b) * T;
   if (nteam == 0) {
@@ -1635,10 +1657,8 @@ __global__ __launch_bounds__(kGrpWaves* kWave)
     }
     for (int qi = 0; qi < nteam; ++qi) {
       const int ch = qi * kGrpTC + cs;
-      const int team = team0 + qi;
-      const int members = tm.count[team];
-      if (cs >= members) continue;  // the whole channel slot sits this team out
-      const int64_t f = tm.order[tm.first[team] + cs];
+      if (ch >= ng) continue;  // the whole channel slot sits this (last) team out
+      const int64_t f = s_order[ch];
       const int64_t row = f * p.B + b;
       c = load_chan(p, f);
       const int64_t base = row * T;
@@ -1665,8 +1685,8 @@ __global__ __launch_bounds__(kGrpWaves* kWave)
         cc = s_pcf[ch];
       }
       // this channel's place in the group sum's order, and the last place
-      const int place = qi * kGrpTC + cs;
-      const int last = (nteam - 1) * kGrpTC + tm.count[team0 + nteam - 1] - 1;
+      const int place = ch;
+      const int last = ng - 1;
       for (int st = st_hi - 1; st >= st_lo; --st) {
         const int tile = st * kGrpTW + tw;
         const int t0 = tile * TILE;
@@ -1790,10 +1810,9 @@ __global__ __launch_bounds__(kGrpWaves* kWave)
   }
   __syncthreads();
   // Per-row fp64 partials of dbias and dtheta: the time slots in fixed order.
-  for (int i = (int)threadIdx.x; i < nteam * kGrpTC; i += NT) {
-    const int team = team0 + i / kGrpTC, m = i % kGrpTC;
-    if (m < tm.count[team]) {
-      const int64_t row = (int64_t)tm.order[tm.first[team] + m] * p.B + b;
+  for (int i = (int)threadIdx.x; i < ng; i += NT) {
+    {
+      const int64_t row = (int64_t)s_order[i] * p.B + b;
       double sb = 0.0, sth = 0.0;
 #pragma unroll
       for (int j = 0; j < kGrpTW; ++j) {
@@ -2098,25 +2117,56 @@ int split_teams(const rqf_selective_inputs* in) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(kMaxSplitTeams, q));
 }
 
+// Channel slots of the group form's blocks (4 x 3 or 3 x 4 wavefronts): the
+// shape that leaves fewer (time slot, channel slot) places idle, with the
+// group size taken as F / G (balanced groups).  RQF_BWD_GRP_TEAM=3|4 picks
+// one for tests and tuning.
+int group_team_size(const rqf_selective_inputs* in) {
+  if (const char* e = std::getenv("RQF_BWD_GRP_TEAM")) {
+    if (!std::strcmp(e, "3")) return 3;
+    if (!std::strcmp(e, "4")) return 4;
+  }
+  const int64_t ntiles = (in->T + kBwdTile - 1) / kBwdTile;
+  const int64_t n = std::max<int64_t>(1, in->F / std::max<int64_t>(1, in->G));
+  int64_t best_idle = -1;
+  int best = 4;
+  for (int tc : {4, 3}) {
+    const int64_t tw = kGrpWaves / tc;
+    const int64_t places = (ntiles + tw - 1) / tw * tw * ((n + tc - 1) / tc * tc);
+    // idle places per 10^4, so that the two shapes compare exactly
+    const int64_t idle = (places - ntiles * n) * 10000 / places;
+    if (best_idle < 0 || idle < best_idle) {
+      best_idle = idle;
+      best = tc;
+    }
+  }
+  return best;
+}
+
 // The group form of the backward needs the warp head and no group with more
-// channels than its LDS parks (F <= kGrpMaxChans).  It runs by default when
-// the (group, batch element) blocks give every CU one and the rows' last
-// super-tile is nearly full (at most 1/32 of the time slots idle): at config 3
-// (T = 16000, 63 tiles in 21 super-tiles) it measured 2.70 against 2.75 ms for
-// the split form, at config 4 (T = 4096, 16 tiles in 6 super-tiles, an eighth
-// of the slots idle) 0.73 / 0.69 against 0.74 / 0.64 ms.  The environment
-// variable RQF_BWD_FORM=group|split picks a form for tests and tuning; setting
-// RQF_BWD_SPLIT_TEAMS picks the split form.
-bool use_group_form(const rqf_selective_inputs* in) {
+// channels than its LDS parks (F <= kGrpMaxChans).  It runs by default on the
+// memory-heavier contract (with the activation's cotangent gx: 48 B per
+// element) when the (group, batch element) blocks give every CU one and its
+// chosen shape leaves at most 1/32 of the places idle.  Measured against the
+// split form: config 3 (T = 16000, teams of 4, 21 super-tiles of 3) 2.70
+// against 2.75 ms; config 4's layer 0 (T = 4096, teams of 3, 4 super-tiles
+// of 4) 0.711-0.715 against 0.738-0.743 ms.  Without gx (40 B per element)
+// the tiles' arithmetic dominates and the form's extra map composition costs
+// more than its overlap gains: config 4's layer 1 ran 0.695-0.702 against
+// 0.647-0.649 ms.  The environment variable RQF_BWD_FORM=group|split picks a
+// form for tests and tuning; setting RQF_BWD_SPLIT_TEAMS picks the split form.
+bool use_group_form(const rqf_selective_inputs* in, bool with_gx) {
   if (!RQF_BWD_TEAMS || !in->has_warp || in->F > kGrpMaxChans) return false;
   if (std::getenv("RQF_BWD_SPLIT_TEAMS")) return false;
   if (const char* e = std::getenv("RQF_BWD_FORM")) {
     if (!std::strcmp(e, "group")) return true;
     if (!std::strcmp(e, "split")) return false;
   }
+  const int tc = group_team_size(in), tw = kGrpWaves / tc;
   const int64_t ntiles = (in->T + kBwdTile - 1) / kBwdTile;
-  const int64_t nst = (ntiles + kGrpTW - 1) / kGrpTW;
-  return in->G * in->B >= kCus && (nst * kGrpTW - ntiles) * 32 <= ntiles;
+  const int64_t n = std::max<int64_t>(1, in->F / std::max<int64_t>(1, in->G));
+  const int64_t places = (ntiles + tw - 1) / tw * tw * ((n + tc - 1) / tc * tc);
+  return with_gx && in->G * in->B >= kCus && (places - ntiles * n) * 32 <= places;
 }
 
 struct SelWs {
@@ -2124,12 +2174,12 @@ struct SelWs {
   int slots, split_slots, Q, G, tsize;
   bool group_form;
 };
-SelWs sel_ws_layout(const rqf_selective_inputs* in, int64_t chunk) {
+SelWs sel_ws_layout(const rqf_selective_inputs* in, int64_t chunk, bool group_form) {
   SelWs w;
   const int64_t R = in->F * in->B;
   w.G = in->has_warp ? (int)in->G : 1;
-  w.group_form = use_group_form(in);
-  w.tsize = kTeam;
+  w.group_form = group_form;
+  w.tsize = w.group_form ? group_team_size(in) : kTeam;
   const int teams = (int)((in->F + w.tsize - 1) / w.tsize);
   w.slots = w.G + teams;  // teams of all groups <= ceil(F/tsize) + G
   w.Q = split_teams(in);
@@ -2140,7 +2190,8 @@ SelWs sel_ws_layout(const rqf_selective_inputs* in, int64_t chunk) {
   if (chunk > kBwdTile)
     off += round256(sizeof(float) * 2 * (size_t)R * ((in->T + kBwdTile - 1) / kBwdTile + 1));
   w.teams = off;
-  off += round256(sizeof(int) * (size_t)(in->F + 5 * w.slots + 4 * w.G + 4));
+  if (!w.group_form)  // the group form builds its channel lists in LDS
+    off += round256(sizeof(int) * (size_t)(in->F + 5 * w.slots + 4 * w.G + 4));
   w.dd = off;
 #if RQF_BWD_TEAMS
   if (in->has_warp && !w.group_form)
@@ -2155,7 +2206,9 @@ SelWs sel_ws_layout(const rqf_selective_inputs* in, int64_t chunk) {
 
 extern "C" size_t rqf_selective_bwd_workspace(const rqf_selective_inputs* in, int64_t chunk) {
   if (!in || in->F < 0 || in->B < 0 || in->T < 0) return 0;
-  return sel_ws_layout(in, chunk).total;
+  // enough for either form of the backward (the form depends on gx)
+  return std::max(sel_ws_layout(in, chunk, false).total,
+                  use_group_form(in, true) ? sel_ws_layout(in, chunk, true).total : size_t(0));
 }
 
 extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
@@ -2176,7 +2229,7 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
     if ((in->has_gamma && !dg) || (in->has_write && !dw) || (in->has_warp && !dd))
       return RQF_ERR_ARG;
   }
-  const SelWs w = sel_ws_layout(in, chunk);
+  const SelWs w = sel_ws_layout(in, chunk, use_group_form(in, gx != nullptr));
   if (workspace_bytes < w.total || (w.total && !workspace)) return RQF_ERR_WORKSPACE;
   if (!aligned8(z) || !aligned8(gy) || !aligned8(gx) || !aligned8(dz) || !aligned8(dzw))
     return RQF_ERR_ALIGN;
@@ -2206,6 +2259,30 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
     o.dd = nullptr;
     o.partial = partial;
 #if RQF_BWD_TEAMS
+    o.dd = in->has_warp ? dd : nullptr;
+    // The group form finds its group's channels itself: no team table.
+    if (w.group_form) {
+      const dim3 grid((unsigned)(in->G * in->B)), block(kGrpWaves * kWave);
+      with_option_set(options_of(in), [&](auto oc) {
+        constexpr int O = decltype(oc)::value;
+        if constexpr (O != kOptRuntime && !(O & kOptWarp)) {
+          return;  // not reached: the group form needs the warp head
+        } else {
+          auto go = [&](auto kern) {
+            hipLaunchKernelGGL(kern, grid, block, 0, s, *in, z, ent, ent_chunk, nc, gy, gx,
+                               (int)truncated, o);
+          };
+          if (w.tsize == 3)
+            vec ? go(selective_bwd_grp_kernel<O, true, 3>)
+                : go(selective_bwd_grp_kernel<O, false, 3>);
+          else
+            vec ? go(selective_bwd_grp_kernel<O, true, 4>)
+                : go(selective_bwd_grp_kernel<O, false, 4>);
+        }
+      });
+      launch_finish(nullptr, nullptr, nullptr, 0, 0, partial, dbias, dtheta, in->F, in->B, s);
+      return launch_status();
+    }
     int* order = (int*)(ws + w.teams);
     int* first = order + in->F;
     int* count = first + w.slots;
@@ -2234,24 +2311,6 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
     tm.nsplits = nsplits;
     tm.gteam = gteam;
     tm.slots = w.split_slots;
-    o.dd = in->has_warp ? dd : nullptr;
-    if (w.group_form) {
-      const dim3 grid((unsigned)(in->G * in->B)), block(kGrpWaves * kWave);
-      with_option_set(options_of(in), [&](auto oc) {
-        constexpr int O = decltype(oc)::value;
-        if constexpr (O != kOptRuntime && !(O & kOptWarp)) {
-          return;  // not reached: the group form needs the warp head
-        } else if (vec) {
-          hipLaunchKernelGGL((selective_bwd_grp_kernel<O, true>), grid, block, 0, s, *in, z, ent,
-                             ent_chunk, nc, gy, gx, (int)truncated, tm, o);
-        } else {
-          hipLaunchKernelGGL((selective_bwd_grp_kernel<O, false>), grid, block, 0, s, *in, z,
-                             ent, ent_chunk, nc, gy, gx, (int)truncated, tm, o);
-        }
-      });
-      launch_finish(nullptr, nullptr, nullptr, 0, 0, partial, dbias, dtheta, in->F, in->B, s);
-      return launch_status();
-    }
     o.dd_part = in->has_warp ? (float*)(ws + w.dd) : nullptr;
     const int64_t bc = (in->B + kXcds - 1) / kXcds;
     const dim3 grid((unsigned)(kXcds * w.split_slots * bc)), block(kTeam * kWave);

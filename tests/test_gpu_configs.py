@@ -113,10 +113,16 @@ def _config4_inputs(F, B, T, layer):
                                       seq_duration=4096.0, device="cuda", seed=layer)
 
 
-@pytest.mark.parametrize("F,B", [(16, 2), (256, 1)])
-def test_config4_two_layer_stack(F, B):
+@pytest.mark.parametrize("F,B,form", [(16, 2, None), (256, 1, None), (256, 1, "group")])
+def test_config4_two_layer_stack(monkeypatch, F, B, form):
+    """Both layers against the fp64 oracle chain.  B = 1 takes the split form
+    of the backward; forced into the group form, F = 256 in 4 groups of 64 at
+    T = 4096 picks the 3 x 4 block shape (16 tiles in 4 full super-tiles, 22
+    teams of 3), the shape the full config-4 grid runs."""
     T, chunk = 4096, 256
-    print(f"case: config 4 stack F={F} B={B} T={T}", flush=True)
+    print(f"case: config 4 stack F={F} B={B} T={T} form={form}", flush=True)
+    if form:
+        monkeypatch.setenv("RQF_BWD_FORM", form)
     rng = np.random.default_rng(4000 + F + B)
     ins = [_config4_inputs(F, B, T, layer) for layer in range(2)]
     assert ins[0].options[1] and ins[0].warp_logits.shape[0] == 4
@@ -295,15 +301,16 @@ def test_config3_team_layout(monkeypatch, form):
                 SELECTIVE_CHANNEL_RTOL)
 
 
-@pytest.mark.parametrize("form", ["group", "split"])
-def test_config3_full_shape_properties(monkeypatch, form):
-    """The full config-3 shape (B = 64) against small-batch calls on the same
-    rows, both in the same form of the backward: per-row outputs bit for bit,
-    warp-logit gradients to rounding (bit for bit in the group form; in the
-    split form the grid's split layout changes the order of the channel sum),
-    and dbias / dtheta as the fp64 sum over the small batches."""
-    F, B, T, chunk, SB = 256, 64, 16000, 256, 4
-    print(f"case: config 3 full shape B={B} vs {B // SB} calls of B={SB} form={form}",
+@pytest.mark.parametrize("cfg,form", [(3, "group"), (3, "split"), (4, "group"), (4, "split")])
+def test_full_shape_properties(monkeypatch, cfg, form):
+    """The full config-3 shape (B = 64), and config 4's layer 0 (T = 4096,
+    4 groups), against small-batch calls on the same rows, both in the same
+    form of the backward: per-row outputs bit for bit, warp-logit gradients to
+    rounding (bit for bit in the group form; in the split form the grid's split
+    layout changes the order of the channel sum), and dbias / dtheta as the
+    fp64 sum over the small batches."""
+    F, B, T, chunk, SB = 256, 64, (16000 if cfg == 3 else 4096), 256, 4
+    print(f"case: config {cfg} full shape B={B} vs {B // SB} calls of B={SB} form={form}",
           flush=True)
     monkeypatch.setenv("RQF_BWD_FORM", form)
     g = torch.Generator(device="cuda").manual_seed(33)
@@ -312,7 +319,7 @@ def test_config3_full_shape_properties(monkeypatch, form):
         return torch.complex(torch.randn(*shape, generator=g, device="cuda"),
                              torch.randn(*shape, generator=g, device="cuda"))
 
-    inp = _config3_inputs(B, T)
+    inp = _config3_inputs(B, T) if cfg == 3 else _config4_inputs(F, B, T, 0)
     z, gy, gx = cn(F, B, T), cn(F, B, T), cn(F, B, T)
     raw, act, ent = selective_forward(z, inp, True, True, chunk)
     full = selective_backward(z, inp, ent, gy, gx, True, False, chunk)

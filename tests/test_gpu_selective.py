@@ -285,15 +285,23 @@ def _empty_groups(inp, z):
     (20, 2, 4500, "grouped", 2, 256, False, None),
     (20, 3, 4500, "global", 1, 256, True, None),
     (9, 2, 2300, "grouped", 5, 256, False, _empty_groups),
+    # super-tiles of 4 tiles (1024 steps) in the 3 x 4 shape; T = 4096 fills 4
+    (6, 2, 1023, "grouped", 2, 256, True, None),
+    (6, 2, 1025, "grouped", 2, 256, False, None),
+    (7, 2, 4096, "grouped", 2, 256, False, None),
+    (7, 2, 4097, "grouped", 2, 256, True, None),
 ])
-def test_group_form(monkeypatch, F, B, T, warp, G, chunk, truncated, edit):
+@pytest.mark.parametrize("team", ["4", "3"])
+def test_group_form(monkeypatch, F, B, T, warp, G, chunk, truncated, edit, team):
     """The group form of the backward (one block per warp group and batch
     element; adjoint maps composed across the time slots of a super-tile, the
     group sum added channel after channel), forced at shapes whose grid would
-    pick the split form."""
+    pick the split form, in both block shapes: 4 channel slots x 3 time slots
+    (teams of 4) and 3 x 4 (teams of 3)."""
     print(f"case: group form F={F} B={B} T={T} warp={warp} G={G} chunk={chunk} "
-          f"truncated={truncated} edit={edit is not None}", flush=True)
+          f"truncated={truncated} edit={edit is not None} team={team}", flush=True)
     monkeypatch.setenv("RQF_BWD_FORM", "group")
+    monkeypatch.setenv("RQF_BWD_GRP_TEAM", team)
     run_case(F, B, T, dict(CASE_ALL, warp=warp), chunk=chunk, G=G, truncated=truncated,
              edit=edit, seed=F + T + chunk)
 
@@ -301,11 +309,14 @@ def test_group_form(monkeypatch, F, B, T, warp, G, chunk, truncated, edit):
 @pytest.mark.parametrize("truncated", [False, True])
 @pytest.mark.parametrize("prospective", [False, True])
 @pytest.mark.parametrize("case", [c for c in CASES if c["warp"] != "none"], ids=case_id)
-def test_group_form_controller_cases(monkeypatch, case, prospective, truncated):
-    """Every controller case with a warp head, through the group form."""
+@pytest.mark.parametrize("team", ["4", "3"])
+def test_group_form_controller_cases(monkeypatch, case, prospective, truncated, team):
+    """Every controller case with a warp head, through the group form in both
+    block shapes."""
     print(f"case: group form {case_id(case)} prospective={prospective} "
-          f"truncated={truncated}", flush=True)
+          f"truncated={truncated} team={team}", flush=True)
     monkeypatch.setenv("RQF_BWD_FORM", "group")
+    monkeypatch.setenv("RQF_BWD_GRP_TEAM", team)
     run_case(5, 2, 1100, case, prospective=prospective, truncated=truncated,
              gamma_horizon=prospective and case["gamma"] and not case["log_shift"],
              chunk=256, seed=len(case_id(case)) + 7)

@@ -956,7 +956,10 @@ def main():
     dom_bytes = plan.bytes[dom]
     achieved = dom_bytes / (per_op[dom] * 1e-3) / 1e9
     all_bytes = sum(plan.bytes.values())
-    traffic = (traffic_from_table(f"config{cfg}", entry)
+    # a per-layer row ("rqf_selective_bwd[L0]") where the table has one, else
+    # the entry point's
+    traffic = ((traffic_from_table(f"config{cfg}", dom) or
+                traffic_from_table(f"config{cfg}", entry))
                if not (args.batch or args.seq_len or args.stack != "none") else None)
     result = {
         "metric": METRIC,

@@ -112,10 +112,57 @@ __device__ __forceinline__ Lane lane_of(int64_t T, int64_t F) {
   return l;
 }
 
-// Inputs of the thread's segment [tb, tb + LS); zero outside [0, T).
+// Global memory goes through buffer descriptors (wave-uniform, in scalar
+// registers).  A Pass names steps [pt, min(T, pt + pass)) of the block's
+// batch element in one tensor; the descriptor of step j of every segment
+// starts j rows further and is j rows shorter, so all steps of a segment use
+// the lane's one byte offset: that of its segment's first step and its
+// filter, or kBufOut for a filter past F.  Steps past T and filters past F
+// then read zero and drop their stores with no test and no per-element
+// address arithmetic (the host keeps pass * F * 8 below 2^31).
+struct Pass {
+  const char* base;
+  int n;          // valid steps from base
+  uint32_t step;  // bytes per time step
+  // (a signed max, not a saturating subtraction of bytes: that has no scalar
+  // instruction, and a descriptor in vector registers costs a loop per access)
+  __device__ __forceinline__ brsrc at(int j) const {
+    return buf_rsrc(base + (uint32_t)j * step, (uint32_t)std::max(n - j, 0) * step);
+  }
+};
+__device__ __forceinline__ uint32_t lane_off(const Lane& l, int LS, int64_t F, int esz) {
+  return l.fv ? (uint32_t)(((int64_t)l.sg * LS * F + l.f) * esz) : kBufOut;
+}
+__device__ __forceinline__ Pass pass_of(const float* p, const Lane& l, int64_t pt, int64_t pass,
+                                        int64_t T, int64_t F, int esz) {
+  // Everything here is wave-uniform; readfirstlane pins it to scalar
+  // registers, which the descriptors need (a 64-bit compare or select the
+  // compiler does in vector registers would otherwise leave them there).
+  const uint64_t base =
+      reinterpret_cast<uint64_t>(p) + (uint64_t)((l.b * T + std::min(pt, T)) * F * esz);
+  Pass s;
+  s.base = reinterpret_cast<const char*>(
+      ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(base >> 32)) << 32) |
+      (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)base));
+  s.n = __builtin_amdgcn_readfirstlane((int)(pt < T ? std::min(T, pt + pass) - pt : 0));
+  s.step = (uint32_t)__builtin_amdgcn_readfirstlane((int)(F * esz));
+  return s;
+}
+
+// Inputs of the thread's segment (lane offset lo in pass s); zero past T and
+// for filters past F.
 template <int LS, bool REAL>
-__device__ __forceinline__ void load_seg(const float* __restrict__ p, const Lane& l, int64_t tb,
-                                         int64_t T, int64_t F, c32 (&v)[LS]) {
+__device__ __forceinline__ void load_seg(const Pass& s, uint32_t lo, c32 (&v)[LS]) {
+#pragma unroll
+  for (int j = 0; j < LS; ++j)
+    v[j] = REAL ? mk(buf_ldf(s.at(j), lo), 0.0f) : buf_ldc(s.at(j), lo);
+}
+// The same through global addresses with an explicit test, for the backward,
+// where the descriptors measured slower (0.47 -> 0.49 ms at config 6: three
+// streams of 8-step segments, a descriptor per step and stream).
+template <int LS, bool REAL>
+__device__ __forceinline__ void load_seg_g(const float* __restrict__ p, const Lane& l, int64_t tb,
+                                           int64_t T, int64_t F, c32 (&v)[LS]) {
 #pragma unroll
   for (int j = 0; j < LS; ++j) {
     const int64_t t = tb + j;
@@ -210,12 +257,14 @@ __global__ __launch_bounds__(W* kWave) void mosc_fwd_kernel(
     }
   }
   __syncthreads();
+  constexpr int kUs = REAL ? 4 : 8;
+  const uint32_t lo_u = lane_off(l, LS, F, kUs), lo_c = lane_off(l, LS, F, 8),
+                 lo_a = lane_off(l, LS, F, 4);
   c32 uv[LS], un[LS];
-  load_seg<LS, REAL>(u, l, (int64_t)l.sg * LS, T, F, uv);
+  load_seg<LS, REAL>(pass_of(u, l, 0, kPass, T, F, kUs), lo_u, uv);
   int p = 0;
   for (int64_t pt = 0; pt < T; pt += kPass) {
-    const int64_t tb = pt + (int64_t)l.sg * LS;
-    if (pt + kPass < T) load_seg<LS, REAL>(u, l, tb + kPass, T, F, un);
+    if (pt + kPass < T) load_seg<LS, REAL>(pass_of(u, l, pt + kPass, kPass, T, F, kUs), lo_u, un);
     // Each oscillator's segment from a zero state.
     c32 w[NP];
 #pragma unroll
@@ -255,6 +304,8 @@ __global__ __launch_bounds__(W* kWave) void mosc_fwd_kernel(
       w[n] = cmad(k.mq[l.q], cw_, w[n]);
     }
     // Replay and write.
+    const Pass sy = pass_of(yout, l, pt, kPass, T, F, ABS ? 4 : 8);
+    const Pass si = pass_of(yin ? yin : yout, l, pt, kPass, T, F, 8);
 #pragma unroll
     for (int j = 0; j < LS; ++j) {
       c32 y = mk(0.0f, 0.0f);
@@ -263,15 +314,11 @@ __global__ __launch_bounds__(W* kWave) void mosc_fwd_kernel(
         w[n] = REAL ? cmadr(a[n], w[n], uv[j].r) : cmad(a[n], w[n], uv[j]);
         if (CW || n == 0) y = cmad(hw[n], w[n], y);
       }
-      const int64_t t = tb + j;
-      if (l.fv && t < T) {
-        const int64_t e = l.base + t * F;
-        if (yin) y = cadd(y, ldc(yin, e));
-        if (ABS)
-          yout[e] = sqrtf(fmaf(y.r, y.r, y.i * y.i));
-        else
-          stc(yout, e, y);
-      }
+      if (yin) y = cadd(y, buf_ldc(si.at(j), lo_c));
+      if (ABS)
+        buf_stf(sy.at(j), lo_a, sqrtf(fmaf(y.r, y.r, y.i * y.i)));
+      else
+        buf_stc(sy.at(j), lo_c, y);
     }
 #pragma unroll
     for (int j = 0; j < LS; ++j) uv[j] = un[j];
@@ -381,13 +428,13 @@ __global__ __launch_bounds__(kThreads) void mosc_bwd_kernel(
   const int64_t npass = (T + kPass - 1) / kPass;
   c32 gv[LS], gn[LS], uv[TAN ? LS : 1], un[TAN ? LS : 1];
   int64_t pt = (npass - 1) * kPass;
-  load_seg<LS, false>(gy, l, pt + (int64_t)l.sg * LS, T, F, gv);
-  if constexpr (TAN) load_seg<LS, REAL>(u, l, pt + (int64_t)l.sg * LS, T, F, uv);
+  load_seg_g<LS, false>(gy, l, pt + (int64_t)l.sg * LS, T, F, gv);
+  if constexpr (TAN) load_seg_g<LS, REAL>(u, l, pt + (int64_t)l.sg * LS, T, F, uv);
   for (; pt >= 0; pt -= kPass) {
     const int64_t tb = pt + (int64_t)l.sg * LS;
     if (pt > 0) {
-      load_seg<LS, false>(gy, l, tb - kPass, T, F, gn);
-      if constexpr (TAN) load_seg<LS, REAL>(u, l, tb - kPass, T, F, un);
+      load_seg_g<LS, false>(gy, l, tb - kPass, T, F, gn);
+      if constexpr (TAN) load_seg_g<LS, REAL>(u, l, tb - kPass, T, F, un);
     }
     // Each oscillator's pair at the segment's first step from a zero pair.
     c32 e[NP], f[NP];
@@ -482,11 +529,10 @@ __global__ __launch_bounds__(kThreads) void mosc_bwd_kernel(
         const int64_t t = tb + j;
         if (l.fv && t < T) {
           const int64_t el = l.base + t * F;
-          if (REAL) {
+          if (REAL)
             gu[el] = go[j].r + (gin ? gin[el] : 0.0f);
-          } else {
+          else
             stc(gu, el, gin ? cadd(go[j], ldc(gin, el)) : go[j]);
-          }
         }
       }
     }
@@ -580,8 +626,11 @@ int pad_osc(int N) {
 
 dim3 mosc_grid(int64_t B, int64_t F) { return dim3((unsigned)(B * ((F + kFC - 1) / kFC))); }
 
+// F <= kMaxFilters keeps every pass's descriptor (at most 2048 steps of F
+// complex elements) below 2^31 bytes.
+constexpr int64_t kMaxFilters = 65536;
 bool bad_shape(int64_t B, int64_t T, int64_t F, int64_t N) {
-  return B < 0 || T < 0 || F < 0 || N < 1 || N > (int64_t)1 << 20;
+  return B < 0 || T < 0 || F < 0 || F > kMaxFilters || N < 1 || N > (int64_t)1 << 20;
 }
 
 // Workspace: forward, a complex (B,T,F) partial when a |y| output needs more
@@ -606,8 +655,10 @@ void launch_fwd(const float* c1, const float* c2, const float* cw, const float* 
                 const float* yin, float* yout, bool abs_out, int64_t B, int64_t T, int64_t F,
                 int N, int n0, hipStream_t s) {
   // 16 wavefronts per block where the kernel fits in 128 VGPRs (real input;
-  // without C-weights, which only one oscillator has, at most two), else 8.
-  constexpr int W = REAL ? 16 : 8, W1 = REAL && NP <= 2 ? 16 : 8;
+  // without C-weights, which only one oscillator has, at most two), 12 where
+  // it fits in 168 (complex input, 4 oscillators: 0.271 -> 0.250 ms at
+  // config 6), else 8.
+  constexpr int W = REAL ? 16 : (NP == 4 ? 12 : 8), W1 = REAL && NP <= 2 ? 16 : 8;
   const dim3 grid = mosc_grid(B, F), block(W * kWave), block1(W1 * kWave);
   if (cw && abs_out)
     hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, true, true, W>), grid, block, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);

@@ -125,6 +125,43 @@ __device__ __forceinline__ int64_t xcd_contiguous(int64_t P, int64_t n) {
 }
 
 // ---------------------------------------------------------------------------
+// Raw buffer access: CDNA buffer instructions through a resource descriptor
+// (base, size in bytes).  A load at a byte offset at or past the size returns
+// zero and a store there is dropped, by the hardware's range check.  A
+// streamed (B,T,F) pass takes its bounds (steps past the end of the sequence,
+// filters past F) from the descriptor instead of a compare, a branch and a
+// 64-bit address per element.  Offsets are 32-bit, passed whole as the vector
+// offset; the scalar offset operand is always 0.
+// ---------------------------------------------------------------------------
+using brsrc = __amdgpu_buffer_rsrc_t;
+constexpr int kBufWord3 = 0x00020000;       // descriptor word 3 on gfx9 (32-bit data format)
+constexpr uint32_t kBufOut = 0x80000000u;  // a lane offset past every resource made here
+__device__ __forceinline__ brsrc buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufWord3);
+}
+__device__ __forceinline__ float buf_ldf(brsrc r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ void buf_stf(brsrc r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, (int)off, 0, 0);
+}
+// The 64-bit forms move a complex value as one <2 x float>: with the two
+// 32-bit halves taken out of the loaded vector one by one, this compiler
+// narrowed the load to its first dword and returned (re, re).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32v2 __attribute__((vector_size(8)));
+__device__ __forceinline__ c32 buf_ldc(brsrc r, uint32_t off) {
+  const f32x2 v = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+  return mk(v.x, v.y);
+}
+__device__ __forceinline__ void buf_stc(brsrc r, uint32_t off, c32 v) {
+  f32x2 w;
+  w.x = v.r;
+  w.y = v.i;
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32v2, w), r, (int)off, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
 // Cross-lane primitives
 // ---------------------------------------------------------------------------
 

@@ -130,3 +130,17 @@ def test_noalloc_rejects_oversized_problems_before_any_device_call(built_lib):
     assert lib.rqf_fbt_recompute_bwd_noalloc(*args, 2 ** 40, 2 ** 40, 16,
                                              None) == _lib.ERR_SCRATCH
     assert lib.rqf_fbt_recompute_bwd_noalloc(*args, -1, 1, 16, None) == -1
+
+
+def test_multi_osc_rejects_more_filters_than_one_buffer_range(built_lib):
+    """The multi-oscillator entry points address each pass of the sequence
+    (up to 2048 steps of F complex values) through one 32-bit buffer range, so
+    F is limited to 65536: beyond it they return RQF_ERR_ARG (-1; and the
+    workspace query 0) before looking at a pointer or calling HIP."""
+    lib = _lib.load()
+    assert lib.rqf_multi_osc_workspace(2, 100, 65537, 4, 1) == 0
+    assert lib.rqf_multi_osc_workspace(2, 100, 65536, 4, 1) > 0
+    assert lib.rqf_multi_osc_fwd(None, None, None, None, 0, None, 0, 2, 100, 65537, 4, None, 0,
+                                 None) == -1
+    assert lib.rqf_multi_osc_bwd(None, None, None, None, 0, None, None, None, None, None, 2, 100,
+                                 65537, 4, None, 0, None) == -1

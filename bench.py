@@ -316,10 +316,11 @@ def plan_selective(cfg, args, dev):
         nbytes[f"rqf_selective_bwd[L{li}]"] = bb
     kernels = {
         "rqf_selective_fwd": "selective_fwd_rb_kernel",
-        "rqf_selective_bwd": ("team_build_kernel + selective_bwd_grp_kernel (group form: "
+        "rqf_selective_bwd": ("selective_bwd_grp_kernel + bwd_finish_kernel (group form: "
                               "G*B >= 256, nearly full super-tiles and a gx cotangent, e.g. "
-                              "config 3 and config 4's layer 0) or selective_bwd_team_kernel "
-                              "(split form, e.g. config 4's layer 1) + bwd_finish_kernel"),
+                              "config 3 and config 4's layer 0), or team_build_kernel + "
+                              "selective_bwd_team_kernel + bwd_finish_kernel (split form, e.g. "
+                              "config 4's layer 1)"),
     }
     if stack != "none":
         contract += f"; encoder residual add (raw + h, act + h) {stack}"

@@ -1495,7 +1495,7 @@ __global__ __launch_bounds__(kTeam* kWave)
 // lists its group's channels itself from `groups` (no team table, no launch
 // before it).  The block
 // is TC x TW = 12 wavefronts, TC channel slots (one team of TC channels) times
-// TW time slots, and walks the rows backwards in super-tiles of TW consecutive
+// TW time slots (6 x 2, 4 x 3 or 3 x 4), and walks the rows backwards in super-tiles of TW consecutive
 // tiles, time slot w taking tile w of each, so that concurrent
 // wavefronts stream adjacent stretches of every row.  A wavefront replays its
 // tile's forward from the stored entry state (entries are kept per tile),
@@ -1514,10 +1514,9 @@ __global__ __launch_bounds__(kTeam* kWave)
 // block barriers per super-tile the 12 wavefronts moved in lockstep: 2.84
 // against 2.78 ms for the split form at config 3.)  Warp values are staged
 // per segment of 12 tiles for all teams, behind block barriers; each
-// channel's carry and fp64 sums are parked in LDS between segments.  Two
-// shapes: 4 x 3 (teams of 4) and 3 x 4 (teams of 3), whichever leaves fewer
-// slots idle at the row length and group size (T = 4096: 16 tiles fill four
-// super-tiles of 4 but leave 2 of 18 slots idle in super-tiles of 3).
+// channel's carry and fp64 sums are parked in LDS between segments.  Three
+// shapes: 6 x 2, 4 x 3 and 3 x 4 (teams of 6, 4 or 3), chosen by the places
+// they leave idle at the row length and group size (group_team_size).
 //
 // Every wait is bounded: one that runs out sets a flag that ends every other
 // wait of the block at once, and the block then writes NaN for its channels'
@@ -2117,20 +2116,26 @@ int split_teams(const rqf_selective_inputs* in) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(kMaxSplitTeams, q));
 }
 
-// Channel slots of the group form's blocks (4 x 3 or 3 x 4 wavefronts): the
-// shape that leaves fewer (time slot, channel slot) places idle, with the
-// group size taken as F / G (balanced groups).  RQF_BWD_GRP_TEAM=3|4 picks
-// one for tests and tuning.
+// Channel slots of the group form's blocks (6 x 2, 4 x 3 or 3 x 4
+// wavefronts): the shape that leaves the fewest (time slot, channel slot)
+// places idle, with the group size taken as F / G (balanced groups); on a tie
+// the one with more channel slots, whose tiles compose fewer maps.  At config
+// 4's layer 0 (16 tiles, 64 channels per group: 3 x 4 and 6 x 2 both leave 2
+// of 66 channel places idle) 6 x 2 measured 0.690 against 0.725 ms; at config
+// 3 (63 tiles, 32 channels) 4 x 3 leaves none idle and measured 2.73 against
+// 2.78 ms for 6 x 2.  (2 x 6 spills registers: 0.745 ms at config 4.)
+// RQF_BWD_GRP_TEAM=3|4|6 picks one for tests and tuning.
 int group_team_size(const rqf_selective_inputs* in) {
   if (const char* e = std::getenv("RQF_BWD_GRP_TEAM")) {
     if (!std::strcmp(e, "3")) return 3;
     if (!std::strcmp(e, "4")) return 4;
+    if (!std::strcmp(e, "6")) return 6;
   }
   const int64_t ntiles = (in->T + kBwdTile - 1) / kBwdTile;
   const int64_t n = std::max<int64_t>(1, in->F / std::max<int64_t>(1, in->G));
   int64_t best_idle = -1;
   int best = 4;
-  for (int tc : {4, 3}) {
+  for (int tc : {6, 4, 3}) {
     const int64_t tw = kGrpWaves / tc;
     const int64_t places = (ntiles + tw - 1) / tw * tw * ((n + tc - 1) / tc * tc);
     // idle places per 10^4, so that the two shapes compare exactly
@@ -2275,6 +2280,9 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
           if (w.tsize == 3)
             vec ? go(selective_bwd_grp_kernel<O, true, 3>)
                 : go(selective_bwd_grp_kernel<O, false, 3>);
+          else if (w.tsize == 6)
+            vec ? go(selective_bwd_grp_kernel<O, true, 6>)
+                : go(selective_bwd_grp_kernel<O, false, 6>);
           else
             vec ? go(selective_bwd_grp_kernel<O, true, 4>)
                 : go(selective_bwd_grp_kernel<O, false, 4>);

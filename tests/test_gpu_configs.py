@@ -117,8 +117,8 @@ def _config4_inputs(F, B, T, layer):
 def test_config4_two_layer_stack(monkeypatch, F, B, form):
     """Both layers against the fp64 oracle chain.  B = 1 takes the split form
     of the backward; forced into the group form, F = 256 in 4 groups of 64 at
-    T = 4096 picks the 3 x 4 block shape (16 tiles in 4 full super-tiles, 22
-    teams of 3), the shape the full config-4 grid runs."""
+    T = 4096 picks the 6 x 2 block shape (16 tiles in 8 full super-tiles, 11
+    teams of 6), the shape the full config-4 grid runs for layer 0."""
     T, chunk = 4096, 256
     print(f"case: config 4 stack F={F} B={B} T={T} form={form}", flush=True)
     if form:

@@ -285,19 +285,20 @@ def _empty_groups(inp, z):
     (20, 2, 4500, "grouped", 2, 256, False, None),
     (20, 3, 4500, "global", 1, 256, True, None),
     (9, 2, 2300, "grouped", 5, 256, False, _empty_groups),
-    # super-tiles of 4 tiles (1024 steps) in the 3 x 4 shape; T = 4096 fills 4
+    # super-tiles of 4 tiles (1024 steps) in the 3 x 4 shape, 2 (512) in 6 x 2;
+    # T = 4096 fills them
     (6, 2, 1023, "grouped", 2, 256, True, None),
     (6, 2, 1025, "grouped", 2, 256, False, None),
     (7, 2, 4096, "grouped", 2, 256, False, None),
     (7, 2, 4097, "grouped", 2, 256, True, None),
 ])
-@pytest.mark.parametrize("team", ["4", "3"])
+@pytest.mark.parametrize("team", ["4", "3", "6"])
 def test_group_form(monkeypatch, F, B, T, warp, G, chunk, truncated, edit, team):
     """The group form of the backward (one block per warp group and batch
     element; adjoint maps composed across the time slots of a super-tile, the
     group sum added channel after channel), forced at shapes whose grid would
-    pick the split form, in both block shapes: 4 channel slots x 3 time slots
-    (teams of 4) and 3 x 4 (teams of 3)."""
+    pick the split form, in every block shape: 4 channel slots x 3 time slots
+    (teams of 4), 3 x 4 (teams of 3) and 6 x 2 (teams of 6)."""
     print(f"case: group form F={F} B={B} T={T} warp={warp} G={G} chunk={chunk} "
           f"truncated={truncated} edit={edit is not None} team={team}", flush=True)
     monkeypatch.setenv("RQF_BWD_FORM", "group")
@@ -309,7 +310,7 @@ def test_group_form(monkeypatch, F, B, T, warp, G, chunk, truncated, edit, team)
 @pytest.mark.parametrize("truncated", [False, True])
 @pytest.mark.parametrize("prospective", [False, True])
 @pytest.mark.parametrize("case", [c for c in CASES if c["warp"] != "none"], ids=case_id)
-@pytest.mark.parametrize("team", ["4", "3"])
+@pytest.mark.parametrize("team", ["4", "3", "6"])
 def test_group_form_controller_cases(monkeypatch, case, prospective, truncated, team):
     """Every controller case with a warp head, through the group form in both
     block shapes."""

@@ -317,10 +317,9 @@ def plan_selective(cfg, args, dev):
     kernels = {
         "rqf_selective_fwd": "selective_fwd_rb_kernel",
         "rqf_selective_bwd": ("selective_bwd_grp_kernel + bwd_finish_kernel (group form: "
-                              "G*B >= 256, nearly full super-tiles and a gx cotangent, e.g. "
-                              "config 3 and config 4's layer 0), or team_build_kernel + "
-                              "selective_bwd_team_kernel + bwd_finish_kernel (split form, e.g. "
-                              "config 4's layer 1)"),
+                              "G*B >= 256, nearly full super-tiles, and a gx cotangent or the "
+                              "6x2 block shape: configs 3 and 4), else team_build_kernel + "
+                              "selective_bwd_team_kernel + bwd_finish_kernel (split form)"),
     }
     if stack != "none":
         contract += f"; encoder residual add (raw + h, act + h) {stack}"

@@ -2149,17 +2149,19 @@ int group_team_size(const rqf_selective_inputs* in) {
 }
 
 // The group form of the backward needs the warp head and no group with more
-// channels than its LDS parks (F <= kGrpMaxChans).  It runs by default on the
-// memory-heavier contract (with the activation's cotangent gx: 48 B per
-// element) when the (group, batch element) blocks give every CU one and its
-// chosen shape leaves at most 1/32 of the places idle.  Measured against the
-// split form: config 3 (T = 16000, teams of 4, 21 super-tiles of 3) 2.70
-// against 2.75 ms; config 4's layer 0 (T = 4096, teams of 3, 4 super-tiles
-// of 4) 0.711-0.715 against 0.738-0.743 ms.  Without gx (40 B per element)
-// the tiles' arithmetic dominates and the form's extra map composition costs
-// more than its overlap gains: config 4's layer 1 ran 0.695-0.702 against
-// 0.647-0.649 ms.  The environment variable RQF_BWD_FORM=group|split picks a
-// form for tests and tuning; setting RQF_BWD_SPLIT_TEAMS picks the split form.
+// channels than its LDS parks (F <= kGrpMaxChans).  It runs by default when
+// the (group, batch element) blocks give every CU one and its chosen shape
+// leaves at most 1/32 of the places idle, on the memory-heavier contract
+// (with the activation's cotangent gx: 48 B per element) or in the 6 x 2
+// shape.  Without gx (40 B per element) the tiles' arithmetic dominates, and
+// composing 3 or 4 tiles' maps costs more than the form's overlap gains.
+// Measured against the split form (ms): config 3's shape, 4 x 3, with gx
+// 2.70-2.75 against 2.75-2.79, without gx 2.58 against 2.52-2.55; config 4's
+// layer 0 (gx) 0.686-0.690 in 6 x 2 against 0.738-0.743; its layer 1 (no gx)
+// 0.651-0.653 in 6 x 2 against 0.667, and 0.695-0.702 in 3 x 4 against
+// 0.647-0.649 (another box).  The environment variable RQF_BWD_FORM=group|split
+// picks a form for tests and tuning; setting RQF_BWD_SPLIT_TEAMS picks the
+// split form.
 bool use_group_form(const rqf_selective_inputs* in, bool with_gx) {
   if (!RQF_BWD_TEAMS || !in->has_warp || in->F > kGrpMaxChans) return false;
   if (std::getenv("RQF_BWD_SPLIT_TEAMS")) return false;
@@ -2171,7 +2173,7 @@ bool use_group_form(const rqf_selective_inputs* in, bool with_gx) {
   const int64_t ntiles = (in->T + kBwdTile - 1) / kBwdTile;
   const int64_t n = std::max<int64_t>(1, in->F / std::max<int64_t>(1, in->G));
   const int64_t places = (ntiles + tw - 1) / tw * tw * ((n + tc - 1) / tc * tc);
-  return with_gx && in->G * in->B >= kCus && (places - ntiles * n) * 32 <= places;
+  return (with_gx || tc == 6) && in->G * in->B >= kCus && (places - ntiles * n) * 32 <= places;
 }
 
 struct SelWs {

@@ -582,21 +582,32 @@ __global__ __launch_bounds__(kRowsPerBlock* kWave)
 // row per wavefront (K = 4); row blocks of 2 / 4 / 8 / 16 waves: 1.765 /
 // 1.729 / 1.688 / - (K = 4), 8 waves with K = 8: 1.644, 16 waves with K = 8:
 // 1.753, 4 waves with K = 16: 1.701; without the LDS transpose 1.837.
+// Calls that write raw only (24 B per element instead of 32) run blocks of
+// kFwdRbWavesRaw = 4 wavefronts: their arithmetic weighs more against their
+// streams, and twice as many independent blocks per CU overlap one block's
+// barrier and replay with another's loads.  Config 4 (T = 4096, K = 8),
+// measured on one box: raw-only layer 1 0.352 -> 0.320 ms with 4 waves;
+// raw+act layer 0 0.403 ms with 8 against 0.425 with 4, config 3 1.668
+// against 1.718.
 #ifndef RQF_FWD_ROWBLOCK
 #define RQF_FWD_ROWBLOCK 1
 #endif
 #ifndef RQF_FWD_RB_WAVES
 #define RQF_FWD_RB_WAVES 8
 #endif
+#ifndef RQF_FWD_RB_WAVES_RAW
+#define RQF_FWD_RB_WAVES_RAW 4
+#endif
 constexpr int kFwdRbWaves = RQF_FWD_RB_WAVES;
+constexpr int kFwdRbWavesRaw = RQF_FWD_RB_WAVES_RAW;
 
-template <int O, bool VEC>
-__global__ __launch_bounds__(kFwdRbWaves* kWave)
+template <int O, bool VEC, int W>
+__global__ __launch_bounds__(W* kWave)
     __attribute__((amdgpu_waves_per_eu(RQF_FWD_WAVES_PER_EU))) void selective_fwd_rb_kernel(
     const rqf_selective_inputs pin, const float* __restrict__ z, const float* __restrict__ skip,
     float* __restrict__ raw, float* __restrict__ act, float* __restrict__ entries, int chunk,
     int nc) {
-  constexpr int K = kFwdK, TILE = kWave * K, W = kFwdRbWaves;
+  constexpr int K = kFwdK, TILE = kWave * K;
   const rqf_selective_inputs p = with_options<O>(pin);
 #if RQF_FWD_LDS_IO
   __shared__ float4 s_io[W][TILE / 2];
@@ -2040,19 +2051,40 @@ void with_option_set(int opts, Fn&& fn) {
   }
 }
 
+// Forward block size: kFwdRbWavesRaw wavefronts for calls that stream only z,
+// the logits and raw; kFwdRbWaves when act or a skip tensor adds streams.
+// RQF_FWD_WAVES=narrow|wide forces one (tests and tuning).
+bool fwd_narrow_blocks(bool extra_streams) {
+  if (const char* e = std::getenv("RQF_FWD_WAVES")) {
+    if (!std::strcmp(e, "narrow")) return true;
+    if (!std::strcmp(e, "wide")) return false;
+  }
+  return !extra_streams;
+}
+
 void launch_fwd(const rqf_selective_inputs* in, const float* z, const float* skip, float* raw,
                 float* act, float* entries, int chunk, int nc, bool vec, hipStream_t s) {
   if (RQF_FWD_ROWBLOCK) {
     const dim3 grid((unsigned)(kXcds * in->F * ((in->B + kXcds - 1) / kXcds)));
-    const dim3 block(kFwdRbWaves * kWave);
+    const bool narrow = fwd_narrow_blocks(act != nullptr || skip != nullptr);
+    const dim3 block((narrow ? kFwdRbWavesRaw : kFwdRbWaves) * kWave);
     with_option_set(options_of(in), [&](auto oc) {
       constexpr int O = decltype(oc)::value;
-      if (vec)
-        hipLaunchKernelGGL((selective_fwd_rb_kernel<O, true>), grid, block, 0, s, *in, z, skip,
-                           raw, act, entries, chunk, nc);
-      else
-        hipLaunchKernelGGL((selective_fwd_rb_kernel<O, false>), grid, block, 0, s, *in, z, skip,
-                           raw, act, entries, chunk, nc);
+      if (narrow) {
+        if (vec)
+          hipLaunchKernelGGL((selective_fwd_rb_kernel<O, true, kFwdRbWavesRaw>), grid, block, 0,
+                             s, *in, z, skip, raw, act, entries, chunk, nc);
+        else
+          hipLaunchKernelGGL((selective_fwd_rb_kernel<O, false, kFwdRbWavesRaw>), grid, block, 0,
+                             s, *in, z, skip, raw, act, entries, chunk, nc);
+      } else {
+        if (vec)
+          hipLaunchKernelGGL((selective_fwd_rb_kernel<O, true, kFwdRbWaves>), grid, block, 0, s,
+                             *in, z, skip, raw, act, entries, chunk, nc);
+        else
+          hipLaunchKernelGGL((selective_fwd_rb_kernel<O, false, kFwdRbWaves>), grid, block, 0,
+                             s, *in, z, skip, raw, act, entries, chunk, nc);
+      }
     });
     return;
   }

@@ -144,6 +144,18 @@ def test_automatic_and_large_chunks(T, chunk, truncated):
     run_case(4, 3, T, CASE_LOG, truncated=truncated, chunk=chunk, seed=T + chunk)
 
 
+@pytest.mark.parametrize("outputs", [(False, True), (True, True)])
+@pytest.mark.parametrize("T", [511, 2047, 2048, 2049, 4096, 4097, 6000])
+@pytest.mark.parametrize("blocks", ["narrow", "wide"])
+def test_forward_block_sizes(monkeypatch, blocks, T, outputs):
+    """Both forward row-block sizes (4 and 8 wavefronts, super-tiles of 2048 and
+    4096 steps) under both output contracts, across super-tile edges."""
+    print(f"case: blocks={blocks} T={T} outputs={outputs}", flush=True)
+    monkeypatch.setenv("RQF_FWD_WAVES", blocks)
+    run_case(3, 2, T, CASE_ALL, activate=outputs[0], write_raw=outputs[1], chunk=256,
+             seed=T + len(blocks))
+
+
 @pytest.mark.parametrize("prospective,truncated", [(False, False), (True, True), (True, False)])
 @pytest.mark.parametrize("maximum,saturated", [(1.25, False), (3.0, True)])
 def test_sigmoid_write_bound_and_saturation(prospective, truncated, maximum, saturated):

@@ -143,6 +143,7 @@ constexpr int kOptSets[] = {
 struct Chan {
   float bias, theta, lo, span, inv_span, eta, horizon, thlo, thhi, inv_theta;
   float inv_write_max, inv_gamma_scale;
+  float thlo_m;  // min(thlo, thhi): the band clamp's median bound
 };
 
 // Warp group of channel f, a row of warp_logits.  The documented precondition
@@ -167,6 +168,7 @@ __device__ __forceinline__ Chan load_chan(const rqf_selective_inputs& p, int64_t
   c.horizon = p.horizon[f];
   c.thlo = p.theta_minimum[f];
   c.thhi = p.theta_maximum[f];
+  c.thlo_m = fminf(c.thlo, c.thhi);
   c.inv_theta = 1.0f / c.theta;
   c.inv_write_max = 1.0f / p.write_max;
   c.inv_gamma_scale = 1.0f / p.gamma_scale;
@@ -211,8 +213,11 @@ __device__ __forceinline__ Ctl controller(const rqf_selective_inputs& p, const C
 }
 
 // The band clamp applies to the warped frequency only (selective_scan_kernel.py:59-64).
+// As one v_med3_f32: med3(th, min(lo, hi), hi) = min(max(th, lo), hi) for
+// every non-NaN th, inverted bounds included (both give hi).  fminf/fmaxf of a
+// loaded bound would also quiet it for NaN semantics on every step.
 __device__ __forceinline__ float clamp_theta(const rqf_selective_inputs& p, const Chan& c, float th) {
-  return p.has_warp && p.bound_warp ? fminf(fmaxf(th, c.thlo), c.thhi) : th;
+  return p.has_warp && p.bound_warp ? __builtin_amdgcn_fmed3f(th, c.thlo_m, c.thhi) : th;
 }
 
 // ratio * gamma of the prospective tap: 1 in gamma-horizon mode (ratio = 1/gamma).
@@ -1524,7 +1529,7 @@ __global__ __launch_bounds__(kTeam* kWave)
 // overlap each other's arithmetic, as independent blocks would.  (With two
 // block barriers per super-tile the 12 wavefronts moved in lockstep: 2.84
 // against 2.78 ms for the split form at config 3.)  Warp values are staged
-// per segment of 12 tiles for all teams, behind block barriers; each
+// per segment of kGrpSegTiles tiles for all teams, behind block barriers; each
 // channel's carry and fp64 sums are parked in LDS between segments.  Three
 // shapes: 6 x 2, 4 x 3 and 3 x 4 (teams of 6, 4 or 3), chosen by the places
 // they leave idle at the row length and group size (group_team_size).
@@ -1537,7 +1542,14 @@ __global__ __launch_bounds__(kTeam* kWave)
 // so none of them is circular.
 // ---------------------------------------------------------------------------
 constexpr int kGrpWaves = 12;      // channel slots x time slots
-constexpr int kGrpSegTiles = 12;   // tiles per staged segment
+// Segments of 24 tiles (6144 steps): config 3 rows restage 3 times instead of
+// 6, config 4 rows (16 tiles) never.  Measured on one box, alternating builds:
+// config 3 backward 2.687-2.694 -> 2.670-2.671 ms, config 4 layer 1
+// 0.623-0.625 -> 0.606 ms; 36 tiles measured the same as 24 with 40% more LDS.
+#ifndef RQF_GRP_SEG_TILES
+#define RQF_GRP_SEG_TILES 24
+#endif
+constexpr int kGrpSegTiles = RQF_GRP_SEG_TILES;  // tiles per staged segment
 constexpr int kGrpMaxChans = 256;  // channels of one group whose state LDS parks
 constexpr int kGrpSpins = 1 << 20;  // bound on one wait (tens of ms)
 

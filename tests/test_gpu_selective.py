@@ -281,20 +281,25 @@ def _empty_groups(inp, z):
     (5, 2, 33, "grouped", 3, 32, True, None),
     (5, 2, 256, "grouped", 3, 256, False, None),
     (5, 2, 257, "grouped", 3, 256, True, None),
-    # super-tile and segment edges (a super-tile is 768 steps, a segment 3072);
-    # odd T runs the unvectorised loads
+    # super-tile and segment edges (in the 4 x 3 shape a super-tile is 768
+    # steps, a segment 24 tiles = 6144); odd T runs the unvectorised loads
     (6, 2, 767, "grouped", 2, 256, False, None),
     (6, 2, 768, "grouped", 2, 256, True, None),
     (6, 2, 1000, "global", 1, 256, False, None),
     (6, 2, 3072, "grouped", 2, 256, False, None),
     (6, 2, 3073, "grouped", 2, 256, True, None),
+    (6, 2, 6143, "grouped", 2, 256, True, None),
+    (6, 2, 6144, "grouped", 2, 256, False, None),
+    (6, 2, 6145, "grouped", 2, 256, True, None),
     (6, 2, 6999, "grouped", 2, 256, False, None),
+    (5, 2, 12289, "grouped", 2, 256, False, None),
     # entry states every 4 steps, and per-tile entries rebuilt from 1024-step chunks
     (6, 2, 2000, "grouped", 2, 4, False, None),
     (6, 2, 3000, "grouped", 2, 1024, True, None),
-    # 10 channels per group (teams of 4, 4 and 2) over two segments; global warp
-    # with 5 teams; two groups without channels
+    # 10 channels per group (teams of 4, 4 and 2) over one and two segments;
+    # global warp with 5 teams; two groups without channels
     (20, 2, 4500, "grouped", 2, 256, False, None),
+    (20, 2, 7000, "grouped", 2, 256, True, None),
     (20, 3, 4500, "global", 1, 256, True, None),
     (9, 2, 2300, "grouped", 5, 256, False, _empty_groups),
     # super-tiles of 4 tiles (1024 steps) in the 3 x 4 shape, 2 (512) in 6 x 2;

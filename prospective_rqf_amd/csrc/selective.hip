@@ -1577,7 +1577,7 @@ __global__ __launch_bounds__(kGrpWaves* kWave)
     __attribute__((amdgpu_waves_per_eu(RQF_BWD_WAVES_PER_EU))) void selective_bwd_grp_kernel(
         const rqf_selective_inputs pin, const float* __restrict__ z,
         const float* __restrict__ entries, int chunk, int nc, const float* __restrict__ gy,
-        const float* __restrict__ gx, int truncated, BwdOut o) {
+        const float* __restrict__ gx, int truncated, BwdOut o, int abort0) {
   const rqf_selective_inputs p = with_options<O>(pin);
   constexpr int kGrpTC = TC, kGrpTW = kGrpWaves / TC, kGrpSegSt = kGrpSegTiles / kGrpTW;
   static_assert(kGrpTC * kGrpTW == kGrpWaves && kGrpSegSt * kGrpTW == kGrpSegTiles,
@@ -1642,7 +1642,9 @@ __global__ __launch_bounds__(kGrpWaves* kWave)
   float* sws = reinterpret_cast<float*>(&s_ws[0]);
   float* sseg = reinterpret_cast<float*>(&s_seg[0]);
   if (threadIdx.x < kGrpTC) s_arrive[threadIdx.x] = 0;
-  if (threadIdx.x == 0) s_abort = 0;
+  // abort0 (a host test switch, read once) starts the block as if a wait had
+  // run out: every wait then gives up unless its count is already there.
+  if (threadIdx.x == 0) s_abort = abort0 != 0;
 
   BwdRow r;
   r.T = T;
@@ -2063,6 +2065,16 @@ void with_option_set(int opts, Fn&& fn) {
   }
 }
 
+// RQF_GRP_FORCE_TIMEOUT=1 starts every block of the group-form backward in
+// the state a wait that ran out leaves (tests of that path): the waits give up
+// at once and the blocks report NaN for their channels' dbias and dtheta,
+// without hanging.  The flag is read once per block, so the wait loops keep
+// their constant bound and no register.
+int grp_force_timeout() {
+  const char* e = std::getenv("RQF_GRP_FORCE_TIMEOUT");
+  return e && !std::strcmp(e, "1") ? 1 : 0;
+}
+
 // Forward block size: kFwdRbWavesRaw wavefronts for calls that stream only z,
 // the logits and raw; kFwdRbWaves when act or a skip tensor adds streams.
 // RQF_FWD_WAVES=narrow|wide forces one (tests and tuning).
@@ -2319,9 +2331,10 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
         if constexpr (O != kOptRuntime && !(O & kOptWarp)) {
           return;  // not reached: the group form needs the warp head
         } else {
+          const int abort0 = grp_force_timeout();
           auto go = [&](auto kern) {
             hipLaunchKernelGGL(kern, grid, block, 0, s, *in, z, ent, ent_chunk, nc, gy, gx,
-                               (int)truncated, o);
+                               (int)truncated, o, abort0);
           };
           if (w.tsize == 3)
             vec ? go(selective_bwd_grp_kernel<O, true, 3>)

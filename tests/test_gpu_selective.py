@@ -324,6 +324,36 @@ def test_group_form(monkeypatch, F, B, T, warp, G, chunk, truncated, edit, team)
              edit=edit, seed=F + T + chunk)
 
 
+def test_group_form_wait_timeout_reports_nan(monkeypatch):
+    """Every wait of the group form is bounded, and a wait that runs out ends
+    the block's other waits.  With RQF_GRP_FORCE_TIMEOUT=1 the host starts
+    every block in that state: the kernel still returns, and each block
+    reports NaN for its channels' dbias and dtheta instead of hanging.
+    Without the switch the same call gives finite results."""
+    F, B, T, G = 8, 2, 2048, 2
+    print(f"case: group form wait timeout F={F} B={B} T={T} G={G}", flush=True)
+    monkeypatch.setenv("RQF_BWD_FORM", "group")
+    monkeypatch.setenv("RQF_BWD_GRP_TEAM", "4")
+    rng = np.random.default_rng(11)
+    inp = rounded_to_f32(make_inputs(F, B, T, CASE_ALL, rng, G=G))
+    ti = to_torch(inp, device="cuda")
+    dev = lambda a: torch.as_tensor(a.astype(np.complex64), device="cuda")  # noqa: E731
+    z, gy, gx = (dev(crandn(rng, F, B, T)) for _ in range(3))
+    raw, act, entries = selective_forward(z, ti, True, True, 256)
+
+    def grads():
+        out = selective_backward(z, ti, entries, gy, gx, True, False, 256)
+        torch.cuda.synchronize()
+        return out[5], out[6]
+
+    monkeypatch.setenv("RQF_GRP_FORCE_TIMEOUT", "1")
+    dbias, dtheta = grads()
+    assert torch.isnan(dbias).all() and torch.isnan(dtheta).all()
+    monkeypatch.delenv("RQF_GRP_FORCE_TIMEOUT")
+    dbias, dtheta = grads()
+    assert torch.isfinite(dbias).all() and torch.isfinite(dtheta).all()
+
+
 @pytest.mark.parametrize("truncated", [False, True])
 @pytest.mark.parametrize("prospective", [False, True])
 @pytest.mark.parametrize("case", [c for c in CASES if c["warp"] != "none"], ids=case_id)

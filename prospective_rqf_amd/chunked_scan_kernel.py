@@ -62,8 +62,8 @@ def _ws(B, T, F, device):
 def _chunked_scan_forward_raw(C1, C2, u):
     """x[t] = C1 x[t-1] + C2 u[t] on (B,T,F); returns complex64 (B,T,F)."""
     C1, C2, u = _c64(C1), _c64(C2), _c64(u)
-    _lib.require_device(C1, C2, u)
     _check_btf(u, C1, C2)
+    _lib.require_device(C1, C2, u)
     B, T, F = u.shape
     out = torch.empty_like(u)
     ws, n = _ws(B, T, F, u.device)
@@ -82,9 +82,9 @@ def _chunked_scan_backward_raw(C1, C2, u, states, grad_output):
     the reference's signature and may be None: the kernel evaluates
     ``grad_C1`` from ``u`` with the order of summation exchanged."""
     C1, C2, u, grad_output = (_c64(t) for t in (C1, C2, u, grad_output))
-    _lib.require_device(C1, C2, u, grad_output)
     _check_btf(u, C1, C2)
     _check_like(u, states=states, grad_output=grad_output)
+    _lib.require_device(C1, C2, u, grad_output)
     B, T, F = u.shape
     grad_u = torch.empty_like(u)
     gc1 = torch.empty(F, dtype=torch.complex64, device=u.device)
@@ -129,8 +129,8 @@ chunked_scan = _triton_chunked_scan
 
 def _chunked_prospective_forward_raw(C1, tap0, tap1, x):
     C1, tap0, tap1, x = (_c64(t) for t in (C1, tap0, tap1, x))
-    _lib.require_device(C1, tap0, tap1, x)
     _check_btf(x, C1, tap0, tap1)
+    _lib.require_device(C1, tap0, tap1, x)
     B, T, F = x.shape
     out = torch.empty_like(x)
     ws, n = _ws(B, T, F, x.device)
@@ -149,12 +149,12 @@ def _chunked_prospective_backward_raw(C1, tap0, tap1, x, states, grad_output):
     (chunked_scan_kernel.py:486), is accepted and may be None: the kernel
     does not read it.  The reference's ``_ChunkedProspectiveScanFunction.backward``
     (chunked_scan_kernel.py:490-504) computes the same with a chunked adjoint
-    scan and five pointwise passes; here one three-phase scan
+    scan and five pointwise passes; here one single-pass scan
     (``rqf_chunked_prospective_bwd``) produces grad_x and the three sums."""
     C1, tap0, tap1, x, grad_output = (_c64(t) for t in (C1, tap0, tap1, x, grad_output))
-    _lib.require_device(C1, tap0, tap1, x, grad_output)
     _check_btf(x, C1, tap0, tap1)
     _check_like(x, states=states, grad_output=grad_output)
+    _lib.require_device(C1, tap0, tap1, x, grad_output)
     B, T, F = x.shape
     grad_x = torch.empty_like(x)
     gc1 = torch.empty(F, dtype=torch.complex64, device=x.device)

@@ -381,9 +381,14 @@ __global__ __launch_bounds__(kL0Threads) void layer0_grads_kernel(
     const float* row = gz + 2 * (f * n + j0);
     float g[2 * kL0Cols];
     if (VEC) {
+      // n % 4 == 0, so a thread with j0 < n owns all kL0Cols columns and one
+      // past the end owns none: it loads nothing and contributes zeros (the
+      // wavefront sums below stay uniform across the wavefront).
+      const bool in = j0 < n;
 #pragma unroll
       for (int q = 0; q < kL0Cols / 2; ++q) {
-        const float4 v = *reinterpret_cast<const float4*>(row + 4 * q);
+        const float4 v = in ? *reinterpret_cast<const float4*>(row + 4 * q)
+                            : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         g[4 * q] = v.x, g[4 * q + 1] = v.y, g[4 * q + 2] = v.z, g[4 * q + 3] = v.w;
       }
     } else {

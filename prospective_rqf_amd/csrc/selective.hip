@@ -8,29 +8,32 @@
 // The coefficients never touch HBM: only z, the logits, the outputs and the
 // per-chunk entry states cross the kernel boundary.
 //
-// Tiles: a wavefront walks one (channel, batch) row in tiles of 64*K steps.
+// Tiles: rows are walked in tiles of 64*K steps, one wavefront per tile.
 // Lane l holds steps [l*K, l*K+K) of a tile, so each global access is one
 // contiguous stretch (float4 when T % 4 == 0).  A tile is scanned as
 //   1. per-lane serial composition of its K affine maps,
-//   2. DPP wave scan of the 64 lane maps (tile entry state folded into lane 0),
-//   3. per-lane serial replay from the lane's entry state,
-// and the tile's exit state is carried to the next tile in a register.  Full
-// tiles run without per-step range masks; only the last (partial) tile has them.
+//   2. DPP wave scan of the 64 lane maps,
+//   3. per-lane serial replay from the lane's entry state.
+// Full tiles run without per-step range masks; only the last (partial) tile
+// has them.
 //
-// Scheduling: each XCD takes one contiguous chunk of the batch (blocks are
-// dealt to the 8 XCDs in contiguous ranges) and walks it channel-major, so all
-// channels of a batch element run on one XCD and share its L2 for the
-// group-wise warp logits, while concurrently streamed rows stay adjacent.
+// Forward: a block owns one (channel, batch) row and walks it in super-tiles
+// of consecutive tiles, one per wavefront; the tiles' maps meet in LDS behind
+// one barrier per super-tile.  Blocks are dealt to the 8 XCDs in contiguous
+// ranges and visit the channels of a warp group together, so concurrently
+// streamed rows stay adjacent and the group's warp-logit rows stay in L2.
 //
 // Backward: the tiles are walked in reverse.  Each tile replays its forward
 // from the stored entry state (ReLU mask and y[t-1]), runs the adjoint
 //   d[t] = e[t] + conj(A[t+1]) d[t+1]
 // with the same three-step structure in suffix order, and forms every
 // gradient in registers (the reference's _backward,
-// selective_scan_kernel.py:250-462).  The warp-logit gradient is written per
-// channel and summed over each group's channels by a separate pass in a fixed
-// order; per-channel parameter gradients are per-row fp64 partial sums reduced
-// in a fixed order.  No floating-point atomics: results are deterministic.
+// selective_scan_kernel.py:250-462).  A block serves the channels of one warp
+// group for one batch element (or a run of them, the split form), stages the
+// group's warp values in LDS and sums the group's warp-logit gradient in LDS
+// in a fixed order; per-channel parameter gradients are per-row fp64 partial
+// sums reduced in a fixed order.  No floating-point atomics: results are
+// deterministic.
 #include "rqf_device.h"
 #include "rqf_scan.h"
 
@@ -53,36 +56,11 @@ using namespace rqf;
 #ifndef RQF_BWD_WAVES_PER_EU
 #define RQF_BWD_WAVES_PER_EU 3
 #endif
-#ifndef RQF_FWD_WAVES_PER_EU
-#define RQF_FWD_WAVES_PER_EU 1
-#endif
-// Forward complex streams through LDS (one contiguous 1 KB per instruction).
-#ifndef RQF_FWD_LDS_IO
-#define RQF_FWD_LDS_IO 1
-#endif
-// Backward form: 1 = teams of channels reduce the warp gradient in LDS;
-// 0 = one wavefront per row, per-channel warp gradient + group pass.
-#ifndef RQF_BWD_TEAMS
-#define RQF_BWD_TEAMS 1
-#endif
-// Optional scheduling fence between the per-step bodies of the backward
-// (keeps the scheduler from interleaving steps, which bounds register pressure).
-#ifdef RQF_BWD_STEP_FENCE
-#define RQF_STEP_FENCE() __builtin_amdgcn_sched_barrier(0)
-#else
-#define RQF_STEP_FENCE() ((void)0)
-#endif
-#ifdef RQF_BWD_PHASE_FENCE
-#define RQF_PHASE_FENCE() __builtin_amdgcn_sched_barrier(0)
-#else
-#define RQF_PHASE_FENCE() ((void)0)
-#endif
 
 namespace {
 
 constexpr int kFwdK = RQF_SEL_FWD_K;  // steps per lane per tile, forward
 constexpr int kBwdK = RQF_SEL_BWD_K;  // steps per lane per tile, backward
-constexpr int kRowsPerBlock = 4;      // wavefronts (rows) per block
 constexpr int kXcds = kXcdCount;      // MI355X: 8 XCDs, blocks dealt round-robin
 
 // XCD x runs a contiguous range of logical blocks.
@@ -240,22 +218,8 @@ __device__ __forceinline__ void step_coef(const rqf_selective_inputs& p, const C
   u = cscale(q.gate, drive);
 }
 
-// Streamed tensors are read and written once: optionally mark the accesses
-// non-temporal so they do not displace the L2-resident warp logits.
-#ifdef RQF_NT_STREAM
-typedef float v4f __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ float4 ld4(const float* p) {
-  const v4f v = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(p));
-  return make_float4(v.x, v.y, v.z, v.w);
-}
-__device__ __forceinline__ void st4(float* p, float4 v) {
-  const v4f w = {v.x, v.y, v.z, v.w};
-  __builtin_nontemporal_store(w, reinterpret_cast<v4f*>(p));
-}
-#else
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 __device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
-#endif
 
 // ---------------------------------------------------------------------------
 // Tile loads / stores with 32-bit in-row offsets.  VEC: T % 4 == 0 and
@@ -401,7 +365,7 @@ template <int K, bool VEC, bool TAIL>
 __device__ __forceinline__ void fwd_load(const FwdRow& r, int t0, int lane, FwdIn<K>& in) {
   const int T = r.T;
   const int tb = t0 + lane * K;
-  if (VEC && !TAIL && RQF_FWD_LDS_IO)
+  if (VEC && !TAIL)
     load_c_lds<K>(r.zr, t0, lane, r.io, in.zv);
   else
     load_c<K, VEC, TAIL>(r.zr, tb, T, in.zv);
@@ -453,7 +417,7 @@ __device__ __forceinline__ void fwd_emit(const FwdRow& r, int t0, int lane, c32 
       }
     }
   }
-  constexpr bool lds_io = VEC && !TAIL && RQF_FWD_LDS_IO;
+  constexpr bool lds_io = VEC && !TAIL;
   c32 sk[K];
   if (r.skr) {
     if (lds_io)
@@ -480,101 +444,6 @@ __device__ __forceinline__ void fwd_emit(const FwdRow& r, int t0, int lane, c32 
   }
 }
 
-template <int K, bool VEC, bool TAIL>
-__device__ __forceinline__ void fwd_compute(const rqf_selective_inputs& p, const Chan& c, FwdRow& r,
-                                            int t0, int lane, const FwdIn<K>& in) {
-  c32 A[K], u[K];
-  fwd_steps<K, TAIL>(p, c, r.T, t0, lane, in, r.zlast, A, u);
-  // 1. lane-local composition
-  c32 P = A[0], s = u[0];
-#pragma unroll
-  for (int k = 1; k < K; ++k) {
-    s = cmad(A[k], s, u[k]);
-    P = cmul(A[k], P);
-  }
-  if (lane == 0) s = cmad(P, r.y, s);
-  // 2. wave scan: s becomes the state after the lane's last step
-  wave_scan_fwd(P, s);
-  // 3. replay from the lane's entry state
-  c32 yk = shift_up(s, r.y, lane);
-  c32 out[K];
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    yk = cmad(A[k], yk, u[k]);
-    out[k] = yk;
-  }
-  fwd_emit<K, VEC, TAIL>(r, t0, lane, out);
-  r.y = readlane(s, kWave - 1);
-  r.zlast = readlane(in.zv[K - 1], kWave - 1);
-}
-
-template <int K, bool VEC, bool TAIL>
-__device__ __forceinline__ void fwd_tile(const rqf_selective_inputs& p, const Chan& c, FwdRow& r,
-                                         int t0, int lane) {
-  FwdIn<K> in;
-  fwd_load<K, VEC, TAIL>(r, t0, lane, in);
-  fwd_compute<K, VEC, TAIL>(p, c, r, t0, lane, in);
-}
-
-template <int O, bool VEC>
-__global__ __launch_bounds__(kRowsPerBlock* kWave)
-    __attribute__((amdgpu_waves_per_eu(RQF_FWD_WAVES_PER_EU))) void selective_fwd_kernel(
-    const rqf_selective_inputs pin, const float* __restrict__ z, const float* __restrict__ skip,
-    float* __restrict__ raw, float* __restrict__ act, float* __restrict__ entries, int chunk,
-    int nc) {
-  constexpr int K = kFwdK, TILE = kWave * K;
-  const rqf_selective_inputs p = with_options<O>(pin);
-#if RQF_FWD_LDS_IO
-  __shared__ float4 s_io[kRowsPerBlock][TILE / 2];
-#endif
-  const int lane = lane_id();
-  const int64_t L = xcd_remap(blockIdx.x, gridDim.x) * kRowsPerBlock + wave_id();
-  const RowId id = row_id(p, L);
-  if (!id.valid) return;  // whole wavefronts exit together
-  const Chan c = load_chan(p, id.f);
-  FwdRow r;
-  r.T = (int)p.T;
-  r.chunk = chunk;
-  const int64_t base = id.row * r.T;
-  r.zr = z + 2 * base;
-  r.gr = p.has_gamma ? p.gamma_logits + base : nullptr;
-  r.wr = p.has_write ? p.write_logits + base : nullptr;
-  r.dr = p.has_warp ? p.warp_logits + (group_of(p, id.f) * p.B + id.b) * r.T : nullptr;
-  r.rawr = raw ? raw + 2 * base : nullptr;
-  r.actr = act ? act + 2 * base : nullptr;
-  r.skr = skip ? skip + 2 * base : nullptr;
-  r.ent = entries + 2 * id.row * nc;
-#if RQF_FWD_LDS_IO
-  r.io = &s_io[wave_id()][0];
-#else
-  r.io = nullptr;
-#endif
-  if (lane == 0) {
-    r.ent[0] = 0.0f;
-    r.ent[1] = 0.0f;
-  }
-  r.y = mk(0.0f, 0.0f);
-  r.zlast = mk(0.0f, 0.0f);
-  const int full = VEC ? r.T / TILE : 0;
-  int t0 = 0;
-#ifdef RQF_FWD_PREFETCH
-  if (full > 0) {
-    // The next tile's loads are issued before the current tile's math.
-    FwdIn<K> cur;
-    fwd_load<K, VEC, false>(r, 0, lane, cur);
-    for (int i = 0; i < full; ++i, t0 += TILE) {
-      FwdIn<K> nxt;
-      if (i + 1 < full) fwd_load<K, VEC, false>(r, t0 + TILE, lane, nxt);
-      fwd_compute<K, VEC, false>(p, c, r, t0, lane, cur);
-      cur = nxt;
-    }
-  }
-#else
-  for (int i = 0; i < full; ++i, t0 += TILE) fwd_tile<K, VEC, false>(p, c, r, t0, lane);
-#endif
-  for (; t0 < r.T; t0 += TILE) fwd_tile<K, VEC, true>(p, c, r, t0, lane);
-}
-
 // Forward, row-block form: a block of kFwdRbWaves wavefronts owns one row and
 // walks it in super-tiles of kFwdRbWaves consecutive tiles, wavefront w
 // taking tile w of each, so that concurrent wavefronts stream adjacent
@@ -594,9 +463,6 @@ __global__ __launch_bounds__(kRowsPerBlock* kWave)
 // measured on one box: raw-only layer 1 0.352 -> 0.320 ms with 4 waves;
 // raw+act layer 0 0.403 ms with 8 against 0.425 with 4, config 3 1.668
 // against 1.718.
-#ifndef RQF_FWD_ROWBLOCK
-#define RQF_FWD_ROWBLOCK 1
-#endif
 #ifndef RQF_FWD_RB_WAVES
 #define RQF_FWD_RB_WAVES 8
 #endif
@@ -608,15 +474,13 @@ constexpr int kFwdRbWavesRaw = RQF_FWD_RB_WAVES_RAW;
 
 template <int O, bool VEC, int W>
 __global__ __launch_bounds__(W* kWave)
-    __attribute__((amdgpu_waves_per_eu(RQF_FWD_WAVES_PER_EU))) void selective_fwd_rb_kernel(
+    void selective_fwd_rb_kernel(
     const rqf_selective_inputs pin, const float* __restrict__ z, const float* __restrict__ skip,
     float* __restrict__ raw, float* __restrict__ act, float* __restrict__ entries, int chunk,
     int nc) {
   constexpr int K = kFwdK, TILE = kWave * K;
   const rqf_selective_inputs p = with_options<O>(pin);
-#if RQF_FWD_LDS_IO
   __shared__ float4 s_io[W][TILE / 2];
-#endif
   __shared__ float4 s_map[2][W];
   const int lane = lane_id();
   const int w = wave_id();
@@ -636,11 +500,7 @@ __global__ __launch_bounds__(W* kWave)
   r.actr = act ? act + 2 * base : nullptr;
   r.skr = skip ? skip + 2 * base : nullptr;
   r.ent = entries + 2 * id.row * nc;
-#if RQF_FWD_LDS_IO
   r.io = &s_io[w][0];
-#else
-  r.io = nullptr;
-#endif
   if (w == 0 && lane == 0) {
     r.ent[0] = 0.0f;
     r.ent[1] = 0.0f;
@@ -709,7 +569,6 @@ struct BwdOut {
   float* dzw;       // W-path drive gradient (== dz when not truncated)
   float* dg;
   float* dw;
-  float* ddc;       // (F, B, T) per-channel warp-logit gradient (per-row kernel)
   float* dd_part;   // (S, B, T) warp-logit gradient summed over each split (team kernel)
   float* dd;        // (G, B, T) warp-logit gradient (team kernel, groups with one split)
   double* partial;  // (2, F*B): per row sums of d/dbias and d/dtheta
@@ -719,7 +578,6 @@ struct BwdRow {
   const float* zr;
   const float* gr;
   const float* wr;
-  const float* dr;
   const float* gyr;
   const float* gxr;
   const float* ent;
@@ -727,8 +585,7 @@ struct BwdRow {
   float* dzwr;
   float* dgr;
   float* dwr;
-  float* ddr;     // per-channel warp-logit gradient (global), or
-  float4* sdd;    // this wavefront's slot of the team's LDS warp-gradient tile
+  float4* sdd;    // this wavefront's slot of the team's LDS warp-gradient tile (or null)
   const float* swg;  // team LDS stage of the tile: warp_scale*(1 - tanh(warp logit)^2)
   const float* sws;  // and exp(warp_scale * tanh(warp logit)) per step
   int T, chunk, truncated;
@@ -738,7 +595,7 @@ struct BwdRow {
   double sum_bias, sum_theta;
 };
 
-// Staged warp values of the lane's K steps (SHARED): the frequency factor
+// Staged warp values of the lane's K steps (from LDS): the frequency factor
 // exp(warp_scale * tanh) and the tanh derivative factor warp_scale*(1 - tanh^2).
 template <int K>
 __device__ __forceinline__ void lds_warp_factor(const BwdRow& r, int lane, float (&ws)[K]) {
@@ -775,54 +632,40 @@ struct BwdTile {
   c32 yprev[K], ecot[K];  // forward state before the step; cotangent on raw
   c32 M;  // product of A over the lane's steps after its first (full tiles)
   // ivd = 1/|a|^2, aim = Im a, dsq = |a|^2 of the ZOH exponent a, reused by the VJP
-  float gam[K], thu[K], gate[K], wtk[K], ivd[K], aim[K], dsq[K];
+  float gam[K], gate[K], ivd[K], aim[K], dsq[K];
   c32 zp0;   // z of the step before the lane's first
   float c0;  // lag-tap weight gate*ratio*gamma of the lane's first step
 };
 
 // Replay phase of a backward tile: the coefficients of every step, the
 // forward replay from the tile's entry state and the cotangent e on raw.
-// SHARED: the warp values of the tile come from the team's LDS stage (r.swg,
-// r.sws) instead of per-lane loads and math.
+// The warp values of the tile come from the block's LDS stage (r.swg, r.sws).
 // zv: the tile's drive; zprev_tile: z[t0 - 1] (0 at t0 = 0).
-template <int K, bool VEC, bool TAIL, bool SHARED>
+template <int K, bool VEC, bool TAIL>
 __device__ __forceinline__ void bwd_tile_replay(const rqf_selective_inputs& p, const Chan& c,
                                                 const BwdRow& r, int t0, int lane,
                                                 const c32 (&zv)[K], c32 zprev_tile,
                                                 BwdTile<K>& s) {
   const int T = r.T;
   const int tb = t0 + lane * K;
-  float gv[K], wv[K], dv[K];
+  float gv[K], wv[K];
   if (r.gr) load_f<K, VEC, TAIL>(r.gr, tb, T, gv); else zero(gv);
   if (r.wr) load_f<K, VEC, TAIL>(r.wr, tb, T, wv); else zero(wv);
-  if (!SHARED && r.dr) load_f<K, VEC, TAIL>(r.dr, tb, T, dv); else zero(dv);
   s.zp0 = shift_up(zv[K - 1], zprev_tile, lane);
 
-  // Coefficients; kept per step: A, phi, gamma, gate and (unless SHARED)
-  // theta_u and tanh(warp logit).
+  // Coefficients; kept per step: A, phi, gamma and gate.
   c32 u[K];
   float sws[K];
-  if (SHARED) lds_warp_factor<K>(r, lane, sws);
+  lds_warp_factor<K>(r, lane, sws);
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    // (only the non-SHARED form keeps the Ctl's tanh)
-    const Ctl q = SHARED ? controller_w(p, c, gv[k], 0.0f, sws[k], wv[k])
-                         : controller(p, c, gv[k], dv[k], wv[k]);
+    const Ctl q = controller_w(p, c, gv[k], 0.0f, sws[k], wv[k]);
     step_coef(p, c, q, zv[k], k ? zv[k - 1] : s.zp0, s.A[k], s.phi[k], u[k], s.ivd[k],
               s.aim[k], s.dsq[k]);
     s.gam[k] = q.gamma;
     s.gate[k] = q.gate;
-    if (!SHARED) {
-      s.thu[k] = q.theta_u;
-      s.wtk[k] = q.wt;
-    }
     if (TAIL && tb + k >= T) u[k] = mk(0.0f, 0.0f);
-    RQF_STEP_FENCE();
   }
-  RQF_PHASE_FENCE();
-#ifdef RQF_LOAD_FENCE
-  __asm__ volatile("" ::: "memory");
-#endif
   // Forward states y[t-1] of every step, and the cotangent e[t] on raw: the
   // raw output plus the split-ReLU cotangent where raw > 0.
   c32 ey[K], ex[K];
@@ -901,7 +744,7 @@ __device__ __forceinline__ void bwd_lane_adjoint(const BwdTile<K>& s, c32 A_lane
 // after the lane's last (the cotangent there when truncated), the decay
 // A_lane_next and the lag-tap weight cn_lane_next of that step.  gd_out
 // (optional) receives the lane's warp-logit gradients.
-template <int K, bool VEC, bool TAIL, bool SHARED>
+template <int K, bool VEC, bool TAIL>
 __device__ __forceinline__ void bwd_tile_grads(const rqf_selective_inputs& p, const Chan& c,
                                                BwdRow& r, int t0, int lane, const c32 (&zv)[K],
                                                const BwdTile<K>& s, c32 dnext, c32 A_lane_next,
@@ -909,12 +752,10 @@ __device__ __forceinline__ void bwd_tile_grads(const rqf_selective_inputs& p, co
   const int T = r.T;
   const int tb = t0 + lane * K;
   float swg[K], sws[K];
-  if (SHARED) {
-    // Re-read the staged warp values here rather than keep them live across
-    // the scans (the compiler barrier stops it from reusing the first read).
-    __asm__ volatile("" ::: "memory");
-    lds_warp<K>(r, lane, swg, sws);
-  }
+  // Re-read the staged warp values here rather than keep them live across
+  // the scans (the compiler barrier stops it from reusing the first read).
+  __asm__ volatile("" ::: "memory");
+  lds_warp<K>(r, lane, swg, sws);
   c32 gz[K], gzw[K];
   float gg[K], gw[K], gd[K];
   float tile_bias = 0.0f, tile_theta = 0.0f;
@@ -958,7 +799,7 @@ __device__ __forceinline__ void bwd_tile_grads(const rqf_selective_inputs& p, co
     // selective_scan_kernel.py:119-148), here to degree 4 for |a| < 1/32
     // (truncation < 1e-10 relative) and (A - phi)/a above, where the
     // cancellation in A - phi costs at most ~1e-5 relative.
-    const float th_u = SHARED ? (p.has_warp ? c.theta * sws[k] : c.theta) : s.thu[k];
+    const float th_u = p.has_warp ? c.theta * sws[k] : c.theta;
     const float theta = clamp_theta(p, c, th_u);
     const c32 a = mk(-gh, s.aim[k]);
     c32 fp;
@@ -998,9 +839,9 @@ __device__ __forceinline__ void bwd_tile_grads(const rqf_selective_inputs& p, co
     }
     if (p.has_warp) {
       // exp(scale*w) = d theta_u / d theta
-      const float ws = SHARED ? sws[k] : s.thu[k] * c.inv_theta;
+      const float ws = sws[k];
       // d exp(scale*tanh(w))/dw = exp(scale*tanh(w)) * scale*(1 - tanh(w)^2)
-      const float wg = SHARED ? swg[k] : p.warp_scale * fmaf(-s.wtk[k], s.wtk[k], 1.0f);
+      const float wg = swg[k];
       // torch.clamp passes the gradient at both exact edges
       if (p.bound_warp && !(th_u >= c.thlo && th_u <= c.thhi)) dth = 0.0f;
       gd[k] = dth * theta * wg;
@@ -1015,7 +856,6 @@ __device__ __forceinline__ void bwd_tile_grads(const rqf_selective_inputs& p, co
     }
     tile_bias += dbias;
     tile_theta += dth;
-    RQF_STEP_FENCE();
   }
   r.sum_bias += (double)tile_bias;
   r.sum_theta += (double)tile_theta;
@@ -1023,7 +863,6 @@ __device__ __forceinline__ void bwd_tile_grads(const rqf_selective_inputs& p, co
   if (r.truncated) store_c<K, VEC, TAIL>(r.dzr, tb, T, gz);
   if (r.dgr) store_f<K, VEC, TAIL>(r.dgr, tb, T, gg);
   if (r.dwr) store_f<K, VEC, TAIL>(r.dwr, tb, T, gw);
-  if (r.ddr) store_f<K, VEC, TAIL>(r.ddr, tb, T, gd);
   if (r.sdd) {
     static_assert(K % 4 == 0, "whole float4s of warp gradient per lane");
 #pragma unroll
@@ -1040,17 +879,16 @@ __device__ __forceinline__ void bwd_tile_grads(const rqf_selective_inputs& p, co
 // One backward tile of a row walked by one wavefront: the tile's exit adjoint
 // state (r.dcarry) and the next tile's first decay and lag-tap weight
 // (r.Afirst, r.cfirst) come in through r and go out for the tile before it.
-template <int K, bool VEC, bool TAIL, bool SHARED>
+template <int K, bool VEC, bool TAIL>
 __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Chan& c, BwdRow& r,
                                          int t0, int lane, const c32 (&zv)[K], c32 zprev_tile) {
   BwdTile<K> s;
-  bwd_tile_replay<K, VEC, TAIL, SHARED>(p, c, r, t0, lane, zv, zprev_tile, s);
+  bwd_tile_replay<K, VEC, TAIL>(p, c, r, t0, lane, zv, zprev_tile, s);
   const c32 A_lane_next = shift_down(s.A[0], r.Afirst, lane);
   const float cn_lane_next = shift_down(s.c0, r.cfirst, lane);
   r.Afirst = readlane(s.A[0], 0);
   r.cfirst = readlane(s.c0, 0);
 
-  RQF_PHASE_FENCE();
   // Adjoint d[t] = e[t] + conj(A[t+1]) d[t+1]  (truncated: d = e).
   c32 dnext;
   if (r.truncated) {
@@ -1065,71 +903,7 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
     r.dcarry = readlane(rr, 0);
   }
 
-  RQF_PHASE_FENCE();
-  bwd_tile_grads<K, VEC, TAIL, SHARED>(p, c, r, t0, lane, zv, s, dnext, A_lane_next,
-                                       cn_lane_next);
-}
-
-template <int O, bool VEC>
-__global__ __launch_bounds__(kRowsPerBlock* kWave)
-    __attribute__((amdgpu_waves_per_eu(RQF_BWD_WAVES_PER_EU))) void selective_bwd_kernel(
-        const rqf_selective_inputs pin, const float* __restrict__ z,
-        const float* __restrict__ entries, int chunk, int nc, const float* __restrict__ gy,
-        const float* __restrict__ gx, int truncated, BwdOut o) {
-  const rqf_selective_inputs p = with_options<O>(pin);
-  constexpr int K = kBwdK, TILE = kWave * K;
-  const int lane = lane_id();
-  const int64_t L = xcd_remap(blockIdx.x, gridDim.x) * kRowsPerBlock + wave_id();
-  const RowId id = row_id(p, L);
-  if (!id.valid) return;
-  const Chan c = load_chan(p, id.f);
-  BwdRow r;
-  r.T = (int)p.T;
-  r.chunk = chunk;
-  r.truncated = truncated;
-  const int64_t base = id.row * r.T;
-  r.zr = z + 2 * base;
-  r.gr = p.has_gamma ? p.gamma_logits + base : nullptr;
-  r.wr = p.has_write ? p.write_logits + base : nullptr;
-  r.dr = p.has_warp ? p.warp_logits + (group_of(p, id.f) * p.B + id.b) * r.T : nullptr;
-  r.gyr = gy ? gy + 2 * base : nullptr;
-  r.gxr = gx ? gx + 2 * base : nullptr;
-  r.ent = entries + 2 * id.row * nc;
-  r.dzr = o.dz + 2 * base;
-  r.dzwr = o.dzw + 2 * base;
-  r.dgr = o.dg ? o.dg + base : nullptr;
-  r.dwr = o.dw ? o.dw + base : nullptr;
-  r.ddr = o.ddc ? o.ddc + base : nullptr;
-  r.sdd = nullptr;
-  r.swg = nullptr;
-  r.sws = nullptr;
-  r.dcarry = mk(0.0f, 0.0f);
-  r.Afirst = mk(0.0f, 0.0f);
-  r.cfirst = 0.0f;
-  r.sum_bias = 0.0;
-  r.sum_theta = 0.0;
-  const int ntiles = (r.T + TILE - 1) / TILE;
-  const int full = VEC ? r.T / TILE : 0;
-  int tile = ntiles - 1;
-  auto zprev = [&](int t0) {
-    return t0 > 0 ? mk(r.zr[2 * (t0 - 1)], r.zr[2 * (t0 - 1) + 1]) : mk(0.0f, 0.0f);
-  };
-  for (; tile >= full; --tile) {
-    c32 zv[K];
-    load_c<K, VEC, true>(r.zr, tile * TILE + lane * K, r.T, zv);
-    bwd_tile<K, VEC, true, false>(p, c, r, tile * TILE, lane, zv, zprev(tile * TILE));
-  }
-  for (; tile >= 0; --tile) {
-    c32 zv[K];
-    load_c<K, VEC, false>(r.zr, tile * TILE + lane * K, r.T, zv);
-    bwd_tile<K, VEC, false, false>(p, c, r, tile * TILE, lane, zv, zprev(tile * TILE));
-  }
-  const double sb = wave_sum(r.sum_bias);
-  const double st = wave_sum(r.sum_theta);
-  if (lane == 0) {
-    o.partial[id.row] = sb;
-    o.partial[p.F * p.B + id.row] = st;
-  }
+  bwd_tile_grads<K, VEC, TAIL>(p, c, r, t0, lane, zv, s, dnext, A_lane_next, cn_lane_next);
 }
 
 // ---------------------------------------------------------------------------
@@ -1341,11 +1115,6 @@ __global__ __launch_bounds__(kTeam* kWave)
   __shared__ float4 s_carry[kChans];               // (dcarry, Afirst) of each channel
   __shared__ float s_cfirst[kChans];
   __shared__ double s_sum[kChans][2];              // dbias, dtheta sums of finished segments
-#ifdef RQF_BWD_LDS_RESERVE_KB
-  // Experiment: reserve LDS to cap the number of resident teams per CU.
-  __shared__ float s_reserve[RQF_BWD_LDS_RESERVE_KB * 256];
-  if (p.T < 0) s_reserve[threadIdx.x] = 0.0f;
-#endif
   const int lane = lane_id();
   const int w = wave_id();
   // Logical block -> (batch chunk, split slot, batch element), XCD-contiguous chunks.
@@ -1377,8 +1146,6 @@ __global__ __launch_bounds__(kTeam* kWave)
   r.T = T;
   r.chunk = chunk;
   r.truncated = truncated;
-  r.dr = nullptr;
-  r.ddr = nullptr;
   r.sdd = nullptr;
   r.swg = swg;
   r.sws = sws;
@@ -1447,10 +1214,10 @@ __global__ __launch_bounds__(kTeam* kWave)
           c32 zv[K];
           if (tile >= full) {
             load_c<K, VEC, true>(r.zr, t0 + lane * K, T, zv);
-            bwd_tile<K, VEC, true, true>(p, c, r, t0, lane, zv, zprev_tile);
+            bwd_tile<K, VEC, true>(p, c, r, t0, lane, zv, zprev_tile);
           } else {
             load_c<K, VEC, false>(r.zr, t0 + lane * K, T, zv);
-            bwd_tile<K, VEC, false, true>(p, c, r, t0, lane, zv, zprev_tile);
+            bwd_tile<K, VEC, false>(p, c, r, t0, lane, zv, zprev_tile);
           }
         }
         if (warp) {
@@ -1650,8 +1417,6 @@ __global__ __launch_bounds__(kGrpWaves* kWave)
   r.T = T;
   r.chunk = chunk;
   r.truncated = truncated;
-  r.dr = nullptr;
-  r.ddr = nullptr;
   r.sdd = nullptr;
   r.swg = swg;
   r.sws = sws;
@@ -1726,10 +1491,10 @@ __global__ __launch_bounds__(kGrpWaves* kWave)
               t0 > 0 ? mk(r.zr[2 * (t0 - 1)], r.zr[2 * (t0 - 1) + 1]) : mk(0.0f, 0.0f);
           if (tile >= full) {
             load_c<K, VEC, true>(r.zr, t0 + lane * K, T, zv);
-            bwd_tile_replay<K, VEC, true, true>(p, c, r, t0, lane, zv, zprev_tile, s);
+            bwd_tile_replay<K, VEC, true>(p, c, r, t0, lane, zv, zprev_tile, s);
           } else {
             load_c<K, VEC, false>(r.zr, t0 + lane * K, T, zv);
-            bwd_tile_replay<K, VEC, false, true>(p, c, r, t0, lane, zv, zprev_tile, s);
+            bwd_tile_replay<K, VEC, false>(p, c, r, t0, lane, zv, zprev_tile, s);
           }
           if (!truncated) {
             // Lane 63's step after its last is the next tile's first: its
@@ -1790,10 +1555,10 @@ __global__ __launch_bounds__(kGrpWaves* kWave)
             dnext = shift_down(dfirst, D1, lane);
           }
           if (tile >= full)
-            bwd_tile_grads<K, VEC, true, true>(p, c, r, t0, lane, zv, s, dnext, A_lane_next,
+            bwd_tile_grads<K, VEC, true>(p, c, r, t0, lane, zv, s, dnext, A_lane_next,
                                                cn_lane_next, gd);
           else
-            bwd_tile_grads<K, VEC, false, true>(p, c, r, t0, lane, zv, s, dnext, A_lane_next,
+            bwd_tile_grads<K, VEC, false>(p, c, r, t0, lane, zv, s, dnext, A_lane_next,
                                                 cn_lane_next, gd);
         }
         // The group sum of this tile's steps, in the fixed (team, channel)
@@ -1833,6 +1598,24 @@ __global__ __launch_bounds__(kGrpWaves* kWave)
     }
   }
   __syncthreads();
+  if (s_abort) {
+    // A wait ran out (block-uniform after the barrier): carries and group sums
+    // may have been composed from maps that had not arrived, so every output
+    // row this block owns is overwritten with NaN, not left finite and wrong.
+    const float nan = __builtin_nanf("");
+    for (int i = 0; i < ng; ++i) {
+      const int64_t base = ((int64_t)s_order[i] * p.B + b) * T;
+      for (int t = (int)threadIdx.x; t < 2 * T; t += NT) {
+        o.dzw[2 * base + t] = nan;
+        if (truncated) o.dz[2 * base + t] = nan;
+      }
+      for (int t = (int)threadIdx.x; t < T; t += NT) {
+        if (o.dg) o.dg[base + t] = nan;
+        if (o.dw) o.dw[base + t] = nan;
+      }
+    }
+    for (int t = (int)threadIdx.x; t < T; t += NT) ddrow[t] = nan;
+  }
   // Per-row fp64 partials of dbias and dtheta: the time slots in fixed order.
   for (int i = (int)threadIdx.x; i < ng; i += NT) {
     {
@@ -1881,41 +1664,6 @@ __device__ __forceinline__ void team_reduce_at(int64_t i, const float* __restric
   }
 }
 
-#if !RQF_BWD_TEAMS
-// dd[g, i] = sum over the channels f of group g (ascending f) of ddc[f, i];
-// i runs over B*T.  Each thread keeps its G accumulators in LDS.
-constexpr int kReduceGroupsLds = 32;
-__global__ __launch_bounds__(256) void group_reduce_kernel(const float* __restrict__ ddc,
-                                                           const int64_t* __restrict__ groups,
-                                                           float* __restrict__ dd, int F, int G,
-                                                           int64_t N) {
-  __shared__ float acc[kReduceGroupsLds][256];
-  const int tid = threadIdx.x;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + tid;
-  const bool in = i < N;
-  if (G <= kReduceGroupsLds) {
-    for (int g = 0; g < G; ++g) acc[g][tid] = 0.0f;
-    int f = 0;
-    for (; f + 4 <= F; f += 4) {
-      float v[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) v[q] = in ? ddc[(int64_t)(f + q) * N + i] : 0.0f;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) acc[clamp_group(groups[f + q], G)][tid] += v[q];
-    }
-    for (; f < F; ++f) acc[clamp_group(groups[f], G)][tid] += in ? ddc[(int64_t)f * N + i] : 0.0f;
-    if (in)
-      for (int g = 0; g < G; ++g) dd[(int64_t)g * N + i] = acc[g][tid];
-  } else if (in) {
-    for (int g = 0; g < G; ++g) {
-      float s = 0.0f;
-      for (int f = 0; f < F; ++f)
-        if (clamp_group(groups[f], G) == g) s += ddc[(int64_t)f * N + i];
-      dd[(int64_t)g * N + i] = s;
-    }
-  }
-}
-#endif
 
 // dbias[f] = sum_b partial[f*B + b] in fp64, same for dtheta: one wavefront
 // per channel, lane l sums b = l, l+64, ... in order, then a fixed-shape wave
@@ -2035,11 +1783,6 @@ bool vec_ok(const rqf_selective_inputs* in, std::initializer_list<const void*> p
   return true;
 }
 
-dim3 row_grid(const rqf_selective_inputs* in) {
-  const int64_t rows = kXcds * in->F * ((in->B + kXcds - 1) / kXcds);  // logical rows
-  return dim3((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
-}
-
 int options_of(const rqf_selective_inputs* in) {
   const int o = (in->has_gamma ? kOptGamma : 0) | (in->log_shift ? kOptLogShift : 0) |
                 (in->has_warp ? kOptWarp : 0) | (in->bound_warp ? kOptBound : 0) |
@@ -2054,9 +1797,6 @@ int options_of(const rqf_selective_inputs* in) {
 template <class Fn>
 void with_option_set(int opts, Fn&& fn) {
   static_assert(sizeof(kOptSets) / sizeof(kOptSets[0]) == 3, "one case per compiled set");
-#ifdef RQF_NO_SPECIALISE
-  opts = kOptRuntime;
-#endif
   switch (opts) {
     case kOptSets[0]: fn(std::integral_constant<int, kOptSets[0]>{}); return;
     case kOptSets[1]: fn(std::integral_constant<int, kOptSets[1]>{}); return;
@@ -2088,39 +1828,26 @@ bool fwd_narrow_blocks(bool extra_streams) {
 
 void launch_fwd(const rqf_selective_inputs* in, const float* z, const float* skip, float* raw,
                 float* act, float* entries, int chunk, int nc, bool vec, hipStream_t s) {
-  if (RQF_FWD_ROWBLOCK) {
-    const dim3 grid((unsigned)(kXcds * in->F * ((in->B + kXcds - 1) / kXcds)));
-    const bool narrow = fwd_narrow_blocks(act != nullptr || skip != nullptr);
-    const dim3 block((narrow ? kFwdRbWavesRaw : kFwdRbWaves) * kWave);
-    with_option_set(options_of(in), [&](auto oc) {
-      constexpr int O = decltype(oc)::value;
-      if (narrow) {
-        if (vec)
-          hipLaunchKernelGGL((selective_fwd_rb_kernel<O, true, kFwdRbWavesRaw>), grid, block, 0,
-                             s, *in, z, skip, raw, act, entries, chunk, nc);
-        else
-          hipLaunchKernelGGL((selective_fwd_rb_kernel<O, false, kFwdRbWavesRaw>), grid, block, 0,
-                             s, *in, z, skip, raw, act, entries, chunk, nc);
-      } else {
-        if (vec)
-          hipLaunchKernelGGL((selective_fwd_rb_kernel<O, true, kFwdRbWaves>), grid, block, 0, s,
-                             *in, z, skip, raw, act, entries, chunk, nc);
-        else
-          hipLaunchKernelGGL((selective_fwd_rb_kernel<O, false, kFwdRbWaves>), grid, block, 0,
-                             s, *in, z, skip, raw, act, entries, chunk, nc);
-      }
-    });
-    return;
-  }
-  const dim3 grid = row_grid(in), block(kRowsPerBlock * kWave);
+  const dim3 grid((unsigned)(kXcds * in->F * ((in->B + kXcds - 1) / kXcds)));
+  const bool narrow = fwd_narrow_blocks(act != nullptr || skip != nullptr);
+  const dim3 block((narrow ? kFwdRbWavesRaw : kFwdRbWaves) * kWave);
   with_option_set(options_of(in), [&](auto oc) {
     constexpr int O = decltype(oc)::value;
-    if (vec)
-      hipLaunchKernelGGL((selective_fwd_kernel<O, true>), grid, block, 0, s, *in, z, skip, raw,
-                         act, entries, chunk, nc);
-    else
-      hipLaunchKernelGGL((selective_fwd_kernel<O, false>), grid, block, 0, s, *in, z, skip, raw,
-                         act, entries, chunk, nc);
+    if (narrow) {
+      if (vec)
+        hipLaunchKernelGGL((selective_fwd_rb_kernel<O, true, kFwdRbWavesRaw>), grid, block, 0, s,
+                           *in, z, skip, raw, act, entries, chunk, nc);
+      else
+        hipLaunchKernelGGL((selective_fwd_rb_kernel<O, false, kFwdRbWavesRaw>), grid, block, 0,
+                           s, *in, z, skip, raw, act, entries, chunk, nc);
+    } else {
+      if (vec)
+        hipLaunchKernelGGL((selective_fwd_rb_kernel<O, true, kFwdRbWaves>), grid, block, 0, s,
+                           *in, z, skip, raw, act, entries, chunk, nc);
+      else
+        hipLaunchKernelGGL((selective_fwd_rb_kernel<O, false, kFwdRbWaves>), grid, block, 0, s,
+                           *in, z, skip, raw, act, entries, chunk, nc);
+    }
   });
 }
 
@@ -2219,7 +1946,7 @@ int group_team_size(const rqf_selective_inputs* in) {
 // picks a form for tests and tuning; setting RQF_BWD_SPLIT_TEAMS picks the
 // split form.
 bool use_group_form(const rqf_selective_inputs* in, bool with_gx) {
-  if (!RQF_BWD_TEAMS || !in->has_warp || in->F > kGrpMaxChans) return false;
+  if (!in->has_warp || in->F > kGrpMaxChans) return false;
   if (std::getenv("RQF_BWD_SPLIT_TEAMS")) return false;
   if (const char* e = std::getenv("RQF_BWD_FORM")) {
     if (!std::strcmp(e, "group")) return true;
@@ -2256,12 +1983,8 @@ SelWs sel_ws_layout(const rqf_selective_inputs* in, int64_t chunk, bool group_fo
   if (!w.group_form)  // the group form builds its channel lists in LDS
     off += round256(sizeof(int) * (size_t)(in->F + 5 * w.slots + 4 * w.G + 4));
   w.dd = off;
-#if RQF_BWD_TEAMS
   if (in->has_warp && !w.group_form)
     off += round256(sizeof(float) * (size_t)w.split_slots * in->B * in->T);
-#else
-  if (in->has_warp) off += round256(sizeof(float) * (size_t)R * (size_t)in->T);
-#endif
   w.total = off;
   return w;
 }
@@ -2317,11 +2040,8 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
     o.dzw = dzw;
     o.dg = in->has_gamma ? dg : nullptr;
     o.dw = in->has_write ? dw : nullptr;
-    o.ddc = nullptr;
     o.dd_part = nullptr;
-    o.dd = nullptr;
     o.partial = partial;
-#if RQF_BWD_TEAMS
     o.dd = in->has_warp ? dd : nullptr;
     // The group form finds its group's channels itself: no team table.
     if (w.group_form) {
@@ -2392,22 +2112,6 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
     });
     launch_finish(o.dd_part, gsplit, dd, in->G, in->B * T, partial, dbias, dtheta, in->F, in->B,
                   s);
-#else
-    o.ddc = in->has_warp ? (float*)(ws + w.dd) : nullptr;
-    const dim3 grid = row_grid(in), block(kRowsPerBlock * kWave);
-    if (vec)
-      hipLaunchKernelGGL((selective_bwd_kernel<kOptRuntime, true>), grid, block, 0, s, *in, z, ent,
-                         ent_chunk, nc, gy, gx, (int)truncated, o);
-    else
-      hipLaunchKernelGGL((selective_bwd_kernel<kOptRuntime, false>), grid, block, 0, s, *in, z,
-                         ent, ent_chunk, nc, gy, gx, (int)truncated, o);
-    if (in->has_warp) {
-      const int64_t N = in->B * T;
-      hipLaunchKernelGGL(group_reduce_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, s,
-                         o.ddc, in->groups, dd, (int)in->F, (int)in->G, N);
-    }
-    launch_finish(nullptr, nullptr, nullptr, 0, 0, partial, dbias, dtheta, in->F, in->B, s);
-#endif
   } else {
     zero_words(partial, 4 * R, s);
     if (in->has_warp && dd) zero_words(dd, in->G * in->B * T, s);

@@ -42,9 +42,11 @@ class _FBTProspectiveScan(torch.autograd.Function):
     @staticmethod
     def forward(ctx, C1, tap0, tap1, x_fbt, fuse_act):
         x = _c64(x_fbt)
-        _lib.require_device(x)
+        if x.dim() != 3:
+            raise ValueError(f"expected (filters, batch, time) input, got shape {tuple(x.shape)}")
         filters, batch, time = x.shape
         C1, tap0, tap1 = _coefs(C1, tap0, tap1, filters)
+        _lib.require_device(x, C1, tap0, tap1)
         raw = torch.empty_like(x)
         act = torch.empty_like(x) if fuse_act else None
         _lib.check(
@@ -63,6 +65,10 @@ class _FBTProspectiveScan(torch.autograd.Function):
         C1, tap0, tap1, x, raw = ctx.saved_tensors
         filters, batch, time = x.shape
         g = _c64(grad_output)
+        if g.shape != x.shape:
+            raise ValueError(f"grad_output must have the input's shape {tuple(x.shape)}, "
+                             f"got {tuple(g.shape)}")
+        _lib.require_device(g)
         grad_z = torch.empty_like(x)
         gc1, gt0, gt1 = _bwd_grads(filters, x.device)
         lib = _lib.load()
@@ -93,7 +99,8 @@ def fbt_recompute_forward_raw(C1, tap0, tap1, x, skip=None):
     kernel's output store: the encoder's residual connection
     (pure.py:530-534) without a separate pass."""
     x = _c64(x)
-    _lib.require_device(x, skip)
+    if x.dim() != 3:
+        raise ValueError(f"expected (filters, batch, time) input, got shape {tuple(x.shape)}")
     filters, batch, time = x.shape
     C1, tap0, tap1 = _coefs(C1, tap0, tap1, filters)
     if skip is not None:
@@ -101,6 +108,7 @@ def fbt_recompute_forward_raw(C1, tap0, tap1, x, skip=None):
             raise ValueError(f"skip must have the drive's shape {tuple(x.shape)}, "
                              f"got {tuple(skip.shape)}")
         skip = _c64(skip)
+    _lib.require_device(x, skip, C1)
     lib = _lib.load()
     nchunks = lib.rqf_fbt_carry_chunks(time)
     act = torch.empty_like(x)

@@ -92,10 +92,10 @@ def _forward(C1, C2, u, cw, num_osc, *, real: bool, absolute: bool):
     C1, C2 = _c64(C1), _c64(C2)
     u = _f32(u) if real else _c64(u)
     cw = None if cw is None else _c64(cw)
-    _lib.require_device(C1, C2, u, cw)
     B, T, F = _check(u, C1, C2, num_osc)
     if cw is not None and cw.shape != (F * num_osc,):
         raise ValueError(f"C-weights must cover {F * num_osc} oscillators, got {tuple(cw.shape)}")
+    _lib.require_device(C1, C2, u, cw)
     out = torch.empty(B, T, F, device=u.device,
                       dtype=torch.float32 if absolute else torch.complex64)
     lib = _lib.load()
@@ -118,7 +118,6 @@ def _backward(C1, C2, u, c_weights, grad_output, num_osc, *, real: bool, compute
     u = _f32(u) if real else _c64(u)
     cw = _c64(_cw_complex(c_weights))
     grad_output = _c64(grad_output)
-    _lib.require_device(C1, C2, u, cw, grad_output)
     B, T, F = _check(u, C1, C2, num_osc)
     if cw.shape != (F * num_osc,):
         raise ValueError(f"c_weights must cover {F * num_osc} oscillators, got "
@@ -126,6 +125,7 @@ def _backward(C1, C2, u, c_weights, grad_output, num_osc, *, real: bool, compute
     if grad_output.shape != (B, T, F):
         raise ValueError(f"grad_output must have shape {(B, T, F)}, got "
                          f"{tuple(grad_output.shape)}")
+    _lib.require_device(C1, C2, u, cw, grad_output)
     dev = u.device
     grad_u = torch.empty_like(u) if compute_grad_u else None
     gc1 = torch.empty(F * num_osc, dtype=torch.complex64, device=dev) if compute_grad_C1 else None

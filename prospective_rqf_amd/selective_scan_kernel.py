@@ -117,6 +117,37 @@ def inputs_struct(z: torch.Tensor, inputs) -> tuple[_lib.SelectiveInputsStruct, 
     return s, [gl, dl, wl, groups, order, *params]
 
 
+def _check_chunk(chunk) -> int:
+    """The chunk must be a positive power of two (selective_scan.py:213-216)."""
+    c = int(chunk)
+    if c <= 0 or c & (c - 1):
+        raise ValueError(f"chunk must be a positive power of two, got {chunk}")
+    return c
+
+
+def _check_drive(z) -> None:
+    if z.dtype != torch.complex64:
+        raise TypeError("the selective scan expects a complex64 drive")
+    if z.dim() != 3:
+        raise ValueError(f"expected a (filters, batch, time) drive, got shape {tuple(z.shape)}")
+
+
+def _check_backward(z, entries, gy, gx, chunk) -> None:
+    """Shapes the backward kernel reads through: every cotangent covers the
+    drive's (F, B, T) and ``entries`` holds one complex64 state per (row,
+    chunk), the forward's ``(F*B, ceil(T/chunk))`` (the reference takes the
+    chunk count from ``entries.shape[1]``, selective_scan_kernel.py:545)."""
+    f, b, t = z.shape
+    for name, g in (("gy", gy), ("gx", gx)):
+        if g is not None and tuple(g.shape) != (f, b, t):
+            raise ValueError(f"{name} must have the drive's shape {(f, b, t)}, "
+                             f"got {tuple(g.shape)}")
+    want = (f * b, -(-t // chunk))
+    if entries.dtype != torch.complex64 or tuple(entries.shape) != want:
+        raise ValueError(f"entries must be complex64 of shape {want} (one state per row and "
+                         f"chunk of {chunk}), got {entries.dtype} {tuple(entries.shape)}")
+
+
 def selective_forward(z, inputs, activate, write_raw, chunk, skip=None):
     """Fused forward: returns ``(raw|None, act|None, entries)``.
 
@@ -126,14 +157,16 @@ def selective_forward(z, inputs, activate, write_raw, chunk, skip=None):
     encoder's residual connection (pure.py:486-496) without separate passes;
     entries stay the scan's own states.
     """
+    _check_drive(z)
+    chunk = _check_chunk(chunk)
+    if not (activate or write_raw):
+        raise ValueError("selective_forward needs activate or write_raw")
+    if skip is not None and skip.shape != z.shape:
+        raise ValueError(f"skip must have the drive's shape {tuple(z.shape)}, "
+                         f"got {tuple(skip.shape)}")
     _lib.require_device(z, skip)
-    if z.dtype != torch.complex64:
-        raise TypeError("selective_forward expects a complex64 drive")
     z = z.resolve_conj().contiguous()
     if skip is not None:
-        if skip.shape != z.shape:
-            raise ValueError(f"skip must have the drive's shape {tuple(z.shape)}, "
-                             f"got {tuple(skip.shape)}")
         skip = skip.to(torch.complex64).resolve_conj().contiguous()
     f, b, t = z.shape
     nc = -(-t // chunk)
@@ -157,8 +190,12 @@ def selective_forward(z, inputs, activate, write_raw, chunk, skip=None):
 def selective_backward(z, inputs, entries, gy, gx, activate, truncated, chunk):
     """Fused backward: ``(dz, dzw, dg|None, dd_group|None, dw|None, dbias, dtheta)``.
 
-    ``dzw`` is the same tensor as ``dz`` unless ``truncated``.
+    ``dzw`` is the same tensor as ``dz`` unless ``truncated``.  Every shape
+    is checked on the host before any launch (``ValueError``).
     """
+    _check_drive(z)
+    chunk = _check_chunk(chunk)
+    _check_backward(z, entries, gy, gx, chunk)
     _lib.require_device(z, entries, gy, gx)
     z = z.resolve_conj().contiguous()
     f, b, t = z.shape

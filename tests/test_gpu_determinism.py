@@ -6,7 +6,7 @@ repeated call on the same inputs must return identical bits (the reference's
 selective path promises this too, docs/selective_rqf.md:114).  The shapes
 are large enough to spread each reduction over many blocks: several splits per
 warp group in the selective backward, many segments and tasks in the
-three-phase scans.
+single-pass (B,T,F) and multi-oscillator scans.
 """
 
 import numpy as np

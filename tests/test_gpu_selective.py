@@ -324,34 +324,44 @@ def test_group_form(monkeypatch, F, B, T, warp, G, chunk, truncated, edit, team)
              edit=edit, seed=F + T + chunk)
 
 
-def test_group_form_wait_timeout_reports_nan(monkeypatch):
+@pytest.mark.parametrize("truncated", [False, True])
+def test_group_form_wait_timeout_reports_nan(monkeypatch, truncated):
     """Every wait of the group form is bounded, and a wait that runs out ends
     the block's other waits.  With RQF_GRP_FORCE_TIMEOUT=1 the host starts
     every block in that state: the kernel still returns, and each block
-    reports NaN for its channels' dbias and dtheta instead of hanging.
-    Without the switch the same call gives finite results."""
+    overwrites every output it owns (dz, dzw, dg, dw, its dd row, and its
+    channels' dbias / dtheta partials) with NaN instead of hanging or leaving
+    finite, wrong values.  The next call without the switch matches the fp64
+    oracle."""
     F, B, T, G = 8, 2, 2048, 2
-    print(f"case: group form wait timeout F={F} B={B} T={T} G={G}", flush=True)
+    print(f"case: group form wait timeout F={F} B={B} T={T} G={G} truncated={truncated}",
+          flush=True)
     monkeypatch.setenv("RQF_BWD_FORM", "group")
     monkeypatch.setenv("RQF_BWD_GRP_TEAM", "4")
     rng = np.random.default_rng(11)
     inp = rounded_to_f32(make_inputs(F, B, T, CASE_ALL, rng, G=G))
     ti = to_torch(inp, device="cuda")
+    zc, gyc, gxc = (_c64(crandn(rng, F, B, T)) for _ in range(3))
     dev = lambda a: torch.as_tensor(a.astype(np.complex64), device="cuda")  # noqa: E731
-    z, gy, gx = (dev(crandn(rng, F, B, T)) for _ in range(3))
+    z, gy, gx = dev(zc), dev(gyc), dev(gxc)
     raw, act, entries = selective_forward(z, ti, True, True, 256)
+    names = ("dz", "dzw", "dg", "dd", "dw", "dbias", "dtheta")
 
     def grads():
-        out = selective_backward(z, ti, entries, gy, gx, True, False, 256)
+        out = selective_backward(z, ti, entries, gy, gx, True, truncated, 256)
         torch.cuda.synchronize()
-        return out[5], out[6]
+        return dict(zip(names, out))
 
     monkeypatch.setenv("RQF_GRP_FORCE_TIMEOUT", "1")
-    dbias, dtheta = grads()
-    assert torch.isnan(dbias).all() and torch.isnan(dtheta).all()
+    forced = grads()
+    for name in names:
+        assert torch.isnan(forced[name]).all(), name
     monkeypatch.delenv("RQF_GRP_FORCE_TIMEOUT")
-    dbias, dtheta = grads()
-    assert torch.isfinite(dbias).all() and torch.isfinite(dtheta).all()
+    got = grads()
+    ref = dict(zip(names, oracle.selective_bwd(zc, inp, gyc, gxc, truncated=truncated)))
+    for name in names:
+        assert torch.isfinite(got[name]).all(), name
+        assert relerr(got[name], ref[name]) <= PARITY_RTOL, name
 
 
 @pytest.mark.parametrize("truncated", [False, True])

@@ -123,3 +123,35 @@ def test_layer0_rejects_bad_shapes_before_launch(bad):
         batch = 3
     with pytest.raises(ValueError):
         fbt_layer0_real_scan(w, h, c, c, c, batch)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("D,n", [(1, 2000), (2, 64000), (2, 4100)])
+def test_layer0_grads_read_no_element_past_grad_z(D, n):
+    """``rqf_layer0_grads`` with 16-byte loads (n % 4 == 0) and n not a
+    multiple of a block's 1024 columns: grad_z is the front of a larger buffer
+    whose tail is NaN, so any load past its end would turn grad_w / grad_h
+    into NaN.  Both must match the fp64 chain rule."""
+    from prospective_rqf_amd.fbt_scan_kernel import _layer0_grads
+
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    print(f"case: layer0 grads NaN tail D={D} n={n}", flush=True)
+    rng = np.random.default_rng(n + D)
+    F = 3
+    w = _f32(rng.standard_normal((2 * F, D)))
+    h = _f32(rng.standard_normal((D, n)))
+    gz = np.asarray(crandn(rng, F, n), np.complex64).astype(np.complex128)
+    buf = torch.full((F * n + 4096,), complex(float("nan"), float("nan")),
+                     dtype=torch.complex64, device="cuda")
+    buf[:F * n] = torch.as_tensor(gz.astype(np.complex64).reshape(-1), device="cuda")
+    gz_dev = buf[:F * n].view(F, n)
+    W = torch.as_tensor(w.astype(np.float32), device="cuda")
+    H = torch.as_tensor(h.astype(np.float32), device="cuda")
+    grad_w, grad_h = _layer0_grads(W, gz_dev, H, True, True)
+    torch.cuda.synchronize()
+    gw_ref = np.concatenate([gz.real @ h.T, gz.imag @ h.T])
+    gh_ref = w[:F].T @ gz.real + w[F:].T @ gz.imag
+    assert torch.isfinite(grad_w).all() and torch.isfinite(grad_h).all()
+    assert relerr(grad_w, gw_ref) <= PARITY_RTOL
+    assert relerr(grad_h, gh_ref) <= PARITY_RTOL

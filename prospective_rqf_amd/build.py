@@ -7,6 +7,7 @@ git-ignored.
 
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import shutil
 import subprocess
@@ -46,18 +47,22 @@ def compile_flags() -> list[str]:
 
 
 def build(verbose: bool = False) -> str:
-    """Compile every HIP source and link the shared library; returns its path."""
-    objs = []
+    """Compile every HIP source (concurrently) and link the shared library;
+    returns its path."""
     build_dir = os.path.join(PKG_DIR, "_objs")
     os.makedirs(build_dir, exist_ok=True)
     cc = hipcc()
-    for src in SOURCES:
-        obj = os.path.join(build_dir, src.replace(".hip", ".o"))
-        cmd = [cc, *compile_flags(), "-c", os.path.join(CSRC, src), "-o", obj]
-        if verbose:
+    objs = [os.path.join(build_dir, src.replace(".hip", ".o")) for src in SOURCES]
+    cmds = [[cc, *compile_flags(), "-c", os.path.join(CSRC, src), "-o", obj]
+            for src, obj in zip(SOURCES, objs)]
+    if verbose:
+        for cmd in cmds:
             print(" ".join(cmd), flush=True)
-        subprocess.run(cmd, check=True)
-        objs.append(obj)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=len(cmds)) as pool:
+        for done in pool.map(lambda c: subprocess.run(c, capture_output=True, text=True), cmds):
+            sys.stderr.write(done.stderr)
+            if done.returncode:
+                raise subprocess.CalledProcessError(done.returncode, done.args)
     tmp = LIB_PATH + ".tmp"
     cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     if verbose:

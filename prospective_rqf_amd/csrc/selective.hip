@@ -595,6 +595,27 @@ struct BwdRow {
   double sum_bias, sum_theta;
 };
 
+// Cotangent set of a backward call.  Calls with a single cotangent (raw
+// only: gy; act only: gx) under full BPTT are compiled with it fixed, so a
+// tile carries no register, load, mask or select for the absent one and no
+// run-time test of the truncation flag: config 4's raw-only layer 1
+// backward 0.608 -> 0.590-0.594 ms (rotated runs on one box).  kCtRuntime
+// reads everything from the call; it also serves calls with both cotangents,
+// whose fixed form measured 0.7% slower at config 3 (2.669 -> 2.688 ms) with
+// 3.4% fewer VALU instructions but more spilled registers.
+enum : int { kCtRuntime = 0, kCtGy = 1, kCtGx = 2 };
+template <int CT>
+struct Cot {
+  static constexpr bool fixed = CT != kCtRuntime;
+  static constexpr bool gy = CT == kCtGy;
+  static constexpr bool gx = CT == kCtGx;
+};
+// Truncated backward (TBPTT(1))?  Never for a fixed cotangent set.
+template <int CT>
+__device__ __forceinline__ bool truncated_of(int truncated) {
+  return Cot<CT>::fixed ? false : truncated != 0;
+}
+
 // Staged warp values of the lane's K steps (from LDS): the frequency factor
 // exp(warp_scale * tanh) and the tanh derivative factor warp_scale*(1 - tanh^2).
 template <int K>
@@ -641,7 +662,7 @@ struct BwdTile {
 // forward replay from the tile's entry state and the cotangent e on raw.
 // The warp values of the tile come from the block's LDS stage (r.swg, r.sws).
 // zv: the tile's drive; zprev_tile: z[t0 - 1] (0 at t0 = 0).
-template <int K, bool VEC, bool TAIL>
+template <int K, bool VEC, bool TAIL, int CT>
 __device__ __forceinline__ void bwd_tile_replay(const rqf_selective_inputs& p, const Chan& c,
                                                 const BwdRow& r, int t0, int lane,
                                                 const c32 (&zv)[K], c32 zprev_tile,
@@ -669,13 +690,13 @@ __device__ __forceinline__ void bwd_tile_replay(const rqf_selective_inputs& p, c
   // Forward states y[t-1] of every step, and the cotangent e[t] on raw: the
   // raw output plus the split-ReLU cotangent where raw > 0.
   c32 ey[K], ex[K];
-  if (r.gyr) {
+  if (Cot<CT>::fixed ? Cot<CT>::gy : r.gyr != nullptr) {
     load_c<K, VEC, TAIL>(r.gyr, tb, T, ey);
   } else {
 #pragma unroll
     for (int k = 0; k < K; ++k) ey[k] = mk(0.0f, 0.0f);
   }
-  if (r.gxr) {
+  if (Cot<CT>::fixed ? Cot<CT>::gx : r.gxr != nullptr) {
     load_c<K, VEC, TAIL>(r.gxr, tb, T, ex);
   } else {
 #pragma unroll
@@ -704,8 +725,13 @@ __device__ __forceinline__ void bwd_tile_replay(const rqf_selective_inputs& p, c
     for (int k = 0; k < K; ++k) {
       s.yprev[k] = yk;
       yk = cmad(Am[k], yk, u[k]);
-      s.ecot[k] = mk(ey[k].r + (yk.r > 0.0f ? ex[k].r : 0.0f),
-                     ey[k].i + (yk.i > 0.0f ? ex[k].i : 0.0f));
+      if constexpr (Cot<CT>::gy)
+        s.ecot[k] = ey[k];
+      else if constexpr (Cot<CT>::gx)
+        s.ecot[k] = mk(yk.r > 0.0f ? ex[k].r : 0.0f, yk.i > 0.0f ? ex[k].i : 0.0f);
+      else
+        s.ecot[k] = mk(ey[k].r + (yk.r > 0.0f ? ex[k].r : 0.0f),
+                       ey[k].i + (yk.i > 0.0f ? ex[k].i : 0.0f));
     }
   }
   if (TAIL) {
@@ -744,7 +770,7 @@ __device__ __forceinline__ void bwd_lane_adjoint(const BwdTile<K>& s, c32 A_lane
 // after the lane's last (the cotangent there when truncated), the decay
 // A_lane_next and the lag-tap weight cn_lane_next of that step.  gd_out
 // (optional) receives the lane's warp-logit gradients.
-template <int K, bool VEC, bool TAIL>
+template <int K, bool VEC, bool TAIL, int CT>
 __device__ __forceinline__ void bwd_tile_grads(const rqf_selective_inputs& p, const Chan& c,
                                                BwdRow& r, int t0, int lane, const c32 (&zv)[K],
                                                const BwdTile<K>& s, c32 dnext, c32 A_lane_next,
@@ -767,7 +793,7 @@ __device__ __forceinline__ void bwd_tile_grads(const rqf_selective_inputs& p, co
       cn = p.prospective ? s.gate[k + 1] * ratio_gamma(p, c, s.gam[k + 1]) : 0.0f;
     else
       cn = cn_lane_next;
-    const c32 d = r.truncated ? s.ecot[k] : cjmad(An, dnext, s.ecot[k]);
+    const c32 d = truncated_of<CT>(r.truncated) ? s.ecot[k] : cjmad(An, dnext, s.ecot[k]);
     const float gamma = s.gam[k], gt = s.gate[k];
     const float rg = p.prospective ? ratio_gamma(p, c, gamma) : 0.0f;
     const float gh = gamma * c.eta;
@@ -860,7 +886,7 @@ __device__ __forceinline__ void bwd_tile_grads(const rqf_selective_inputs& p, co
   r.sum_bias += (double)tile_bias;
   r.sum_theta += (double)tile_theta;
   store_c<K, VEC, TAIL>(r.dzwr, tb, T, gzw);
-  if (r.truncated) store_c<K, VEC, TAIL>(r.dzr, tb, T, gz);
+  if (truncated_of<CT>(r.truncated)) store_c<K, VEC, TAIL>(r.dzr, tb, T, gz);
   if (r.dgr) store_f<K, VEC, TAIL>(r.dgr, tb, T, gg);
   if (r.dwr) store_f<K, VEC, TAIL>(r.dwr, tb, T, gw);
   if (r.sdd) {
@@ -879,11 +905,11 @@ __device__ __forceinline__ void bwd_tile_grads(const rqf_selective_inputs& p, co
 // One backward tile of a row walked by one wavefront: the tile's exit adjoint
 // state (r.dcarry) and the next tile's first decay and lag-tap weight
 // (r.Afirst, r.cfirst) come in through r and go out for the tile before it.
-template <int K, bool VEC, bool TAIL>
+template <int K, bool VEC, bool TAIL, int CT>
 __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Chan& c, BwdRow& r,
                                          int t0, int lane, const c32 (&zv)[K], c32 zprev_tile) {
   BwdTile<K> s;
-  bwd_tile_replay<K, VEC, TAIL>(p, c, r, t0, lane, zv, zprev_tile, s);
+  bwd_tile_replay<K, VEC, TAIL, CT>(p, c, r, t0, lane, zv, zprev_tile, s);
   const c32 A_lane_next = shift_down(s.A[0], r.Afirst, lane);
   const float cn_lane_next = shift_down(s.c0, r.cfirst, lane);
   r.Afirst = readlane(s.A[0], 0);
@@ -891,7 +917,7 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
 
   // Adjoint d[t] = e[t] + conj(A[t+1]) d[t+1]  (truncated: d = e).
   c32 dnext;
-  if (r.truncated) {
+  if (truncated_of<CT>(r.truncated)) {
     dnext = shift_down(s.ecot[0], r.dcarry, lane);
     r.dcarry = readlane(s.ecot[0], 0);
   } else {
@@ -903,7 +929,7 @@ __device__ __forceinline__ void bwd_tile(const rqf_selective_inputs& p, const Ch
     r.dcarry = readlane(rr, 0);
   }
 
-  bwd_tile_grads<K, VEC, TAIL>(p, c, r, t0, lane, zv, s, dnext, A_lane_next, cn_lane_next);
+  bwd_tile_grads<K, VEC, TAIL, CT>(p, c, r, t0, lane, zv, s, dnext, A_lane_next, cn_lane_next);
 }
 
 // ---------------------------------------------------------------------------
@@ -1098,7 +1124,7 @@ __global__ __launch_bounds__(256) void team_build_kernel(const int64_t* __restri
   }
 }
 
-template <int O, bool VEC>
+template <int O, bool VEC, int CT>
 __global__ __launch_bounds__(kTeam* kWave)
     __attribute__((amdgpu_waves_per_eu(RQF_BWD_WAVES_PER_EU))) void selective_bwd_team_kernel(
         const rqf_selective_inputs pin, const float* __restrict__ z,
@@ -1214,10 +1240,10 @@ __global__ __launch_bounds__(kTeam* kWave)
           c32 zv[K];
           if (tile >= full) {
             load_c<K, VEC, true>(r.zr, t0 + lane * K, T, zv);
-            bwd_tile<K, VEC, true>(p, c, r, t0, lane, zv, zprev_tile);
+            bwd_tile<K, VEC, true, CT>(p, c, r, t0, lane, zv, zprev_tile);
           } else {
             load_c<K, VEC, false>(r.zr, t0 + lane * K, T, zv);
-            bwd_tile<K, VEC, false>(p, c, r, t0, lane, zv, zprev_tile);
+            bwd_tile<K, VEC, false, CT>(p, c, r, t0, lane, zv, zprev_tile);
           }
         }
         if (warp) {
@@ -1339,13 +1365,14 @@ __device__ __forceinline__ void lds_release_add(int* counter, int lane) {
   if (lane == 0) __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-template <int O, bool VEC, int TC>
+template <int O, bool VEC, int TC, int CT>
 __global__ __launch_bounds__(kGrpWaves* kWave)
     __attribute__((amdgpu_waves_per_eu(RQF_BWD_WAVES_PER_EU))) void selective_bwd_grp_kernel(
         const rqf_selective_inputs pin, const float* __restrict__ z,
         const float* __restrict__ entries, int chunk, int nc, const float* __restrict__ gy,
         const float* __restrict__ gx, int truncated, BwdOut o, int abort0) {
   const rqf_selective_inputs p = with_options<O>(pin);
+  const bool trunc = truncated_of<CT>(truncated);
   constexpr int kGrpTC = TC, kGrpTW = kGrpWaves / TC, kGrpSegSt = kGrpSegTiles / kGrpTW;
   static_assert(kGrpTC * kGrpTW == kGrpWaves && kGrpSegSt * kGrpTW == kGrpSegTiles,
                 "slot shape");
@@ -1491,12 +1518,12 @@ __global__ __launch_bounds__(kGrpWaves* kWave)
               t0 > 0 ? mk(r.zr[2 * (t0 - 1)], r.zr[2 * (t0 - 1) + 1]) : mk(0.0f, 0.0f);
           if (tile >= full) {
             load_c<K, VEC, true>(r.zr, t0 + lane * K, T, zv);
-            bwd_tile_replay<K, VEC, true>(p, c, r, t0, lane, zv, zprev_tile, s);
+            bwd_tile_replay<K, VEC, true, CT>(p, c, r, t0, lane, zv, zprev_tile, s);
           } else {
             load_c<K, VEC, false>(r.zr, t0 + lane * K, T, zv);
-            bwd_tile_replay<K, VEC, false>(p, c, r, t0, lane, zv, zprev_tile, s);
+            bwd_tile_replay<K, VEC, false, CT>(p, c, r, t0, lane, zv, zprev_tile, s);
           }
-          if (!truncated) {
+          if (!trunc) {
             // Lane 63's step after its last is the next tile's first: its
             // decay stays out of the tile's own map (1 here) and comes in with D'.
             const c32 A_ln = shift_down(s.A[0], mk(1.0f, 0.0f), lane);
@@ -1507,7 +1534,7 @@ __global__ __launch_bounds__(kGrpWaves* kWave)
             wave_scan_rev(Q, rr, lane);
           }
           if (lane == 0) {
-            s_map[buf][cs][tw][0] = truncated ? make_float4(s.ecot[0].r, s.ecot[0].i, 0.0f, 0.0f)
+            s_map[buf][cs][tw][0] = trunc ? make_float4(s.ecot[0].r, s.ecot[0].i, 0.0f, 0.0f)
                                               : make_float4(rr.r, rr.i, Q.r, Q.i);
             s_map[buf][cs][tw][1] = make_float4(s.A[0].r, s.A[0].i, s.c0, 0.0f);
           }
@@ -1533,7 +1560,7 @@ __global__ __launch_bounds__(kGrpWaves* kWave)
             c1 = cn;
           }
           const float4 m0 = s_map[buf][cs][j][0], m1 = s_map[buf][cs][j][1];
-          Dn = truncated ? mk(m0.x, m0.y) : cmad(mk(m0.z, m0.w), cjmul(An, Dn), mk(m0.x, m0.y));
+          Dn = trunc ? mk(m0.x, m0.y) : cmad(mk(m0.z, m0.w), cjmul(An, Dn), mk(m0.x, m0.y));
           An = mk(m1.x, m1.y);
           cn = m1.z;
         }
@@ -1547,7 +1574,7 @@ __global__ __launch_bounds__(kGrpWaves* kWave)
           const c32 A_lane_next = shift_down(s.A[0], A1, lane);
           const float cn_lane_next = shift_down(s.c0, c1, lane);
           c32 dnext;
-          if (truncated) {
+          if (trunc) {
             dnext = shift_down(s.ecot[0], D1, lane);
           } else {
             // the lane's adjoint at its first step, then the next lane's
@@ -1555,10 +1582,10 @@ __global__ __launch_bounds__(kGrpWaves* kWave)
             dnext = shift_down(dfirst, D1, lane);
           }
           if (tile >= full)
-            bwd_tile_grads<K, VEC, true>(p, c, r, t0, lane, zv, s, dnext, A_lane_next,
+            bwd_tile_grads<K, VEC, true, CT>(p, c, r, t0, lane, zv, s, dnext, A_lane_next,
                                                cn_lane_next, gd);
           else
-            bwd_tile_grads<K, VEC, false>(p, c, r, t0, lane, zv, s, dnext, A_lane_next,
+            bwd_tile_grads<K, VEC, false, CT>(p, c, r, t0, lane, zv, s, dnext, A_lane_next,
                                                 cn_lane_next, gd);
         }
         // The group sum of this tile's steps, in the fixed (team, channel)
@@ -1805,6 +1832,24 @@ void with_option_set(int opts, Fn&& fn) {
   }
 }
 
+// Cotangent set a backward call is compiled for: fixed for one cotangent
+// under full BPTT with float4 rows and a compiled option set, else run time.
+int cotangent_set(int opts, bool vec, const float* gy, const float* gx, bool truncated) {
+  if (truncated || !vec || opts == kOptRuntime || (gy != nullptr) == (gx != nullptr))
+    return kCtRuntime;
+  return gy ? kCtGy : kCtGx;
+}
+
+// Calls fn(std::integral_constant<int, CT>) with CT the compiled cotangent set.
+template <class Fn>
+void with_cotangent_set(int ct, Fn&& fn) {
+  switch (ct) {
+    case kCtGy: fn(std::integral_constant<int, kCtGy>{}); return;
+    case kCtGx: fn(std::integral_constant<int, kCtGx>{}); return;
+    default: fn(std::integral_constant<int, kCtRuntime>{}); return;
+  }
+}
+
 // RQF_GRP_FORCE_TIMEOUT=1 starts every block of the group-form backward in
 // the state a wait that ran out leaves (tests of that path): the waits give up
 // at once and the blocks report NaN for their channels' dbias and dtheta,
@@ -2046,25 +2091,40 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
     // The group form finds its group's channels itself: no team table.
     if (w.group_form) {
       const dim3 grid((unsigned)(in->G * in->B)), block(kGrpWaves * kWave);
-      with_option_set(options_of(in), [&](auto oc) {
+      const int abort0 = grp_force_timeout();
+      auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, block, 0, s, *in, z, ent, ent_chunk, nc, gy, gx,
+                           (int)truncated, o, abort0);
+      };
+      const int opts = options_of(in);
+      with_option_set(opts, [&](auto oc) {
         constexpr int O = decltype(oc)::value;
         if constexpr (O != kOptRuntime && !(O & kOptWarp)) {
           return;  // not reached: the group form needs the warp head
         } else {
-          const int abort0 = grp_force_timeout();
-          auto go = [&](auto kern) {
-            hipLaunchKernelGGL(kern, grid, block, 0, s, *in, z, ent, ent_chunk, nc, gy, gx,
-                               (int)truncated, o, abort0);
-          };
-          if (w.tsize == 3)
-            vec ? go(selective_bwd_grp_kernel<O, true, 3>)
-                : go(selective_bwd_grp_kernel<O, false, 3>);
-          else if (w.tsize == 6)
-            vec ? go(selective_bwd_grp_kernel<O, true, 6>)
-                : go(selective_bwd_grp_kernel<O, false, 6>);
-          else
-            vec ? go(selective_bwd_grp_kernel<O, true, 4>)
-                : go(selective_bwd_grp_kernel<O, false, 4>);
+          with_cotangent_set(cotangent_set(O, vec, gy, gx, truncated), [&](auto cc) {
+            constexpr int CT = decltype(cc)::value;
+            if constexpr (CT != kCtRuntime) {
+              // fixed sets: float4 rows under a compiled option set only
+              if constexpr (O != kOptRuntime) {
+                if (w.tsize == 3)
+                  go(selective_bwd_grp_kernel<O, true, 3, CT>);
+                else if (w.tsize == 6)
+                  go(selective_bwd_grp_kernel<O, true, 6, CT>);
+                else
+                  go(selective_bwd_grp_kernel<O, true, 4, CT>);
+              }
+            } else if (w.tsize == 3) {
+              vec ? go(selective_bwd_grp_kernel<O, true, 3, CT>)
+                  : go(selective_bwd_grp_kernel<O, false, 3, CT>);
+            } else if (w.tsize == 6) {
+              vec ? go(selective_bwd_grp_kernel<O, true, 6, CT>)
+                  : go(selective_bwd_grp_kernel<O, false, 6, CT>);
+            } else {
+              vec ? go(selective_bwd_grp_kernel<O, true, 4, CT>)
+                  : go(selective_bwd_grp_kernel<O, false, 4, CT>);
+            }
+          });
         }
       });
       launch_finish(nullptr, nullptr, nullptr, 0, 0, partial, dbias, dtheta, in->F, in->B, s);
@@ -2103,12 +2163,20 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
     const dim3 grid((unsigned)(kXcds * w.split_slots * bc)), block(kTeam * kWave);
     with_option_set(options_of(in), [&](auto oc) {
       constexpr int O = decltype(oc)::value;
-      if (vec)
-        hipLaunchKernelGGL((selective_bwd_team_kernel<O, true>), grid, block, 0, s, *in, z, ent,
-                           ent_chunk, nc, gy, gx, (int)truncated, tm, o);
-      else
-        hipLaunchKernelGGL((selective_bwd_team_kernel<O, false>), grid, block, 0, s, *in, z, ent,
-                           ent_chunk, nc, gy, gx, (int)truncated, tm, o);
+      with_cotangent_set(cotangent_set(O, vec, gy, gx, truncated), [&](auto cc) {
+        constexpr int CT = decltype(cc)::value;
+        if constexpr (CT != kCtRuntime) {
+          if constexpr (O != kOptRuntime)
+            hipLaunchKernelGGL((selective_bwd_team_kernel<O, true, CT>), grid, block, 0, s, *in,
+                               z, ent, ent_chunk, nc, gy, gx, (int)truncated, tm, o);
+        } else if (vec) {
+          hipLaunchKernelGGL((selective_bwd_team_kernel<O, true, CT>), grid, block, 0, s, *in, z,
+                             ent, ent_chunk, nc, gy, gx, (int)truncated, tm, o);
+        } else {
+          hipLaunchKernelGGL((selective_bwd_team_kernel<O, false, CT>), grid, block, 0, s, *in, z,
+                             ent, ent_chunk, nc, gy, gx, (int)truncated, tm, o);
+        }
+      });
     });
     launch_finish(o.dd_part, gsplit, dd, in->G, in->B * T, partial, dbias, dtheta, in->F, in->B,
                   s);

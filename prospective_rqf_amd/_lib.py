@@ -153,14 +153,21 @@ def check(code: int, what: str) -> None:
 
 
 def ptr(t: torch.Tensor | None):
-    """Device pointer of a tensor (None -> NULL)."""
+    """Device pointer of a tensor as an int (None -> NULL); the bound
+    functions declare ``c_void_p`` arguments, which take either."""
     if t is None:
         return None
-    return ctypes.c_void_p(t.data_ptr())
+    return t.data_ptr()
 
 
 def stream_of(t: torch.Tensor):
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    """Handle of torch's current stream on the tensor's device (the launch
+    stream), read without building a ``torch.cuda.Stream`` object: this is on
+    every call's path, and small calls are bound by their host time."""
+    return _raw_stream(t.get_device())
+
+
+_raw_stream = torch._C._cuda_getCurrentRawStream
 
 
 def require_device(*tensors: torch.Tensor | None) -> None:

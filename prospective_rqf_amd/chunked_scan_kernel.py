@@ -33,6 +33,8 @@ def _pick_chunk(filters: int, batch: int) -> int:
 def _c64(t: torch.Tensor | None) -> torch.Tensor | None:
     if t is None:
         return None
+    if t.dtype is torch.complex64 and t.is_contiguous() and not t.is_conj():
+        return t  # the common case, without a conversion call
     if not t.is_complex():
         t = t.to(torch.cfloat)
     return t.to(torch.complex64).resolve_conj().contiguous()
@@ -54,8 +56,15 @@ def _check_like(u: torch.Tensor, **tensors) -> None:
                              f"got {tuple(t.shape)}")
 
 
+_WS_BYTES: dict = {}
+
+
 def _ws(B, T, F, device):
-    n = _lib.load().rqf_btf_scan_workspace(B, T, F)
+    """The backward's workspace (fp64 partial sums); its size per shape is
+    asked of the library once."""
+    n = _WS_BYTES.get((B, T, F))
+    if n is None:
+        n = _WS_BYTES[(B, T, F)] = _lib.load().rqf_btf_scan_workspace(B, T, F)
     return _lib.workspace(n, device), n
 
 
@@ -66,10 +75,10 @@ def _chunked_scan_forward_raw(C1, C2, u):
     _lib.require_device(C1, C2, u)
     B, T, F = u.shape
     out = torch.empty_like(u)
-    ws, n = _ws(B, T, F, u.device)
+    # the single-pass forward needs no workspace
     _lib.check(
         _lib.load().rqf_chunked_scan_fwd(_lib.ptr(C1), _lib.ptr(C2), _lib.ptr(u), _lib.ptr(out),
-                                         B, T, F, _lib.ptr(ws), n, _lib.stream_of(u)),
+                                         B, T, F, None, 0, _lib.stream_of(u)),
         "rqf_chunked_scan_fwd",
     )
     return out
@@ -133,11 +142,10 @@ def _chunked_prospective_forward_raw(C1, tap0, tap1, x):
     _lib.require_device(C1, tap0, tap1, x)
     B, T, F = x.shape
     out = torch.empty_like(x)
-    ws, n = _ws(B, T, F, x.device)
     _lib.check(
         _lib.load().rqf_chunked_prospective_fwd(
             _lib.ptr(C1), _lib.ptr(tap0), _lib.ptr(tap1), _lib.ptr(x), _lib.ptr(out), B, T, F,
-            _lib.ptr(ws), n, _lib.stream_of(x)),
+            None, 0, _lib.stream_of(x)),
         "rqf_chunked_prospective_fwd",
     )
     return out

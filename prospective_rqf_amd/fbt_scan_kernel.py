@@ -19,6 +19,8 @@ from prospective_rqf_amd import _lib
 
 
 def _c64(t):
+    if t.dtype is torch.complex64 and t.is_contiguous() and not t.is_conj():
+        return t  # the common case, without a conversion call
     if not t.is_complex():
         t = t.to(torch.cfloat)
     return t.to(torch.complex64).resolve_conj().contiguous()

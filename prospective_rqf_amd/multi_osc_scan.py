@@ -47,6 +47,8 @@ MAX_FILTERS = 1 << 16  # the forward addresses each pass of the sequence through
 
 
 def _c64(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype is torch.complex64 and t.is_contiguous() and not t.is_conj():
+        return t  # the common case, without a conversion call
     if not t.is_complex():
         t = t.to(torch.cfloat)
     return t.to(torch.complex64).resolve_conj().contiguous()

@@ -74,8 +74,12 @@ def inputs_struct(z: torch.Tensor, inputs) -> tuple[_lib.SelectiveInputsStruct, 
     o = inputs.options
     has_gamma, has_warp, has_write = bool(o[0]), bool(o[1]), bool(o[2])
 
+    dev = z.device
+
     def vec(v):
-        return v.to(device=z.device, dtype=torch.float32).contiguous()
+        if v.dtype is torch.float32 and v.device == dev and v.is_contiguous():
+            return v  # the common case, without a conversion call
+        return v.to(device=dev, dtype=torch.float32).contiguous()
 
     gl = vec(inputs.gamma_logits) if has_gamma else None
     dl = vec(inputs.warp_logits) if has_warp else None
@@ -97,7 +101,7 @@ def inputs_struct(z: torch.Tensor, inputs) -> tuple[_lib.SelectiveInputsStruct, 
             raise ValueError("groups must be a (F,) index tensor when the warp head is on")
         if inputs.groups.is_complex() or inputs.groups.is_floating_point():
             raise ValueError("groups must be an integer index tensor")
-        groups, order = _check_groups(inputs.groups, g, z.device)
+        groups, order = _check_groups(inputs.groups, g, dev)
     for name, v in zip(("bias", "theta", "minimum", "span", "step", "horizon",
                         "theta_minimum", "theta_maximum"), params):
         if v.shape != (f,):

@@ -361,17 +361,21 @@ struct FwdIn {
   float gv[K], wv[K], dv[K];
 };
 
+// The heads' presence is taken from the options (compile-time constants of a
+// compiled option set), not from the row pointers: a pointer plus an offset
+// is not provably non-null, and a run-time test keeps a mask alive per head.
 template <int K, bool VEC, bool TAIL>
-__device__ __forceinline__ void fwd_load(const FwdRow& r, int t0, int lane, FwdIn<K>& in) {
+__device__ __forceinline__ void fwd_load(const rqf_selective_inputs& p, const FwdRow& r, int t0,
+                                         int lane, FwdIn<K>& in) {
   const int T = r.T;
   const int tb = t0 + lane * K;
   if (VEC && !TAIL)
     load_c_lds<K>(r.zr, t0, lane, r.io, in.zv);
   else
     load_c<K, VEC, TAIL>(r.zr, tb, T, in.zv);
-  if (r.gr) load_f<K, VEC, TAIL>(r.gr, tb, T, in.gv); else zero(in.gv);
-  if (r.wr) load_f<K, VEC, TAIL>(r.wr, tb, T, in.wv); else zero(in.wv);
-  if (r.dr) load_f<K, VEC, TAIL>(r.dr, tb, T, in.dv); else zero(in.dv);
+  if (p.has_gamma) load_f<K, VEC, TAIL>(r.gr, tb, T, in.gv); else zero(in.gv);
+  if (p.has_write) load_f<K, VEC, TAIL>(r.wr, tb, T, in.wv); else zero(in.wv);
+  if (p.has_warp) load_f<K, VEC, TAIL>(r.dr, tb, T, in.dv); else zero(in.dv);
 }
 
 // Per-step coefficients of one tile: A (decay) and u (drive) of each of the
@@ -517,10 +521,10 @@ __global__ __launch_bounds__(W* kWave)
       const c32 zlast = t0 > 0 ? mk(r.zr[2 * (t0 - 1)], r.zr[2 * (t0 - 1) + 1]) : mk(0.0f, 0.0f);
       FwdIn<K> in;
       if (t0 / TILE < full) {
-        fwd_load<K, VEC, false>(r, t0, lane, in);
+        fwd_load<K, VEC, false>(p, r, t0, lane, in);
         fwd_steps<K, false>(p, c, T, t0, lane, in, zlast, A, u);
       } else {
-        fwd_load<K, VEC, true>(r, t0, lane, in);
+        fwd_load<K, VEC, true>(p, r, t0, lane, in);
         fwd_steps<K, true>(p, c, T, t0, lane, in, zlast, A, u);
       }
       P = A[0];
@@ -595,20 +599,23 @@ struct BwdRow {
   double sum_bias, sum_theta;
 };
 
-// Cotangent set of a backward call.  Calls with a single cotangent (raw
-// only: gy; act only: gx) under full BPTT are compiled with it fixed, so a
-// tile carries no register, load, mask or select for the absent one and no
-// run-time test of the truncation flag: config 4's raw-only layer 1
-// backward 0.608 -> 0.590-0.594 ms (rotated runs on one box).  kCtRuntime
-// reads everything from the call; it also serves calls with both cotangents,
-// whose fixed form measured 0.7% slower at config 3 (2.669 -> 2.688 ms) with
-// 3.4% fewer VALU instructions but more spilled registers.
-enum : int { kCtRuntime = 0, kCtGy = 1, kCtGx = 2 };
+// Cotangent set of a backward call.  Calls under full BPTT with float4 rows
+// and a compiled option set are compiled with it fixed (gy only, gx only or
+// both), so a tile carries no register, load, mask or select for an absent
+// cotangent, no run-time test of the truncation flag or of the heads'
+// pointers.  Measured with rotated runs on one box: config 4's raw-only
+// layer 1 backward 0.608 -> 0.590-0.594 ms; with both cotangents (config 3,
+// config 4's layer 0) 2.698 -> 2.676 and 0.691 -> 0.686 ms, once the
+// cotangent loads are kept below the tile's coefficient math (a scheduling
+// barrier; hoisted above it they raised the register pressure and the
+// fixed form ran 0.7% slower than the run-time one).  kCtRuntime reads
+// everything from the call.
+enum : int { kCtRuntime = 0, kCtGy = 1, kCtGx = 2, kCtGyGx = 3 };
 template <int CT>
 struct Cot {
   static constexpr bool fixed = CT != kCtRuntime;
-  static constexpr bool gy = CT == kCtGy;
-  static constexpr bool gx = CT == kCtGx;
+  static constexpr bool gy = CT == kCtGy || CT == kCtGyGx;
+  static constexpr bool gx = CT == kCtGx || CT == kCtGyGx;
 };
 // Truncated backward (TBPTT(1))?  Never for a fixed cotangent set.
 template <int CT>
@@ -670,8 +677,16 @@ __device__ __forceinline__ void bwd_tile_replay(const rqf_selective_inputs& p, c
   const int T = r.T;
   const int tb = t0 + lane * K;
   float gv[K], wv[K];
-  if (r.gr) load_f<K, VEC, TAIL>(r.gr, tb, T, gv); else zero(gv);
-  if (r.wr) load_f<K, VEC, TAIL>(r.wr, tb, T, wv); else zero(wv);
+  // A fixed cotangent set takes the heads' presence from the options, like
+  // the forward (the run-time form keeps its pointer tests).
+  if (Cot<CT>::fixed ? p.has_gamma : r.gr != nullptr)
+    load_f<K, VEC, TAIL>(r.gr, tb, T, gv);
+  else
+    zero(gv);
+  if (Cot<CT>::fixed ? p.has_write : r.wr != nullptr)
+    load_f<K, VEC, TAIL>(r.wr, tb, T, wv);
+  else
+    zero(wv);
   s.zp0 = shift_up(zv[K - 1], zprev_tile, lane);
 
   // Coefficients; kept per step: A, phi, gamma and gate.
@@ -690,6 +705,9 @@ __device__ __forceinline__ void bwd_tile_replay(const rqf_selective_inputs& p, c
   // Forward states y[t-1] of every step, and the cotangent e[t] on raw: the
   // raw output plus the split-ReLU cotangent where raw > 0.
   c32 ey[K], ex[K];
+  // Keep the cotangent loads below the coefficient math: hoisted above it
+  // they raise the register pressure across the tile's busiest stretch.
+  if (Cot<CT>::fixed) __builtin_amdgcn_sched_barrier(0);
   if (Cot<CT>::fixed ? Cot<CT>::gy : r.gyr != nullptr) {
     load_c<K, VEC, TAIL>(r.gyr, tb, T, ey);
   } else {
@@ -725,9 +743,9 @@ __device__ __forceinline__ void bwd_tile_replay(const rqf_selective_inputs& p, c
     for (int k = 0; k < K; ++k) {
       s.yprev[k] = yk;
       yk = cmad(Am[k], yk, u[k]);
-      if constexpr (Cot<CT>::gy)
+      if constexpr (Cot<CT>::gy && !Cot<CT>::gx)
         s.ecot[k] = ey[k];
-      else if constexpr (Cot<CT>::gx)
+      else if constexpr (Cot<CT>::gx && !Cot<CT>::gy)
         s.ecot[k] = mk(yk.r > 0.0f ? ex[k].r : 0.0f, yk.i > 0.0f ? ex[k].i : 0.0f);
       else
         s.ecot[k] = mk(ey[k].r + (yk.r > 0.0f ? ex[k].r : 0.0f),
@@ -887,8 +905,8 @@ __device__ __forceinline__ void bwd_tile_grads(const rqf_selective_inputs& p, co
   r.sum_theta += (double)tile_theta;
   store_c<K, VEC, TAIL>(r.dzwr, tb, T, gzw);
   if (truncated_of<CT>(r.truncated)) store_c<K, VEC, TAIL>(r.dzr, tb, T, gz);
-  if (r.dgr) store_f<K, VEC, TAIL>(r.dgr, tb, T, gg);
-  if (r.dwr) store_f<K, VEC, TAIL>(r.dwr, tb, T, gw);
+  if (Cot<CT>::fixed ? p.has_gamma : r.dgr != nullptr) store_f<K, VEC, TAIL>(r.dgr, tb, T, gg);
+  if (Cot<CT>::fixed ? p.has_write : r.dwr != nullptr) store_f<K, VEC, TAIL>(r.dwr, tb, T, gw);
   if (r.sdd) {
     static_assert(K % 4 == 0, "whole float4s of warp gradient per lane");
 #pragma unroll
@@ -1832,12 +1850,11 @@ void with_option_set(int opts, Fn&& fn) {
   }
 }
 
-// Cotangent set a backward call is compiled for: fixed for one cotangent
-// under full BPTT with float4 rows and a compiled option set, else run time.
+// Cotangent set a backward call is compiled for: fixed under full BPTT with
+// float4 rows and a compiled option set, else run time.
 int cotangent_set(int opts, bool vec, const float* gy, const float* gx, bool truncated) {
-  if (truncated || !vec || opts == kOptRuntime || (gy != nullptr) == (gx != nullptr))
-    return kCtRuntime;
-  return gy ? kCtGy : kCtGx;
+  if (truncated || !vec || opts == kOptRuntime || (!gy && !gx)) return kCtRuntime;
+  return gy && gx ? kCtGyGx : (gy ? kCtGy : kCtGx);
 }
 
 // Calls fn(std::integral_constant<int, CT>) with CT the compiled cotangent set.
@@ -1845,6 +1862,7 @@ template <class Fn>
 void with_cotangent_set(int ct, Fn&& fn) {
   switch (ct) {
     case kCtGy: fn(std::integral_constant<int, kCtGy>{}); return;
+    case kCtGyGx: fn(std::integral_constant<int, kCtGyGx>{}); return;
     case kCtGx: fn(std::integral_constant<int, kCtGx>{}); return;
     default: fn(std::integral_constant<int, kCtRuntime>{}); return;
   }

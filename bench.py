@@ -334,8 +334,15 @@ def plan_selective(cfg, args, dev):
     cpu_steps = args.cpu_steps or (500 if cfg == 3 else 100)
 
     def cpu():
-        return cpu_baseline_selective(F, args.cpu_batch or min(B, 64), G, cpu_steps, log_scale,
+        base = cpu_baseline_selective(F, args.cpu_batch or min(B, 64), G, cpu_steps, log_scale,
                                       samp, tau, seq, layers)
+        if cfg == 3 and not (args.cpu_steps or args.cpu_batch):
+            # The planned T = 2000 sample, at B = 16 (one run of ~40 s; the
+            # reference's per-element cost grows with T, so this is the more
+            # faithful rate), reported next to the T = 500 one.
+            base["long_sample"] = cpu_baseline_selective(F, 16, G, 2000, log_scale, samp, tau,
+                                                         seq, layers, reps=1, warmup=False)
+        return base
 
     return Plan(name, config, F * B * T * len(layers), (state, ops), nbytes, kernels, cpu,
                 contract)
@@ -703,13 +710,13 @@ def _cpu_threads():
 CPU_REPS = 3
 
 
-def _median_time(run, reps=None):
-    """Median wall time of ``reps`` runs after one warm-up run; each run's time
-    goes to stderr as it ends (long samples would otherwise print nothing for
-    minutes)."""
+def _median_time(run, reps=None, warmup=True):
+    """Median wall time of ``reps`` runs after one warm-up run (none without
+    ``warmup``); each run's time goes to stderr as it ends (long samples would
+    otherwise print nothing for minutes)."""
     reps = CPU_REPS if reps is None else reps
     times = []
-    for i in range(reps + 1):
+    for i in range(0 if warmup else 1, reps + 1):
         t0 = time.perf_counter()
         run()
         dt = time.perf_counter() - t0
@@ -732,7 +739,8 @@ def _cpu_model():
     return platform.processor() or platform.machine()
 
 
-def cpu_baseline_selective(F, B, G, steps, log_scale, samp, tau, seq, layers):
+def cpu_baseline_selective(F, B, G, steps, log_scale, samp, tau, seq, layers, reps=None,
+                           warmup=True):
     import torch
 
     from oracle import torch_ref
@@ -761,7 +769,10 @@ def cpu_baseline_selective(F, B, G, steps, log_scale, samp, tau, seq, layers):
                 loss = loss + (cot.conj() * torch_ref.split_relu(raw)).real.sum()
             loss.backward()
 
-    t = _median_time(run)
+    reps = CPU_REPS if reps is None else reps
+    t = _median_time(run, reps, warmup)
+    timing = (f"median of {reps} after 1 warm-up" if warmup
+              else f"{'one run' if reps == 1 else f'median of {reps}'}, no warm-up")
     return {
         "value": F * B * steps * len(layers) / t / 1e9,
         "unit": "Gelem/s",
@@ -772,9 +783,8 @@ def cpu_baseline_selective(F, B, G, steps, log_scale, samp, tau, seq, layers):
                    f"B={B} T={steps} (T reduced from the GPU shape: like the reference's loop, "
                    f"whose backward of each A[..., t] select materialises a full (F,B,T) "
                    f"gradient, the cost per element grows with T, about 8x from T=200 to "
-                   f"T=1000, so T=2000 takes minutes per run), median of {CPU_REPS} after 1 "
-                   f"warm-up; torch threads={threads} (the GPU box's CPU share is 16 "
-                   f"threads), os.cpu_count()={os.cpu_count()}, cpu={_cpu_model()}"),
+                   f"T=1000), {timing}; torch threads={threads} (the GPU box's CPU share is "
+                   f"16 threads), os.cpu_count()={os.cpu_count()}, cpu={_cpu_model()}"),
     }
 
 

@@ -108,9 +108,10 @@ int rqf_chunked_prospective_bwd(const float *c1, const float *tap0, const float 
  * ------------------------------------------------------------------------ */
 
 /* Workspace bytes of rqf_multi_osc_fwd (backward = 0) or _bwd (backward = 1);
- * 0 for a shape they reject (N < 1, F > 65536).  The forward needs none
- * unless N > 4 with out_abs.  F is limited to 65536 filters: the forward
- * addresses each pass of up to 2048 steps through one 32-bit buffer range. */
+ * 0 for a shape they reject (N < 1 or N > 2^20, B*ceil(F/16) or F*N past
+ * 2^31 - 1).  The forward needs none unless N > 4 with out_abs.  Up to
+ * 65536 filters the forward addresses each pass of up to 2048 steps through
+ * one 32-bit buffer range; wider rows run it with 64-bit addresses. */
 size_t rqf_multi_osc_workspace(int64_t B, int64_t T, int64_t F, int64_t N, int32_t backward);
 
 /* Replaces `_sequential_scan_multi_osc_kernel[grid](...)` with EPILOGUE 0 / 1

@@ -57,6 +57,7 @@
 #include "rqf_scan.h"
 
 #include <algorithm>
+#include <cstdint>
 
 using namespace rqf;
 
@@ -233,9 +234,11 @@ __device__ __forceinline__ FwdMaps fwd_maps(c32 a) {
 // Forward.  yin (optional, complex (B,T,F)) is added to this chunk's y: the
 // earlier chunks' share.  yout receives y (complex) or |y| (ABS).  A block
 // has W wavefronts: 16 (4 per SIMD) where the registers allow it, to hide
-// more memory latency per CU, else 8.
+// more memory latency per CU, else 8.  G64: 64-bit global addresses with a
+// test per element instead of the buffer descriptors, for rows too wide for
+// one 32-bit range per pass (F > kDescFilters).
 // ---------------------------------------------------------------------------
-template <int NP, bool REAL, bool CW, bool ABS, int W>
+template <int NP, bool REAL, bool CW, bool ABS, int W, bool G64>
 __global__ __launch_bounds__(W* kWave) void mosc_fwd_kernel(
     const float* __restrict__ c1, const float* __restrict__ c2, const float* __restrict__ cw,
     const float* __restrict__ u, const float* yin, float* yout, int64_t T, int64_t F, int N,
@@ -261,10 +264,16 @@ __global__ __launch_bounds__(W* kWave) void mosc_fwd_kernel(
   const uint32_t lo_u = lane_off(l, LS, F, kUs), lo_c = lane_off(l, LS, F, 8),
                  lo_a = lane_off(l, LS, F, 4);
   c32 uv[LS], un[LS];
-  load_seg<LS, REAL>(pass_of(u, l, 0, kPass, T, F, kUs), lo_u, uv);
+  auto load_pass = [&](int64_t pt, c32(&v)[LS]) {
+    if constexpr (G64)
+      load_seg_g<LS, REAL>(u, l, pt + (int64_t)l.sg * LS, T, F, v);
+    else
+      load_seg<LS, REAL>(pass_of(u, l, pt, kPass, T, F, kUs), lo_u, v);
+  };
+  load_pass(0, uv);
   int p = 0;
   for (int64_t pt = 0; pt < T; pt += kPass) {
-    if (pt + kPass < T) load_seg<LS, REAL>(pass_of(u, l, pt + kPass, kPass, T, F, kUs), lo_u, un);
+    if (pt + kPass < T) load_pass(pt + kPass, un);
     // Each oscillator's segment from a zero state.
     c32 w[NP];
 #pragma unroll
@@ -306,6 +315,7 @@ __global__ __launch_bounds__(W* kWave) void mosc_fwd_kernel(
     // Replay and write.
     const Pass sy = pass_of(yout, l, pt, kPass, T, F, ABS ? 4 : 8);
     const Pass si = pass_of(yin ? yin : yout, l, pt, kPass, T, F, 8);
+    const int64_t tb = pt + (int64_t)l.sg * LS;
 #pragma unroll
     for (int j = 0; j < LS; ++j) {
       c32 y = mk(0.0f, 0.0f);
@@ -314,11 +324,23 @@ __global__ __launch_bounds__(W* kWave) void mosc_fwd_kernel(
         w[n] = REAL ? cmadr(a[n], w[n], uv[j].r) : cmad(a[n], w[n], uv[j]);
         if (CW || n == 0) y = cmad(hw[n], w[n], y);
       }
-      if (yin) y = cadd(y, buf_ldc(si.at(j), lo_c));
-      if (ABS)
-        buf_stf(sy.at(j), lo_a, sqrtf(fmaf(y.r, y.r, y.i * y.i)));
-      else
-        buf_stc(sy.at(j), lo_c, y);
+      if constexpr (G64) {
+        const bool in = l.fv && tb + j < T;
+        const int64_t e = l.base + (tb + j) * F;
+        if (yin && in) y = cadd(y, ldc(yin, e));
+        if (in) {
+          if (ABS)
+            yout[e] = sqrtf(fmaf(y.r, y.r, y.i * y.i));
+          else
+            stc(yout, e, y);
+        }
+      } else {
+        if (yin) y = cadd(y, buf_ldc(si.at(j), lo_c));
+        if (ABS)
+          buf_stf(sy.at(j), lo_a, sqrtf(fmaf(y.r, y.r, y.i * y.i)));
+        else
+          buf_stc(sy.at(j), lo_c, y);
+      }
     }
 #pragma unroll
     for (int j = 0; j < LS; ++j) uv[j] = un[j];
@@ -626,11 +648,14 @@ int pad_osc(int N) {
 
 dim3 mosc_grid(int64_t B, int64_t F) { return dim3((unsigned)(B * ((F + kFC - 1) / kFC))); }
 
-// F <= kMaxFilters keeps every pass's descriptor (at most 2048 steps of F
-// complex elements) below 2^31 bytes.
-constexpr int64_t kMaxFilters = 65536;
+// F <= kDescFilters keeps every pass's descriptor (at most 2048 steps of F
+// complex elements) below 2^31 bytes; wider rows run the forward with 64-bit
+// addresses (the backward always does).  The grids bound the rest: B blocks
+// per 16 filters, and one coefficient reduction per (filter, oscillator).
+constexpr int64_t kDescFilters = 65536;
 bool bad_shape(int64_t B, int64_t T, int64_t F, int64_t N) {
-  return B < 0 || T < 0 || F < 0 || F > kMaxFilters || N < 1 || N > (int64_t)1 << 20;
+  if (B < 0 || T < 0 || F < 0 || N < 1 || N > (int64_t)1 << 20) return true;
+  return B * ((F + kFC - 1) / kFC) > INT32_MAX || F * N > INT32_MAX;
 }
 
 // Workspace: forward, a complex (B,T,F) partial when a |y| output needs more
@@ -650,7 +675,7 @@ void with_np(int np, Fn&& fn) {
   }
 }
 
-template <int NP, bool REAL>
+template <int NP, bool REAL, bool G64>
 void launch_fwd(const float* c1, const float* c2, const float* cw, const float* u,
                 const float* yin, float* yout, bool abs_out, int64_t B, int64_t T, int64_t F,
                 int N, int n0, hipStream_t s) {
@@ -661,13 +686,13 @@ void launch_fwd(const float* c1, const float* c2, const float* cw, const float* 
   constexpr int W = REAL ? 16 : (NP == 4 ? 12 : 8), W1 = REAL && NP <= 2 ? 16 : 8;
   const dim3 grid = mosc_grid(B, F), block(W * kWave), block1(W1 * kWave);
   if (cw && abs_out)
-    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, true, true, W>), grid, block, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
+    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, true, true, W, G64>), grid, block, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
   else if (cw)
-    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, true, false, W>), grid, block, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
+    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, true, false, W, G64>), grid, block, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
   else if (abs_out)
-    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, false, true, W1>), grid, block1, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
+    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, false, true, W1, G64>), grid, block1, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
   else
-    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, false, false, W1>), grid, block1, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
+    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, false, false, W1, G64>), grid, block1, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
 }
 
 template <int NP, bool REAL>
@@ -719,10 +744,16 @@ extern "C" int rqf_multi_osc_fwd(const float* c1, const float* c2, const float* 
     const bool abs_here = last && out_abs;
     with_np(np, [&](auto npc) {
       constexpr int NP = decltype(npc)::value;
-      if (u_real)
-        launch_fwd<NP, true>(c1, c2, cw, u, yin, yout, abs_here, B, T, F, (int)N, n0, s);
-      else
-        launch_fwd<NP, false>(c1, c2, cw, u, yin, yout, abs_here, B, T, F, (int)N, n0, s);
+      if (F > kDescFilters) {
+        if (u_real)
+          launch_fwd<NP, true, true>(c1, c2, cw, u, yin, yout, abs_here, B, T, F, (int)N, n0, s);
+        else
+          launch_fwd<NP, false, true>(c1, c2, cw, u, yin, yout, abs_here, B, T, F, (int)N, n0, s);
+      } else if (u_real) {
+        launch_fwd<NP, true, false>(c1, c2, cw, u, yin, yout, abs_here, B, T, F, (int)N, n0, s);
+      } else {
+        launch_fwd<NP, false, false>(c1, c2, cw, u, yin, yout, abs_here, B, T, F, (int)N, n0, s);
+      }
     });
   }
   return launch_status();

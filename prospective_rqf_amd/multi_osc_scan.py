@@ -43,7 +43,6 @@ from torch.autograd.function import once_differentiable
 from prospective_rqf_amd import _lib
 
 MAX_OSC = 1 << 20  # a bound on the C ABI's argument, not on the kernels
-MAX_FILTERS = 1 << 16  # the forward addresses each pass of the sequence through one 32-bit buffer range
 
 
 def _c64(t: torch.Tensor) -> torch.Tensor:
@@ -82,8 +81,6 @@ def _check(u: torch.Tensor, C1: torch.Tensor, C2: torch.Tensor, num_osc: int) ->
     if not 1 <= num_osc <= MAX_OSC:
         raise ValueError(f"num_osc must be in [1, {MAX_OSC}], got {num_osc}")
     B, T, F = u.shape
-    if F > MAX_FILTERS:
-        raise ValueError(f"at most {MAX_FILTERS} filters per call, got {F}")
     if C1.shape != (F * num_osc,) or C2.shape != (F * num_osc,):
         raise ValueError(f"C1/C2 must have shape ({F * num_osc},) for {F} filters x {num_osc} "
                          f"oscillators, got {tuple(C1.shape)}, {tuple(C2.shape)}")

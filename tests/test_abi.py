@@ -132,15 +132,19 @@ def test_noalloc_rejects_oversized_problems_before_any_device_call(built_lib):
     assert lib.rqf_fbt_recompute_bwd_noalloc(*args, -1, 1, 16, None) == -1
 
 
-def test_multi_osc_rejects_more_filters_than_one_buffer_range(built_lib):
-    """The multi-oscillator entry points address each pass of the sequence
-    (up to 2048 steps of F complex values) through one 32-bit buffer range, so
-    F is limited to 65536: beyond it they return RQF_ERR_ARG (-1; and the
+def test_multi_osc_rejects_grids_past_int32(built_lib):
+    """The multi-oscillator entry points take any number of filters (past
+    65536 the forward addresses its passes with 64-bit addresses); only a
+    grid past 2^31 - 1 blocks is refused, with RQF_ERR_ARG (-1; and the
     workspace query 0) before looking at a pointer or calling HIP."""
     lib = _lib.load()
-    assert lib.rqf_multi_osc_workspace(2, 100, 65537, 4, 1) == 0
+    assert lib.rqf_multi_osc_workspace(2, 100, 65537, 4, 1) > 0
     assert lib.rqf_multi_osc_workspace(2, 100, 65536, 4, 1) > 0
-    assert lib.rqf_multi_osc_fwd(None, None, None, None, 0, None, 0, 2, 100, 65537, 4, None, 0,
+    big_b = 2 ** 31 // 4 + 1  # B * ceil(F / 16) blocks past 2^31 - 1 with F = 64
+    assert lib.rqf_multi_osc_workspace(big_b, 1, 64, 1, 1) == 0
+    assert lib.rqf_multi_osc_fwd(None, None, None, None, 0, None, 0, big_b, 1, 64, 1, None, 0,
                                  None) == -1
-    assert lib.rqf_multi_osc_bwd(None, None, None, None, 0, None, None, None, None, None, 2, 100,
-                                 65537, 4, None, 0, None) == -1
+    assert lib.rqf_multi_osc_bwd(None, None, None, None, 0, None, None, None, None, None, big_b,
+                                 1, 64, 1, None, 0, None) == -1
+    assert lib.rqf_multi_osc_fwd(None, None, None, None, 0, None, 0, 1, 1, 2 ** 20, 4096, None,
+                                 0, None) == -1  # F * N coefficient reductions past 2^31 - 1

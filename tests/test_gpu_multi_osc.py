@@ -92,6 +92,37 @@ def test_multi_osc_forward_backward(shape, N, real):
     assert not bad, errs
 
 
+@pytest.mark.parametrize("N,real", [(1, True), (2, True), (4, False), (5, False)])
+def test_more_filters_than_one_descriptor_range(N, real):
+    """F above 65536: a pass of the forward no longer fits one 32-bit buffer
+    range, so it runs with 64-bit addresses (the reference's grid has no
+    filter limit, triton_scan_kernel.py:1991-2015).  Same checks as above,
+    |y| included; T = 70 spans a ragged last pass."""
+    B, T, F = 1, 70, 65536 + 40
+    print(f"case: multi-osc wide rows {(B, T, F)} N={N} real={real}", flush=True)
+    rng = np.random.default_rng(N + 7 * real)
+    c1, c2, cw, u = _problem(rng, B, T, F, N, real)
+    gy = _c64(crandn(rng, B, T, F))
+    y_ref, yabs_ref = oracle.mosc_fwd(c1, c2, cw, u, N)
+    gu_ref, gc1_ref, gc2_ref, gcw_ref = oracle.mosc_bwd(c1, c2, cw, u, gy, N)
+    C1, C2, U, CW = _t(c1, True), _t(c2, True), _t(u, True), _cw_param(cw, True)
+    fn = mo._triton_sequential_scan_multi_osc_real if real else mo._triton_sequential_scan_multi_osc
+    y = fn(C1, C2, U, CW, N)
+    y.backward(_t(gy))
+    gcw_got = CW.grad[:, 0].double() + 1j * CW.grad[:, 1].double()
+    errs = {"y": relerr(y, y_ref), "gc1": relerr(C1.grad, gc1_ref),
+            "gc2": relerr(C2.grad, gc2_ref), "gcw": relerr(gcw_got.cpu(), gcw_ref),
+            "gu": relerr(U.grad, gu_ref.real if real else gu_ref)}
+    with torch.no_grad():
+        if real:
+            yabs = mo._sequential_scan_multi_osc_real_forward_abs_raw(C1, C2, U, CW, N)
+        else:
+            yabs = mo._sequential_scan_multi_osc_forward_abs_raw(C1, C2, U, CW[:, 0], CW[:, 1], N)
+    errs["|y|"] = relerr(yabs, yabs_ref)
+    bad = {k: v for k, v in errs.items() if not v <= PARITY_RTOL}
+    assert not bad, errs
+
+
 def test_needs_input_grad_gating_and_parallel_alias():
     rng = np.random.default_rng(5)
     B, T, F, N = 2, 300, 6, 4

@@ -685,14 +685,16 @@ void launch_fwd(const float* c1, const float* c2, const float* cw, const float* 
   // config 6), else 8.
   constexpr int W = REAL ? 16 : (NP == 4 ? 12 : 8), W1 = REAL && NP <= 2 ? 16 : 8;
   const dim3 grid = mosc_grid(B, F), block(W * kWave), block1(W1 * kWave);
-  if (cw && abs_out)
+  if (cw && abs_out) {
     hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, true, true, W, G64>), grid, block, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
-  else if (cw)
+  } else if (cw) {
     hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, true, false, W, G64>), grid, block, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
-  else if (abs_out)
-    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, false, true, W1, G64>), grid, block1, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
-  else
-    hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, false, false, W1, G64>), grid, block1, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
+  } else if constexpr (NP == 1) {  // without C-weights N is 1 (checked by the caller)
+    if (abs_out)
+      hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, false, true, W1, G64>), grid, block1, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
+    else
+      hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, false, false, W1, G64>), grid, block1, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
+  }
 }
 
 template <int NP, bool REAL>

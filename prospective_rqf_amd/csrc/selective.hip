@@ -1981,6 +1981,7 @@ int group_team_size(const rqf_selective_inputs* in) {
   const int64_t n = std::max<int64_t>(1, in->F / std::max<int64_t>(1, in->G));
   int64_t best_idle = -1;
   int best = 4;
+  if (ntiles == 0) return best;  // no tiles (T = 0): any shape, and no places to divide by
   for (int tc : {6, 4, 3}) {
     const int64_t tw = kGrpWaves / tc;
     const int64_t places = (ntiles + tw - 1) / tw * tw * ((n + tc - 1) / tc * tc);
@@ -2019,7 +2020,8 @@ bool use_group_form(const rqf_selective_inputs* in, bool with_gx) {
   const int64_t ntiles = (in->T + kBwdTile - 1) / kBwdTile;
   const int64_t n = std::max<int64_t>(1, in->F / std::max<int64_t>(1, in->G));
   const int64_t places = (ntiles + tw - 1) / tw * tw * ((n + tc - 1) / tc * tc);
-  return (with_gx || tc == 6) && in->G * in->B >= kCus && (places - ntiles * n) * 32 <= places;
+  return (with_gx || tc == 6) && in->G * in->B >= kCus && places > 0 &&
+         (places - ntiles * n) * 32 <= places;
 }
 
 struct SelWs {

@@ -34,11 +34,6 @@ static __device__ __align__(256) unsigned char scratch[RQF_NOALLOC_SCRATCH_BYTES
 
 namespace {
 
-// Loads of the next tile are issued before the current tile's scan.
-#ifndef RQF_TI_PREFETCH
-#define RQF_TI_PREFETCH 1
-#endif
-
 // Steps per lane of the one-row-per-wavefront kernels.  4 (a 32-byte stretch
 // per lane, 2 KB per wavefront load) streams faster than 8 (64 bytes per
 // lane) on gfx950: wider per-lane stretches make each load instruction's
@@ -167,68 +162,6 @@ __device__ __forceinline__ void drive_tile(const RowDrive& r, int64_t t0, int64_
 }
 
 // ---------------------------------------------------------------------------
-// FBT forward: raw (optional), split-ReLU act (optional), entry carry per tile
-// (optional).
-// ---------------------------------------------------------------------------
-template <bool VEC>
-__global__ __launch_bounds__(kTiWaves* kWave) void fbt_fwd_kernel(
-    const float* __restrict__ c1, const float* __restrict__ tap0, const float* __restrict__ tap1,
-    const float* __restrict__ z, float* __restrict__ raw, float* __restrict__ act,
-    float* __restrict__ carry, int64_t F, int64_t B, int64_t T, int64_t nc) {
-  const int lane = lane_id();
-  const int64_t row = (int64_t)blockIdx.x * kTiWaves + wave_id();
-  if (row >= F * B) return;
-  const int64_t f = row / B;
-  const c32 a = ldc(c1, f), k0 = ldc(tap0, f), k1 = ldc(tap1, f);
-  const ScanPow pw = scan_pow_fwd(dpow(widen(a), kTiK), lane);
-  const float* zr = z + 2 * row * T;
-  float* rawr = raw ? raw + 2 * row * T : nullptr;
-  float* actr = act ? act + 2 * row * T : nullptr;
-  c32 y = mk(0.0f, 0.0f), zlast = mk(0.0f, 0.0f);
-#if RQF_TI_PREFETCH
-  // The next tile's drive is loaded before this tile's scan (software pipeline).
-  c32 znext[kTiK];
-  load8<VEC>(zr, lane * kTiK, T, znext);
-#endif
-  for (int64_t t0 = 0, tile = 0; t0 < T; t0 += kTiTile, ++tile) {
-    if (carry && lane == 0) stc(carry, row * nc + tile, y);
-    const int64_t tb = t0 + lane * kTiK;
-    c32 zv[kTiK];
-#if RQF_TI_PREFETCH
-#pragma unroll
-    for (int k = 0; k < kTiK; ++k) zv[k] = znext[k];
-    if (t0 + kTiTile < T) load8<VEC>(zr, tb + kTiTile, T, znext);
-#else
-    load8<VEC>(zr, tb, T, zv);
-#endif
-    const c32 zp0 = shift_up(zv[kTiK - 1], zlast, lane);
-    c32 u[kTiK];
-#pragma unroll
-    for (int k = 0; k < kTiK; ++k) u[k] = cmad(k1, k ? zv[k - 1] : zp0, cmul(k0, zv[k]));
-    c32 s = mk(0.0f, 0.0f);
-#pragma unroll
-    for (int k = 0; k < kTiK; ++k) s = cmad(a, s, u[k]);
-    if (lane == 0) s = cmad(pw.p[0], y, s);
-    wave_scan_fwd_pow(s, pw);
-    c32 yk = shift_up(s, y, lane);
-    c32 out[kTiK];
-#pragma unroll
-    for (int k = 0; k < kTiK; ++k) {
-      yk = cmad(a, yk, u[k]);
-      out[k] = yk;
-    }
-    if (rawr) store8<VEC>(rawr, tb, T, out);
-    if (actr) {
-#pragma unroll
-      for (int k = 0; k < kTiK; ++k) out[k] = relu2(out[k]);
-      store8<VEC>(actr, tb, T, out);
-    }
-    y = readlane(s, kWave - 1);
-    zlast = readlane(zv[kTiK - 1], kWave - 1);
-  }
-}
-
-// ---------------------------------------------------------------------------
 // FBT forward, row-block form: a block of kTfWaves wavefronts owns one row and
 // walks it in super-tiles of kTfWaves tiles of kTfTile steps (kTfK per lane),
 // wavefront w taking tile w of each, so that concurrent wavefronts stream
@@ -239,9 +172,6 @@ __global__ __launch_bounds__(kTiWaves* kWave) void fbt_fwd_kernel(
 // contiguous 1 KB per global instruction).  Entry carries stay at the
 // backward's kTiTile granularity.
 // ---------------------------------------------------------------------------
-#ifndef RQF_TI_FWD_RB
-#define RQF_TI_FWD_RB 1
-#endif
 #ifndef RQF_TI_FWD_K
 #define RQF_TI_FWD_K 8
 #endif
@@ -383,16 +313,8 @@ __global__ __launch_bounds__(kTfWaves* kWave) void fbt_fwd_rb_kernel(
 #ifndef RQF_TI_RB_WAVES
 #define RQF_TI_RB_WAVES 4
 #endif
-// 0 disables the row-block backward, 1 selects it for 2 KB-aligned rows,
-// 2 for all rows (experiments).
-#ifndef RQF_TI_ROWBLOCK
-#define RQF_TI_ROWBLOCK 1
-#endif
 #ifndef RQF_TI_BWD_K
 #define RQF_TI_BWD_K 8
-#endif
-#ifndef RQF_TI_BWD_LDS_IO
-#define RQF_TI_BWD_LDS_IO 1
 #endif
 constexpr int kTbK = RQF_TI_BWD_K, kTbTile = kWave * kTbK;
 static_assert(kTbTile % kTiTile == 0, "backward tiles start on carry tiles");
@@ -400,20 +322,12 @@ constexpr int kRbWaves = RQF_TI_RB_WAVES;
 
 // Super-tiles are walked from the end; wavefront w takes tile w of each.
 // Complex tile of K steps per lane: full tiles through the wavefront's LDS
-// slice (RQF_TI_BWD_LDS_IO) or as lane-contiguous float4s, partial tiles
-// element by element.
+// slice, partial tiles element by element.
 template <int K>
 __device__ __forceinline__ void ld_tile(const float* __restrict__ row, int64_t t0, int64_t tb,
                                         int64_t T, int lane, bool full, float4* io, c32 (&v)[K]) {
-  if (full && RQF_TI_BWD_LDS_IO) {
+  if (full) {
     load_c_lds<K>(row, (int)t0, lane, io, v);
-  } else if (full) {
-#pragma unroll
-    for (int j = 0; j < K / 2; ++j) {
-      const float4 q = *reinterpret_cast<const float4*>(row + 2 * tb + 4 * j);
-      v[2 * j] = mk(q.x, q.y);
-      v[2 * j + 1] = mk(q.z, q.w);
-    }
   } else {
 #pragma unroll
     for (int k = 0; k < K; ++k) v[k] = (tb + k < T) ? ldc(row, tb + k) : mk(0.0f, 0.0f);
@@ -422,13 +336,8 @@ __device__ __forceinline__ void ld_tile(const float* __restrict__ row, int64_t t
 template <int K>
 __device__ __forceinline__ void st_tile(float* __restrict__ row, int64_t t0, int64_t tb, int64_t T,
                                         int lane, bool full, float4* io, const c32 (&v)[K]) {
-  if (full && RQF_TI_BWD_LDS_IO) {
+  if (full) {
     store_c_lds<K>(row, (int)t0, lane, io, v);
-  } else if (full) {
-#pragma unroll
-    for (int j = 0; j < K / 2; ++j)
-      *reinterpret_cast<float4*>(row + 2 * tb + 4 * j) =
-          make_float4(v[2 * j].r, v[2 * j].i, v[2 * j + 1].r, v[2 * j + 1].i);
   } else {
 #pragma unroll
     for (int k = 0; k < K; ++k)
@@ -447,16 +356,10 @@ __global__ __launch_bounds__(kRbWaves* kWave) void fbt_bwd_rb_kernel(
   constexpr int K = kTbK, TILE = kTbTile, W = kRbWaves;
   __shared__ float2 s_map[2][W];  // offset of each wavefront's tile suffix map (power ptile)
   __shared__ double s_part[W][6];
-#if RQF_TI_BWD_LDS_IO
   __shared__ float4 s_io[W][TILE / 2];
-#endif
   const int lane = lane_id();
   const int w = wave_id();
-#if RQF_TI_BWD_LDS_IO
   float4* io = &s_io[w][0];
-#else
-  float4* io = nullptr;
-#endif
   const int64_t row = blockIdx.x;
   const int64_t f = row / B;
   const c32 a = ldc(c1, f), k0 = ldc(tap0, f), k1 = ldc(tap1, f);
@@ -486,7 +389,7 @@ __global__ __launch_bounds__(kRbWaves* kWave) void fbt_bwd_rb_kernel(
     c32 zp0 = mk(0.0f, 0.0f), yp0 = mk(0.0f, 0.0f);
     c32 r = mk(0.0f, 0.0f);
     if (has) {
-      drive_tile<K, L0, RQF_TI_BWD_LDS_IO>(rd, t0, tb, T, lane, full, io, zv);
+      drive_tile<K, L0, true>(rd, t0, tb, T, lane, full, io, zv);
       ld_tile<K>(gr, t0, tb, T, lane, full, io, ev);
       const c32 zprev_tile = drive_at<L0>(rd, t0 - 1, T);
       zp0 = shift_up(zv[K - 1], zprev_tile, lane);
@@ -612,19 +515,16 @@ __global__ __launch_bounds__(kTiWaves* kWave) void fbt_bwd_kernel(
   auto load_z = [&](int64_t tb, c32(&v)[kTiK]) {
     drive_tile<kTiK, L0, false>(rd, 0, tb, T, lane, VEC && tb + kTiK <= T, nullptr, v);
   };
-#if RQF_TI_PREFETCH
   // The previous tile's (in walk order: next) drive and cotangent are loaded
   // before this tile's scans (software pipeline).
   c32 znext[kTiK], enext[kTiK];
   load_z((ntiles - 1) * kTiTile + lane * kTiK, znext);
   load8<VEC>(gr, (ntiles - 1) * kTiTile + lane * kTiK, T, enext);
-#endif
   for (int64_t tile = ntiles - 1; tile >= 0; --tile) {
     const int64_t t0 = tile * kTiTile;
     const int64_t tb = t0 + lane * kTiK;
     const int cnt = (int)min<int64_t>(max<int64_t>(T - tb, 0), kTiK);
     c32 zv[kTiK], yv[kTiK], ev[kTiK];
-#if RQF_TI_PREFETCH
 #pragma unroll
     for (int k = 0; k < kTiK; ++k) {
       zv[k] = znext[k];
@@ -634,10 +534,6 @@ __global__ __launch_bounds__(kTiWaves* kWave) void fbt_bwd_kernel(
       load_z(tb - kTiTile, znext);
       load8<VEC>(gr, tb - kTiTile, T, enext);
     }
-#else
-    load_z(tb, zv);
-    load8<VEC>(gr, tb, T, ev);
-#endif
     const c32 zprev_tile = drive_at<L0>(rd, t0 - 1, T);
     const c32 zp0 = shift_up(zv[kTiK - 1], zprev_tile, lane);
     c32 yp0;
@@ -778,9 +674,7 @@ int fbt_fwd(const float* c1, const float* t0, const float* t1, Drive drv, const 
   const int64_t nc = (T + kTiTile - 1) / kTiTile;
   const bool vec = T % 2 == 0 && (l0 ? T % 4 == 0 && aligned16(drv.x) : aligned16(drv.z)) &&
                    aligned16(skip) && aligned16(raw) && aligned16(act);
-  // the per-row forward has no skip input and no layer-0 drive
-  if (!RQF_TI_FWD_RB && (skip || l0)) return RQF_ERR_ARG;
-  if (RQF_TI_FWD_RB) {
+  {
     const dim3 grid((unsigned)R), block(kTfWaves * kWave);
     if (l0 && vec)
       hipLaunchKernelGGL((fbt_fwd_rb_kernel<true, true>), grid, block, 0, s, c1, t0, t1, drv.z, drv.x, drv.wz,
@@ -794,15 +688,7 @@ int fbt_fwd(const float* c1, const float* t0, const float* t1, Drive drv, const 
     else
       hipLaunchKernelGGL((fbt_fwd_rb_kernel<false, false>), grid, block, 0, s, c1, t0, t1, drv.z, drv.x, drv.wz,
                          skip, raw, act, carry, F, B, T, nc);
-    return launch_status();
   }
-  const dim3 grid((unsigned)((R + kTiWaves - 1) / kTiWaves)), block(kTiWaves * kWave);
-  if (vec)
-    hipLaunchKernelGGL(fbt_fwd_kernel<true>, grid, block, 0, s, c1, t0, t1, drv.z, raw, act,
-                       carry, F, B, T, nc);
-  else
-    hipLaunchKernelGGL(fbt_fwd_kernel<false>, grid, block, 0, s, c1, t0, t1, drv.z, raw, act,
-                       carry, F, B, T, nc);
   return launch_status();
 }
 
@@ -819,18 +705,19 @@ void launch_fbt_bwd_kernels(bool rowblock, bool vec, const float* c1, const floa
 #define RQF_FBT_BWD(KERNEL, V, REPLAY)                                                         \
   hipLaunchKernelGGL((KERNEL<V, REPLAY, L0>), grid, block, 0, s, c1, t0, t1, drv.z, drv.x,      \
                      drv.wz, raw, carry, gout, mask, gz, partial, F, B, T, nc)
+  // The layer-0 drive comes only with the recompute form (carries, no raw).
   if (rowblock) {
     if (carry) {
       if (vec) RQF_FBT_BWD(fbt_bwd_rb_kernel, true, true);
       else RQF_FBT_BWD(fbt_bwd_rb_kernel, false, true);
-    } else {
+    } else if constexpr (!L0) {
       if (vec) RQF_FBT_BWD(fbt_bwd_rb_kernel, true, false);
       else RQF_FBT_BWD(fbt_bwd_rb_kernel, false, false);
     }
   } else if (carry) {
     if (vec) RQF_FBT_BWD(fbt_bwd_kernel, true, true);
     else RQF_FBT_BWD(fbt_bwd_kernel, false, true);
-  } else {
+  } else if constexpr (!L0) {
     if (vec) RQF_FBT_BWD(fbt_bwd_kernel, true, false);
     else RQF_FBT_BWD(fbt_bwd_kernel, false, false);
   }
@@ -860,7 +747,8 @@ int fbt_bwd(const float* c1, const float* t0, const float* t1, Drive drv, const 
     const int64_t nc = (T + kTiTile - 1) / kTiTile;
     const bool vec = T % 2 == 0 && (l0 ? T % 4 == 0 && aligned16(drv.x) : aligned16(drv.z)) &&
                      aligned16(raw) && aligned16(gout) && aligned16(gz);
-    const bool rowblock = RQF_TI_ROWBLOCK == 2 || (RQF_TI_ROWBLOCK == 1 && T % kTiTile == 0);
+    // the row-block backward on 2 KB-aligned rows, the per-row one otherwise
+    const bool rowblock = T % kTiTile == 0;
     if (l0)
       launch_fbt_bwd_kernels<true>(rowblock, vec, c1, t0, t1, drv, raw, carry, gout, mask, gz,
                                    partial, F, B, T, nc, s);

@@ -148,3 +148,37 @@ def test_multi_osc_rejects_grids_past_int32(built_lib):
                                  1, 64, 1, None, 0, None) == -1
     assert lib.rqf_multi_osc_fwd(None, None, None, None, 0, None, 0, 1, 1, 2 ** 20, 4096, None,
                                  0, None) == -1  # F * N coefficient reductions past 2^31 - 1
+
+
+def test_shape_queries_take_edge_shapes_without_crashing(built_lib):
+    """The host-side shape logic (workspace sizes, the backward's form and
+    block shape) runs before any launch and must take empty and degenerate
+    shapes: zero batch, time or filters, a warp head with no rows.  Run in a
+    child process, so that a host crash (an integer division by zero, as an
+    empty-time selective call with a warp head once caused) fails this test
+    rather than the suite."""
+    import subprocess
+    import sys
+
+    code = """
+import ctypes, itertools
+from prospective_rqf_amd import _lib
+lib = _lib.load()
+for F, B, T, G, warp, chunk in itertools.product((0, 1, 7, 256), (0, 1, 3), (0, 1, 255, 256, 257),
+                                                 (0, 1, 3), (0, 1), (1, 256, 1024)):
+    s = _lib.SelectiveInputsStruct()
+    s.F, s.B, s.T, s.G = F, B, T, G
+    s.has_warp, s.has_gamma, s.has_write = warp, 1, 1
+    lib.rqf_selective_bwd_workspace(ctypes.byref(s), chunk)
+for B, T, F, N in itertools.product((0, 1, 5), (0, 1, 300), (0, 1, 17), (1, 4, 5)):
+    lib.rqf_btf_scan_workspace(B, T, F)
+    lib.rqf_fbt_workspace(F, B, T)
+    lib.rqf_fbt_carry_chunks(T)
+    lib.rqf_multi_osc_workspace(B, T, F, N, 0)
+    lib.rqf_multi_osc_workspace(B, T, F, N, 1)
+    lib.rqf_layer0_grads_workspace(F, 1, T)
+print("ok")
+"""
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True,
+                         timeout=120, cwd=os.path.dirname(os.path.dirname(__file__)))
+    assert out.returncode == 0 and out.stdout.strip() == "ok", (out.returncode, out.stderr[-2000:])

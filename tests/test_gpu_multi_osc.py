@@ -92,7 +92,8 @@ def test_multi_osc_forward_backward(shape, N, real):
     assert not bad, errs
 
 
-@pytest.mark.parametrize("N,real", [(1, True), (2, True), (4, False), (5, False)])
+@pytest.mark.parametrize("N,real", [(1, True), (2, True), (4, True), (1, False), (2, False),
+                                    (4, False), (5, False)])
 def test_more_filters_than_one_descriptor_range(N, real):
     """F above 65536: a pass of the forward no longer fits one 32-bit buffer
     range, so it runs with 64-bit addresses (the reference's grid has no
@@ -123,6 +124,36 @@ def test_more_filters_than_one_descriptor_range(N, real):
     assert not bad, errs
 
 
+@pytest.mark.parametrize("F", [40, 65536 + 40])
+@pytest.mark.parametrize("real", [False, True])
+def test_scan_without_c_weights(F, real):
+    """``rqf_multi_osc_fwd`` with no C-weights and N = 1 is the plain scan
+    x[t] = C1 x[t-1] + C2 u[t] (complex output), or its magnitude; the Python
+    names reach the magnitude (``sequential_scan_abs``), so the complex
+    output is called through the C ABI.  Against the oracle's scan; narrow
+    rows and rows past one 32-bit descriptor range."""
+    from prospective_rqf_amd import _lib
+
+    B, T = 2, 70
+    print(f"case: multi-osc no C-weights F={F} real={real}", flush=True)
+    rng = np.random.default_rng(F + real)
+    c1 = _c64(rng.uniform(0.7, 0.995, F) * np.exp(1j * rng.uniform(0, 2 * np.pi, F)))
+    c2 = _c64(0.5 * crandn(rng, F))
+    u = rng.standard_normal((B, T, F)) if real else crandn(rng, B, T, F)
+    u = np.asarray(u, np.float32).astype(np.float64) if real else _c64(u)
+    want = oracle.twotap_fwd(c1, c2, None, np.asarray(u, np.complex128))
+    C1, C2, U = _t(c1), _t(c2), _t(u)
+    lib = _lib.load()
+    for absolute in (False, True):
+        out = torch.empty(B, T, F, device="cuda",
+                          dtype=torch.float32 if absolute else torch.complex64)
+        _lib.check(lib.rqf_multi_osc_fwd(_lib.ptr(C1), _lib.ptr(C2), None, _lib.ptr(U),
+                                         int(real), _lib.ptr(out), int(absolute), B, T, F, 1,
+                                         None, 0, _lib.stream_of(U)), "rqf_multi_osc_fwd")
+        torch.cuda.synchronize()
+        assert relerr(out, np.abs(want) if absolute else want) <= PARITY_RTOL, absolute
+
+
 def test_needs_input_grad_gating_and_parallel_alias():
     rng = np.random.default_rng(5)
     B, T, F, N = 2, 300, 6, 4
@@ -149,7 +180,8 @@ def test_needs_input_grad_gating_and_parallel_alias():
 
 
 @pytest.mark.parametrize("real", [False, True])
-@pytest.mark.parametrize("shape,N", [((2, 37, 3), 3), ((3, 2000, 40), 4), ((2, 600, 130), 8)])
+@pytest.mark.parametrize("shape,N", [((2, 37, 3), 3), ((3, 2000, 40), 4), ((2, 600, 130), 8),
+                                     ((2, 300, 20), 1), ((3, 257, 17), 2)])
 def test_gradient_subsets_launch_their_own_variants(shape, N, real):
     """grad_u alone skips the adjoint's C1 tangent and the coefficient sums;
     the coefficient gradients alone skip grad_u.  Each variant runs the same

@@ -123,6 +123,39 @@ def test_fbt_matches_oracle(variant, shape):
             assert err <= PARITY_RTOL, (name + "/channel", err)
 
 
+@pytest.mark.parametrize("variant", ["raw", "act", "recompute"])
+@pytest.mark.parametrize("T", [512, 513])
+def test_fbt_rows_not_16_byte_aligned(variant, T):
+    """A drive tensor that starts 8 bytes past a 16-byte boundary (a view at
+    an odd complex offset): the kernels take their element-wise row forms,
+    the row-block backward included (T = 512, a multiple of the 256-step
+    tile)."""
+    F, B = 3, 2
+    print(f"case: fbt misaligned {variant} T={T}", flush=True)
+    rng = np.random.default_rng(T + len(variant))
+    c1, t0, t1 = _coeffs(rng, F)
+    z = _c64(crandn(rng, F, B, T))
+    gy = _c64(crandn(rng, F, B, T))
+    mask = variant != "raw"
+    y_ref, act_ref = oracle.twotap_fwd(c1, t0, t1, z, layout=oracle.FBT, act=True)
+    gz_ref, gc1_ref, gt0_ref, gt1_ref = oracle.twotap_bwd(c1, t0, t1, z, y_ref, gy,
+                                                          layout=oracle.FBT, mask_act=mask)
+    buf = torch.zeros(F * B * T + 1, dtype=torch.complex64, device="cuda")
+    buf[1:] = torch.as_tensor(z.astype(np.complex64).reshape(-1), device="cuda")
+    Z = buf[1:].view(F, B, T).detach().requires_grad_(True)
+    assert Z.data_ptr() % 16 == 8
+    C1, T0, T1 = _dev(c1), _dev(t0), _dev(t1)
+    if variant == "recompute":
+        y = fbt_recompute_scan(C1, T0, T1, Z)
+    else:
+        y = fbt_prospective_scan(C1, T0, T1, Z, fuse_act=variant == "act")
+    y.backward(torch.as_tensor(gy.astype(np.complex64), device="cuda"))
+    for name, got, want in (("out", y, act_ref if mask else y_ref), ("grad_z", Z.grad, gz_ref),
+                            ("grad_C1", C1.grad, gc1_ref), ("grad_tap0", T0.grad, gt0_ref),
+                            ("grad_tap1", T1.grad, gt1_ref)):
+        assert relerr(got, want) <= PARITY_RTOL, name
+
+
 @pytest.mark.parametrize("is_complex", [False, True])
 def test_dispatch_real_complex_and_single_feature(is_complex):
     print(f"case: dispatch complex={is_complex}", flush=True)

@@ -41,7 +41,10 @@ def _f32(a):
 @pytest.mark.gpu
 @pytest.mark.parametrize("F,D,B,T", [(16, 1, 2, 1000), (8, 20, 3, 4096), (5, 64, 2, 1023),
                                      (3, 2, 1, 1), (32, 1, 4, 16000), (6, 16, 2, 777),
-                                     (4, 3, 3, 501)])
+                                     (4, 3, 3, 501),
+                                     # one feature: 256-step-aligned rows (row-block
+                                     # backward) and rows of odd length (element loads)
+                                     (8, 1, 2, 1024), (5, 1, 3, 777)])
 def test_layer0_matches_fp64_composition(F, D, B, T):
     from oracle import oracle
 
@@ -155,3 +158,75 @@ def test_layer0_grads_read_no_element_past_grad_z(D, n):
     assert torch.isfinite(grad_w).all() and torch.isfinite(grad_h).all()
     assert relerr(grad_w, gw_ref) <= PARITY_RTOL
     assert relerr(grad_h, gh_ref) <= PARITY_RTOL
+
+
+@pytest.mark.gpu
+def test_layer0_input_not_16_byte_aligned():
+    """One input feature whose row starts 4 bytes past a 16-byte boundary:
+    the scan kernels form the drive with element loads (the row-block
+    backward on 256-step-aligned rows included)."""
+    from oracle import oracle
+
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    F, D, B, T = 6, 1, 2, 512
+    print(f"case: layer0 misaligned F={F} B={B} T={T}", flush=True)
+    rng = np.random.default_rng(17)
+    c1, t0, t1 = _coeffs(rng, F)
+    w = _f32(rng.standard_normal((2 * F, D)))
+    h = _f32(rng.standard_normal((D, B * T)))
+    gy = np.asarray(crandn(rng, F, B, T), np.complex64).astype(np.complex128)
+    z = ((w[:F] + 1j * w[F:]) @ h).reshape(F, B, T)
+    y_ref, act_ref = oracle.twotap_fwd(c1, t0, t1, z, layout=oracle.FBT, act=True)
+    gy, _ = cotangent_off_relu_kink(y_ref, gy)
+    gy = gy.astype(np.complex64).astype(np.complex128)
+    gz_ref, gc1_ref, _, _ = oracle.twotap_bwd(c1, t0, t1, z, y_ref, gy, layout=oracle.FBT,
+                                              mask_act=True)
+    gh_ref = w[:F].T @ gz_ref.reshape(F, B * T).real + w[F:].T @ gz_ref.reshape(F, B * T).imag
+    buf = torch.zeros(B * T + 1, dtype=torch.float32, device="cuda")
+    buf[1:] = torch.as_tensor(h.astype(np.float32).reshape(-1), device="cuda")
+    H = buf[1:].view(D, B * T).detach().requires_grad_(True)
+    assert H.data_ptr() % 16 == 4
+    W = torch.as_tensor(w.astype(np.float32), device="cuda").requires_grad_(True)
+    C1 = torch.as_tensor(c1.astype(np.complex64), device="cuda").requires_grad_(True)
+    T0, T1 = (torch.as_tensor(v.astype(np.complex64), device="cuda") for v in (t0, t1))
+    act = fbt_layer0_real_scan(W, H, C1, T0, T1, B)
+    act.backward(torch.as_tensor(gy.astype(np.complex64), device="cuda"))
+    for name, got, want in (("act", act, act_ref), ("grad_h", H.grad, gh_ref),
+                            ("grad_C1", C1.grad, gc1_ref)):
+        assert relerr(got, want) <= PARITY_RTOL, name
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("D", [1, 2, 3, 5, 9])
+@pytest.mark.parametrize("need", ["both", "weights", "input"])
+@pytest.mark.parametrize("n", [2000, 2001])
+def test_layer0_grads_every_variant(D, need, n):
+    """``rqf_layer0_grads`` for each input width class (1, 2; 3-4, 5-8, 9-16
+    for the input gradient alone), each gradient subset the one-pass kernel
+    serves, and rows of 16-byte and element loads (n % 4 == 0 or not).
+    Against the fp64 chain rule."""
+    from prospective_rqf_amd.fbt_scan_kernel import _layer0_grads
+
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    need_w, need_h = need in ("both", "weights"), need in ("both", "input")
+    print(f"case: layer0 grads D={D} need={need} n={n}", flush=True)
+    rng = np.random.default_rng(D * 10 + n)
+    F = 4
+    w = _f32(rng.standard_normal((2 * F, D)))
+    h = _f32(rng.standard_normal((D, n)))
+    gz = np.asarray(crandn(rng, F, n), np.complex64).astype(np.complex128)
+    W = torch.as_tensor(w.astype(np.float32), device="cuda")
+    H = torch.as_tensor(h.astype(np.float32), device="cuda")
+    GZ = torch.as_tensor(gz.astype(np.complex64), device="cuda")
+    grad_w, grad_h = _layer0_grads(W, GZ, H, need_w, need_h)
+    torch.cuda.synchronize()
+    if need_w:
+        assert relerr(grad_w, np.concatenate([gz.real @ h.T, gz.imag @ h.T])) <= PARITY_RTOL
+    else:
+        assert grad_w is None
+    if need_h:
+        assert relerr(grad_h, w[:F].T @ gz.real + w[F:].T @ gz.imag) <= PARITY_RTOL
+    else:
+        assert grad_h is None

@@ -1346,9 +1346,11 @@ __global__ __launch_bounds__(kTeam* kWave)
 // they leave idle at the row length and group size (group_team_size).
 //
 // Every wait is bounded: one that runs out sets a flag that ends every other
-// wait of the block at once, and the block then writes NaN for its channels'
-// dbias and dtheta partials, so a broken dependency shows as NaN gradients
-// instead of hanging the GPU.  The waits only point to earlier channels of the
+// wait of the block at once. After its last barrier the block then writes
+// NaN over every output it owns: its channels' dz / dzw, dg and dw rows, its
+// dd row, and its dbias / dtheta partials. A broken dependency therefore
+// shows as NaN gradients, not as a hang or as finite values composed from
+// maps that never arrived.  The waits only point to earlier channels of the
 // same super-tile or to the channel's own wavefronts at the same super-tile,
 // so none of them is circular.
 // ---------------------------------------------------------------------------
@@ -1870,8 +1872,8 @@ void with_cotangent_set(int ct, Fn&& fn) {
 
 // RQF_GRP_FORCE_TIMEOUT=1 starts every block of the group-form backward in
 // the state a wait that ran out leaves (tests of that path): the waits give up
-// at once and the blocks report NaN for their channels' dbias and dtheta,
-// without hanging.  The flag is read once per block, so the wait loops keep
+// at once and every output the blocks own is written as NaN, without
+// hanging.  The flag is read once per block, so the wait loops keep
 // their constant bound and no register.
 int grp_force_timeout() {
   const char* e = std::getenv("RQF_GRP_FORCE_TIMEOUT");

@@ -22,6 +22,12 @@ reference's model classes:
 straight-through clamp, horizon broadcast, theta band, options tuple).
 Benchmarks and tests call ``assemble`` with seeded logits.
 
+This module is input-building infrastructure, not part of the operator path.
+No scan entry point imports it: they take ``SelectiveScanInputs`` from the
+caller's own controller. Only ``workloads.py`` uses it, to build the inputs
+of the benchmark, the smoke run and the tests. It matches the reference's
+controller bit for bit, pinned by the committed golden fixture.
+
 The reference's ``_SplitProjection`` (selective.py:82-97) exists to skip
 zero-gradient blocks and autocast in backward; its forward is the one GEMM
 ``cat(weights) @ v`` split by head, which is what ``project`` computes.

@@ -158,9 +158,46 @@ __device__ __forceinline__ void load_seg(const Pass& s, uint32_t lo, c32 (&v)[LS
   for (int j = 0; j < LS; ++j)
     v[j] = REAL ? mk(buf_ldf(s.at(j), lo), 0.0f) : buf_ldc(s.at(j), lo);
 }
-// The same through global addresses with an explicit test, for the backward,
-// where the descriptors measured slower (0.47 -> 0.49 ms at config 6: three
-// streams of 8-step segments, a descriptor per step and stream).
+// The backward goes through global addresses: descriptors measured slower
+// there (0.47 -> 0.49 ms at config 6: three streams of 8-step segments, a
+// descriptor per step and stream).  A pass that lies wholly inside [0, T)
+// (every pass but the last) is addressed from a wave-uniform base per step
+// (scalar arithmetic) plus the lane's fixed offset, one 64-bit add per
+// element and no test; the per-element multiply, the range test and its
+// exec mask of load_seg_g dropped the pass loop from 1326 to 1176 VALU
+// instructions per lane at config 6 (backward 0.479 -> 0.468 ms).
+//
+// Byte offset of step pt of the lane's batch element in a (B,T,F) stream.
+// The offset, not the pointer, goes through readfirstlane: a pointer rebuilt
+// from integers loses its address space and its stores become flat ones.
+__device__ __forceinline__ int64_t pass_off(const Lane& l, int64_t pt, int64_t T, int64_t F,
+                                            int esz) {
+  const uint64_t o = (uint64_t)((l.b * T + pt) * F * esz);
+  return (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(o >> 32))
+                    << 32) |
+                   (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)o));
+}
+// The lane's byte offset from its pass's base: its segment's first step and
+// its filter (filter 0 for a lane past F, whose values are never stored).
+__device__ __forceinline__ uint64_t seg_off(const Lane& l, int LS, int64_t F, int esz) {
+  return (uint64_t)(((int64_t)l.sg * LS * F + (l.fv ? l.f : 0)) * esz);
+}
+// A whole segment: base pb of the pass, lane offset lo, stp bytes per step.
+template <int LS, bool REAL>
+__device__ __forceinline__ void load_seg_w(const char* pb, uint64_t lo, uint32_t stp,
+                                           c32 (&v)[LS]) {
+#pragma unroll
+  for (int j = 0; j < LS; ++j) {
+    const char* q = (pb + (uint64_t)j * stp) + lo;
+    if (REAL) {
+      v[j] = mk(*reinterpret_cast<const float*>(q), 0.0f);
+    } else {
+      const float2 x = *reinterpret_cast<const float2*>(q);
+      v[j] = mk(x.x, x.y);
+    }
+  }
+}
+// Any segment, with a test per element (the last pass, which may pass T).
 template <int LS, bool REAL>
 __device__ __forceinline__ void load_seg_g(const float* __restrict__ p, const Lane& l, int64_t tb,
                                            int64_t T, int64_t F, c32 (&v)[LS]) {
@@ -444,10 +481,18 @@ __global__ __launch_bounds__(kThreads) void mosc_bwd_kernel(
     }
   }
   __syncthreads();
+  // Q and R partial sums of the lane's segments, accumulated straight from
+  // every step (fp32 within the lane, fp64 across lanes and batches).
   float qr[NP][4];
 #pragma unroll
   for (int n = 0; n < NP; ++n) qr[n][0] = qr[n][1] = qr[n][2] = qr[n][3] = 0.0f;
   const int64_t npass = (T + kPass - 1) / kPass;
+  constexpr int kUs = REAL ? 4 : 8;  // bytes per element of u and grad_u
+  const uint64_t lo8 = seg_off(l, LS, F, 8), lou = seg_off(l, LS, F, kUs);
+  const uint32_t stp8 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(F * 8));
+  const uint32_t stpu = (uint32_t)__builtin_amdgcn_readfirstlane((int)(F * kUs));
+  const char* const gyb = reinterpret_cast<const char*>(gy);
+  const char* const ub = reinterpret_cast<const char*>(u);
   c32 gv[LS], gn[LS], uv[TAN ? LS : 1], un[TAN ? LS : 1];
   int64_t pt = (npass - 1) * kPass;
   load_seg_g<LS, false>(gy, l, pt + (int64_t)l.sg * LS, T, F, gv);
@@ -455,8 +500,10 @@ __global__ __launch_bounds__(kThreads) void mosc_bwd_kernel(
   for (; pt >= 0; pt -= kPass) {
     const int64_t tb = pt + (int64_t)l.sg * LS;
     if (pt > 0) {
-      load_seg_g<LS, false>(gy, l, tb - kPass, T, F, gn);
-      if constexpr (TAN) load_seg_g<LS, REAL>(u, l, tb - kPass, T, F, un);
+      // Every pass before the last lies wholly inside [0, T).
+      load_seg_w<LS, false>(gyb + pass_off(l, pt - kPass, T, F, 8), lo8, stp8, gn);
+      if constexpr (TAN)
+        load_seg_w<LS, REAL>(ub + pass_off(l, pt - kPass, T, F, kUs), lou, stpu, un);
     }
     // Each oscillator's pair at the segment's first step from a zero pair.
     c32 e[NP], f[NP];
@@ -515,9 +562,6 @@ __global__ __launch_bounds__(kThreads) void mosc_bwd_kernel(
       f[n] = ch;
     }
     // Replay: grad_u and the coefficient sums.
-    float pq[NP][4];
-#pragma unroll
-    for (int n = 0; n < NP; ++n) pq[n][0] = pq[n][1] = pq[n][2] = pq[n][3] = 0.0f;
     c32 go[GU ? LS : 1];
 #pragma unroll
     for (int j = LS - 1; j >= 0; --j) {
@@ -530,38 +574,45 @@ __global__ __launch_bounds__(kThreads) void mosc_bwd_kernel(
         if constexpr (TAN) {
           // Q += e conj(u), R += f conj(u), as fused multiply-adds.
           const c32 uj = uv[j];
-          pq[n][0] = fmaf(uj.r, e[n].r, pq[n][0]);
-          pq[n][1] = fmaf(uj.r, e[n].i, pq[n][1]);
-          pq[n][2] = fmaf(uj.r, f[n].r, pq[n][2]);
-          pq[n][3] = fmaf(uj.r, f[n].i, pq[n][3]);
+          qr[n][0] = fmaf(uj.r, e[n].r, qr[n][0]);
+          qr[n][1] = fmaf(uj.r, e[n].i, qr[n][1]);
+          qr[n][2] = fmaf(uj.r, f[n].r, qr[n][2]);
+          qr[n][3] = fmaf(uj.r, f[n].i, qr[n][3]);
           if (!REAL) {
-            pq[n][0] = fmaf(uj.i, e[n].i, pq[n][0]);
-            pq[n][1] = fmaf(-uj.i, e[n].r, pq[n][1]);
-            pq[n][2] = fmaf(uj.i, f[n].i, pq[n][2]);
-            pq[n][3] = fmaf(-uj.i, f[n].r, pq[n][3]);
+            qr[n][0] = fmaf(uj.i, e[n].i, qr[n][0]);
+            qr[n][1] = fmaf(-uj.i, e[n].r, qr[n][1]);
+            qr[n][2] = fmaf(uj.i, f[n].i, qr[n][2]);
+            qr[n][3] = fmaf(-uj.i, f[n].r, qr[n][3]);
           }
         }
       }
       if constexpr (GU) go[j] = g;
     }
     if constexpr (GU) {
-      // grad_u of the segment, after its steps (no stores inside the chain)
+      // grad_u of the segment, after its steps (no stores inside the chain);
+      // only the last pass can pass T.
+      const bool whole = pt + kPass <= T;
+      const int64_t po = pass_off(l, pt, T, F, kUs);
+      char* const gb = reinterpret_cast<char*>(gu) + po;
+      const char* const ib = gin ? reinterpret_cast<const char*>(gin) + po : nullptr;
 #pragma unroll
       for (int j = 0; j < LS; ++j) {
-        const int64_t t = tb + j;
-        if (l.fv && t < T) {
-          const int64_t el = l.base + t * F;
-          if (REAL)
-            gu[el] = go[j].r + (gin ? gin[el] : 0.0f);
-          else
-            stc(gu, el, gin ? cadd(go[j], ldc(gin, el)) : go[j]);
+        if (l.fv && (whole || tb + j < T)) {
+          const uint64_t o = (uint64_t)j * stpu + lou;
+          if (REAL) {
+            *reinterpret_cast<float*>(gb + o) =
+                go[j].r + (ib ? *reinterpret_cast<const float*>(ib + o) : 0.0f);
+          } else {
+            c32 v = go[j];
+            if (ib) {
+              const float2 x = *reinterpret_cast<const float2*>(ib + o);
+              v = cadd(v, mk(x.x, x.y));
+            }
+            *reinterpret_cast<float2*>(gb + o) = make_float2(v.r, v.i);
+          }
         }
       }
     }
-#pragma unroll
-    for (int n = 0; n < NP; ++n)
-#pragma unroll
-      for (int k = 0; k < 4; ++k) qr[n][k] += pq[n][k];
 #pragma unroll
     for (int j = 0; j < LS; ++j) {
       gv[j] = gn[j];

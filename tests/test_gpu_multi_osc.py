@@ -54,8 +54,11 @@ def _cw_param(cw, grad=False):
                            device="cuda").requires_grad_(grad)
 
 
+# (2, 512, 19): passes that all lie inside [0, T), the last one included, for
+# 2 to 4 oscillators (256-step backward passes), and one whole 512-step pass
+# for one oscillator.
 SHAPES = [(2, 1, 5), (2, 37, 3), (3, 256, 4), (2, 257, 3), (1, 1000, 2), (4, 3000, 64),
-          (2, 600, 130)]
+          (2, 600, 130), (2, 512, 19)]
 
 
 @pytest.mark.parametrize("real", [False, True])

@@ -967,10 +967,13 @@ def main():
     achieved = dom_bytes / (per_op[dom] * 1e-3) / 1e9
     all_bytes = sum(plan.bytes.values())
     # a per-layer row ("rqf_selective_bwd[L0]") where the table has one, else
-    # the entry point's
-    traffic = ((traffic_from_table(f"config{cfg}", dom) or
-                traffic_from_table(f"config{cfg}", entry))
-               if not (args.batch or args.seq_len or args.stack != "none") else None)
+    # the entry point's; the table's rows are the default workloads and the
+    # (B,T,F) layout of config 2, so other variants report none
+    key = f"config{cfg}" + (" (B,T,F)" if cfg == 2 and args.layout == "btf" else "")
+    variant = (args.batch or args.seq_len or args.stack != "none" or args.act_only or
+               (cfg == 2 and args.layer0))
+    traffic = (None if variant else
+               traffic_from_table(key, dom) or traffic_from_table(key, entry))
     result = {
         "metric": METRIC,
         "value": round(value, 3),

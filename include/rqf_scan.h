@@ -18,6 +18,14 @@
  *     stream).  No function synchronises the host.
  *   - Return value: RQF_OK (0) on success; a negative RQF_ERR_* for a bad
  *     argument; a positive hipError_t when a launch fails.
+ *   - Size limit: a dispatch counts its work-items in 32 bits, and a larger
+ *     grid would run truncated with no launch error.  A call whose scan grid
+ *     needs more than 2^32 - 1 work-items returns RQF_ERR_ARG before launching
+ *     anything.  For example, the (B,T,F) scans take B * ceil(F / 16) <=
+ *     8388607 blocks of 512 threads (F <= 134217712 at B = 1).  The FBT and
+ *     selective forwards take up to 8388607 rows (F * B, rounded up per XCD
+ *     chunk of the batch).  Reductions over filters or channels stride, so
+ *     they take any size.
  *   - Results are deterministic: coefficient gradients are reduced from
  *     per-row partial sums in a fixed order (no floating-point atomics).
  *   - Calls are reentrant.  No mutable global state exists, except for the
@@ -108,8 +116,8 @@ int rqf_chunked_prospective_bwd(const float *c1, const float *tap0, const float 
  * ------------------------------------------------------------------------ */
 
 /* Workspace bytes of rqf_multi_osc_fwd (backward = 0) or _bwd (backward = 1);
- * 0 for a shape they reject (N < 1 or N > 2^20, B*ceil(F/16) or F*N past
- * 2^31 - 1).  The forward needs none unless N > 4 with out_abs.  Up to
+ * 0 for a shape they reject (N < 1 or N > 2^20, B*ceil(F/16) past 4194303
+ * blocks of up to 1024 threads, F*N past 2^31 - 1).  The forward needs none unless N > 4 with out_abs.  Up to
  * 65536 filters the forward addresses each pass of up to 2048 steps through
  * one 32-bit buffer range; wider rows run it with 64-bit addresses. */
 size_t rqf_multi_osc_workspace(int64_t B, int64_t T, int64_t F, int64_t N, int32_t backward);

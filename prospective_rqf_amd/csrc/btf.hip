@@ -97,6 +97,12 @@ __device__ __forceinline__ void load_seg(const float* __restrict__ p, const Lane
   }
 }
 
+// A wave-uniform 64-bit value pinned to scalar registers.
+__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
+  return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32)) << 32) |
+         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+}
+
 // A pass that lies wholly inside [0, T) is addressed from a wave-uniform
 // base per step (scalar arithmetic) plus the lane's fixed offset: one 64-bit
 // add per element and no test, where load_seg multiplies and tests each one.
@@ -108,10 +114,7 @@ __device__ __forceinline__ void load_seg(const float* __restrict__ p, const Lane
 // pointer, goes through readfirstlane: a pointer rebuilt from integers loses
 // its address space and its stores become flat ones.
 __device__ __forceinline__ int64_t pass_off(const Lane& l, int64_t pt, int64_t T, int64_t F) {
-  const uint64_t o = (uint64_t)((l.b * T + pt) * F * 8);
-  return (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(o >> 32))
-                    << 32) |
-                   (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)o));
+  return (int64_t)uniform64((uint64_t)((l.b * T + pt) * F * 8));
 }
 // The lane's byte offset from its pass's base: its segment's first step and
 // its filter (filter 0 for a lane past F, whose values are never stored).
@@ -120,7 +123,7 @@ __device__ __forceinline__ uint64_t seg_off(const Lane& l, int LS, int64_t F) {
 }
 // A whole segment: base pb of the pass, lane offset lo, stp bytes per step.
 template <int LS>
-__device__ __forceinline__ void load_seg_w(const char* pb, uint64_t lo, uint32_t stp,
+__device__ __forceinline__ void load_seg_w(const char* pb, uint64_t lo, uint64_t stp,
                                            c32 (&v)[LS]) {
 #pragma unroll
   for (int j = 0; j < LS; ++j) {
@@ -128,7 +131,7 @@ __device__ __forceinline__ void load_seg_w(const char* pb, uint64_t lo, uint32_t
     v[j] = mk(x.x, x.y);
   }
 }
-__device__ __forceinline__ void st_w(char* pb, uint64_t lo, uint32_t stp, int j, c32 v) {
+__device__ __forceinline__ void st_w(char* pb, uint64_t lo, uint64_t stp, int j, c32 v) {
   *reinterpret_cast<float2*>((pb + (uint64_t)j * stp) + lo) = make_float2(v.r, v.i);
 }
 
@@ -163,7 +166,7 @@ __global__ __launch_bounds__(kThreads) void btf_fwd_kernel(const float* __restri
   const c64d aLq = dpow(aL, q), aLG = dpow(aL, kWave / kFC);
   if (l.sg == 0) s_carry[0][l.fl] = make_double2(0.0, 0.0);
   const uint64_t lo = seg_off(l, kLS, F);
-  const uint32_t stp = (uint32_t)__builtin_amdgcn_readfirstlane((int)(F * 8));
+  const uint64_t stp = uniform64((uint64_t)F * 8);
   const char* const xb = reinterpret_cast<const char*>(x);
   c32 xv[kLS], xn[kLS];
   load_seg(x, l, (int64_t)l.sg * kLS, T, F, xv);
@@ -256,7 +259,7 @@ __global__ __launch_bounds__(kThreads) void btf_bwd_kernel(
   if (l.sg == 0) s_carry[0][l.fl] = Pair{make_double2(0.0, 0.0), make_double2(0.0, 0.0)};
   const int64_t npass = (T + kPass - 1) / kPass;
   const uint64_t lo = seg_off(l, kLS, F);
-  const uint32_t stp = (uint32_t)__builtin_amdgcn_readfirstlane((int)(F * 8));
+  const uint64_t stp = uniform64((uint64_t)F * 8);
   const char* const gyb = reinterpret_cast<const char*>(gy);
   const char* const xb = reinterpret_cast<const char*>(x);
   c32 gv[kLS], xv[kLS], gn[kLS], xn[kLS];
@@ -362,31 +365,32 @@ __global__ __launch_bounds__(kThreads) void btf_bwd_kernel(
 }
 
 // grad[f] = sum over b of partial[6*(b*F + f) + j] in fp64: one wavefront per
-// filter, lane l sums b = l, l + 64, ... in order, then a fixed-shape wave
-// reduction.
+// filter (block f, f + gridDim.x, ...), lane l sums b = l, l + 64, ... in
+// order, then a fixed-shape wave reduction.
 __global__ __launch_bounds__(kWave) void btf_coef_reduce_kernel(const double* __restrict__ partial,
                                                                 int64_t B, int64_t F,
                                                                 float* __restrict__ gc1,
                                                                 float* __restrict__ gk0,
                                                                 float* __restrict__ gk1) {
-  const int64_t f = blockIdx.x;
   const int lane = threadIdx.x;
-  double s[6] = {0, 0, 0, 0, 0, 0};
-  for (int64_t b = lane; b < B; b += kWave) {
-    const double* p = partial + 6 * (b * F + f);
+  for (int64_t f = blockIdx.x; f < F; f += gridDim.x) {
+    double s[6] = {0, 0, 0, 0, 0, 0};
+    for (int64_t b = lane; b < B; b += kWave) {
+      const double* p = partial + 6 * (b * F + f);
 #pragma unroll
-    for (int j = 0; j < 6; ++j) s[j] += p[j];
-  }
+      for (int j = 0; j < 6; ++j) s[j] += p[j];
+    }
 #pragma unroll
-  for (int j = 0; j < 6; ++j) s[j] = wave_sum(s[j]);
-  if (lane == 0) {
-    gc1[2 * f] = (float)s[0];
-    gc1[2 * f + 1] = (float)s[1];
-    gk0[2 * f] = (float)s[2];
-    gk0[2 * f + 1] = (float)s[3];
-    if (gk1) {
-      gk1[2 * f] = (float)s[4];
-      gk1[2 * f + 1] = (float)s[5];
+    for (int j = 0; j < 6; ++j) s[j] = wave_sum(s[j]);
+    if (lane == 0) {
+      gc1[2 * f] = (float)s[0];
+      gc1[2 * f + 1] = (float)s[1];
+      gk0[2 * f] = (float)s[2];
+      gk0[2 * f + 1] = (float)s[3];
+      if (gk1) {
+        gk1[2 * f] = (float)s[4];
+        gk1[2 * f + 1] = (float)s[5];
+      }
     }
   }
 }
@@ -399,7 +403,8 @@ int launch_status() {
   return err == hipSuccess ? RQF_OK : (int)err;
 }
 
-dim3 btf_grid(int64_t B, int64_t F) { return dim3((unsigned)(B * ((F + kFC - 1) / kFC))); }
+int64_t btf_blocks(int64_t B, int64_t F) { return B * ((F + kFC - 1) / kFC); }
+dim3 btf_grid(int64_t B, int64_t F) { return dim3((unsigned)btf_blocks(B, F)); }
 
 // The backward's per-(batch, filter) partial sums; the forward needs none.
 size_t btf_ws(int64_t B, int64_t T, int64_t F) {
@@ -414,6 +419,7 @@ int btf_fwd(const float* c1, const float* k0, const float* k1, const float* x, f
   if (B < 0 || T < 0 || F < 0) return RQF_ERR_ARG;
   if (B * T * F == 0) return RQF_OK;
   if (!c1 || !k0 || !x || !out) return RQF_ERR_ARG;
+  if (!grid_fits(btf_blocks(B, F), kThreads)) return RQF_ERR_ARG;
   if (!aligned8(x) || !aligned8(out)) return RQF_ERR_ALIGN;
   if (k1)
     hipLaunchKernelGGL(btf_fwd_kernel<true>, btf_grid(B, F), dim3(kThreads), 0, s, c1, k0, k1, x,
@@ -433,6 +439,7 @@ int btf_bwd(const float* c1, const float* k0, const float* k1, const float* x,
   if (!c1 || !k0 || !gc1 || !gk0 || (k1 && !gk1)) return RQF_ERR_ARG;
   (void)states;  // grad_c1 comes from x (see btf_bwd_kernel)
   if (B * T > 0 && (!x || !gout || !gx)) return RQF_ERR_ARG;
+  if (B * T > 0 && !grid_fits(btf_blocks(B, F), kThreads)) return RQF_ERR_ARG;
   if (!aligned8(x) || !aligned8(states) || !aligned8(gout) || !aligned8(gx)) return RQF_ERR_ALIGN;
   const size_t need = btf_ws(B, T, F);
   if (!ws || ws_bytes < need) return RQF_ERR_WORKSPACE;
@@ -445,7 +452,7 @@ int btf_bwd(const float* c1, const float* k0, const float* k1, const float* x,
       hipLaunchKernelGGL(btf_bwd_kernel<false>, btf_grid(B, F), dim3(kThreads), 0, s, c1, k0, k1,
                          x, gout, gx, partial, T, F);
   }
-  hipLaunchKernelGGL(btf_coef_reduce_kernel, dim3((unsigned)F), dim3(kWave), 0, s, partial,
+  hipLaunchKernelGGL(btf_coef_reduce_kernel, dim3(stride_blocks(F)), dim3(kWave), 0, s, partial,
                      B * T > 0 ? B : (int64_t)0, F, gc1, gk0, gk1);
   return launch_status();
 }

@@ -158,6 +158,13 @@ __device__ __forceinline__ void load_seg(const Pass& s, uint32_t lo, c32 (&v)[LS
   for (int j = 0; j < LS; ++j)
     v[j] = REAL ? mk(buf_ldf(s.at(j), lo), 0.0f) : buf_ldc(s.at(j), lo);
 }
+
+// A wave-uniform 64-bit value pinned to scalar registers.
+__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
+  return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32)) << 32) |
+         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+}
+
 // The backward goes through global addresses: descriptors measured slower
 // there (0.47 -> 0.49 ms at config 6: three streams of 8-step segments, a
 // descriptor per step and stream).  A pass that lies wholly inside [0, T)
@@ -172,10 +179,7 @@ __device__ __forceinline__ void load_seg(const Pass& s, uint32_t lo, c32 (&v)[LS
 // from integers loses its address space and its stores become flat ones.
 __device__ __forceinline__ int64_t pass_off(const Lane& l, int64_t pt, int64_t T, int64_t F,
                                             int esz) {
-  const uint64_t o = (uint64_t)((l.b * T + pt) * F * esz);
-  return (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(o >> 32))
-                    << 32) |
-                   (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)o));
+  return (int64_t)uniform64((uint64_t)((l.b * T + pt) * F * esz));
 }
 // The lane's byte offset from its pass's base: its segment's first step and
 // its filter (filter 0 for a lane past F, whose values are never stored).
@@ -184,7 +188,7 @@ __device__ __forceinline__ uint64_t seg_off(const Lane& l, int LS, int64_t F, in
 }
 // A whole segment: base pb of the pass, lane offset lo, stp bytes per step.
 template <int LS, bool REAL>
-__device__ __forceinline__ void load_seg_w(const char* pb, uint64_t lo, uint32_t stp,
+__device__ __forceinline__ void load_seg_w(const char* pb, uint64_t lo, uint64_t stp,
                                            c32 (&v)[LS]) {
 #pragma unroll
   for (int j = 0; j < LS; ++j) {
@@ -489,8 +493,8 @@ __global__ __launch_bounds__(kThreads) void mosc_bwd_kernel(
   const int64_t npass = (T + kPass - 1) / kPass;
   constexpr int kUs = REAL ? 4 : 8;  // bytes per element of u and grad_u
   const uint64_t lo8 = seg_off(l, LS, F, 8), lou = seg_off(l, LS, F, kUs);
-  const uint32_t stp8 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(F * 8));
-  const uint32_t stpu = (uint32_t)__builtin_amdgcn_readfirstlane((int)(F * kUs));
+  const uint64_t stp8 = uniform64((uint64_t)F * 8);
+  const uint64_t stpu = uniform64((uint64_t)F * kUs);
   const char* const gyb = reinterpret_cast<const char*>(gy);
   const char* const ub = reinterpret_cast<const char*>(u);
   c32 gv[LS], gn[LS], uv[TAN ? LS : 1], un[TAN ? LS : 1];
@@ -663,22 +667,23 @@ __global__ __launch_bounds__(kWave) void mosc_coef_kernel(const double* __restri
                                                           float* __restrict__ gc1,
                                                           float* __restrict__ gc2,
                                                           float* __restrict__ gcw) {
-  const int64_t fn = blockIdx.x;  // f*N + n
   const int lane = threadIdx.x;
-  double s[4] = {0, 0, 0, 0};
-  for (int64_t b = lane; b < B; b += kWave) {
-    const double* p = part + (b * F * N + fn) * 4;
+  for (int64_t fn = blockIdx.x; fn < F * N; fn += gridDim.x) {  // fn = f*N + n
+    double s[4] = {0, 0, 0, 0};
+    for (int64_t b = lane; b < B; b += kWave) {
+      const double* p = part + (b * F * N + fn) * 4;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) s[k] += p[k];
-  }
+      for (int k = 0; k < 4; ++k) s[k] += p[k];
+    }
 #pragma unroll
-  for (int k = 0; k < 4; ++k) s[k] = wave_sum(s[k]);
-  if (lane == 0) {
-    const c64d q = mkd(s[0], s[1]), r = mkd(s[2], s[3]);
-    const c64d g2 = dconj(widen(ldc(c2, fn))), gw = dconj(widen(ldc(cw, fn)));
-    if (gc1) stc(gc1, fn, narrow(dmul(dmul(gw, g2), r)));
-    if (gc2) stc(gc2, fn, narrow(dmul(gw, q)));
-    if (gcw) stc(gcw, fn, narrow(dmul(g2, q)));
+    for (int k = 0; k < 4; ++k) s[k] = wave_sum(s[k]);
+    if (lane == 0) {
+      const c64d q = mkd(s[0], s[1]), r = mkd(s[2], s[3]);
+      const c64d g2 = dconj(widen(ldc(c2, fn))), gw = dconj(widen(ldc(cw, fn)));
+      if (gc1) stc(gc1, fn, narrow(dmul(dmul(gw, g2), r)));
+      if (gc2) stc(gc2, fn, narrow(dmul(gw, q)));
+      if (gcw) stc(gcw, fn, narrow(dmul(g2, q)));
+    }
   }
 }
 
@@ -701,12 +706,17 @@ dim3 mosc_grid(int64_t B, int64_t F) { return dim3((unsigned)(B * ((F + kFC - 1)
 
 // F <= kDescFilters keeps every pass's descriptor (at most 2048 steps of F
 // complex elements) below 2^31 bytes; wider rows run the forward with 64-bit
-// addresses (the backward always does).  The grids bound the rest: B blocks
-// per 16 filters, and one coefficient reduction per (filter, oscillator).
+// addresses (the backward always does).  The scan grids bound the rest: B
+// blocks per 16 filters, of up to kMaxBlockThreads work-items each, within
+// one dispatch's 32-bit work-item count (grid_fits).  The coefficient
+// reduction strides over the (filter, oscillator) pairs, so it takes any F*N
+// below 2^31.
 constexpr int64_t kDescFilters = 65536;
+constexpr int kMaxBlockThreads = 16 * kWave;
+static_assert(kThreads <= kMaxBlockThreads, "the backward's blocks within the grid bound");
 bool bad_shape(int64_t B, int64_t T, int64_t F, int64_t N) {
   if (B < 0 || T < 0 || F < 0 || N < 1 || N > (int64_t)1 << 20) return true;
-  return B * ((F + kFC - 1) / kFC) > INT32_MAX || F * N > INT32_MAX;
+  return !grid_fits(B * ((F + kFC - 1) / kFC), kMaxBlockThreads) || F * N > INT32_MAX;
 }
 
 // Workspace: forward, a complex (B,T,F) partial when a |y| output needs more
@@ -735,6 +745,7 @@ void launch_fwd(const float* c1, const float* c2, const float* cw, const float* 
   // it fits in 168 (complex input, 4 oscillators: 0.271 -> 0.250 ms at
   // config 6), else 8.
   constexpr int W = REAL ? 16 : (NP == 4 ? 12 : 8), W1 = REAL && NP <= 2 ? 16 : 8;
+  static_assert(W * kWave <= kMaxBlockThreads && W1 * kWave <= kMaxBlockThreads, "grid bound");
   const dim3 grid = mosc_grid(B, F), block(W * kWave), block1(W1 * kWave);
   if (cw && abs_out) {
     hipLaunchKernelGGL((mosc_fwd_kernel<NP, REAL, true, true, W, G64>), grid, block, 0, s, c1, c2, cw, u, yin, yout, T, F, N, n0);
@@ -848,7 +859,7 @@ extern "C" int rqf_multi_osc_bwd(const float* c1, const float* c2, const float* 
     }
   }
   if (coefs)
-    hipLaunchKernelGGL(mosc_coef_kernel, dim3((unsigned)(F * N)), dim3(kWave), 0, s, part,
+    hipLaunchKernelGGL(mosc_coef_kernel, dim3(stride_blocks(F * N)), dim3(kWave), 0, s, part,
                        B * T > 0 ? B : (int64_t)0, F, (int)N, c2, cw, grad_c1, grad_c2, grad_cw);
   return launch_status();
 }

@@ -315,7 +315,7 @@ extern "C" int rqf_proj_gemm(const rqf_proj_gemm_args* args, rqf_stream_t stream
   const bool vec = g.n % 2 == 0 && aligned(g.b_cplx, 16) && aligned(g.b_real, 8);
   const int64_t m_tiles = (g.m_pad + kPM - 1) / kPM, n_tiles = (g.n + kPN - 1) / kPN;
   const int64_t tiles = m_tiles * n_tiles;
-  if (tiles > 0x7fffffff) return RQF_ERR_ARG;
+  if (!grid_fits(tiles, kPThreads)) return RQF_ERR_ARG;
   hipStream_t s = (hipStream_t)stream;
   const bool fast = vec && g.n >= 2 && (2 * g.b_cplx_rows) % kPK == 0;
   if (fast)
@@ -440,23 +440,25 @@ __global__ __launch_bounds__(kL0Threads) void layer0_grads_kernel(
 
 // grad_w_stacked[f][d] = sum over the P partials (fixed order, fp64) of the
 // real parts, grad_w_stacked[F + f][d] of the imaginary parts; one wavefront
-// per (f, d), lane l adding partials l, l + 64, ...
+// per (f, d) (block fd, fd + gridDim.x, ...), lane l adding partials l,
+// l + 64, ...
 __global__ __launch_bounds__(kWave) void layer0_wpart_reduce_kernel(const float* __restrict__ wpart,
                                                                     int64_t P, int64_t F, int D,
                                                                     float* __restrict__ gw) {
-  const int64_t fd = blockIdx.x;  // f * D + d
   const int lane = threadIdx.x;
-  double sr = 0.0, si = 0.0;
-  for (int64_t p = lane; p < P; p += kWave) {
-    sr += wpart[(p * F * D + fd) * 2];
-    si += wpart[(p * F * D + fd) * 2 + 1];
-  }
-  sr = wave_sum(sr);
-  si = wave_sum(si);
-  if (lane == 0) {
-    const int64_t f = fd / D, d = fd % D;
-    gw[f * D + d] = (float)sr;
-    gw[(F + f) * D + d] = (float)si;
+  for (int64_t fd = blockIdx.x; fd < F * D; fd += gridDim.x) {  // fd = f * D + d
+    double sr = 0.0, si = 0.0;
+    for (int64_t p = lane; p < P; p += kWave) {
+      sr += wpart[(p * F * D + fd) * 2];
+      si += wpart[(p * F * D + fd) * 2 + 1];
+    }
+    sr = wave_sum(sr);
+    si = wave_sum(si);
+    if (lane == 0) {
+      const int64_t f = fd / D, d = fd % D;
+      gw[f * D + d] = (float)sr;
+      gw[(F + f) * D + d] = (float)si;
+    }
   }
 }
 
@@ -513,7 +515,7 @@ extern "C" int rqf_layer0_grads(const float* w_stacked, const float* grad_z, con
   if (!aligned(w_stacked, 4) || !aligned(grad_z, 8) || !aligned(h, 4) || !aligned(grad_h, 4) ||
       !aligned(grad_w_stacked, 4))
     return RQF_ERR_ALIGN;
-  if (layer0_blocks(n) > 0x7fffffff || F * D > 0x7fffffff) return RQF_ERR_ARG;
+  if (!grid_fits(layer0_blocks(n), kL0Threads) || F * D > 0x7fffffff) return RQF_ERR_ARG;
   float* wpart = nullptr;
   if (grad_w_stacked) {
     const size_t need = rqf_layer0_grads_workspace(F, D, n);
@@ -536,7 +538,7 @@ extern "C" int rqf_layer0_grads(const float* w_stacked, const float* grad_z, con
     launch_layer0_d<16>(w_stacked, grad_z, h, grad_h, wpart, F, d, n, vec, s);
   if (grad_w_stacked && F > 0) {
     const int64_t P = layer0_blocks(n) * (kL0Threads / kWave);
-    hipLaunchKernelGGL(layer0_wpart_reduce_kernel, dim3((unsigned)(F * D)), dim3(kWave), 0, s,
+    hipLaunchKernelGGL(layer0_wpart_reduce_kernel, dim3(stride_blocks(F * D)), dim3(kWave), 0, s,
                        wpart, P, F, d, grad_w_stacked);
   }
   const hipError_t err = hipGetLastError();

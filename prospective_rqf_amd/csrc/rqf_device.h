@@ -124,6 +124,20 @@ __device__ __forceinline__ int64_t xcd_contiguous(int64_t P, int64_t n) {
   return x * q + (x < r ? x : r) + j;
 }
 
+// A dispatch packet holds the grid size in work-items as a 32-bit value per
+// dimension: a launch of `blocks` x `threads` past 2^32 - 1 work-items would
+// run a truncated grid, with no error from the launch.  Entry points check
+// each of their grids with this before launching anything.
+__host__ __device__ constexpr bool grid_fits(int64_t blocks, int64_t threads) {
+  return blocks >= 0 && threads > 0 && blocks <= (int64_t)0xFFFFFFFF / threads;
+}
+// Blocks of a grid-stride launch over n items, one per block: at most
+// kStrideBlocks, so that it always fits.
+constexpr int64_t kStrideBlocks = (int64_t)1 << 20;
+__host__ __device__ constexpr unsigned stride_blocks(int64_t n) {
+  return (unsigned)(n < 1 ? 1 : (n < kStrideBlocks ? n : kStrideBlocks));
+}
+
 // ---------------------------------------------------------------------------
 // Raw buffer access: CDNA buffer instructions through a resource descriptor
 // (base, size in bytes).  A load at a byte offset at or past the size returns

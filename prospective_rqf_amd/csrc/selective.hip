@@ -1752,13 +1752,22 @@ __global__ __launch_bounds__(kFinishThreads) void bwd_finish_kernel(
   if (f < F) partial_reduce_at(f, lane_id(), partial, dbias, dtheta, F, B);
 }
 
+// Blocks of the finishing pass: the dd items (float4s with `vec`), then one
+// wavefront per channel.
+int64_t finish_dd_blocks(int64_t G, int64_t N, bool with_dd, bool vec) {
+  const int64_t items = with_dd ? (vec ? G * (N / 4) : G * N) : 0;
+  return (items + kFinishThreads - 1) / kFinishThreads;
+}
+int64_t finish_pr_blocks(int64_t F) {
+  return (F + kFinishThreads / kWave - 1) / (kFinishThreads / kWave);
+}
+
 void launch_finish(const float* dd_part, const int* gsplit, float* dd, int64_t G, int64_t N,
                    const double* partial, float* dbias, float* dtheta, int64_t F, int64_t B,
                    hipStream_t s) {
   const bool vec = dd_part && N % 4 == 0 && ((uintptr_t)dd & 15) == 0;
-  const int64_t items = dd_part ? (vec ? G * (N / 4) : G * N) : 0;
-  const int64_t dd_blocks = (items + kFinishThreads - 1) / kFinishThreads;
-  const int64_t pr_blocks = (F + kFinishThreads / kWave - 1) / (kFinishThreads / kWave);
+  const int64_t dd_blocks = finish_dd_blocks(G, N, dd_part != nullptr, vec);
+  const int64_t pr_blocks = finish_pr_blocks(F);
   const dim3 grid((unsigned)(dd_blocks + pr_blocks)), block(kFinishThreads);
   if (dd_blocks + pr_blocks == 0) return;
   if (vec)
@@ -1769,16 +1778,18 @@ void launch_finish(const float* dd_part, const int* gsplit, float* dd, int64_t G
                        dd_blocks, partial, dbias, dtheta, F, B);
 }
 
-// Zero-fill of n 32-bit words (graph-capture safe, unlike a memset node).
+// Zero-fill of n 32-bit words (graph-capture safe, unlike a memset node),
+// grid-stride over at most stride_blocks blocks.
 __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* __restrict__ p, int64_t n) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0u;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
 }
 
 void zero_words(void* p, int64_t nwords, hipStream_t s) {
   if (nwords > 0)
-    hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((nwords + 255) / 256)), dim3(256), 0, s,
-                       (uint32_t*)p, nwords);
+    hipLaunchKernelGGL(zero_words_kernel, dim3(stride_blocks((nwords + 255) / 256)), dim3(256), 0,
+                       s, (uint32_t*)p, nwords);
 }
 
 __global__ void wave_scan_selftest_kernel(const float* in, float* out_fwd, float* out_rev) {
@@ -1891,9 +1902,16 @@ bool fwd_narrow_blocks(bool extra_streams) {
   return !extra_streams;
 }
 
+// Logical rows of the forward's grid: the batch in kXcds chunks of
+// ceil(B / kXcds) elements, times F channels (row_id).
+int64_t fwd_blocks(const rqf_selective_inputs* in) {
+  return kXcds * in->F * ((in->B + kXcds - 1) / kXcds);
+}
+constexpr int kFwdMaxThreads = std::max(kFwdRbWaves, kFwdRbWavesRaw) * kWave;
+
 void launch_fwd(const rqf_selective_inputs* in, const float* z, const float* skip, float* raw,
                 float* act, float* entries, int chunk, int nc, bool vec, hipStream_t s) {
-  const dim3 grid((unsigned)(kXcds * in->F * ((in->B + kXcds - 1) / kXcds)));
+  const dim3 grid((unsigned)fwd_blocks(in));
   const bool narrow = fwd_narrow_blocks(act != nullptr || skip != nullptr);
   const dim3 block((narrow ? kFwdRbWavesRaw : kFwdRbWaves) * kWave);
   with_option_set(options_of(in), [&](auto oc) {
@@ -1929,6 +1947,7 @@ int selective_fwd(const rqf_selective_inputs* in, const float* z, int64_t chunk,
   int st = check_inputs(in);
   if (st) return st;
   if (!z || !entries || (!raw && !act)) return RQF_ERR_ARG;
+  if (!grid_fits(fwd_blocks(in), kFwdMaxThreads)) return RQF_ERR_ARG;
   if (!aligned8(z) || !aligned8(skip) || !aligned8(raw) || !aligned8(act) || !aligned8(entries))
     return RQF_ERR_ALIGN;
   const int nc = (int)((in->T + chunk - 1) / chunk);
@@ -2055,6 +2074,22 @@ SelWs sel_ws_layout(const rqf_selective_inputs* in, int64_t chunk, bool group_fo
   w.total = off;
   return w;
 }
+
+// Every grid a non-empty backward launches, within one dispatch's work-item
+// count: the forward that rebuilds tile entries (chunk > one tile), the
+// group form's (group, batch element) blocks or the split form's team
+// blocks, and the finishing pass (the split form's dd items, one wavefront
+// per channel).
+bool bwd_grids_fit(const rqf_selective_inputs* in, const SelWs& w, int64_t chunk) {
+  if (chunk > kBwdTile && !grid_fits(fwd_blocks(in), kFwdMaxThreads)) return false;
+  const int64_t pr = finish_pr_blocks(in->F);
+  if (w.group_form)
+    return grid_fits(in->G * in->B, kGrpWaves * kWave) && grid_fits(pr, kFinishThreads);
+  const int64_t bc = (in->B + kXcds - 1) / kXcds;
+  const int64_t dd = finish_dd_blocks(in->G, in->B * in->T, in->has_warp, false);
+  return grid_fits(kXcds * w.split_slots * bc, kTeam * kWave) &&
+         grid_fits(dd + pr, kFinishThreads);
+}
 }  // namespace
 
 extern "C" size_t rqf_selective_bwd_workspace(const rqf_selective_inputs* in, int64_t chunk) {
@@ -2083,6 +2118,7 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
       return RQF_ERR_ARG;
   }
   const SelWs w = sel_ws_layout(in, chunk, use_group_form(in, gx != nullptr));
+  if (nonempty && !bwd_grids_fit(in, w, chunk)) return RQF_ERR_ARG;
   if (workspace_bytes < w.total || (w.total && !workspace)) return RQF_ERR_WORKSPACE;
   if (!aligned8(z) || !aligned8(gy) || !aligned8(gx) || !aligned8(dz) || !aligned8(dzw))
     return RQF_ERR_ALIGN;

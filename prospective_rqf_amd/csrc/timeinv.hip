@@ -625,24 +625,25 @@ __global__ __launch_bounds__(kWave) void coef_reduce_kernel(const double* __rest
                                                             float* __restrict__ gc1,
                                                             float* __restrict__ gk0,
                                                             float* __restrict__ gk1) {
-  const int64_t f = blockIdx.x;
   const int lane = threadIdx.x;
-  double s[6] = {0, 0, 0, 0, 0, 0};
-  for (int64_t m = lane; m < M; m += kWave) {
-    const double* p = partial + 6 * (f * stride_f + m * stride_m);
+  for (int64_t f = blockIdx.x; f < F; f += gridDim.x) {
+    double s[6] = {0, 0, 0, 0, 0, 0};
+    for (int64_t m = lane; m < M; m += kWave) {
+      const double* p = partial + 6 * (f * stride_f + m * stride_m);
 #pragma unroll
-    for (int j = 0; j < 6; ++j) s[j] += p[j];
-  }
+      for (int j = 0; j < 6; ++j) s[j] += p[j];
+    }
 #pragma unroll
-  for (int j = 0; j < 6; ++j) s[j] = wave_sum(s[j]);
-  if (lane == 0) {
-    gc1[2 * f] = (float)s[0];
-    gc1[2 * f + 1] = (float)s[1];
-    gk0[2 * f] = (float)s[2];
-    gk0[2 * f + 1] = (float)s[3];
-    if (gk1) {
-      gk1[2 * f] = (float)s[4];
-      gk1[2 * f + 1] = (float)s[5];
+    for (int j = 0; j < 6; ++j) s[j] = wave_sum(s[j]);
+    if (lane == 0) {
+      gc1[2 * f] = (float)s[0];
+      gc1[2 * f + 1] = (float)s[1];
+      gk0[2 * f] = (float)s[2];
+      gk0[2 * f + 1] = (float)s[3];
+      if (gk1) {
+        gk1[2 * f] = (float)s[4];
+        gk1[2 * f + 1] = (float)s[5];
+      }
     }
   }
 }
@@ -671,6 +672,7 @@ int fbt_fwd(const float* c1, const float* t0, const float* t1, Drive drv, const 
       !aligned8(raw) || !aligned8(act) || !aligned8(carry))
     return RQF_ERR_ALIGN;
   if (skip && !act) return RQF_ERR_ARG;
+  if (!grid_fits(R, kTfWaves * kWave)) return RQF_ERR_ARG;
   const int64_t nc = (T + kTiTile - 1) / kTiTile;
   const bool vec = T % 2 == 0 && (l0 ? T % 4 == 0 && aligned16(drv.x) : aligned16(drv.z)) &&
                    aligned16(skip) && aligned16(raw) && aligned16(act);
@@ -739,26 +741,30 @@ int fbt_bwd(const float* c1, const float* t0, const float* t1, Drive drv, const 
   if (!aligned8(drv.z) || !aligned8(drv.wz) || !aligned4(drv.x) || !aligned8(raw) ||
       !aligned8(gout) || !aligned8(gz))
     return RQF_ERR_ALIGN;
+  const int64_t R = F * B;
+  // the row-block backward on 2 KB-aligned rows, the per-row one otherwise
+  const bool rowblock = T % kTiTile == 0;
+  if (R > 0 && T > 0 &&
+      !(rowblock ? grid_fits(R, kRbWaves * kWave)
+                 : grid_fits((R + kTiWaves - 1) / kTiWaves, kTiWaves * kWave)))
+    return RQF_ERR_ARG;
   const size_t need = fbt_ws(F, B);
   if (need && (!ws || ws_bytes < need)) return RQF_ERR_WORKSPACE;
   double* partial = (double*)ws;
-  const int64_t R = F * B;
   if (R > 0 && T > 0) {
     const int64_t nc = (T + kTiTile - 1) / kTiTile;
     const bool vec = T % 2 == 0 && (l0 ? T % 4 == 0 && aligned16(drv.x) : aligned16(drv.z)) &&
                      aligned16(raw) && aligned16(gout) && aligned16(gz);
-    // the row-block backward on 2 KB-aligned rows, the per-row one otherwise
-    const bool rowblock = T % kTiTile == 0;
     if (l0)
       launch_fbt_bwd_kernels<true>(rowblock, vec, c1, t0, t1, drv, raw, carry, gout, mask, gz,
                                    partial, F, B, T, nc, s);
     else
       launch_fbt_bwd_kernels<false>(rowblock, vec, c1, t0, t1, drv, raw, carry, gout, mask, gz,
                                     partial, F, B, T, nc, s);
-    hipLaunchKernelGGL(coef_reduce_kernel, dim3((unsigned)F), dim3(kWave), 0, s,
+    hipLaunchKernelGGL(coef_reduce_kernel, dim3(stride_blocks(F)), dim3(kWave), 0, s,
                        partial, F, B, B, (int64_t)1, gc1, gt0, gt1);
   } else {
-    hipLaunchKernelGGL(coef_reduce_kernel, dim3((unsigned)F), dim3(kWave), 0, s,
+    hipLaunchKernelGGL(coef_reduce_kernel, dim3(stride_blocks(F)), dim3(kWave), 0, s,
                        partial, F, (int64_t)0, B, (int64_t)1, gc1, gt0, gt1);
   }
   return launch_status();

@@ -132,15 +132,17 @@ def test_noalloc_rejects_oversized_problems_before_any_device_call(built_lib):
     assert lib.rqf_fbt_recompute_bwd_noalloc(*args, -1, 1, 16, None) == -1
 
 
-def test_multi_osc_rejects_grids_past_int32(built_lib):
-    """The multi-oscillator entry points take any number of filters (past
-    65536 the forward addresses its passes with 64-bit addresses); only a
-    grid past 2^31 - 1 blocks is refused, with RQF_ERR_ARG (-1; and the
-    workspace query 0) before looking at a pointer or calling HIP."""
+def test_multi_osc_rejects_oversized_grids(built_lib):
+    """The multi-oscillator entry points take any number of filters whose
+    grid fits one dispatch (past 65536 the forward addresses its passes with
+    64-bit addresses).  Grids past 2^32 - 1 work-items (B * ceil(F / 16) past
+    4194303 blocks of up to 1024 threads), and F * N past 2^31 - 1, are
+    refused with RQF_ERR_ARG (-1; and the workspace query 0) before looking at
+    a pointer or calling HIP.  The exact bound is in test_grid_limits.py."""
     lib = _lib.load()
     assert lib.rqf_multi_osc_workspace(2, 100, 65537, 4, 1) > 0
     assert lib.rqf_multi_osc_workspace(2, 100, 65536, 4, 1) > 0
-    big_b = 2 ** 31 // 4 + 1  # B * ceil(F / 16) blocks past 2^31 - 1 with F = 64
+    big_b = 2 ** 31 // 4 + 1  # B * ceil(F / 16) = 2^31 + 4 blocks with F = 64
     assert lib.rqf_multi_osc_workspace(big_b, 1, 64, 1, 1) == 0
     assert lib.rqf_multi_osc_fwd(None, None, None, None, 0, None, 0, big_b, 1, 64, 1, None, 0,
                                  None) == -1

@@ -2118,7 +2118,9 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
       return RQF_ERR_ARG;
   }
   const SelWs w = sel_ws_layout(in, chunk, use_group_form(in, gx != nullptr));
-  if (nonempty && !bwd_grids_fit(in, w, chunk)) return RQF_ERR_ARG;
+  if (nonempty ? !bwd_grids_fit(in, w, chunk)
+               : !grid_fits(finish_pr_blocks(in->F), kFinishThreads))
+    return RQF_ERR_ARG;
   if (workspace_bytes < w.total || (w.total && !workspace)) return RQF_ERR_WORKSPACE;
   if (!aligned8(z) || !aligned8(gy) || !aligned8(gx) || !aligned8(dz) || !aligned8(dzw))
     return RQF_ERR_ALIGN;

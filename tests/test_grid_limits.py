@@ -103,6 +103,12 @@ def test_selective(lib, monkeypatch):
         rc = lib.rqf_selective_bwd(ctypes.byref(s), P, P, 256, P, P, 1, 0, P, P, P, P, P, P, P,
                                    P, WS, None)
         assert rc == ERR_ARG, (warp, rc)
+    # an empty backward (T = 0) still reduces dbias / dtheta, one wavefront
+    # per channel in 4-wavefront blocks
+    s = _selective(4 * ((2**32 - 1) // 256 + 1), 1, 0, 1)
+    rc = lib.rqf_selective_bwd(ctypes.byref(s), P, P, 256, P, P, 1, 0, P, P, P, P, P, P, P, P,
+                               WS, None)
+    assert rc == ERR_ARG, rc
 
 
 def test_layer0_grads(lib):

@@ -46,7 +46,7 @@ typedef void *rqf_stream_t; /* hipStream_t */
 
 enum {
   RQF_OK = 0,
-  RQF_ERR_ARG = -1,       /* null pointer, bad shape, or bad chunk */
+  RQF_ERR_ARG = -1,       /* null pointer, bad shape or chunk, or an oversized grid */
   RQF_ERR_WORKSPACE = -2, /* workspace missing or too small */
   RQF_ERR_ALIGN = -3,     /* a tensor is not 8-byte aligned */
   RQF_ERR_SCRATCH = -4    /* problem exceeds the static scratch of a no-allocation entry */

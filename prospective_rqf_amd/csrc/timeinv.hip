@@ -886,7 +886,8 @@ extern "C" const char* rqf_error_string(int code) {
     case RQF_OK:
       return "ok";
     case RQF_ERR_ARG:
-      return "invalid argument (null pointer, shape or chunk)";
+      return "invalid argument (null pointer, shape, chunk, or a grid past one dispatch's "
+             "2^32 - 1 work-items)";
     case RQF_ERR_WORKSPACE:
       return "workspace missing or too small";
     case RQF_ERR_ALIGN:

@@ -93,6 +93,10 @@ def _args():
                          "[Wr; Wi] projection of the waveform on the MFMA projection GEMM, the "
                          "recompute scan, and in the backward grad_h and grad_[Wr; Wi] besides "
                          "the coefficient gradients")
+    ap.add_argument("--chunk", type=int, default=0,
+                    help="configs 3 and 4: the selective scans' chunk (default 256, the "
+                         "reference's min(256, next_pow2(T)); a longer one makes the backward "
+                         "rebuild its 256-step tile entries from the chunk entries)")
     ap.add_argument("--act-only", action="store_true",
                     help="config 3 with the act-only contract (no raw output, no gy)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -190,7 +194,9 @@ def plan_selective(cfg, args, dev):
     if args.seq_len:
         T = args.seq_len
         name += f" [sequence length overridden to {T}]"
-    chunk = 256
+    chunk = args.chunk or 256
+    if args.chunk:
+        name += f" [chunk {chunk}: the backward rebuilds its tile entries first]"
     g = torch.Generator(device=dev).manual_seed(1)
     state = {}
     layer_inputs = []
@@ -971,7 +977,7 @@ def main():
     # (B,T,F) layout of config 2, so other variants report none
     key = f"config{cfg}" + (" (B,T,F)" if cfg == 2 and args.layout == "btf" else "")
     variant = (args.batch or args.seq_len or args.stack != "none" or args.act_only or
-               (cfg == 2 and args.layer0))
+               args.chunk or (cfg == 2 and args.layer0))
     traffic = (None if variant else
                traffic_from_table(key, dom) or traffic_from_table(key, entry))
     result = {

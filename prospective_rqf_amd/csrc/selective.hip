@@ -1936,6 +1936,91 @@ void launch_fwd(const rqf_selective_inputs* in, const float* z, const float* ski
 
 constexpr int kBwdTile = kWave * kBwdK;
 
+// Entry states of every backward tile for a call whose chunk is longer than
+// one tile.  The forward kept the state entering each chunk.  One wavefront
+// per (row, chunk) starts from it and replays the chunk's tiles except the
+// last, whose exit is the next chunk's entry.  It records the state entering
+// each tile.  A tile is the coefficients of its steps, the lanes' composed
+// maps and one wave scan; its exit is the scan's total applied to the carry.
+// Against a full forward, a chunk of c tiles reads and computes c - 1 of them
+// and writes no outputs, and its wavefronts run every (row, chunk) at once.
+// Every replayed tile ends before T (its exit enters a tile that exists), so
+// no tile is ragged.
+constexpr int kRebuildWaves = 4;
+template <int O, bool VEC>
+__global__ __launch_bounds__(kRebuildWaves* kWave) void selective_rebuild_kernel(
+    const rqf_selective_inputs pin, const float* __restrict__ z,
+    const float* __restrict__ entries, int chunk, int nc, float* __restrict__ tile_entries,
+    int nt, int64_t tasks) {
+  constexpr int K = kBwdK, TILE = kBwdTile;
+  const rqf_selective_inputs p = with_options<O>(pin);
+  __shared__ float4 s_io[kRebuildWaves][TILE / 2];
+  const int lane = lane_id();
+  const int64_t task = (int64_t)blockIdx.x * kRebuildWaves + wave_id();
+  if (task >= tasks) return;  // wave-uniform
+  const int64_t row = task / nc;
+  const int ci = (int)(task - row * nc);
+  const int64_t f = row / p.B, b = row - f * p.B;
+  const Chan c = load_chan(p, f);
+  FwdRow r;
+  r.T = (int)p.T;
+  const int T = r.T;
+  const int64_t base = row * T;
+  r.zr = z + 2 * base;
+  r.gr = p.has_gamma ? p.gamma_logits + base : nullptr;
+  r.wr = p.has_write ? p.write_logits + base : nullptr;
+  r.dr = p.has_warp ? p.warp_logits + (group_of(p, f) * p.B + b) * T : nullptr;
+  r.io = &s_io[wave_id()][0];
+  const int per = chunk / TILE;  // tiles per chunk
+  const int tile0 = ci * per;
+  c32 y = mk(entries[2 * (row * nc + ci)], entries[2 * (row * nc + ci) + 1]);
+  float* te = tile_entries + 2 * row * nt;
+  if (lane == 0) {
+    te[2 * tile0] = y.r;
+    te[2 * tile0 + 1] = y.i;
+  }
+  for (int j = 0; j + 1 < per && tile0 + j + 1 < nt; ++j) {
+    const int t0 = (tile0 + j) * TILE;
+    const c32 zlast = t0 > 0 ? mk(r.zr[2 * (t0 - 1)], r.zr[2 * (t0 - 1) + 1]) : mk(0.0f, 0.0f);
+    FwdIn<K> in;
+    c32 A[K], u[K];
+    fwd_load<K, VEC, false>(p, r, t0, lane, in);
+    fwd_steps<K, false>(p, c, T, t0, lane, in, zlast, A, u);
+    c32 P = A[0], s = u[0];
+#pragma unroll
+    for (int k = 1; k < K; ++k) {
+      s = cmad(A[k], s, u[k]);
+      P = cmul(A[k], P);
+    }
+    wave_scan_fwd(P, s);  // lane 63: the whole tile's map
+    y = cmad(readlane(P, kWave - 1), y, readlane(s, kWave - 1));
+    if (lane == 0) {
+      te[2 * (tile0 + j + 1)] = y.r;
+      te[2 * (tile0 + j + 1) + 1] = y.i;
+    }
+  }
+}
+
+int64_t rebuild_tasks(const rqf_selective_inputs* in, int nc) { return in->F * in->B * nc; }
+int64_t rebuild_blocks(const rqf_selective_inputs* in, int nc) {
+  return (rebuild_tasks(in, nc) + kRebuildWaves - 1) / kRebuildWaves;
+}
+
+void launch_rebuild(const rqf_selective_inputs* in, const float* z, const float* entries,
+                    int chunk, int nc, float* tile_entries, int nt, bool vec, hipStream_t s) {
+  const dim3 grid((unsigned)rebuild_blocks(in, nc)), block(kRebuildWaves * kWave);
+  const int64_t tasks = rebuild_tasks(in, nc);
+  with_option_set(options_of(in), [&](auto oc) {
+    constexpr int O = decltype(oc)::value;
+    if (vec)
+      hipLaunchKernelGGL((selective_rebuild_kernel<O, true>), grid, block, 0, s, *in, z, entries,
+                         chunk, nc, tile_entries, nt, tasks);
+    else
+      hipLaunchKernelGGL((selective_rebuild_kernel<O, false>), grid, block, 0, s, *in, z, entries,
+                         chunk, nc, tile_entries, nt, tasks);
+  });
+}
+
 }  // namespace
 
 namespace {
@@ -2076,12 +2161,13 @@ SelWs sel_ws_layout(const rqf_selective_inputs* in, int64_t chunk, bool group_fo
 }
 
 // Every grid a non-empty backward launches, within one dispatch's work-item
-// count: the forward that rebuilds tile entries (chunk > one tile), the
-// group form's (group, batch element) blocks or the split form's team
-// blocks, and the finishing pass (the split form's dd items, one wavefront
-// per channel).
+// count: the tile-entry rebuild (chunk > one tile), the group form's (group,
+// batch element) blocks or the split form's team blocks, and the finishing
+// pass (the split form's dd items, one wavefront per channel).
 bool bwd_grids_fit(const rqf_selective_inputs* in, const SelWs& w, int64_t chunk) {
-  if (chunk > kBwdTile && !grid_fits(fwd_blocks(in), kFwdMaxThreads)) return false;
+  const int nc = (int)((in->T + chunk - 1) / chunk);
+  if (chunk > kBwdTile && !grid_fits(rebuild_blocks(in, nc), kRebuildWaves * kWave))
+    return false;
   const int64_t pr = finish_pr_blocks(in->F);
   if (w.group_form)
     return grid_fits(in->G * in->B, kGrpWaves * kWave) && grid_fits(pr, kFinishThreads);
@@ -2133,12 +2219,13 @@ extern "C" int rqf_selective_bwd(const rqf_selective_inputs* in, const float* z,
     const float* ent = entries;
     int ent_chunk = chunk_int(chunk), nc = (int)((T + chunk - 1) / chunk);
     if (chunk > kBwdTile) {
-      // Entry states at every backward tile: replay the forward once.
+      // Entry states at every backward tile, replayed from the chunk entries.
       float* te = (float*)(ws + w.tile_entries);
-      ent_chunk = kBwdTile;
-      nc = (int)((T + kBwdTile - 1) / kBwdTile);
-      launch_fwd(in, z, nullptr, nullptr, nullptr, te, ent_chunk, nc, vec, s);
+      const int nt = (int)((T + kBwdTile - 1) / kBwdTile);
+      launch_rebuild(in, z, entries, ent_chunk, nc, te, nt, vec_ok(in, {z}), s);
       ent = te;
+      ent_chunk = kBwdTile;
+      nc = nt;
     }
     BwdOut o;
     o.dz = dz;

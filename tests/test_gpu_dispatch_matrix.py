@@ -96,3 +96,18 @@ def test_team_table_without_lds_staging(F, G):
     print(f"case: team table F={F} G={G}", flush=True)
     case = dict(CASE_ALL, warp="grouped")
     run_case(F, 1, 12, case, chunk=256, G=G, seed=F + G, prospective=True, gamma_horizon=False)
+
+
+@pytest.mark.parametrize("name", list(SETS))
+@pytest.mark.parametrize("T,chunk", [(1024, 512), (1023, 512), (1024, 2048), (700, 1024)])
+def test_tile_entry_rebuild_variants(monkeypatch, name, T, chunk):
+    """A chunk longer than the backward's 256-step tile: the backward first
+    rebuilds the state entering every tile from the forward's chunk entries
+    (selective_rebuild_kernel, compiled per option set and row layout).
+    float4 rows (T % 4 == 0) and element rows; several chunks, one chunk
+    longer than the row, a ragged last chunk."""
+    print(f"case: tile-entry rebuild {name} T={T} chunk={chunk}", flush=True)
+    case, opts = SETS[name]
+    monkeypatch.setenv("RQF_BWD_FORM", "split")
+    run_case(7, 2, T, case, truncated=False, activate=True, write_raw=True, chunk=chunk, G=3,
+             seed=T + chunk + len(name), **opts)

@@ -118,8 +118,9 @@ def selective_layer_scan(
     """Complex ``(I,B,T)`` selective layer on the HIP kernels.
 
     Same signature, validation and return convention as the reference.  Inputs
-    the kernels cannot serve raise ``RuntimeError``: the caller's reference
-    path handles them.
+    the kernels cannot serve raise ``RuntimeError``; the caller keeps its own
+    ``reference_layer_scan`` for those (the reference routes them there,
+    selective_scan.py:190-212).
 
     ``skip=True`` (not in the reference's signature) returns ``(raw + x,
     act + x)``: the encoder's residual connection (pure.py:486-496), added in

@@ -1,6 +1,7 @@
 """GPU parity with the trained coefficients of the reference's packaged checkpoints.
 
-Every RQF block of the 60 Pure RQF / RQF-S4 checkpoints (pretrained/, README.md:172-240)
+Every RQF block of the 60 Pure RQF / RQF-S4 checkpoints (the reference's pretrained/, listed
+in the reference's README.md:172-240)
 is run through the scan its model calls, with the coefficients its trained
 parameters give (prospective_rqf_amd/coefficients.py, rounded to complex64 as the
 callers do before the scan: pure.py:225-232, block.py:710-716):

@@ -1962,7 +1962,7 @@ __global__ __launch_bounds__(kRebuildWaves* kWave) void selective_rebuild_kernel
   const int ci = (int)(task - row * nc);
   const int64_t f = row / p.B, b = row - f * p.B;
   const Chan c = load_chan(p, f);
-  FwdRow r;
+  FwdRow r{};  // inputs only: no outputs, skip or entries are written through it
   r.T = (int)p.T;
   const int T = r.T;
   const int64_t base = row * T;

@@ -47,7 +47,7 @@ def _args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5, 6, 7],
                     help="1-5: BASELINE.json configs; 6: multi-oscillator C-weighted scan; "
                          "7: fused |y| readout scan")

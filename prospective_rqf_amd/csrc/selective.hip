@@ -460,13 +460,14 @@ __device__ __forceinline__ void fwd_emit(const FwdRow& r, int t0, int lane, c32 
 // row per wavefront (K = 4); row blocks of 2 / 4 / 8 / 16 waves: 1.765 /
 // 1.729 / 1.688 / - (K = 4), 8 waves with K = 8: 1.644, 16 waves with K = 8:
 // 1.753, 4 waves with K = 16: 1.701; without the LDS transpose 1.837.
-// Calls that write raw only (24 B per element instead of 32) run blocks of
-// kFwdRbWavesRaw = 4 wavefronts: their arithmetic weighs more against their
-// streams, and twice as many independent blocks per CU overlap one block's
-// barrier and replay with another's loads.  Config 4 (T = 4096, K = 8),
-// measured on one box: raw-only layer 1 0.352 -> 0.320 ms with 4 waves;
-// raw+act layer 0 0.403 ms with 8 against 0.425 with 4, config 3 1.668
-// against 1.718.
+// Calls that write one complex output, raw or act (24 B per element instead
+// of 32), run blocks of kFwdRbWavesRaw = 4 wavefronts: their arithmetic
+// weighs more against their streams, and twice as many independent blocks
+// per CU overlap one block's barrier and replay with another's loads.
+// Config 4 (T = 4096, K = 8), measured on one box: raw-only layer 1 0.352 ->
+// 0.320 ms with 4 waves; raw+act layer 0 0.403 ms with 8 against 0.425 with
+// 4, config 3 1.668 against 1.718; config 3's act-only contract 1.314 ->
+// 1.282 ms with 4.
 #ifndef RQF_FWD_RB_WAVES
 #define RQF_FWD_RB_WAVES 8
 #endif
@@ -1891,8 +1892,10 @@ int grp_force_timeout() {
   return e && !std::strcmp(e, "1") ? 1 : 0;
 }
 
-// Forward block size: kFwdRbWavesRaw wavefronts for calls that stream only z,
-// the logits and raw; kFwdRbWaves when act or a skip tensor adds streams.
+// Forward block size: kFwdRbWavesRaw wavefronts for calls that stream z, the
+// logits and one complex output (raw or act); kFwdRbWaves when both outputs
+// or a skip tensor add streams.  The act-only contract at config 3's shape,
+// rotated runs on one box: 1.314 -> 1.282 ms with the narrow blocks.
 // RQF_FWD_WAVES=narrow|wide forces one (tests and tuning).
 bool fwd_narrow_blocks(bool extra_streams) {
   if (const char* e = std::getenv("RQF_FWD_WAVES")) {
@@ -1912,7 +1915,7 @@ constexpr int kFwdMaxThreads = std::max(kFwdRbWaves, kFwdRbWavesRaw) * kWave;
 void launch_fwd(const rqf_selective_inputs* in, const float* z, const float* skip, float* raw,
                 float* act, float* entries, int chunk, int nc, bool vec, hipStream_t s) {
   const dim3 grid((unsigned)fwd_blocks(in));
-  const bool narrow = fwd_narrow_blocks(act != nullptr || skip != nullptr);
+  const bool narrow = fwd_narrow_blocks((raw != nullptr && act != nullptr) || skip != nullptr);
   const dim3 block((narrow ? kFwdRbWavesRaw : kFwdRbWaves) * kWave);
   with_option_set(options_of(in), [&](auto oc) {
     constexpr int O = decltype(oc)::value;

@@ -144,12 +144,13 @@ def test_automatic_and_large_chunks(T, chunk, truncated):
     run_case(4, 3, T, CASE_LOG, truncated=truncated, chunk=chunk, seed=T + chunk)
 
 
-@pytest.mark.parametrize("outputs", [(False, True), (True, True)])
+@pytest.mark.parametrize("outputs", [(False, True), (True, False), (True, True)])
 @pytest.mark.parametrize("T", [511, 2047, 2048, 2049, 4096, 4097, 6000])
 @pytest.mark.parametrize("blocks", ["narrow", "wide"])
 def test_forward_block_sizes(monkeypatch, blocks, T, outputs):
     """Both forward row-block sizes (4 and 8 wavefronts, super-tiles of 2048 and
-    4096 steps) under both output contracts, across super-tile edges."""
+    4096 steps) under the raw-only, act-only and raw+act output contracts,
+    across super-tile edges."""
     print(f"case: blocks={blocks} T={T} outputs={outputs}", flush=True)
     monkeypatch.setenv("RQF_FWD_WAVES", blocks)
     run_case(3, 2, T, CASE_ALL, activate=outputs[0], write_raw=outputs[1], chunk=256,

@@ -171,13 +171,31 @@ _raw_stream = torch._C._cuda_getCurrentRawStream
 
 
 def require_device(*tensors: torch.Tensor | None) -> None:
-    """Every kernel input must live on a HIP device; raise otherwise."""
+    """Every kernel input must live on one HIP device, the current one (the
+    library launches there, on torch's current stream of the inputs' device);
+    raise otherwise, before any pointer reaches a kernel."""
+    dev = None
     for t in tensors:
-        if t is not None and not t.is_cuda:
+        if t is None:
+            continue
+        if not t.is_cuda:
             raise RQFError(
                 "prospective_rqf_amd kernels run on HIP devices only; got a tensor on "
                 f"{t.device}"
             )
+        d = t.get_device()
+        if dev is None:
+            dev = d
+        elif d != dev:
+            raise RQFError(f"kernel inputs on different devices: cuda:{dev} and cuda:{d}")
+    if dev is not None and dev != _current_device():
+        raise RQFError(
+            f"kernel inputs on cuda:{dev} while cuda:{_current_device()} is current; "
+            f"call under torch.cuda.device({dev})"
+        )
+
+
+_current_device = torch._C._cuda_getDevice
 
 
 def workspace(nbytes: int, device) -> torch.Tensor | None:

@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 import torch
 
+from prospective_rqf_amd import _lib
 from prospective_rqf_amd import multi_osc_scan as mo
 from prospective_rqf_amd.chunked_scan_kernel import (
     _chunked_prospective_backward_raw,
@@ -168,3 +169,29 @@ def test_valid_arguments_pass_validation_and_reach_the_device_check():
     for call in calls:
         with pytest.raises(RQFError):
             call()
+
+
+class _OnDevice:
+    """Stand-in for a device tensor: only what require_device reads."""
+
+    is_cuda = True
+
+    def __init__(self, index):
+        self.index = index
+
+    def get_device(self):
+        return self.index
+
+
+def test_device_check_rejects_mixed_and_non_current_devices(monkeypatch):
+    """Inputs on two devices, or on a device that is not the current one, are
+    refused before any pointer reaches a kernel; one device that is current
+    passes, and None entries (absent optional inputs) are skipped."""
+    monkeypatch.setattr(_lib, "_current_device", lambda: 0)
+    _lib.require_device(_OnDevice(0), None, _OnDevice(0))
+    with pytest.raises(_lib.RQFError, match="different devices"):
+        _lib.require_device(_OnDevice(0), _OnDevice(1))
+    with pytest.raises(_lib.RQFError, match="is current"):
+        _lib.require_device(_OnDevice(1), None, _OnDevice(1))
+    with pytest.raises(_lib.RQFError, match="HIP devices only"):
+        _lib.require_device(_OnDevice(0), torch.zeros(1))

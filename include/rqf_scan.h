@@ -26,6 +26,8 @@
  *     selective forwards take up to 8388607 rows (F * B, rounded up per XCD
  *     chunk of the batch).  Reductions over filters or channels stride, so
  *     they take any size.
+ *   - Row length: the selective scans take T < 2^30 steps (RQF_ERR_ARG
+ *     otherwise); the time-invariant and multi-oscillator scans take any T.
  *   - Results are deterministic: coefficient gradients are reduced from
  *     per-row partial sums in a fixed order (no floating-point atomics).
  *   - Calls are reentrant.  No mutable global state exists, except for the

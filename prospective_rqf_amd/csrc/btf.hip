@@ -97,12 +97,6 @@ __device__ __forceinline__ void load_seg(const float* __restrict__ p, const Lane
   }
 }
 
-// A wave-uniform 64-bit value pinned to scalar registers.
-__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
-  return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32)) << 32) |
-         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
-}
-
 // A pass that lies wholly inside [0, T) is addressed from a wave-uniform
 // base per step (scalar arithmetic) plus the lane's fixed offset: one 64-bit
 // add per element and no test, where load_seg multiplies and tests each one.

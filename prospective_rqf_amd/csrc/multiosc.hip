@@ -159,12 +159,6 @@ __device__ __forceinline__ void load_seg(const Pass& s, uint32_t lo, c32 (&v)[LS
     v[j] = REAL ? mk(buf_ldf(s.at(j), lo), 0.0f) : buf_ldc(s.at(j), lo);
 }
 
-// A wave-uniform 64-bit value pinned to scalar registers.
-__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
-  return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32)) << 32) |
-         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
-}
-
 // The backward goes through global addresses: descriptors measured slower
 // there (0.47 -> 0.49 ms at config 6: three streams of 8-step segments, a
 // descriptor per step and stream).  A pass that lies wholly inside [0, T)

@@ -317,6 +317,13 @@ __device__ __forceinline__ float uniform(float v) {
   return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
 }
 __device__ __forceinline__ c32 uniform(c32 v) { return mk(uniform(v.r), uniform(v.i)); }
+// A wave-uniform 64-bit value pinned to scalar registers.  Pass byte offsets
+// through it, not pointers: a pointer rebuilt from integers loses its
+// address space, and its stores become flat ones.
+__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
+  return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32)) << 32) |
+         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+}
 
 // Powers for wave_scan_fwd_pow: lane i covers lanes 16*(i/16)..i before the
 // first cross-row step and 32*(i/32)..i before the second.

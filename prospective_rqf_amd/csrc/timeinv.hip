@@ -57,6 +57,15 @@ __device__ __forceinline__ c32 mask_by(c32 g, c32 raw) {
   return mk(raw.r > 0.0f ? g.r : 0.0f, raw.i > 0.0f ? g.i : 0.0f);
 }
 
+// A complex row advanced to step t0 (wave-uniform), its 64-bit offset pinned
+// to scalar registers: the LDS-transposed tile I/O then addresses each lane
+// from a scalar base plus a 32-bit offset, for rows of any length (a 32-bit
+// step offset would overflow past 2^30 steps).
+template <class P>
+__device__ __forceinline__ P* at_step(P* row, int64_t t0) {
+  return row + (int64_t)uniform64((uint64_t)(2 * t0));
+}
+
 // VEC: T even and 16-byte aligned rows: a lane's K steps are all in or all out
 // of range when T % K == 0; otherwise the tail uses guarded scalar access.
 template <bool VEC>
@@ -147,7 +156,7 @@ __device__ __forceinline__ void drive_tile(const RowDrive& r, int64_t t0, int64_
       for (int k = 0; k < K; ++k) v[k] = tb + k < T ? cscale(r.xr[tb + k], r.wz) : mk(0.0f, 0.0f);
     }
   } else if (full && LDS) {
-    load_c_lds<K>(r.zr, (int)t0, lane, io, v);
+    load_c_lds<K>(at_step(r.zr, t0), 0, lane, io, v);
   } else if (full) {
 #pragma unroll
     for (int j = 0; j < K / 2; ++j) {
@@ -256,7 +265,7 @@ __global__ __launch_bounds__(kTfWaves* kWave) void fbt_fwd_rb_kernel(
       }
       if (rawr) {
         if (full) {
-          store_c_lds<K>(rawr, (int)t0, lane, io, out);
+          store_c_lds<K>(at_step(rawr, t0), 0, lane, io, out);
         } else {
 #pragma unroll
           for (int k = 0; k < K; ++k)
@@ -269,7 +278,7 @@ __global__ __launch_bounds__(kTfWaves* kWave) void fbt_fwd_rb_kernel(
         if (skr) {
           c32 sk[K];
           if (full) {
-            load_c_lds<K>(skr, (int)t0, lane, io, sk);
+            load_c_lds<K>(at_step(skr, t0), 0, lane, io, sk);
           } else {
 #pragma unroll
             for (int k = 0; k < K; ++k) sk[k] = (tb + k < T) ? ldc(skr, tb + k) : mk(0.0f, 0.0f);
@@ -278,7 +287,7 @@ __global__ __launch_bounds__(kTfWaves* kWave) void fbt_fwd_rb_kernel(
           for (int k = 0; k < K; ++k) out[k] = cadd(out[k], sk[k]);
         }
         if (full) {
-          store_c_lds<K>(actr, (int)t0, lane, io, out);
+          store_c_lds<K>(at_step(actr, t0), 0, lane, io, out);
         } else {
 #pragma unroll
           for (int k = 0; k < K; ++k)
@@ -327,7 +336,7 @@ template <int K>
 __device__ __forceinline__ void ld_tile(const float* __restrict__ row, int64_t t0, int64_t tb,
                                         int64_t T, int lane, bool full, float4* io, c32 (&v)[K]) {
   if (full) {
-    load_c_lds<K>(row, (int)t0, lane, io, v);
+    load_c_lds<K>(at_step(row, t0), 0, lane, io, v);
   } else {
 #pragma unroll
     for (int k = 0; k < K; ++k) v[k] = (tb + k < T) ? ldc(row, tb + k) : mk(0.0f, 0.0f);
@@ -337,7 +346,7 @@ template <int K>
 __device__ __forceinline__ void st_tile(float* __restrict__ row, int64_t t0, int64_t tb, int64_t T,
                                         int lane, bool full, float4* io, const c32 (&v)[K]) {
   if (full) {
-    store_c_lds<K>(row, (int)t0, lane, io, v);
+    store_c_lds<K>(at_step(row, t0), 0, lane, io, v);
   } else {
 #pragma unroll
     for (int k = 0; k < K; ++k)
